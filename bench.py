@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""Benchmark of the three recurrent operators on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+A step is one SelectiveScanFn call over the Mamba-2.8B-layer workload
+(batch 8, d_inner 5120, seqlen 2048, dstate 16, variable B/C, softplus, D,
+delta_bias, z present), inputs resident in HBM.  W untimed steps, then K
+timed steps bracketed by torch.cuda.synchronize(); rank 0 prints one JSON
+line on stdout (progress goes to stderr).  GatedDeltaNet2Fn (4 x 4096 x 16
+heads, dk = dv = 128, with initial state) and Mamba3SisoFn (4 x 4096 x 32
+heads, P = 64, N = 128) are timed the same way and reported under "ops".
+
+Throughput is tokens/s = batch * seqlen / time; the roofline figures use the
+algorithmic bytes of xmetai_onnx_plugins.workloads (unique input bytes the
+output depends on + output bytes) over the HIP-event time of the kernel(s).
+The CPU baseline is the NumPy fp32 sequential recurrence of oracle/ (the
+reference CPU path) on a bounded sample of the same workload, timed on this
+host, scaled to the full workload by its (linear) cost.
+
+--mode profile-<op> runs only that operator (for rocprofv3), --mode copy
+runs the plain device copy used to calibrate the FETCH_SIZE/WRITE_SIZE
+counters.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "xmetai-onnx-plugins_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "tokens/s per op (GDN-2, sel-scan, Mamba-3) + % HBM roofline, 1 MI355X"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def make_ops():
+    from xmetai_onnx_plugins import workloads as W
+    import xmetai_onnx_plugins as xp
+
+    def ss():
+        s = W.SS_2P8B
+        keys = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+        # z is a dead input of output 0 (never read by the kernel); it is drawn
+        # on the device instead of on the host to keep the set-up short.
+        host_shape = W.SelectiveScanShape(s.batch, s.dim, s.seqlen, s.dstate, has_z=False)
+        return dict(name="selective_scan", workload="selective_scan_b8_d5120_l2048_n16", shape=s,
+                    gen=lambda: W.selective_scan_inputs(host_shape, seed=0), keys=keys,
+                    device_extra=lambda dev: dict(z=_device_normal((s.batch, s.dim, s.seqlen), dev, seed=0)),
+                    call=lambda d: xp.selective_scan_fn(*(d[k] for k in keys), delta_softplus=True),
+                    tokens=s.batch * s.seqlen, nbytes=W.selective_scan_bytes(s),
+                    config=dict(batch=s.batch, dim=s.dim, seqlen=s.seqlen, dstate=s.dstate, variable_B_C=True,
+                                delta_softplus=True, has_D=True, has_z=True, has_delta_bias=True))
+
+    def gdn2():
+        s = W.GDN2_MAIN
+        keys = ("q", "k", "v", "g", "beta", "w", "initial_state")
+        return dict(name="gated_deltanet2", workload="gated_deltanet2_b4_t4096_h16_k128_v128", shape=s,
+                    gen=lambda: W.gated_deltanet2_inputs(s, seed=0), keys=keys,
+                    call=lambda d: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale),
+                    tokens=s.batch * s.seqlen, nbytes=W.gated_deltanet2_bytes(s),
+                    config=dict(batch=s.batch, seqlen=s.seqlen, nheads=s.nheads, dk=s.dk, dv=s.dv,
+                                initial_state=True, l2norm=True))
+
+    def m3():
+        s = W.M3_MAIN
+        keys = ("Q", "K", "V", "ADT", "DT", "Trap", "Q_bias", "K_bias", "Angles", "D", "Z")
+        return dict(name="mamba3_siso", workload="mamba3_siso_b4_t4096_h32_p64_n128", shape=s,
+                    gen=lambda: W.mamba3_siso_inputs(s, seed=0), keys=keys,
+                    call=lambda d: xp.mamba3_siso_fn(*(d[k] for k in keys)),
+                    tokens=s.batch * s.seqlen, nbytes=W.mamba3_siso_bytes(s),
+                    config=dict(batch=s.batch, seqlen=s.seqlen, nheads=s.nheads, headdim=s.headdim,
+                                dstate=s.dstate, angles=s.a, has_d=True, has_z=False))
+
+    return {"selective_scan": ss, "gated_deltanet2": gdn2, "mamba3_siso": m3}
+
+
+def _device_normal(shape, dev, seed):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+
+
+def to_device(inputs, dev):
+    import numpy as np
+    import torch
+    return {k: (None if v is None else torch.from_numpy(np.ascontiguousarray(v)).to(dev)) for k, v in inputs.items()}
+
+
+def time_op(op, dev_inputs, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        op["call"](dev_inputs)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        op["call"](dev_inputs)
+        b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [a.elapsed_time(b) for a, b in ev]
+    return wall, per
+
+
+def achievable_hbm(dev):
+    """Streaming read+write copy over 2 x 2 GiB buffers (device copy kernel)."""
+    import torch
+    n = (2 << 30) // 4
+    src = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * n * 4 / (ms / 1e3) / 1e9
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (reference CPU path: NumPy fp32 sequential recurrences)
+# ---------------------------------------------------------------------------
+
+def cpu_env():
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return dict(host_cores_available=cores, OMP_NUM_THREADS=os.environ.get("OMP_NUM_THREADS"),
+                OPENBLAS_NUM_THREADS=os.environ.get("OPENBLAS_NUM_THREADS"))
+
+
+def cpu_baseline(op, inputs, budget_s):
+    """Times the NumPy fp32 oracle on a slice of the workload that finishes in
+    about `budget_s` seconds and scales to the full workload (cost is linear in
+    the sliced axis).  NumPy's elementwise loops run on one core."""
+    import numpy as np
+    from oracle import numpy_ref
+
+    s = op["shape"]
+    name = op["name"]
+
+    if name == "selective_scan":
+        full_units = s.batch * s.dim
+
+        def run(nch):
+            sub = {k: inputs[k] for k in op["keys"]}
+            for k in ("u", "delta"):
+                sub[k] = np.ascontiguousarray(inputs[k][:1, :nch])
+            for k in ("A", "D", "delta_bias"):
+                sub[k] = np.ascontiguousarray(inputs[k][:nch])
+            sub["B"] = np.ascontiguousarray(inputs["B"][:1])
+            sub["C"] = np.ascontiguousarray(inputs["C"][:1])
+            sub["z"] = None
+            t = time.perf_counter()
+            numpy_ref.selective_scan(**sub, delta_softplus=True, dtype=np.float32)
+            return time.perf_counter() - t
+
+        unit = "channels"
+        sample_fmt = "batch 1 x {n} of {d} channels x {L} tokens, dstate {N} (NumPy fp32 oracle), scaled by channel count"
+        fmt_args = dict(d=s.dim, L=s.seqlen, N=s.dstate)
+        max_units = s.dim
+    else:
+        full_units = s.batch * s.nheads
+
+        def run(nh):
+            sub = {}
+            for k in op["keys"]:
+                v = inputs[k]
+                if v is None:
+                    sub[k] = None
+                elif k in ("ADT", "DT", "Trap", "initial_state"):
+                    sub[k] = np.ascontiguousarray(v[:1, :nh])
+                elif k in ("Q_bias", "K_bias", "D"):
+                    sub[k] = np.ascontiguousarray(v[:nh])
+                else:
+                    sub[k] = np.ascontiguousarray(v[:1, :, :nh])
+            t = time.perf_counter()
+            if name == "gated_deltanet2":
+                numpy_ref.gated_deltanet2(*(sub[k] for k in op["keys"]), scale=s.scale, dtype=np.float32)
+            else:
+                numpy_ref.mamba3_siso(*(sub[k] for k in op["keys"]), dtype=np.float32)
+            return time.perf_counter() - t
+
+        unit = "heads"
+        sample_fmt = "batch 1 x {n} of {h} heads x {T} tokens (NumPy fp32 oracle), scaled by (batch, head) count"
+        fmt_args = dict(h=s.nheads, T=s.seqlen)
+        max_units = s.nheads
+
+    # calibrate on growing slices until one takes >= 0.5 s, then size the
+    # measured slice to the budget
+    n = 1
+    t = run(n)
+    while t < 0.5 and n < max_units:
+        n = min(max_units, n * 4)
+        t = run(n)
+    if t < budget_s * 0.8 and n < max_units:
+        n = min(max_units, max(n + 1, int(n * budget_s / max(t, 1e-3))))
+        t = run(n)
+    t_full = t * full_units / n
+    tokens = op["tokens"]
+    return dict(value=tokens / t_full, unit="tokens/s", cores=1, kind="port",
+                sample=sample_fmt.format(n=n, **fmt_args), sample_seconds=round(t, 3),
+                sampled_units=n, unit_axis=unit, **cpu_env())
+
+
+# ---------------------------------------------------------------------------
+
+def traffic_from_profiles(workload):
+    path = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ops", default="selective_scan,gated_deltanet2,mamba3_siso")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget for the headline op")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", default="bench",
+                    help="bench | copy | profile-selective_scan | profile-gated_deltanet2 | profile-mamba3_siso")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: the operators are single-GPU ORT kernels with no "
+              "collectives; --gpus above 1 is not supported (multi-GPU sharding is design-only).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.mode == "copy":
+        n = (1 << 30) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 1 GiB x 3")
+        return
+
+    builders = make_ops()
+    if args.mode.startswith("profile-"):
+        name = args.mode[len("profile-"):]
+        op = builders[name]()
+        d = to_device(op["gen"](), dev)
+        if "device_extra" in op:
+            d.update(op["device_extra"](dev))
+        wall, per = time_op(op, d, args.steps, args.warmup)
+        log(f"{name}: {statistics.median(per):.3f} ms/call (median of {args.steps})")
+        return
+
+    names = [n for n in args.ops.split(",") if n]
+    if "selective_scan" not in names:
+        names.insert(0, "selective_scan")
+    results = {}
+    headline = None
+    for name in names:
+        op = builders[name]()
+        log(f"{name}: generating {op['workload']}")
+        host = op["gen"]()
+        d = to_device(host, dev)
+        if "device_extra" in op:
+            d.update(op["device_extra"](dev))
+        torch.cuda.synchronize()
+        log(f"{name}: timing {args.warmup} warmup + {args.steps} steps")
+        wall, per = time_op(op, d, args.steps, args.warmup)
+        ev_ms = sum(per) / len(per)
+        med_ms = statistics.median(per)
+        gbps = op["nbytes"] / (med_ms / 1e3) / 1e9
+        r = dict(workload=op["workload"], config=op["config"], tokens_per_call=op["tokens"],
+                 ms_per_call_median=round(med_ms, 4), ms_per_call_mean=round(ev_ms, 4),
+                 tokens_per_s=op["tokens"] / (med_ms / 1e3), algorithmic_bytes=op["nbytes"],
+                 achieved_GBps=round(gbps, 1), frac_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
+        log(f"{name}: {med_ms:.3f} ms/call, {r['tokens_per_s']:.4g} tokens/s, {gbps:.0f} GB/s")
+        if not args.no_cpu_baseline:
+            budget = args.cpu_seconds if name == "selective_scan" else args.cpu_seconds / 2
+            log(f"{name}: CPU baseline (~{budget:.0f} s)")
+            r["cpu_baseline"] = cpu_baseline(op, host, budget)
+            log(f"{name}: CPU {r['cpu_baseline']['value']:.4g} tokens/s ({r['cpu_baseline']['sample']})")
+        results[name] = r
+        if name == "selective_scan":
+            headline = dict(wall=wall, per=per, op=op)
+        del d, host
+        torch.cuda.empty_cache()
+
+    log("achievable HBM: 2 GiB device copy")
+    ach = achievable_hbm(dev)
+    for r in results.values():
+        r["frac_achievable_hbm"] = round(r["achieved_GBps"] / ach, 4)
+
+    op = headline["op"]
+    steps = args.steps
+    wall = headline["wall"]
+    ev_avg_ms = sum(headline["per"]) / len(headline["per"])
+    achieved = op["nbytes"] / (ev_avg_ms / 1e3) / 1e9
+    ss = results["selective_scan"]
+    line = {
+        "metric": METRIC,
+        "value": op["tokens"] * steps / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded NumPy draws with the reference configs' distributions, resident in HBM",
+        "config": dict(workload=op["workload"], **op["config"]),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic_from_profiles(op["workload"]),
+            "kernel": "SelectiveScanFwdKernel<4,4,true,true>",
+            "algorithmic_bytes_per_launch": op["nbytes"],
+            "kernel_ms_avg": round(ev_avg_ms, 4),
+            "frac_of_achievable": round(achieved / ach, 4),
+        },
+        "cpu_baseline": ss.get("cpu_baseline"),
+        "achievable_hbm_GBps": round(ach, 1),
+        "ops": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

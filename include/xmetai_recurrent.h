@@ -1,0 +1,163 @@
+/*
+ * xmetai_recurrent.h — C ABI of the MI355X (gfx950) recurrent operators.
+ *
+ * Three operators of the ONNX domain "xmetai_plugins", with the reference's
+ * input order, attribute names, defaults and validation:
+ *
+ *   SelectiveScanFn   (8 inputs)  reference: csrc/selective_scan/selective_scan_fn_ort.cpp:48-246
+ *   Mamba3SisoFn      (11 inputs) reference: csrc/mamba3_siso/mamba3_siso_fn_ort.cpp:41-246
+ *   GatedDeltaNet2Fn  (7 inputs)  reference: csrc/gated_deltanet2/gated_deltanet2_fn_ort.cpp:44-237
+ *
+ * The ONNX Runtime custom-op layer (RegisterCustomOps, declared in
+ * xmetai_onnx_plugins_ort.h) unpacks OrtValues into xm_tensor_t descriptors,
+ * reads node attributes into the attrs structs below and calls these entry
+ * points with the ROCm EP compute stream and an allocator that forwards to
+ * KernelContext_GetScratchBuffer.  A harness can call them directly with its
+ * own device buffers and stream.
+ *
+ * Conventions
+ *  - Every input is REQUIRED; an "optional" input is a tensor with zero
+ *    elements (reference: ort_common.h:93-95).  Its data pointer may be NULL.
+ *  - Tensors are dense, row-major, fp32 (elem_type == XM_ELEM_FLOAT), on the
+ *    device that is current when the entry point is called.
+ *  - Entry points return XM_OK or an xm_status_t error and, on error, write a
+ *    NUL-terminated message into errbuf (when errbuf != NULL, errlen > 0).
+ *    Messages match the reference's exception text where the reference has one.
+ *  - *_forward never synchronises the host with the device, keeps no state
+ *    between calls and is reentrant: concurrent calls on different streams
+ *    are independent.  Work is enqueued on `stream` (a hipStream_t; NULL means
+ *    the null stream).  Scratch comes from `alloc` in stream order; when
+ *    `alloc` is NULL the library uses its own stream-ordered pool
+ *    (hipMallocFromPoolAsync / hipFreeAsync on `stream`).
+ *  - No host-visible side effects besides the output tensor.
+ */
+#ifndef XMETAI_RECURRENT_H_
+#define XMETAI_RECURRENT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XM_MAX_RANK 8
+#define XM_ELEM_FLOAT 1 /* ONNX TensorProto FLOAT */
+
+typedef enum xm_status {
+    XM_OK = 0,
+    XM_ERR_INVALID_ARGUMENT = 1, /* shape, rank, dtype or attribute rejected */
+    XM_ERR_UNSUPPORTED = 2,      /* a feature the operator does not support (v1 limits) */
+    XM_ERR_DEVICE = 3,           /* a HIP runtime or launch error */
+    XM_ERR_ALLOC = 4             /* the scratch allocator returned NULL */
+} xm_status_t;
+
+/* A borrowed device tensor. */
+typedef struct xm_tensor {
+    const void *data;              /* device pointer, may be NULL when a dim is 0 */
+    int64_t shape[XM_MAX_RANK];
+    int32_t rank;
+    int32_t elem_type;             /* XM_ELEM_FLOAT */
+} xm_tensor_t;
+
+/* Stream-ordered scratch allocator.  alloc() must return memory that is
+ * usable by work enqueued on the operator's stream after the call; free() may
+ * be called right after the operator enqueues its last kernel (the memory is
+ * reused only in stream order).  Reference: gated_deltanet2_fn_ort.cpp:89-111. */
+typedef struct xm_allocator {
+    void *ctx;
+    void *(*alloc)(void *ctx, size_t bytes);
+    void (*free)(void *ctx, void *ptr);
+} xm_allocator_t;
+
+/* ---- SelectiveScanFn ------------------------------------------------------
+ * Inputs: 0 u [B,D,L]; 1 delta [B,D,L]; 2 A [D,N]; 3 B [D,N] | [B,N,L] |
+ * [B,G,N,L]; 4 C (same forms); 5 D [D] or empty; 6 z [B,D,L] or empty;
+ * 7 delta_bias [D] or empty.  Output 0: y [B,D,L], the un-gated scan output
+ * (reference: selective_scan_fwd_kernel.cuh:272-281; z only feeds a discarded
+ * buffer there, :283-301, so y never depends on z).
+ * Attributes (reference: selective_scan_fn_ort.cpp:50-56): delta_softplus
+ * (int, default 0), return_last_state (int, default 0; non-zero rejected).  */
+typedef struct xm_selective_scan_attrs {
+    int64_t delta_softplus;
+    int64_t return_last_state;
+} xm_selective_scan_attrs_t;
+
+void xm_selective_scan_attrs_default(xm_selective_scan_attrs_t *attrs);
+/* Session-time check of the attributes (reference: constructor, :50-56). */
+int xm_selective_scan_check_attrs(const xm_selective_scan_attrs_t *attrs, char *errbuf, size_t errlen);
+/* Run-time shape validation without touching the device (reference:
+ * Compute, :58-117).  Writes the output shape and the scratch bytes the call
+ * will request from the allocator. */
+int xm_selective_scan_validate(const xm_tensor_t *inputs, size_t n_inputs,
+                               const xm_selective_scan_attrs_t *attrs, int64_t *out_shape,
+                               int32_t *out_rank, size_t *scratch_bytes, char *errbuf, size_t errlen);
+/* Validate and enqueue.  `out` is a device buffer of prod(out_shape) floats. */
+int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs,
+                              const xm_selective_scan_attrs_t *attrs, float *out, void *stream,
+                              const xm_allocator_t *alloc, char *errbuf, size_t errlen);
+
+/* ---- Mamba3SisoFn ---------------------------------------------------------
+ * Inputs: 0 Q [B,T,Hq,N]; 1 K [B,T,Hq,N]; 2 V [B,T,H,P]; 3 ADT [B,H,T];
+ * 4 DT [B,H,T]; 5 Trap [B,H,T]; 6 Q_bias [H,N]; 7 K_bias [H,N];
+ * 8 Angles [B,T,H,A]; 9 D [H] or empty; 10 Z [B,T,H,P] or empty.
+ * Output 0: [B,T,H,P] (reference: mamba3_siso_fn_ort.cpp:61-111).
+ * Attributes (reference: :43-59): chunk_size (default 64, must be > 0, not
+ * otherwise used), has_d and has_z (default 1, must match the presence of D
+ * and Z), return_final_states, has_input_states, has_cu_seqlens (default 0;
+ * non-zero rejected).  */
+typedef struct xm_mamba3_siso_attrs {
+    int64_t chunk_size;
+    int64_t has_d;
+    int64_t has_z;
+    int64_t return_final_states;
+    int64_t has_input_states;
+    int64_t has_cu_seqlens;
+} xm_mamba3_siso_attrs_t;
+
+void xm_mamba3_siso_attrs_default(xm_mamba3_siso_attrs_t *attrs);
+int xm_mamba3_siso_check_attrs(const xm_mamba3_siso_attrs_t *attrs, char *errbuf, size_t errlen);
+int xm_mamba3_siso_validate(const xm_tensor_t *inputs, size_t n_inputs,
+                            const xm_mamba3_siso_attrs_t *attrs, int64_t *out_shape,
+                            int32_t *out_rank, size_t *scratch_bytes, char *errbuf, size_t errlen);
+int xm_mamba3_siso_forward(const xm_tensor_t *inputs, size_t n_inputs,
+                           const xm_mamba3_siso_attrs_t *attrs, float *out, void *stream,
+                           const xm_allocator_t *alloc, char *errbuf, size_t errlen);
+
+/* ---- GatedDeltaNet2Fn -----------------------------------------------------
+ * Inputs: 0 q [B,T,H,K]; 1 k [B,T,H,K]; 2 v [B,T,H,V]; 3 g [B,T,H,K]
+ * (log decay, per key); 4 beta [B,T,H,K]; 5 w [B,T,H,V] (write gate);
+ * 6 initial_state [B,H,K,V] or empty.  Output 0: [B,T,H,V]
+ * (reference: gated_deltanet2_fn_ort.cpp:66-142, :187-219).
+ * Attributes (reference: :46-64): scale (float, default 1.0, positive and
+ * finite), use_qk_l2norm_in_kernel (default 1), output_final_state,
+ * use_gate_in_kernel, has_cu_seqlens, state_v_first (default 0; non-zero
+ * rejected).  */
+typedef struct xm_gated_deltanet2_attrs {
+    float scale;
+    int64_t use_qk_l2norm_in_kernel;
+    int64_t output_final_state;
+    int64_t use_gate_in_kernel;
+    int64_t has_cu_seqlens;
+    int64_t state_v_first;
+} xm_gated_deltanet2_attrs_t;
+
+void xm_gated_deltanet2_attrs_default(xm_gated_deltanet2_attrs_t *attrs);
+int xm_gated_deltanet2_check_attrs(const xm_gated_deltanet2_attrs_t *attrs, char *errbuf, size_t errlen);
+int xm_gated_deltanet2_validate(const xm_tensor_t *inputs, size_t n_inputs,
+                                const xm_gated_deltanet2_attrs_t *attrs, int64_t *out_shape,
+                                int32_t *out_rank, size_t *scratch_bytes, char *errbuf,
+                                size_t errlen);
+int xm_gated_deltanet2_forward(const xm_tensor_t *inputs, size_t n_inputs,
+                               const xm_gated_deltanet2_attrs_t *attrs, float *out, void *stream,
+                               const xm_allocator_t *alloc, char *errbuf, size_t errlen);
+
+/* ---- Library ---------------------------------------------------------------
+ * Version string and a description of the build (target, kernel variants). */
+const char *xm_version(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* XMETAI_RECURRENT_H_ */

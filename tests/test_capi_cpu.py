@@ -1,0 +1,265 @@
+"""Host-side tests of the C ABI (no GPU): the library loads, exports every
+function include/xmetai_recurrent.h declares, and its attribute checks and
+shape validation reproduce the reference adapters' behaviour and messages
+(selective_scan_fn_ort.cpp:50-117, mamba3_siso_fn_ort.cpp:43-227,
+gated_deltanet2_fn_ort.cpp:46-219)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import xmetai_onnx_plugins as xp
+from xmetai_onnx_plugins import XmError, validate, check_attrs
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(xm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_lists_the_c_abi():
+    fns = header_functions(os.path.join(ROOT, "include", "xmetai_recurrent.h"))
+    assert sorted(fns) == sorted(xp.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = xp.lib()
+    out = subprocess.run(["nm", "-D", "--defined-only", xp.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (\w+)$", out, flags=re.M))
+    for name in header_functions(os.path.join(ROOT, "include", "xmetai_recurrent.h")):
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+    assert "gfx950" in xp.version()
+
+
+def test_no_cpu_fallback_symbols():
+    # The library is device code plus validation; it must not carry a host
+    # implementation of the recurrences (those live only in oracle/).
+    out = subprocess.run(["nm", "-DC", xp.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    assert "xmo_" not in out
+
+
+# ---------------------------------------------------------------------------
+# attributes (session-time checks, reference constructors)
+# ---------------------------------------------------------------------------
+
+def _attrs(op):
+    t = xp._capi.OPS[op][0]()
+    getattr(xp.lib(), f"xm_{op}_attrs_default")(ctypes.byref(t))
+    return t
+
+
+def test_attribute_defaults_match_reference():
+    a = _attrs("selective_scan")
+    assert (a.delta_softplus, a.return_last_state) == (0, 0)
+    a = _attrs("mamba3_siso")
+    assert (a.chunk_size, a.has_d, a.has_z, a.return_final_states, a.has_input_states, a.has_cu_seqlens) == (64, 1, 1, 0, 0, 0)
+    a = _attrs("gated_deltanet2")
+    assert a.scale == 1.0 and a.use_qk_l2norm_in_kernel == 1
+    assert (a.output_final_state, a.use_gate_in_kernel, a.has_cu_seqlens, a.state_v_first) == (0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("op,kw,msg,status", [
+    ("selective_scan", dict(return_last_state=1), "SelectiveScanFn does not support return_last_state=1 in ORT kernel", xp.XM_ERR_UNSUPPORTED),
+    ("mamba3_siso", dict(chunk_size=0), "Mamba3SisoFn requires chunk_size > 0", xp.XM_ERR_INVALID_ARGUMENT),
+    ("mamba3_siso", dict(return_final_states=1), "Mamba3SisoFn v1 does not support return_final_states", xp.XM_ERR_UNSUPPORTED),
+    ("mamba3_siso", dict(has_input_states=1), "Mamba3SisoFn v1 does not support input states", xp.XM_ERR_UNSUPPORTED),
+    ("mamba3_siso", dict(has_cu_seqlens=1), "Mamba3SisoFn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
+    ("gated_deltanet2", dict(output_final_state=1), "GatedDeltaNet2Fn v1 does not support output_final_state", xp.XM_ERR_UNSUPPORTED),
+    ("gated_deltanet2", dict(use_gate_in_kernel=1), "GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel", xp.XM_ERR_UNSUPPORTED),
+    ("gated_deltanet2", dict(has_cu_seqlens=1), "GatedDeltaNet2Fn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
+    ("gated_deltanet2", dict(state_v_first=1), "GatedDeltaNet2Fn v1 expects state layout (batch, head, key, value)", xp.XM_ERR_UNSUPPORTED),
+    ("gated_deltanet2", dict(scale=0.0), "GatedDeltaNet2Fn requires a positive finite scale", xp.XM_ERR_INVALID_ARGUMENT),
+    ("gated_deltanet2", dict(scale=-1.0), "GatedDeltaNet2Fn requires a positive finite scale", xp.XM_ERR_INVALID_ARGUMENT),
+    ("gated_deltanet2", dict(scale=float("inf")), "GatedDeltaNet2Fn requires a positive finite scale", xp.XM_ERR_INVALID_ARGUMENT),
+    ("gated_deltanet2", dict(scale=float("nan")), "GatedDeltaNet2Fn requires a positive finite scale", xp.XM_ERR_INVALID_ARGUMENT),
+])
+def test_attribute_rejections(op, kw, msg, status):
+    with pytest.raises(XmError) as e:
+        check_attrs(op, **kw)
+    assert e.value.message == msg
+    assert e.value.status == status
+
+
+def test_attribute_check_order_matches_reference():
+    # The GDN-2 constructor checks output_final_state before the scale.
+    with pytest.raises(XmError, match="output_final_state"):
+        check_attrs("gated_deltanet2", output_final_state=1, scale=-1.0)
+
+
+# ---------------------------------------------------------------------------
+# SelectiveScanFn shapes
+# ---------------------------------------------------------------------------
+
+def ss_shapes(B=2, D=8, L=16, N=4, G=None, bvar=True, cvar=True, has_d=True, has_z=True, has_bias=True):
+    def bc(var):
+        if not var:
+            return (D, N)
+        return (B, N, L) if G is None else (B, G, N, L)
+    return [(B, D, L), (B, D, L), (D, N), bc(bvar), bc(cvar), (D,) if has_d else None,
+            (B, D, L) if has_z else None, (D,) if has_bias else None]
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(G=2), dict(bvar=False), dict(cvar=False), dict(bvar=False, cvar=False),
+                                dict(has_d=False, has_z=False, has_bias=False), dict(N=256), dict(N=1)])
+def test_ss_valid_shapes(kw):
+    shapes = ss_shapes(**kw)
+    out, scratch = validate("selective_scan", shapes, delta_softplus=1)
+    assert out == shapes[0]
+    assert scratch == 0
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda s: s.__setitem__(0, (2, 8)), "u must be 3-D"),
+    (lambda s: s.__setitem__(1, (2, 8, 15)), "delta must have same shape as u"),
+    (lambda s: s.__setitem__(2, (8, 4, 1)), "A must be 2-D"),
+    (lambda s: s.__setitem__(3, (8,)), "B must have rank >= 2"),
+    (lambda s: s.__setitem__(4, (4,)), "C must have rank >= 2"),
+    (lambda s: s.__setitem__(2, (7, 4)), "A dimension mismatch with u"),
+    (lambda s: (s.__setitem__(2, (8, 257)), s.__setitem__(3, (2, 257, 16)), s.__setitem__(4, (2, 257, 16))),
+     "selective_scan supports d_state up to 256"),
+    (lambda s: (s.__setitem__(3, (2, 3, 4, 16)), s.__setitem__(4, (2, 3, 4, 16))), "dim must be divisible by n_groups"),
+])
+def test_ss_reference_rejections(mutate, msg):
+    shapes = ss_shapes()
+    mutate(shapes)
+    with pytest.raises(XmError) as e:
+        validate("selective_scan", shapes)
+    assert e.value.message == msg
+    assert e.value.status == xp.XM_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("idx,shape,msg", [
+    (3, (2, 4, 15), "B must have shape (batch, n_groups, dstate, seqlen) when variable"),
+    (3, (3, 4, 16), "B must have shape (batch, n_groups, dstate, seqlen) when variable"),
+    (4, (2, 5, 16), "C must have shape (batch, n_groups, dstate, seqlen) when variable"),
+    (5, (7,), "D must have shape (dim,)"),
+    (6, (2, 8, 15), "z must have same shape as u"),
+    (7, (9,), "delta_bias must have shape (dim,)"),
+])
+def test_ss_extent_checks_beyond_reference(idx, shape, msg):
+    # The reference does not check these extents and reads out of bounds on them.
+    shapes = ss_shapes()
+    shapes[idx] = shape
+    with pytest.raises(XmError) as e:
+        validate("selective_scan", shapes)
+    assert e.value.message == msg
+
+
+def test_ss_empty_sequence_is_a_no_op():
+    out, _ = validate("selective_scan", ss_shapes(L=0))
+    assert out == (2, 8, 0)
+
+
+def test_ss_non_float_input_rejected():
+    descs = [xp._desc_from_shape(s if s is not None else (0,)) for s in ss_shapes()]
+    descs[1].elem_type = 10  # FLOAT16
+    arr = (xp._capi.XmTensor * 8)(*descs)
+    a = _attrs("selective_scan")
+    err = ctypes.create_string_buffer(256)
+    st = xp.lib().xm_selective_scan_validate(arr, 8, ctypes.byref(a), None, None, None, err, 256)
+    assert st == xp.XM_ERR_INVALID_ARGUMENT
+    assert err.value.decode() == "TensorView expects float32 tensors"
+
+
+def test_wrong_input_count():
+    with pytest.raises(TypeError):
+        validate("selective_scan", ss_shapes()[:7])
+
+
+# ---------------------------------------------------------------------------
+# GatedDeltaNet2Fn shapes
+# ---------------------------------------------------------------------------
+
+def gdn_shapes(B=2, T=5, H=3, K=16, V=8, s0=True):
+    qk = (B, T, H, K)
+    vv = (B, T, H, V)
+    return [qk, qk, vv, qk, qk, vv, (B, H, K, V) if s0 else None]
+
+
+def test_gdn2_valid_and_scratch():
+    out, scratch = validate("gated_deltanet2", gdn_shapes(), scale=0.25)
+    assert out == (2, 5, 3, 8)
+    # prepared chunk: 4 vectors x B*H*min(T,1024) rows x padded K (16); no state carry for T <= 1024
+    assert scratch == 4 * 2 * 3 * 5 * 16 * 4
+    _, scratch_long = validate("gated_deltanet2", gdn_shapes(T=3000, K=128, V=64))
+    prep = 4 * 2 * 3 * 1024 * 128 * 4
+    assert scratch_long == (prep + 255) // 256 * 256 + 2 * 3 * 128 * 64 * 4
+
+
+@pytest.mark.parametrize("idx,shape,msg", [
+    (0, (2, 5, 3), "q must have rank 4"),
+    (1, (2, 5, 3, 8), "q shape must match k"),
+    (3, (2, 5, 3, 8), "q shape must match g"),
+    (4, (2, 5, 3, 8), "q shape must match beta"),
+    (2, (2, 4, 3, 8), "v batch/seqlen/head dimensions must match q"),
+    (5, (2, 5, 3, 7), "v shape must match w"),
+    (6, (2, 3, 16), "initial_state must have rank 4"),
+    (6, (2, 3, 16, 9), "initial_state must have shape (batch, head, headdim_k, headdim_v)"),
+])
+def test_gdn2_reference_rejections(idx, shape, msg):
+    shapes = gdn_shapes()
+    shapes[idx] = shape
+    with pytest.raises(XmError) as e:
+        validate("gated_deltanet2", shapes)
+    assert e.value.message == msg
+
+
+def test_gdn2_zero_dims_rejected_like_reference():
+    with pytest.raises(XmError, match="seqlen dimension is out of range"):
+        validate("gated_deltanet2", gdn_shapes(T=0))
+
+
+def test_gdn2_absent_initial_state():
+    out, _ = validate("gated_deltanet2", gdn_shapes(s0=False))
+    assert out == (2, 5, 3, 8)
+
+
+# ---------------------------------------------------------------------------
+# Mamba3SisoFn shapes
+# ---------------------------------------------------------------------------
+
+def m3_shapes(B=2, T=7, H=4, Hq=2, P=8, N=16, A=8, has_d=True, has_z=False):
+    return [(B, T, Hq, N), (B, T, Hq, N), (B, T, H, P), (B, H, T), (B, H, T), (B, H, T), (H, N), (H, N),
+            (B, T, H, A), (H,) if has_d else None, (B, T, H, P) if has_z else None]
+
+
+def test_m3_valid():
+    out, scratch = validate("mamba3_siso", m3_shapes(), has_d=1, has_z=0)
+    assert out == (2, 7, 4, 8) and scratch == 0
+    out, _ = validate("mamba3_siso", m3_shapes(has_z=True), has_d=1, has_z=1)
+    assert out == (2, 7, 4, 8)
+
+
+@pytest.mark.parametrize("mutate,attrs,msg", [
+    (lambda s: s.__setitem__(3, (2, 4)), {}, "ADT must have rank 3"),
+    (lambda s: s.__setitem__(1, (2, 7, 2, 14)), {}, "Q shape must match K"),
+    (lambda s: s.__setitem__(4, (2, 4, 6)), {}, "ADT shape must match DT"),
+    (lambda s: s.__setitem__(2, (2, 6, 4, 8)), {}, "V batch/seqlen must match Q"),
+    (lambda s: s.__setitem__(6, (4, 14)), {}, "Q_bias must have shape (nheads, headdim_qk)"),
+    (lambda s: s.__setitem__(8, (2, 7, 3, 8)), {}, "Angles must have shape (batch, seqlen, nheads, headdim_angles)"),
+    (lambda s: s.__setitem__(8, (2, 7, 4, 9)), {}, "Mamba3SisoFn requires 0 < headdim_angles <= headdim_qk / 2"),
+    (lambda s: s.__setitem__(9, None), {}, "Mamba3SisoFn has_d attribute does not match D input"),
+    (lambda s: s.__setitem__(10, (2, 7, 4, 8)), {}, "Mamba3SisoFn has_z attribute does not match Z input"),
+    (lambda s: s.__setitem__(9, (3,)), {}, "D must have shape (nheads,)"),
+])
+def test_m3_reference_rejections(mutate, attrs, msg):
+    shapes = m3_shapes()
+    mutate(shapes)
+    with pytest.raises(XmError) as e:
+        validate("mamba3_siso", shapes, has_d=1, has_z=0, **attrs)
+    assert e.value.message == msg
+
+
+def test_m3_head_divisibility_and_odd_dim():
+    with pytest.raises(XmError, match="nheads divisible by nheads_qk"):
+        validate("mamba3_siso", m3_shapes(H=3, Hq=2), has_d=1, has_z=0)
+    shapes = m3_shapes(N=15, A=4)
+    with pytest.raises(XmError, match="positive even headdim_qk"):
+        validate("mamba3_siso", shapes, has_d=1, has_z=0)

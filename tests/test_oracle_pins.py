@@ -1,0 +1,465 @@
+"""Pins the oracle (both restatements: NumPy and C) against what the
+mathematics fixes: closed forms, brute-force formulas written differently
+from the recurrences, special cases and invariants.  Each check is chosen so
+that a plausible slip in the oracle (a dropped term, a wrong sign or index, a
+transposed operand, a misplaced decay) fails at least one of them.
+
+The reference ships no golden vectors or tests for these operators (its
+tests/ directory is not in the release), so these pins and the committed
+fixtures under tests/golden/ are what anchor parity.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import cref, numpy_ref
+
+IMPLS = {"numpy": numpy_ref, "c": cref}
+F64 = np.float64
+PI_F = float(np.float32(np.pi))
+TWO_PI_F = float(np.float32(2.0) * np.float32(np.pi))
+
+
+@pytest.fixture(params=sorted(IMPLS))
+def impl(request):
+    return IMPLS[request.param]
+
+
+def rnd(rng, *shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+
+def softplus64(x):
+    x = np.asarray(x, F64)
+    return np.where(x <= 20.0, np.log1p(np.exp(np.minimum(x, 20.0))), x)
+
+
+# ---------------------------------------------------------------------------
+# SelectiveScanFn
+# ---------------------------------------------------------------------------
+
+def ss_closed_form(u, delta, A, B, C, D, bias, softplus, groups=1):
+    """y_t = D u_t + sum_n C[n,t] sum_{s<=t} exp(A_n sum_{r=s+1..t} delta'_r) B[n,s] delta'_s u_s,
+    evaluated with explicit cumulative sums (no recurrence).  B, C variable [Bt,G,N,L]."""
+    u = u.astype(F64); delta = delta.astype(F64); A = A.astype(F64)
+    B = B.astype(F64); C = C.astype(F64)
+    Bt, Dm, L = u.shape
+    N = A.shape[1]
+    dl = delta + (0 if bias is None else bias.astype(F64)[None, :, None])
+    if softplus:
+        dl = softplus64(dl)
+    y = np.zeros((Bt, Dm, L))
+    ratio = Dm // groups
+    cs = np.cumsum(dl, axis=-1)                      # sum_{r<=t}
+    for b in range(Bt):
+        for d in range(Dm):
+            g = d // ratio
+            for n in range(N):
+                # E[t, s] = exp(A (cs[t] - cs[s])) for s <= t
+                diff = cs[b, d][:, None] - cs[b, d][None, :]
+                E = np.tril(np.exp(A[d, n] * np.tril(diff)))
+                src = B[b, g, n] * dl[b, d] * u[b, d]
+                y[b, d] += C[b, g, n] * (E @ src)
+    if D is not None:
+        y += D.astype(F64)[None, :, None] * u
+    return y
+
+
+def test_ss_zero_delta_gives_skip_exactly(impl):
+    rng = np.random.default_rng(1)
+    u = rnd(rng, 2, 3, 9)
+    delta = np.zeros_like(u)
+    A = -np.exp(rng.uniform(0, 2, (3, 4))).astype(np.float32)
+    B = rnd(rng, 2, 4, 9); C = rnd(rng, 2, 4, 9); D = rnd(rng, 3)
+    y = impl.selective_scan(u, delta, A, B, C, D, None, None, delta_softplus=False, dtype=F64)
+    np.testing.assert_array_equal(y, D.astype(F64)[None, :, None] * u.astype(F64))
+
+
+def test_ss_zero_A_is_a_prefix_sum(impl):
+    rng = np.random.default_rng(2)
+    Bt, Dm, L, N = 2, 3, 11, 4
+    u = rnd(rng, Bt, Dm, L); delta = rnd(rng, Bt, Dm, L)
+    A = np.zeros((Dm, N), np.float32)
+    B = rnd(rng, Bt, N, L); C = rnd(rng, Bt, N, L); D = rnd(rng, Dm)
+    bias = rng.uniform(-1, 1, Dm).astype(np.float32)
+    y = impl.selective_scan(u, delta, A, B, C, D, None, bias, delta_softplus=True, dtype=F64)
+    dl = softplus64(delta.astype(F64) + bias.astype(F64)[None, :, None])
+    h = np.cumsum(B.astype(F64)[:, None] * (dl * u)[:, :, None], axis=-1)   # [Bt,D,N,L]
+    ref = D.astype(F64)[None, :, None] * u + (C.astype(F64)[:, None] * h).sum(2)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("groups", [1, 2])
+@pytest.mark.parametrize("softplus", [False, True])
+def test_ss_matches_closed_form(impl, groups, softplus):
+    rng = np.random.default_rng(3 + groups)
+    Bt, Dm, L, N = 2, 4, 13, 3
+    u = rnd(rng, Bt, Dm, L); delta = rnd(rng, Bt, Dm, L, scale=0.5)
+    A = (-np.exp(rng.uniform(0, np.log(16), (Dm, N)))).astype(np.float32)
+    Bv = rnd(rng, Bt, groups, N, L); Cv = rnd(rng, Bt, groups, N, L); D = rnd(rng, Dm)
+    bias = rng.uniform(-4, -2, Dm).astype(np.float32)
+    if not softplus:
+        delta = np.abs(delta)   # keep delta' >= 0 so exp(A * sum) stays bounded
+        bias = np.zeros_like(bias)
+    Bin = Bv[:, 0] if groups == 1 else Bv
+    Cin = Cv[:, 0] if groups == 1 else Cv
+    y = impl.selective_scan(u, delta, A, Bin, Cin, D, None, bias, delta_softplus=softplus, dtype=F64)
+    ref = ss_closed_form(u, delta, A, Bv, Cv, D, bias, softplus, groups)
+    np.testing.assert_allclose(y, ref, rtol=1e-10, atol=1e-11)
+
+
+def test_ss_constant_bc_equal_broadcast_variable(impl):
+    # One channel per group, so a per-(group) variable B equals a per-channel constant B.
+    rng = np.random.default_rng(5)
+    Bt, Dm, L, N = 2, 3, 10, 4
+    u = rnd(rng, Bt, Dm, L); delta = rnd(rng, Bt, Dm, L)
+    A = (-np.exp(rng.uniform(0, 2, (Dm, N)))).astype(np.float32)
+    Bc = rnd(rng, Dm, N); Cc = rnd(rng, Dm, N); D = rnd(rng, Dm)
+    Bv = np.ascontiguousarray(np.broadcast_to(Bc[None, :, :, None], (Bt, Dm, N, L)))
+    Cv = np.ascontiguousarray(np.broadcast_to(Cc[None, :, :, None], (Bt, Dm, N, L)))
+    ref = impl.selective_scan(u, delta, A, Bv, Cv, D, None, None, delta_softplus=True, dtype=F64)
+    for Bx, Cx in ((Bc, Cc), (Bv, Cc), (Bc, Cv)):
+        if Bx is Bc and Cx is Cv:
+            continue  # constant B with variable C reads C group 0 only (checked below)
+        y = impl.selective_scan(u, delta, A, Bx, Cx, D, None, None, delta_softplus=True, dtype=F64)
+        np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_ss_constant_b_variable_c_reads_group_zero(impl):
+    # n_groups comes from B (selective_scan_fn_ort.cpp:109): with B constant every
+    # channel uses C group 0, whatever C's group count.
+    rng = np.random.default_rng(6)
+    Bt, Dm, L, N = 1, 4, 8, 2
+    u = rnd(rng, Bt, Dm, L); delta = rnd(rng, Bt, Dm, L)
+    A = (-np.exp(rng.uniform(0, 2, (Dm, N)))).astype(np.float32)
+    Bc = rnd(rng, Dm, N); Cv = rnd(rng, Bt, 2, N, L)
+    y1 = impl.selective_scan(u, delta, A, Bc, Cv, None, None, None, delta_softplus=True, dtype=F64)
+    C2 = Cv.copy(); C2[:, 1] = 1e6
+    y2 = impl.selective_scan(u, delta, A, Bc, C2, None, None, None, delta_softplus=True, dtype=F64)
+    np.testing.assert_array_equal(y1, y2)
+    # and equals the explicit formula with C group 0 and y += (B*C_t) h, h over delta*u
+    Bv = np.ascontiguousarray(np.broadcast_to(Bc[None, :, :, None], (Bt, Dm, N, L)))
+    ref = ss_closed_form(u, delta, A, Bv.reshape(Bt, Dm, N, L),
+                         np.ascontiguousarray(np.broadcast_to(Cv[:, :1], (Bt, Dm, N, L))), None, None, True, Dm)
+    np.testing.assert_allclose(y1, ref, rtol=1e-10, atol=1e-11)
+
+
+def test_ss_softplus_branch(impl):
+    # One token per channel, A = 0, B = C = 1, D absent, u = 1: y = delta' exactly.
+    x = np.array([-30.0, -1.0, 0.0, 3.0, 19.5, 20.0, 20.5, 25.0, 60.0], np.float32)[None, :, None]
+    u = np.ones_like(x)
+    A = np.zeros((x.shape[1], 1), np.float32)
+    one = np.ones((x.shape[1], 1), np.float32)
+    y = impl.selective_scan(u, x, A, one, one, None, None, None, delta_softplus=True, dtype=F64)
+    dl = y[0, :, 0]
+    xs = x[0, :, 0].astype(F64)
+    expect = np.where(xs <= 20, np.log1p(np.exp(xs)), xs)
+    np.testing.assert_allclose(dl, expect, rtol=1e-12, atol=1e-15)
+    assert dl[-1] == 60.0 and dl[-2] == 25.0   # identity above 20 (kernel.cuh:158)
+
+
+def test_ss_linear_in_u_and_ignores_z(impl):
+    rng = np.random.default_rng(7)
+    Bt, Dm, L, N = 1, 3, 12, 3
+    delta = rnd(rng, Bt, Dm, L)
+    A = (-np.exp(rng.uniform(0, 2, (Dm, N)))).astype(np.float32)
+    B = rnd(rng, Bt, N, L); C = rnd(rng, Bt, N, L); D = rnd(rng, Dm)
+    # dyadic values keep 2*u1 - 3*u2 exact in fp32
+    u1 = (rng.integers(-8, 8, (Bt, Dm, L)) / 4).astype(np.float32)
+    u2 = (rng.integers(-8, 8, (Bt, Dm, L)) / 4).astype(np.float32)
+    f = lambda u, z=None: impl.selective_scan(u, delta, A, B, C, D, z, None, delta_softplus=True, dtype=F64)
+    lhs = f((2.0 * u1 - 3.0 * u2).astype(np.float32))
+    np.testing.assert_allclose(lhs, 2 * f(u1) - 3 * f(u2), rtol=1e-9, atol=1e-10)
+    np.testing.assert_array_equal(f(u1), f(u1, rnd(rng, Bt, Dm, L)))
+
+
+def test_ss_numpy_and_c_agree():
+    rng = np.random.default_rng(8)
+    Bt, Dm, L, N = 2, 5, 37, 16
+    args = dict(u=rnd(rng, Bt, Dm, L), delta=rnd(rng, Bt, Dm, L),
+                A=(-np.exp(rng.uniform(0, np.log(16), (Dm, N)))).astype(np.float32),
+                B=rnd(rng, Bt, N, L), C=rnd(rng, Bt, N, L), D=rnd(rng, Dm),
+                delta_bias=rng.uniform(-4, -2, Dm).astype(np.float32))
+    for dt, tol in ((F64, 1e-12), (np.float32, 2e-5)):
+        a = numpy_ref.selective_scan(**args, delta_softplus=True, dtype=dt)
+        b = cref.selective_scan(**args, delta_softplus=True, dtype=dt)
+        np.testing.assert_allclose(a, b, rtol=tol, atol=tol)
+
+
+# ---------------------------------------------------------------------------
+# GatedDeltaNet2Fn
+# ---------------------------------------------------------------------------
+
+def gdn2_normalise(q, k, scale, l2):
+    q = q.astype(F64); k = k.astype(F64)
+    if l2:
+        qn = q * scale / np.sqrt((q * q).sum(-1, keepdims=True) + float(np.float32(1e-6)))
+        kn = k / np.sqrt((k * k).sum(-1, keepdims=True) + float(np.float32(1e-6)))
+    else:
+        qn, kn = q * scale, k
+    return qn, kn
+
+
+def gdn2_matrix_form(q, k, v, g, beta, w, s0, scale, l2):
+    """S_t = (I - khat (beta*khat)^T) diag(exp g) S_{t-1} + khat (w*v)^T;  o_t = qhat^T S_t."""
+    qn, kn = gdn2_normalise(q, k, float(np.float32(scale)), l2)
+    Bt, T, H, K = q.shape
+    V = v.shape[-1]
+    out = np.zeros((Bt, T, H, V))
+    for b in range(Bt):
+        for h in range(H):
+            S = np.zeros((K, V)) if s0 is None else s0[b, h].astype(F64)
+            for t in range(T):
+                kk = kn[b, t, h][:, None]
+                bk = (beta[b, t, h].astype(F64) * kn[b, t, h])[:, None]
+                M = np.eye(K) - kk @ bk.T
+                S = M @ (np.exp(g[b, t, h].astype(F64))[:, None] * S) + kk @ (w[b, t, h].astype(F64) * v[b, t, h])[None, :]
+                out[b, t, h] = qn[b, t, h] @ S
+    return out
+
+
+def gdn2_rand(rng, Bt, T, H, K, V, s0=True, per_key=True):
+    q = rnd(rng, Bt, T, H, K); k = rnd(rng, Bt, T, H, K); v = rnd(rng, Bt, T, H, V)
+    gs = (Bt, T, H, K) if per_key else (Bt, T, H, 1)
+    g = np.broadcast_to(-np.logaddexp(0, rng.standard_normal(gs)), (Bt, T, H, K)).astype(np.float32)
+    beta = np.broadcast_to(1 / (1 + np.exp(-rng.standard_normal(gs))), (Bt, T, H, K)).astype(np.float32)
+    w = (1 / (1 + np.exp(-rng.standard_normal((Bt, T, H, V))))).astype(np.float32)
+    S0 = rnd(rng, Bt, H, K, V, scale=0.05) if s0 else None
+    return q, k, v, g, beta, w, S0
+
+
+@pytest.mark.parametrize("l2", [True, False])
+def test_gdn2_matches_matrix_form(impl, l2):
+    rng = np.random.default_rng(11)
+    q, k, v, g, beta, w, S0 = gdn2_rand(rng, 2, 9, 2, 5, 3)
+    if not l2:
+        q *= 0.3; k *= 0.3
+    o = impl.gated_deltanet2(q, k, v, g, beta, w, S0, scale=0.7, use_qk_l2norm=l2, dtype=F64)
+    ref = gdn2_matrix_form(q, k, v, g, beta, w, S0, 0.7, l2)
+    np.testing.assert_allclose(o, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_gdn2_linear_attention_special_case(impl):
+    # g = 0 and beta = 0: o_t = qhat_t^T S0 + sum_{s<=t} (qhat_t . khat_s) w_s v_s  (causal mask).
+    rng = np.random.default_rng(12)
+    q, k, v, _, _, w, S0 = gdn2_rand(rng, 1, 10, 2, 6, 4)
+    zero = np.zeros_like(q)
+    o = impl.gated_deltanet2(q, k, v, zero, zero, w, S0, scale=0.5, use_qk_l2norm=True, dtype=F64)
+    qn, kn = gdn2_normalise(q, k, 0.5, True)
+    A = np.einsum("bthk,bshk->bhts", qn, kn) * np.tril(np.ones((10, 10)))
+    ref = np.einsum("bhts,bshv->bthv", A, w.astype(F64) * v) + np.einsum("bthk,bhkv->bthv", qn, S0.astype(F64))
+    np.testing.assert_allclose(o, ref, rtol=1e-11, atol=1e-12)
+
+
+def test_gdn2_delta_rule_projection(impl):
+    # One token, beta = 1, g = 0, q = k, scale = 1: o = khat^T S1 with
+    # S1 = S0 + khat (w v - khat^T S0), so khat^T S1 = w v + (1 - |khat|^2)(khat^T S0 - w v).
+    rng = np.random.default_rng(13)
+    q, k, v, _, _, w, S0 = gdn2_rand(rng, 1, 1, 1, 8, 5)
+    one = np.ones_like(k); zero = np.zeros_like(k)
+    o = impl.gated_deltanet2(k, k, v, zero, one, w, S0, scale=1.0, use_qk_l2norm=True, dtype=F64)
+    _, kn = gdn2_normalise(k, k, 1.0, True)
+    kk = kn[0, 0, 0]
+    n2 = kk @ kk
+    wv = (w.astype(F64) * v)[0, 0, 0]
+    ks0 = kk @ S0[0, 0].astype(F64)
+    np.testing.assert_allclose(o[0, 0, 0], wv + (1 - n2) * (ks0 - wv), rtol=1e-12, atol=1e-13)
+    assert abs(n2 - 1) < 1e-6   # the eps sits inside the rsqrt
+
+
+def test_gdn2_eps_inside_rsqrt(impl):
+    # |q|^2 = 1e-6 = eps: qhat = q / sqrt(2e-6) exactly (gated_deltanet2_fwd.cu:14, :60).
+    K, V = 4, 4
+    q = np.zeros((1, 1, 1, K), np.float32); q[..., 0] = 1e-3
+    k = np.ones((1, 1, 1, K), np.float32)
+    S0 = np.eye(K, V, dtype=np.float32)[None, None]
+    zero = np.zeros((1, 1, 1, K), np.float32)
+    zv = np.zeros((1, 1, 1, V), np.float32)
+    o = impl.gated_deltanet2(q, k, zv, zero, zero, zv, S0, scale=1.0, use_qk_l2norm=True, dtype=F64)
+    expect = 1e-3 / np.sqrt(float(np.float32(1e-3)) ** 2 + float(np.float32(1e-6)))
+    np.testing.assert_allclose(o[0, 0, 0, 0], float(np.float32(1e-3)) / np.sqrt(float(np.float32(1e-3)) ** 2 + float(np.float32(1e-6))), rtol=1e-12)
+    assert abs(o[0, 0, 0, 0] - expect) < 1e-6
+
+
+def test_gdn2_pure_decay(impl):
+    # beta = 0, w = 0: o_t = qhat_t^T diag(exp(sum_{s<=t} g_s)) S0.
+    rng = np.random.default_rng(14)
+    q, k, v, g, _, _, S0 = gdn2_rand(rng, 1, 7, 2, 5, 3)
+    zero = np.zeros_like(q); zw = np.zeros_like(v)
+    o = impl.gated_deltanet2(q, k, v, g, zero, zw, S0, scale=1.0, use_qk_l2norm=True, dtype=F64)
+    qn, _ = gdn2_normalise(q, k, 1.0, True)
+    cum = np.exp(np.cumsum(g.astype(F64), axis=1))
+    ref = np.einsum("bthk,bhkv->bthv", qn * cum, S0.astype(F64))
+    np.testing.assert_allclose(o, ref, rtol=1e-11, atol=1e-13)
+
+
+def test_gdn2_invariances(impl):
+    rng = np.random.default_rng(15)
+    q, k, v, g, beta, w, S0 = gdn2_rand(rng, 1, 6, 2, 8, 4)
+    f = lambda **kw: impl.gated_deltanet2(**{**dict(q=q, k=k, v=v, g=g, beta=beta, w=w, initial_state=S0,
+                                                     scale=0.25, use_qk_l2norm=True, dtype=F64), **kw})
+    base = f()
+    # positive rescaling of q and k (by powers of two, exact in fp32) is invisible
+    # with the L2 norm on, up to the eps inside the rsqrt (|q|^2 ~ 8 >> 1e-6)
+    np.testing.assert_allclose(f(q=q * np.float32(4.0), k=k * np.float32(0.5)), base, rtol=2e-6, atol=1e-9)
+    # linear in scale
+    np.testing.assert_allclose(f(scale=0.5), 2 * base, rtol=1e-12, atol=1e-14)
+
+
+def test_gdn2_column_independence(impl):
+    rng = np.random.default_rng(16)
+    q, k, v, g, beta, w, S0 = gdn2_rand(rng, 1, 5, 2, 6, 8)
+    full = impl.gated_deltanet2(q, k, v, g, beta, w, S0, scale=0.4, dtype=F64)
+    part = impl.gated_deltanet2(q, k, np.ascontiguousarray(v[..., :3]), g, beta, np.ascontiguousarray(w[..., :3]),
+                                np.ascontiguousarray(S0[..., :3]), scale=0.4, dtype=F64)
+    np.testing.assert_array_equal(part, full[..., :3])
+
+
+def test_gdn2_numpy_and_c_agree():
+    rng = np.random.default_rng(17)
+    args = dict(zip(("q", "k", "v", "g", "beta", "w", "initial_state"), gdn2_rand(rng, 2, 40, 3, 16, 12)))
+    for dt, tol in ((F64, 1e-12), (np.float32, 1e-5)):
+        a = numpy_ref.gated_deltanet2(**args, scale=0.25, dtype=dt)
+        b = cref.gated_deltanet2(**args, scale=0.25, dtype=dt)
+        np.testing.assert_allclose(a, b, rtol=tol, atol=tol)
+
+
+# ---------------------------------------------------------------------------
+# Mamba3SisoFn
+# ---------------------------------------------------------------------------
+
+def m3_rand(rng, Bt, T, H, P, N, A, Hq=None, z=False):
+    Hq = Hq or H
+    V = rnd(rng, Bt, T, H, P)
+    DT = np.logaddexp(0, rng.standard_normal((Bt, H, T)) - 1).astype(np.float32)
+    ADT = (-rng.uniform(0.1, 2.0, (1, H, 1)) * DT).astype(np.float32)
+    Q = rnd(rng, Bt, T, Hq, N, scale=N ** -0.5); K = rnd(rng, Bt, T, Hq, N, scale=N ** -0.5)
+    Trap = rng.uniform(0, 1, (Bt, H, T)).astype(np.float32)
+    Qb = rnd(rng, H, N, scale=N ** -0.5); Kb = rnd(rng, H, N, scale=N ** -0.5)
+    Ang = rng.uniform(0, 1, (Bt, T, H, A)).astype(np.float32)
+    D = rnd(rng, H)
+    Z = rnd(rng, Bt, T, H, P) if z else None
+    return dict(Q=Q, K=K, V=V, ADT=ADT, DT=DT, Trap=Trap, Q_bias=Qb, K_bias=Kb, Angles=Ang, D=D, Z=Z)
+
+
+def sig64(x):
+    return 1 / (1 + np.exp(-np.asarray(x, F64)))
+
+
+def m3_closed_form(a):
+    """y_t = sum_{s<t} exp(sum_{r=s+1..t} ADT_r) (R_t q_t).(R_s k_s)(gamma_s + look_s) V_s
+           + (D + q_t.k_t gamma_t) V_t  (* silu Z), with theta_t = (sum_{s<=t} tanh(ang_s) dt_s pi) mod 2pi
+    and R_t the rotation of pair p < A by theta_t[p] (explicit 2x2 matrices)."""
+    Q, K, V = a["Q"].astype(F64), a["K"].astype(F64), a["V"].astype(F64)
+    ADT, DT, Trap = a["ADT"].astype(F64), a["DT"].astype(F64), a["Trap"].astype(F64)
+    Qb, Kb, Ang = a["Q_bias"].astype(F64), a["K_bias"].astype(F64), a["Angles"].astype(F64)
+    D = a["D"]; Z = a["Z"]
+    Bt, T, Hq, N = Q.shape
+    H, P = V.shape[2], V.shape[3]
+    Adim = Ang.shape[3]
+    out = np.zeros((Bt, T, H, P))
+    for b in range(Bt):
+        for h in range(H):
+            g = h // (H // Hq)
+            q = Q[b, :, g] + Qb[h]; k = K[b, :, g] + Kb[h]               # [T,N]
+            inc = np.tanh(Ang[b, :, h]) * DT[b, h][:, None] * PI_F        # [T,A]
+            theta = np.mod(np.cumsum(inc, axis=0), TWO_PI_F)
+            def rot(x):
+                y = x.copy()
+                for p in range(Adim):
+                    c, s = np.cos(theta[:, p]), np.sin(theta[:, p])
+                    x0, x1 = x[:, 2 * p], x[:, 2 * p + 1]
+                    y[:, 2 * p] = c * x0 - s * x1
+                    y[:, 2 * p + 1] = s * x0 + c * x1
+                return y
+            qr, kr = rot(q), rot(k)
+            gam = DT[b, h] * sig64(Trap[b, h])
+            look = np.zeros(T); look[:-1] = DT[b, h, 1:] * (1 - sig64(Trap[b, h, 1:]))
+            cs = np.cumsum(ADT[b, h])
+            Dec = np.exp(cs[:, None] - cs[None, :]) * np.tril(np.ones((T, T)), -1)  # s < t
+            W = (qr @ kr.T) * Dec * (gam + look)[None, :]
+            y = W @ V[b, :, h] + ((0 if D is None else float(D[h])) + (q * k).sum(1) * gam)[:, None] * V[b, :, h]
+            if Z is not None:
+                zz = Z[b, :, h].astype(F64)
+                y = y * zz * sig64(zz)
+            out[b, :, h] = y
+    return out
+
+
+@pytest.mark.parametrize("hq,adim,z", [(2, 4, False), (1, 2, True), (2, 1, False)])
+def test_m3_matches_closed_form(impl, hq, adim, z):
+    rng = np.random.default_rng(21 + adim)
+    a = m3_rand(rng, 2, 11, 2, 3, 8, adim, Hq=hq, z=z)
+    y = impl.mamba3_siso(**a, dtype=F64)
+    np.testing.assert_allclose(y, m3_closed_form(a), rtol=1e-9, atol=1e-11)
+
+
+def test_m3_single_token(impl):
+    rng = np.random.default_rng(22)
+    a = m3_rand(rng, 2, 1, 3, 4, 6, 3, z=True)
+    y = impl.mamba3_siso(**a, dtype=F64)
+    q = a["Q"].astype(F64)[:, 0] + a["Q_bias"]; k = a["K"].astype(F64)[:, 0] + a["K_bias"]
+    gam = a["DT"].astype(F64)[:, :, 0] * sig64(a["Trap"][:, :, 0])
+    diag = a["D"].astype(F64)[None] + (q * k).sum(-1) * gam
+    zz = a["Z"].astype(F64)[:, 0]
+    ref = diag[..., None] * a["V"].astype(F64)[:, 0] * zz * sig64(zz)
+    np.testing.assert_allclose(y[:, 0], ref, rtol=1e-13, atol=1e-14)
+
+
+def test_m3_zero_q_gives_skip(impl):
+    rng = np.random.default_rng(23)
+    a = m3_rand(rng, 1, 9, 2, 3, 4, 2)
+    a["Q"] = np.broadcast_to(-a["Q_bias"][None, None], a["Q"].shape).astype(np.float32).copy()
+    y = impl.mamba3_siso(**a, dtype=F64)
+    np.testing.assert_allclose(y, a["D"].astype(F64)[None, None, :, None] * a["V"], rtol=0, atol=1e-15)
+
+
+def test_m3_trap_saturated_is_euler(impl):
+    # sigmoid(Trap) = 1 exactly in fp64 for Trap = 60: the look-ahead term vanishes.
+    rng = np.random.default_rng(24)
+    a = m3_rand(rng, 1, 8, 1, 2, 4, 2)
+    a["Trap"] = np.full_like(a["Trap"], 60.0)
+    y = impl.mamba3_siso(**a, dtype=F64)
+    ref = m3_closed_form(a)
+    np.testing.assert_allclose(y, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_m3_partial_angles_equal_zero_padded(impl):
+    rng = np.random.default_rng(25)
+    a = m3_rand(rng, 1, 10, 2, 3, 8, 2)
+    full = dict(a)
+    ang = np.zeros(a["Angles"].shape[:3] + (4,), np.float32)
+    ang[..., :2] = a["Angles"]
+    full["Angles"] = ang
+    np.testing.assert_allclose(impl.mamba3_siso(**a, dtype=F64), impl.mamba3_siso(**full, dtype=F64), rtol=0, atol=1e-15)
+
+
+def test_m3_grouped_qk_equals_repeated(impl):
+    rng = np.random.default_rng(26)
+    a = m3_rand(rng, 1, 7, 4, 2, 4, 2, Hq=2)
+    rep = dict(a)
+    rep["Q"] = np.repeat(a["Q"], 2, axis=2)
+    rep["K"] = np.repeat(a["K"], 2, axis=2)
+    np.testing.assert_allclose(impl.mamba3_siso(**a, dtype=F64), impl.mamba3_siso(**rep, dtype=F64), rtol=0, atol=0)
+
+
+def test_m3_numpy_and_c_agree():
+    rng = np.random.default_rng(27)
+    a = m3_rand(rng, 2, 33, 3, 5, 8, 3, z=True)
+    for dt, tol in ((F64, 1e-12), (np.float32, 2e-5)):
+        np.testing.assert_allclose(numpy_ref.mamba3_siso(**a, dtype=dt), cref.mamba3_siso(**a, dtype=dt), rtol=tol, atol=tol)
+
+
+# ---------------------------------------------------------------------------
+# SoftmaxCPU
+# ---------------------------------------------------------------------------
+
+def test_softmax_cpu_textbook():
+    rng = np.random.default_rng(31)
+    x = rnd(rng, 3, 5, 7)
+    for axis in (-1, 0, 1):
+        y = numpy_ref.softmax_cpu(x, axis)
+        e = np.exp(x.astype(F64) - x.astype(F64).max(axis, keepdims=True))
+        np.testing.assert_allclose(y, e / e.sum(axis, keepdims=True), rtol=1e-6, atol=1e-7)
+    # all -inf row: exp(-inf - -inf) is nan in the textbook; max-subtract with
+    # -inf max yields nan, matching std::exp(nan) in the reference loop.

@@ -1,0 +1,431 @@
+// GatedDeltaNet2Fn forward for gfx950 (CDNA4, wave64).
+//
+// Math (reference gated_deltanet2_fwd.cu:39-140, identical in :142-233):
+// per (b,h) a dk x dv state S; per token
+//     qhat = q*scale*rsqrt(|q|^2+1e-6), khat = k*rsqrt(|k|^2+1e-6)  (when L2 norm is on)
+//     S[i,:] *= exp(g_i);  e_j = sum_i beta_i khat_i S[i,j];  u_j = w_j v_j - e_j
+//     S[i,j] += khat_i u_j; o_j = sum_i qhat_i S[i,j]
+// Every value column j evolves independently given the per-token vectors.
+//
+// Kernels:
+//  * Gdn2PrepKernel: one wave per (b,t,h) row of a token chunk (<= 1024
+//    tokens, so scratch does not grow with seqlen).  Writes khat, qhat, exp(g)
+//    and beta*khat, zero-padded to dk_pad, head-major so that one (b,h)'s
+//    token stream is contiguous.
+//  * Gdn2RecurKernel (dk <= 256): the state lives in VGPRs.  A wave is 4 rows
+//    of 16 lanes; the 16 lanes of a row split the keys (KT each) of CL value
+//    columns, so the two reductions over keys per token are 4-step DPP row
+//    sums with no barrier.  The 4 waves of a workgroup (16*CL columns of one
+//    (b,h)) share the per-token vectors, staged through LDS a block of tokens
+//    at a time with coalesced 16-byte loads prefetched one block ahead.
+//  * Gdn2RecurLdsKernel (dk > 256): same lane layout, the state tile
+//    [dk_pad x 16 columns] lives in LDS and the per-token vectors are read
+//    from the prepared chunk in global memory.
+// The fp32 state crosses chunk boundaries through the state scratch buffer
+// (reference :101-102, :133-139).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "xm_hip.h"
+#include "xm_params.h"
+
+namespace xm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunkTokens = 1024;   // reference kGatedDeltaNet2PrepareTokens (gated_deltanet2.h:11)
+constexpr int kRegKeyLimit = 256;    // reference kGatedDeltaNet2RegisterKeyLimit (gated_deltanet2.h:10)
+constexpr int kMaxLdsKeys = 2048;    // LDS-state path: dk_pad * 16 columns * 4 B <= 128 KiB
+constexpr int kTB = 8;               // tokens per staged block in the register path
+constexpr float kL2Eps = 1.0e-6f;    // reference kL2NormEps (gated_deltanet2_fwd.cu:14)
+
+// ---------------------------------------------------------------------------
+// Preparation
+// ---------------------------------------------------------------------------
+template <int KPL>
+__global__ __launch_bounds__(kThreads) void Gdn2PrepKernel(GatedDeltaNet2Params p, int t0, int tc) {
+    const int lane = threadIdx.x & 63;
+    const long long row = static_cast<long long>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    const long long rows = static_cast<long long>(p.batch) * p.nheads * tc;
+    if (row >= rows) return;  // uniform per wave
+    const int tl = static_cast<int>(row % tc);
+    const int bh = static_cast<int>(row / tc);
+    const int b = bh / p.nheads, h = bh % p.nheads;
+    const int t = t0 + tl;
+    const int dk = p.dk, kp = p.dk_pad;
+    const size_t src = ((static_cast<size_t>(b) * p.seqlen + t) * p.nheads + h) * static_cast<size_t>(dk);
+    float q[KPL], k[KPL];
+    float qs = 0.0f, ks = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+        const int kd = lane + 64 * j;
+        q[j] = kd < dk ? p.q[src + kd] : 0.0f;
+        k[j] = kd < dk ? p.k[src + kd] : 0.0f;
+        qs = fmaf(q[j], q[j], qs);
+        ks = fmaf(k[j], k[j], ks);
+    }
+    float q_mul = p.scale, k_mul = 1.0f;
+    if (p.l2norm) {
+        // reference :58-62: q_mul = scale * rsqrt(sum + eps); k_mul = rsqrt(sum + eps)
+        q_mul *= rsqrtf(WaveSum64(qs) + kL2Eps);
+        k_mul = rsqrtf(WaveSum64(ks) + kL2Eps);
+    }
+    float *dst = p.prepared + (static_cast<size_t>(bh) * p.chunk_cap + tl) * 4 * static_cast<size_t>(kp);
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+        const int kd = lane + 64 * j;
+        if (kd < kp) {
+            const bool ok = kd < dk;
+            const float kn = k[j] * k_mul;
+            dst[kd] = ok ? kn : 0.0f;                                  // khat
+            dst[kp + kd] = ok ? q[j] * q_mul : 0.0f;                   // qhat
+            dst[2 * kp + kd] = ok ? expf(p.g[src + kd]) : 0.0f;        // exp(g)
+            dst[3 * kp + kd] = ok ? p.beta[src + kd] * kn : 0.0f;      // beta * khat
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Register-state recurrence (dk <= 256)
+// ---------------------------------------------------------------------------
+template <int KT>
+__device__ __forceinline__ void LoadKeys(const float *src, float (&x)[KT]) {
+    if constexpr (KT % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < KT; j += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + j);
+            x[j] = v.x; x[j + 1] = v.y; x[j + 2] = v.z; x[j + 3] = v.w;
+        }
+    } else if constexpr (KT % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < KT; j += 2) {
+            const float2 v = *reinterpret_cast<const float2 *>(src + j);
+            x[j] = v.x; x[j + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KT; ++j) x[j] = src[j];
+    }
+}
+
+template <int KT, int CL>
+__global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params p, int t0, int tc) {
+    constexpr int KP = 16 * KT;               // padded keys (== p.dk_pad)
+    constexpr int VEC = 4 * KP;               // floats per token: khat, qhat, decay, beta*khat
+    constexpr int COLS = 16 * CL;             // value columns per workgroup
+    constexpr int VEC4 = kTB * VEC / 4;       // float4 per staged block
+    constexpr int VPT = (VEC4 + kThreads - 1) / kThreads;
+    constexpr int WVPT = (kTB * COLS + kThreads - 1) / kThreads;
+
+    __shared__ __attribute__((aligned(16))) float sVec[kTB * VEC];
+    __shared__ float sWV[kTB * COLS];
+    __shared__ float sOut[kTB * COLS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int kg = lane & 15, cg = lane >> 4;
+    const int nvb = (p.dv + COLS - 1) / COLS;
+    const int vb = blockIdx.x % nvb;
+    const int bh = blockIdx.x / nvb;
+    const int b = bh / p.nheads, h = bh % p.nheads;
+    const int dk = p.dk, dv = p.dv;
+    const int v0 = vb * COLS;
+
+    // State init: initial_state for the first chunk, else the carried state.
+    float S[CL][KT];
+    const float *sinit = nullptr;
+    if (t0 > 0) sinit = p.state;
+    else if (p.initial_state) sinit = p.initial_state;
+    const size_t sbase = static_cast<size_t>(bh) * dk * dv;
+#pragma unroll
+    for (int c = 0; c < CL; ++c) {
+        const int col = v0 + (w * 4 + cg) * CL + c;
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+            const int kd = kg * KT + j;
+            S[c][j] = (sinit && kd < dk && col < dv) ? sinit[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
+        }
+    }
+
+    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * VEC;
+    float4 vreg[VPT];
+    float wreg[WVPT], vvreg[WVPT];
+    auto load_block = [&](int tb0) {
+        const int nt = min(kTB, tc - tb0);
+        const float4 *src = reinterpret_cast<const float4 *>(prep + static_cast<size_t>(tb0) * VEC);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < VEC4 && i < nt * (VEC / 4)) vreg[k] = src[i];
+            else vreg[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < WVPT; ++k) {
+            const int i = tid + k * kThreads;
+            const int tt = i / COLS, cc = i % COLS;
+            const int col = v0 + cc;
+            wreg[k] = 0.0f;
+            vvreg[k] = 0.0f;
+            if (i < kTB * COLS && tt < nt && col < dv) {
+                const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
+                wreg[k] = p.w[idx];
+                vvreg[k] = p.v[idx];
+            }
+        }
+    };
+
+    load_block(0);
+    for (int tb0 = 0; tb0 < tc; tb0 += kTB) {
+        const int nt = min(kTB, tc - tb0);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < VEC4) reinterpret_cast<float4 *>(sVec)[i] = vreg[k];
+        }
+#pragma unroll
+        for (int k = 0; k < WVPT; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < kTB * COLS) sWV[i] = wreg[k] * vvreg[k];   // w * v (reference :120)
+        }
+        __syncthreads();
+        if (tb0 + kTB < tc) load_block(tb0 + kTB);
+
+        for (int tt = 0; tt < nt; ++tt) {
+            const float *vt = sVec + tt * VEC + kg * KT;
+            float kn[KT], qn[KT], dec[KT], bk[KT];
+            LoadKeys<KT>(vt, kn);
+            LoadKeys<KT>(vt + KP, qn);
+            LoadKeys<KT>(vt + 2 * KP, dec);
+            LoadKeys<KT>(vt + 3 * KP, bk);
+#pragma unroll
+            for (int c = 0; c < CL; ++c) {
+                const int cl = (w * 4 + cg) * CL + c;
+                float e = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KT; ++j) {
+                    S[c][j] *= dec[j];
+                    e = fmaf(bk[j], S[c][j], e);
+                }
+                e = RowSum16(e);
+                const float u = sWV[tt * COLS + cl] - e;
+                float o = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KT; ++j) {
+                    S[c][j] = fmaf(kn[j], u, S[c][j]);
+                    o = fmaf(qn[j], S[c][j], o);
+                }
+                o = RowSum16(o);
+                if (kg == 0) sOut[tt * COLS + cl] = o;
+            }
+        }
+        __syncthreads();
+        // Coalesced store of the block's outputs (COLS contiguous floats per token).
+        for (int i = tid; i < nt * COLS; i += kThreads) {
+            const int tt = i / COLS, cc = i % COLS;
+            const int col = v0 + cc;
+            if (col < dv) {
+                const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
+                p.out[idx] = sOut[i];
+            }
+        }
+        // The next iteration rewrites sVec/sWV (last read before the barrier
+        // above) and sOut only after its own barrier, so none is needed here.
+    }
+
+    if (t0 + tc < p.seqlen) {
+#pragma unroll
+        for (int c = 0; c < CL; ++c) {
+            const int col = v0 + (w * 4 + cg) * CL + c;
+#pragma unroll
+            for (int j = 0; j < KT; ++j) {
+                const int kd = kg * KT + j;
+                if (kd < dk && col < dv) p.state[sbase + static_cast<size_t>(kd) * dv + col] = S[c][j];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-state recurrence (dk > 256)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Params p, int t0, int tc) {
+    // State tile: key kd = kg*kt + j of column cl lives at (j*16 + cl)*16 + kg, so
+    // the 16 lanes of a row touch 16 consecutive floats (no bank conflicts).
+    extern __shared__ __attribute__((aligned(16))) float sS[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int kg = lane & 15, cg = lane >> 4;
+    const int cl = w * 4 + cg;                  // column within the workgroup (16 per workgroup)
+    const int nvb = (p.dv + 15) / 16;
+    const int vb = blockIdx.x % nvb;
+    const int bh = blockIdx.x / nvb;
+    const int b = bh / p.nheads, h = bh % p.nheads;
+    const int dk = p.dk, dv = p.dv, kp = p.dk_pad;
+    const int kt = kp / 16;                     // keys per lane (multiple of 4)
+    const int col = vb * 16 + cl;
+    const bool col_ok = col < dv;
+
+    const float *sinit = nullptr;
+    if (t0 > 0) sinit = p.state;
+    else if (p.initial_state) sinit = p.initial_state;
+    const size_t sbase = static_cast<size_t>(bh) * dk * dv;
+    for (int j = 0; j < kt; ++j) {
+        const int kd = kg * kt + j;
+        sS[(j * 16 + cl) * 16 + kg] = (sinit && kd < dk && col_ok) ? sinit[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
+    }
+    // Each lane touches only its own (key, column) cells: no barrier needed.
+
+    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * 4 * static_cast<size_t>(kp);
+    for (int tt = 0; tt < tc; ++tt) {
+        const float *vt = prep + static_cast<size_t>(tt) * 4 * kp + kg * kt;
+        const size_t vidx = ((static_cast<size_t>(b) * p.seqlen + t0 + tt) * p.nheads + h) * dv + col;
+        const float wv = col_ok ? p.w[vidx] * p.v[vidx] : 0.0f;
+        float e = 0.0f;
+        for (int j = 0; j < kt; j += 4) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(vt + 2 * kp + j);
+            const float4 b4 = *reinterpret_cast<const float4 *>(vt + 3 * kp + j);
+            const float dd[4] = {d4.x, d4.y, d4.z, d4.w}, bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                float &s = sS[((j + x) * 16 + cl) * 16 + kg];
+                s *= dd[x];
+                e = fmaf(bb[x], s, e);
+            }
+        }
+        e = RowSum16(e);
+        const float u = wv - e;
+        float o = 0.0f;
+        for (int j = 0; j < kt; j += 4) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(vt + j);
+            const float4 q4 = *reinterpret_cast<const float4 *>(vt + kp + j);
+            const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                float &s = sS[((j + x) * 16 + cl) * 16 + kg];
+                s = fmaf(kk[x], u, s);
+                o = fmaf(qq[x], s, o);
+            }
+        }
+        o = RowSum16(o);
+        if (kg == 0 && col_ok) p.out[vidx] = o;
+    }
+    if (t0 + tc < p.seqlen) {
+        for (int j = 0; j < kt; ++j) {
+            const int kd = kg * kt + j;
+            if (kd < dk && col_ok) p.state[sbase + static_cast<size_t>(kd) * dv + col] = sS[(j * 16 + cl) * 16 + kg];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+int KeyTile(int dk) {
+    // keys per lane for the 16-lane rows of the register kernel
+    const int kt = (dk + 15) / 16;
+    if (kt <= 1) return 1;
+    if (kt <= 2) return 2;
+    if (kt <= 4) return 4;
+    if (kt <= 8) return 8;
+    if (kt <= 12) return 12;
+    return 16;
+}
+
+int PadKeys(int dk) {
+    if (dk <= kRegKeyLimit) return 16 * KeyTile(dk);
+    return (dk + 63) / 64 * 64;
+}
+
+int ColumnsPerLane(int batch, int nheads, int dv) {
+    const char *env = std::getenv("XM_GDN2_CL");
+    const int forced = env ? std::atoi(env) : 0;
+    if (forced == 1 || forced == 2) return forced;
+    const long long wg2 = static_cast<long long>(batch) * nheads * ((dv + 31) / 32);
+    return wg2 >= 256 ? 2 : 1;
+}
+
+template <int KT, int CL>
+void LaunchRecur(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.dv + 16 * CL - 1) / (16 * CL));
+    hipLaunchKernelGGL((Gdn2RecurKernel<KT, CL>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, p, t0, tc);
+}
+
+template <int KT>
+void LaunchRecurKT(const GatedDeltaNet2Params &p, int cl, int t0, int tc, hipStream_t stream) {
+    if (cl == 2) LaunchRecur<KT, 2>(p, t0, tc, stream);
+    else LaunchRecur<KT, 1>(p, t0, tc, stream);
+}
+
+template <int KPL>
+void LaunchPrep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
+    const long long rows = static_cast<long long>(p.batch) * p.nheads * tc;
+    const long long blocks = (rows + 3) / 4;
+    hipLaunchKernelGGL((Gdn2PrepKernel<KPL>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, p, t0, tc);
+}
+
+void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
+    const int kpl = (p.dk_pad + 63) / 64;
+    if (kpl <= 1) LaunchPrep<1>(p, t0, tc, stream);
+    else if (kpl <= 2) LaunchPrep<2>(p, t0, tc, stream);
+    else if (kpl <= 4) LaunchPrep<4>(p, t0, tc, stream);
+    else if (kpl <= 8) LaunchPrep<8>(p, t0, tc, stream);
+    else if (kpl <= 16) LaunchPrep<16>(p, t0, tc, stream);
+    else LaunchPrep<32>(p, t0, tc, stream);
+}
+
+}  // namespace
+
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
+    const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
+    const size_t prepared = static_cast<size_t>(batch) * nheads * cap * 4 * PadKeys(dk);
+    const size_t state = seqlen > kChunkTokens ? static_cast<size_t>(batch) * nheads * dk * dv : 0;
+    // 256-byte alignment of the second region
+    return (prepared * sizeof(float) + 255) / 256 * 256 + state * sizeof(float);
+}
+
+void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_v);
+    if (p.dk > kMaxLdsKeys)
+        throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");
+    p.dk_pad = PadKeys(p.dk);
+    p.chunk_cap = std::min(p.seqlen, kChunkTokens);
+    const size_t prepared = static_cast<size_t>(p.batch) * p.nheads * p.chunk_cap * 4 * p.dk_pad;
+    p.prepared = static_cast<float *>(scratch);
+    p.state = p.seqlen > kChunkTokens
+                  ? reinterpret_cast<float *>(static_cast<char *>(scratch) + (prepared * sizeof(float) + 255) / 256 * 256)
+                  : nullptr;
+    const long long bh = static_cast<long long>(p.batch) * p.nheads;
+    if (bh * ((p.dv + 15) / 16) > 2147483647LL || bh * kChunkTokens / 4 > 2147483647LL)
+        throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    const int cl = ColumnsPerLane(p.batch, p.nheads, p.dv);
+    const int kt = KeyTile(p.dk);
+    if (p.dk > kRegKeyLimit) {
+        const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
+        XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    }
+    for (int t0 = 0; t0 < p.seqlen; t0 += p.chunk_cap) {
+        const int tc = std::min(p.chunk_cap, p.seqlen - t0);
+        Prep(p, t0, tc, stream);
+        XM_LAUNCH_CHECK("GatedDeltaNet2Fn preparation");
+        if (p.dk > kRegKeyLimit) {
+            const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
+            const long long blocks = bh * ((p.dv + 15) / 16);
+            hipLaunchKernelGGL(Gdn2RecurLdsKernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, p, t0, tc);
+        } else {
+            switch (kt) {
+                case 1: LaunchRecurKT<1>(p, cl, t0, tc, stream); break;
+                case 2: LaunchRecurKT<2>(p, cl, t0, tc, stream); break;
+                case 4: LaunchRecurKT<4>(p, cl, t0, tc, stream); break;
+                case 8: LaunchRecurKT<8>(p, cl, t0, tc, stream); break;
+                case 12: LaunchRecurKT<12>(p, cl, t0, tc, stream); break;
+                default: LaunchRecurKT<16>(p, cl, t0, tc, stream); break;
+            }
+        }
+        XM_LAUNCH_CHECK("GatedDeltaNet2Fn recurrence");
+    }
+}
+
+}  // namespace xm

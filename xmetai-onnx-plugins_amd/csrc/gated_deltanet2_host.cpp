@@ -1,0 +1,127 @@
+// GatedDeltaNet2Fn host layer: attribute checks, shape validation, scratch
+// and launch.  Mirrors gated_deltanet2_fn_ort.cpp:46-219 of the reference
+// (constructor checks in the same order, ValidateInputs and its messages,
+// ToIntDim, output shape = v.shape).
+//
+// Scratch (requested from the caller's allocator, reference :86-111): the
+// prepared per-token vectors of one <=1024-token chunk, and the fp32 state
+// carried between chunks when seqlen > 1024.
+#include <cmath>
+
+#include "xm_common.h"
+#include "xm_params.h"
+
+namespace xm {
+namespace {
+
+constexpr size_t kNumInputs = 7;
+
+void CheckAttrs(const xm_gated_deltanet2_attrs_t &a) {
+    if (a.output_final_state != 0) Unsupported("GatedDeltaNet2Fn v1 does not support output_final_state");
+    if (a.use_gate_in_kernel != 0)
+        Unsupported("GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel");
+    if (a.has_cu_seqlens != 0) Unsupported("GatedDeltaNet2Fn v1 does not support cu_seqlens");
+    if (a.state_v_first != 0) Unsupported("GatedDeltaNet2Fn v1 expects state layout (batch, head, key, value)");
+    if (!(a.scale > 0.0f) || !std::isfinite(a.scale)) Invalid("GatedDeltaNet2Fn requires a positive finite scale");
+}
+
+struct Plan {
+    GatedDeltaNet2Params params{};
+    std::vector<int64_t> out_shape;
+    size_t scratch = 0;
+};
+
+Plan Validate(const std::vector<View> &in, const xm_gated_deltanet2_attrs_t &attrs) {
+    const View &q = in[0], &k = in[1], &v = in[2], &g = in[3], &beta = in[4], &w = in[5], &s0 = in[6];
+    // ValidateInputs (reference :187-219)
+    RequireRank(q, 4, "q");
+    RequireRank(k, 4, "k");
+    RequireRank(v, 4, "v");
+    RequireRank(g, 4, "g");
+    RequireRank(beta, 4, "beta");
+    RequireRank(w, 4, "w");
+    RequireSameShape(q, k, "q", "k");
+    RequireSameShape(q, g, "q", "g");
+    RequireSameShape(q, beta, "q", "beta");
+    if (v.shape[0] != q.shape[0] || v.shape[1] != q.shape[1] || v.shape[2] != q.shape[2])
+        Invalid("v batch/seqlen/head dimensions must match q");
+    RequireSameShape(v, w, "v", "w");
+    if (s0.present()) {
+        RequireRank(s0, 4, "initial_state");
+        if (s0.shape[0] != q.shape[0] || s0.shape[1] != q.shape[2] || s0.shape[2] != q.shape[3] ||
+            s0.shape[3] != v.shape[3])
+            Invalid("initial_state must have shape (batch, head, headdim_k, headdim_v)");
+    }
+    Plan plan;
+    plan.out_shape = v.shape;
+    GatedDeltaNet2Params &p = plan.params;
+    p.batch = ToIntDim(q.shape[0], "batch");
+    p.seqlen = ToIntDim(q.shape[1], "seqlen");
+    p.nheads = ToIntDim(q.shape[2], "nheads");
+    p.dk = ToIntDim(q.shape[3], "headdim_k");
+    p.dv = ToIntDim(v.shape[3], "headdim_v");
+    if (p.dk > 2048) Unsupported("GatedDeltaNet2Fn supports headdim_k up to 2048");
+    p.q = q.data;
+    p.k = k.data;
+    p.v = v.data;
+    p.g = g.data;
+    p.beta = beta.data;
+    p.w = w.data;
+    p.initial_state = s0.present() ? s0.data : nullptr;
+    p.l2norm = attrs.use_qk_l2norm_in_kernel != 0;
+    p.scale = attrs.scale;
+    plan.scratch = GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv);
+    return plan;
+}
+
+}  // namespace
+}  // namespace xm
+
+extern "C" {
+
+void xm_gated_deltanet2_attrs_default(xm_gated_deltanet2_attrs_t *attrs) {
+    if (attrs == nullptr) return;
+    attrs->scale = 1.0f;                   // reference :47
+    attrs->use_qk_l2norm_in_kernel = 1;    // reference :48
+    attrs->output_final_state = 0;
+    attrs->use_gate_in_kernel = 0;
+    attrs->has_cu_seqlens = 0;
+    attrs->state_v_first = 0;
+}
+
+int xm_gated_deltanet2_check_attrs(const xm_gated_deltanet2_attrs_t *attrs, char *errbuf, size_t errlen) {
+    return xm::Guard(errbuf, errlen, [&] {
+        if (attrs == nullptr) xm::Invalid("attrs is null");
+        xm::CheckAttrs(*attrs);
+    });
+}
+
+int xm_gated_deltanet2_validate(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t *attrs,
+                                int64_t *out_shape, int32_t *out_rank, size_t *scratch_bytes, char *errbuf,
+                                size_t errlen) {
+    return xm::Guard(errbuf, errlen, [&] {
+        if (attrs == nullptr) xm::Invalid("attrs is null");
+        xm::CheckAttrs(*attrs);
+        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "GatedDeltaNet2Fn");
+        xm::Plan plan = xm::Validate(views, *attrs);
+        xm::WriteShape(plan.out_shape, out_shape, out_rank);
+        if (scratch_bytes) *scratch_bytes = plan.scratch;
+    });
+}
+
+int xm_gated_deltanet2_forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t *attrs,
+                               float *out, void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
+    return xm::Guard(errbuf, errlen, [&] {
+        if (attrs == nullptr) xm::Invalid("attrs is null");
+        xm::CheckAttrs(*attrs);
+        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "GatedDeltaNet2Fn");
+        xm::Plan plan = xm::Validate(views, *attrs);
+        if (out == nullptr) xm::Invalid("output pointer is null");
+        plan.params.out = out;
+        xm::Scratch scratch(alloc, stream);
+        void *buf = scratch.Get(plan.scratch);
+        xm::LaunchGatedDeltaNet2(plan.params, buf, stream);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// HIP error mapping and small device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "xm_common.h"
+
+#define XM_HIP_CHECK(expr)                                                                         \
+    do {                                                                                           \
+        hipError_t xm_err_ = (expr);                                                               \
+        if (xm_err_ != hipSuccess)                                                                 \
+            throw ::xm::Error(XM_ERR_DEVICE, std::string(#expr) + " failed: " + hipGetErrorString(xm_err_)); \
+    } while (0)
+
+// Reports a failed launch (reference: XM_CUDA_KERNEL_CHECK, cuda_common.h:27-36).
+#define XM_LAUNCH_CHECK(what)                                                                      \
+    do {                                                                                           \
+        hipError_t xm_err_ = hipGetLastError();                                                    \
+        if (xm_err_ != hipSuccess)                                                                 \
+            throw ::xm::Error(XM_ERR_DEVICE, std::string(what) + " kernel launch failed: " + hipGetErrorString(xm_err_)); \
+    } while (0)
+
+namespace xm {
+
+constexpr float kLog2eF = 1.4426950408889634f;  // M_LOG2E as float
+
+// Moves `x` across lanes with a DPP control (row-local patterns only).
+template <int CTRL>
+__device__ __forceinline__ float DppF(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over the 16 lanes of a DPP row, result in every lane of the row.
+// xor 1 and xor 2 (quad_perm), xor 7 (row_half_mirror), xor 8 (row_ror:8)
+// span all 16 lanes; each step folds into one v_add_f32_dpp.
+__device__ __forceinline__ float RowSum16(float x) {
+    x += DppF<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += DppF<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += DppF<0x141>(x);  // row_half_mirror
+    x += DppF<0x128>(x);  // row_ror:8
+    return x;
+}
+
+// Sum over 64 lanes, result in every lane (a row sum, then the two cross-row
+// steps through __shfl_xor).
+__device__ __forceinline__ float WaveSum64(float x) {
+    x = RowSum16(x);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+__device__ __forceinline__ double WaveSum64d(double x) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+}  // namespace xm

@@ -1,0 +1,65 @@
+// Plain-old-data launch parameters passed from the host layer to the HIP
+// launchers.  Tensors are dense row-major fp32 in the layouts documented on
+// each field; index arithmetic in the kernels is 64-bit where a product of
+// dimensions can exceed 2^31.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace xm {
+
+// SelectiveScanFn (reference parameter block: selective_scan.h:26-69).
+struct SelectiveScanParams {
+    const float *u;          // [batch, dim, seqlen]
+    const float *delta;      // [batch, dim, seqlen]
+    const float *A;          // [dim, dstate]
+    const float *B;          // b_var ? [batch, groups_b, dstate, seqlen] : [dim, dstate]
+    const float *C;          // c_var ? [batch, groups_c, dstate, seqlen] : [dim, dstate]
+    const float *D;          // [dim] or nullptr
+    const float *delta_bias; // [dim] or nullptr
+    float *out;              // [batch, dim, seqlen]
+    int batch, dim, seqlen, dstate;
+    int b_var, c_var;
+    int groups_b;            // n_groups (from B; 1 when B is constant)
+    int groups_c;            // C.shape[1] when C is variable
+    int dim_per_group;       // dim / groups_b
+    int delta_softplus;
+};
+
+// GatedDeltaNet2Fn (reference parameter block: gated_deltanet2.h:13-40).
+struct GatedDeltaNet2Params {
+    const float *q, *k, *g, *beta;  // [batch, seqlen, nheads, dk]
+    const float *v, *w;             // [batch, seqlen, nheads, dv]
+    const float *initial_state;     // [batch, nheads, dk, dv] or nullptr
+    float *out;                     // [batch, seqlen, nheads, dv]
+    float *state;                   // carry between token chunks, [batch, nheads, dk, dv]
+    float *prepared;                // [batch*nheads, chunk_cap, 4, dk_pad]: khat, qhat, exp(g), beta*khat
+    int batch, seqlen, nheads, dk, dv;
+    int dk_pad;                     // dk rounded up to the recurrence's key tiling
+    int chunk_cap;                  // tokens per preparation chunk (<= 1024)
+    int l2norm;
+    float scale;
+};
+
+// Mamba3SisoFn (reference parameter block: mamba3_siso.h:10-36).
+struct Mamba3SisoParams {
+    const float *Q, *K;             // [batch, seqlen, nheads_qk, n]
+    const float *V;                 // [batch, seqlen, nheads, p]
+    const float *ADT, *DT, *Trap;   // [batch, nheads, seqlen]
+    const float *Q_bias, *K_bias;   // [nheads, n]
+    const float *Angles;            // [batch, seqlen, nheads, a]
+    const float *D;                 // [nheads] or nullptr
+    const float *Z;                 // [batch, seqlen, nheads, p] or nullptr
+    float *out;                     // [batch, seqlen, nheads, p]
+    int batch, seqlen, nheads, nheads_qk, n, p, a;
+};
+
+// Launchers (defined in the .hip translation units).  They enqueue on
+// `stream` and throw xm::Error on a launch failure.
+void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
+void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
+void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
+
+}  // namespace xm

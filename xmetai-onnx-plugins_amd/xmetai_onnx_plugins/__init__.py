@@ -1,0 +1,248 @@
+"""MI355X (gfx950) recurrent operators of the ONNX domain ``xmetai_plugins``.
+
+Python front end of ``libxmetai_recurrent.so`` (C ABI in
+``include/xmetai_recurrent.h``).  The three functions take the operators'
+inputs in the reference's order, as fp32 torch tensors on a ROCm device, and
+enqueue the HIP kernels on the current torch stream:
+
+* :func:`selective_scan_fn`   -- ``SelectiveScanFn``  (selective_scan_fn_ort.cpp:48-246)
+* :func:`mamba3_siso_fn`      -- ``Mamba3SisoFn``     (mamba3_siso_fn_ort.cpp:41-246)
+* :func:`gated_deltanet2_fn`  -- ``GatedDeltaNet2Fn`` (gated_deltanet2_fn_ort.cpp:44-237)
+
+"Optional" inputs are passed as ``None`` or a zero-element tensor, exactly as
+the ONNX graphs pass them (every input of the reference ops is REQUIRED; an
+empty tensor means absent).  Errors raise :class:`XmError` carrying the C
+status code and the reference's message.  There is no CPU fallback: without
+the built library, or without a GPU, the forward functions raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional, Sequence
+
+from . import _capi
+from ._capi import (XM_ERR_ALLOC, XM_ERR_DEVICE, XM_ERR_INVALID_ARGUMENT, XM_ERR_UNSUPPORTED, XM_OK,
+                    EXPORTED_SYMBOLS, LIB_PATH)
+
+__all__ = [
+    "XmError", "lib", "version", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn",
+    "validate", "TorchAllocator", "EXPORTED_SYMBOLS", "LIB_PATH",
+    "XM_OK", "XM_ERR_INVALID_ARGUMENT", "XM_ERR_UNSUPPORTED", "XM_ERR_DEVICE", "XM_ERR_ALLOC",
+]
+
+DOMAIN = "xmetai_plugins"
+OP_NAMES = ("SelectiveScanFn", "Mamba3SisoFn", "GatedDeltaNet2Fn")
+
+_lib = None
+
+
+class XmError(RuntimeError):
+    """An error status returned by the C ABI."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{_capi.STATUS_NAMES.get(status, status)}] {message}")
+        self.status = status
+        self.message = message
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the in-tree library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python xmetai-onnx-plugins_amd/build.py` "
+                "(there is no fallback implementation)")
+        _lib = _capi.declare(ctypes.CDLL(LIB_PATH))
+    return _lib
+
+
+def version() -> str:
+    return lib().xm_version().decode()
+
+
+# ---------------------------------------------------------------------------
+# tensor descriptors
+# ---------------------------------------------------------------------------
+
+_DUMMY = ctypes.c_void_p(16)  # non-null address for shape-only validation; never dereferenced
+
+
+def _desc_from_shape(shape: Sequence[int], data_ptr: Optional[int] = None, elem_type: int = 1) -> _capi.XmTensor:
+    t = _capi.XmTensor()
+    if len(shape) > _capi.XM_MAX_RANK:
+        raise XmError(XM_ERR_INVALID_ARGUMENT, "tensor rank out of range")
+    t.rank = len(shape)
+    for i, d in enumerate(shape):
+        t.shape[i] = int(d)
+    t.elem_type = elem_type
+    n = math.prod(int(d) for d in shape) if len(shape) else 1
+    if data_ptr is not None:
+        t.data = data_ptr
+    else:
+        t.data = _DUMMY.value if n > 0 else None
+    return t
+
+
+def _desc_from_tensor(x) -> _capi.XmTensor:
+    import torch
+    if x is None:
+        return _desc_from_shape((0,))
+    if not isinstance(x, torch.Tensor):
+        raise TypeError("inputs must be torch tensors or None")
+    elem = 1 if x.dtype == torch.float32 else 0
+    if x.numel() > 0:
+        if not x.is_cuda:
+            raise XmError(XM_ERR_INVALID_ARGUMENT, "inputs must be device tensors")
+        if not x.is_contiguous():
+            raise XmError(XM_ERR_INVALID_ARGUMENT, "inputs must be contiguous (row-major)")
+    return _desc_from_shape(tuple(x.shape), x.data_ptr() if x.numel() > 0 else None, elem)
+
+
+def _attrs(op: str, **kw):
+    attrs_t, _ = _capi.OPS[op]
+    a = attrs_t()
+    getattr(lib(), f"xm_{op}_attrs_default")(ctypes.byref(a))
+    for k, v in kw.items():
+        if v is None:
+            continue
+        if not hasattr(a, k):
+            raise TypeError(f"unknown attribute {k} for {op}")
+        setattr(a, k, float(v) if k == "scale" else int(v))
+    return a
+
+
+def _check(status: int, err: ctypes.Array) -> None:
+    if status != XM_OK:
+        raise XmError(status, err.value.decode(errors="replace"))
+
+
+def validate(op: str, shapes: Sequence[Optional[Sequence[int]]], **attrs):
+    """Runs the operator's host-side validation on shapes only (no device).
+
+    ``op`` is ``"selective_scan"``, ``"mamba3_siso"`` or ``"gated_deltanet2"``;
+    ``shapes`` lists one shape per input (``None`` = absent).  Returns
+    ``(output_shape, scratch_bytes)`` or raises :class:`XmError`.
+    """
+    _, n = _capi.OPS[op]
+    if len(shapes) != n:
+        raise TypeError(f"{op} takes {n} inputs")
+    arr = (_capi.XmTensor * n)(*[_desc_from_shape(s if s is not None else (0,)) for s in shapes])
+    a = _attrs(op, **attrs)
+    out_shape = (ctypes.c_int64 * _capi.XM_MAX_RANK)()
+    out_rank = ctypes.c_int32()
+    scratch = ctypes.c_size_t()
+    err = ctypes.create_string_buffer(512)
+    st = getattr(lib(), f"xm_{op}_validate")(arr, n, ctypes.byref(a), out_shape, ctypes.byref(out_rank),
+                                             ctypes.byref(scratch), err, len(err))
+    _check(st, err)
+    return tuple(out_shape[i] for i in range(out_rank.value)), scratch.value
+
+
+def check_attrs(op: str, **attrs) -> None:
+    """Session-time attribute checks (the reference's kernel constructors)."""
+    a = _attrs(op, **attrs)
+    err = ctypes.create_string_buffer(512)
+    _check(getattr(lib(), f"xm_{op}_check_attrs")(ctypes.byref(a), err, len(err)), err)
+
+
+# ---------------------------------------------------------------------------
+# allocator over torch's caching allocator (stream-ordered)
+# ---------------------------------------------------------------------------
+
+class TorchAllocator:
+    """Scratch from torch's caching allocator on a given stream.
+
+    torch reuses a freed block only in the order of the stream it was
+    allocated on, which is the stream the operator runs on, so returning the
+    block right after the launches is safe (the contract of xm_allocator_t).
+    """
+
+    def __init__(self, device=None, stream=None):
+        import torch
+        self._torch = torch
+        self.device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        self.stream = stream
+        self.live = 0
+
+        def _alloc(ctx, nbytes):
+            s = self.stream if self.stream is not None else torch.cuda.current_stream(self.device)
+            try:
+                ptr = torch.cuda.caching_allocator_alloc(int(nbytes), self.device.index, s)
+            except Exception:
+                return None
+            self.live += 1
+            return ptr
+
+        def _free(ctx, ptr):
+            if ptr:
+                torch.cuda.caching_allocator_delete(ptr)
+                self.live -= 1
+
+        self._alloc_cb = _capi.ALLOC_FN(_alloc)
+        self._free_cb = _capi.FREE_FN(_free)
+        self.struct = _capi.XmAllocator(None, self._alloc_cb, self._free_cb)
+
+
+# ---------------------------------------------------------------------------
+# operators
+# ---------------------------------------------------------------------------
+
+def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocator], stream, **attrs):
+    import torch
+    _, n = _capi.OPS[op]
+    descs = [_desc_from_tensor(x) for x in inputs]
+    arr = (_capi.XmTensor * n)(*descs)
+    a = _attrs(op, **attrs)
+    err = ctypes.create_string_buffer(512)
+    out_shape = (ctypes.c_int64 * _capi.XM_MAX_RANK)()
+    out_rank = ctypes.c_int32()
+    scratch = ctypes.c_size_t()
+    _check(getattr(lib(), f"xm_{op}_validate")(arr, n, ctypes.byref(a), out_shape, ctypes.byref(out_rank),
+                                               ctypes.byref(scratch), err, len(err)), err)
+    ref = inputs[out_like_index]
+    out = torch.empty(tuple(out_shape[i] for i in range(out_rank.value)), dtype=torch.float32, device=ref.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(ref.device)
+    alloc_ptr = ctypes.byref(allocator.struct) if allocator is not None else None
+    with torch.cuda.device(ref.device):
+        st = getattr(lib(), f"xm_{op}_forward")(arr, n, ctypes.byref(a), ctypes.c_void_p(out.data_ptr() if out.numel() else None),
+                                                ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
+    _check(st, err)
+    return out
+
+
+def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, delta_softplus=False,
+                      return_last_state=False, allocator=None, stream=None):
+    """SelectiveScanFn: returns y [B,D,L] (the un-gated scan output; z is
+    validated and otherwise unused, as in selective_scan_fwd_kernel.cuh:272-301)."""
+    return _run("selective_scan", [u, delta, A, B, C, D, z, delta_bias], 0, allocator, stream,
+                delta_softplus=int(bool(delta_softplus)), return_last_state=int(bool(return_last_state)))
+
+
+def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None, *, chunk_size=64,
+                   has_d=None, has_z=None, return_final_states=False, has_input_states=False,
+                   has_cu_seqlens=False, allocator=None, stream=None):
+    """Mamba3SisoFn: returns [B,T,H,P].  ``has_d``/``has_z`` default to the
+    presence of D/Z (an exported graph sets them explicitly; default 1)."""
+    def present(x):
+        return x is not None and x.numel() > 0
+    has_d = present(D) if has_d is None else has_d
+    has_z = present(Z) if has_z is None else has_z
+    return _run("mamba3_siso", [Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z], 2, allocator, stream,
+                chunk_size=chunk_size, has_d=int(bool(has_d)), has_z=int(bool(has_z)),
+                return_final_states=int(bool(return_final_states)), has_input_states=int(bool(has_input_states)),
+                has_cu_seqlens=int(bool(has_cu_seqlens)))
+
+
+def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, use_qk_l2norm_in_kernel=True,
+                       output_final_state=False, use_gate_in_kernel=False, has_cu_seqlens=False,
+                       state_v_first=False, allocator=None, stream=None):
+    """GatedDeltaNet2Fn: returns [B,T,H,V]."""
+    return _run("gated_deltanet2", [q, k, v, g, beta, w, initial_state], 2, allocator, stream,
+                scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
+                output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
+                has_cu_seqlens=int(bool(has_cu_seqlens)), state_v_first=int(bool(state_v_first)))

@@ -1,0 +1,105 @@
+"""ctypes declarations of the C ABI in include/xmetai_recurrent.h."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+XM_MAX_RANK = 8
+XM_ELEM_FLOAT = 1
+
+XM_OK = 0
+XM_ERR_INVALID_ARGUMENT = 1
+XM_ERR_UNSUPPORTED = 2
+XM_ERR_DEVICE = 3
+XM_ERR_ALLOC = 4
+
+STATUS_NAMES = {
+    XM_OK: "XM_OK",
+    XM_ERR_INVALID_ARGUMENT: "XM_ERR_INVALID_ARGUMENT",
+    XM_ERR_UNSUPPORTED: "XM_ERR_UNSUPPORTED",
+    XM_ERR_DEVICE: "XM_ERR_DEVICE",
+    XM_ERR_ALLOC: "XM_ERR_ALLOC",
+}
+
+LIB_NAME = "libxmetai_recurrent.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+
+class XmTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("shape", ctypes.c_int64 * XM_MAX_RANK),
+        ("rank", ctypes.c_int32),
+        ("elem_type", ctypes.c_int32),
+    ]
+
+
+ALLOC_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t)
+FREE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p)
+
+
+class XmAllocator(ctypes.Structure):
+    _fields_ = [("ctx", ctypes.c_void_p), ("alloc", ALLOC_FN), ("free", FREE_FN)]
+
+
+class SelectiveScanAttrs(ctypes.Structure):
+    _fields_ = [("delta_softplus", ctypes.c_int64), ("return_last_state", ctypes.c_int64)]
+
+
+class Mamba3SisoAttrs(ctypes.Structure):
+    _fields_ = [
+        ("chunk_size", ctypes.c_int64),
+        ("has_d", ctypes.c_int64),
+        ("has_z", ctypes.c_int64),
+        ("return_final_states", ctypes.c_int64),
+        ("has_input_states", ctypes.c_int64),
+        ("has_cu_seqlens", ctypes.c_int64),
+    ]
+
+
+class GatedDeltaNet2Attrs(ctypes.Structure):
+    _fields_ = [
+        ("scale", ctypes.c_float),
+        ("use_qk_l2norm_in_kernel", ctypes.c_int64),
+        ("output_final_state", ctypes.c_int64),
+        ("use_gate_in_kernel", ctypes.c_int64),
+        ("has_cu_seqlens", ctypes.c_int64),
+        ("state_v_first", ctypes.c_int64),
+    ]
+
+
+# (op prefix, attrs struct, number of inputs)
+OPS = {
+    "selective_scan": (SelectiveScanAttrs, 8),
+    "mamba3_siso": (Mamba3SisoAttrs, 11),
+    "gated_deltanet2": (GatedDeltaNet2Attrs, 7),
+}
+
+# Every symbol include/xmetai_recurrent.h declares.
+EXPORTED_SYMBOLS = [
+    f"xm_{op}_{fn}" for op in OPS for fn in ("attrs_default", "check_attrs", "validate", "forward")
+] + ["xm_version"]
+
+
+def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
+    T = ctypes.POINTER(XmTensor)
+    for op, (attrs_t, _) in OPS.items():
+        A = ctypes.POINTER(attrs_t)
+        f = getattr(lib, f"xm_{op}_attrs_default")
+        f.argtypes = [A]
+        f.restype = None
+        f = getattr(lib, f"xm_{op}_check_attrs")
+        f.argtypes = [A, ctypes.c_char_p, ctypes.c_size_t]
+        f.restype = ctypes.c_int
+        f = getattr(lib, f"xm_{op}_validate")
+        f.argtypes = [T, ctypes.c_size_t, A, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
+                      ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p, ctypes.c_size_t]
+        f.restype = ctypes.c_int
+        f = getattr(lib, f"xm_{op}_forward")
+        f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(XmAllocator),
+                      ctypes.c_char_p, ctypes.c_size_t]
+        f.restype = ctypes.c_int
+    lib.xm_version.argtypes = []
+    lib.xm_version.restype = ctypes.c_char_p
+    return lib
