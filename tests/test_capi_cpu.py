@@ -186,11 +186,13 @@ def gdn_shapes(B=2, T=5, H=3, K=16, V=8, s0=True):
 def test_gdn2_valid_and_scratch():
     out, scratch = validate("gated_deltanet2", gdn_shapes(), scale=0.25)
     assert out == (2, 5, 3, 8)
-    # prepared chunk: 4 vectors x B*H*min(T,1024) rows x padded K (16); no state carry for T <= 1024
-    assert scratch == 4 * 2 * 3 * 5 * 16 * 4
+    # prepared chunk: B*H*min(T,1024) rows of 4 vectors x padded K (16), one
+    # q.k float per row; no state carry for T <= 1024
+    a256 = lambda n: (n + 255) // 256 * 256
+    assert scratch == a256(2 * 3 * 5 * 4 * 16 * 4) + a256(2 * 3 * 5 * 4)
     _, scratch_long = validate("gated_deltanet2", gdn_shapes(T=3000, K=128, V=64))
-    prep = 4 * 2 * 3 * 1024 * 128 * 4
-    assert scratch_long == (prep + 255) // 256 * 256 + 2 * 3 * 128 * 64 * 4
+    rows = 2 * 3 * 1024
+    assert scratch_long == a256(rows * 4 * 128 * 4) + a256(rows * 4) + 2 * 3 * 128 * 64 * 4
 
 
 @pytest.mark.parametrize("idx,shape,msg", [

@@ -7,17 +7,29 @@
 //     S[i,j] += khat_i u_j; o_j = sum_i qhat_i S[i,j]
 // Every value column j evolves independently given the per-token vectors.
 //
+// Evaluation order on the device.  With d = exp(g) and S the state before
+// the token, both sums the token needs read the same S:
+//     e_j = sum_i (beta_i khat_i d_i) S[i,j]       r_j = sum_i (qhat_i d_i) S[i,j]
+//     u_j = w_j v_j - e_j                          o_j = r_j + (qhat . khat) u_j
+//     S[i,j] <- fma(khat_i, u_j, S[i,j] * d_i)     (the reference's decay-then-update)
+// so one cross-lane reduction phase (of two values) per token sits on the
+// recurrence's critical path instead of two, and the readout leaves it.  The
+// state itself is updated with the reference's operations; e and o differ from
+// the reference only in the association of their products.
+//
 // Kernels:
 //  * Gdn2PrepKernel: one wave per (b,t,h) row of a token chunk (<= 1024
-//    tokens, so scratch does not grow with seqlen).  Writes khat, qhat, exp(g)
-//    and beta*khat, zero-padded to dk_pad, head-major so that one (b,h)'s
-//    token stream is contiguous.
+//    tokens, so scratch does not grow with seqlen).  Writes khat, beta*khat*d,
+//    qhat*d, d (each zero-padded to dk_pad) and qhat.khat, head-major so that
+//    one (b,h)'s token stream is contiguous.
 //  * Gdn2RecurKernel (dk <= 256): the state lives in VGPRs.  A wave is 4 rows
 //    of 16 lanes; the 16 lanes of a row split the keys (KT each) of CL value
-//    columns, so the two reductions over keys per token are 4-step DPP row
-//    sums with no barrier.  The 4 waves of a workgroup (16*CL columns of one
-//    (b,h)) share the per-token vectors, staged through LDS a block of tokens
-//    at a time with coalesced 16-byte loads prefetched one block ahead.
+//    columns, so the reduction over keys is a 4-step DPP row sum with no
+//    barrier.  The 4 waves of a workgroup (16*CL columns of one (b,h)) share
+//    the per-token vectors, staged through LDS a block of tokens at a time
+//    with coalesced 16-byte loads prefetched one block ahead; the LDS copy
+//    inserts 4 floats every 32 keys so the key-sliced 16-byte reads of a row
+//    hit distinct banks.
 //  * Gdn2RecurLdsKernel (dk > 256): same lane layout, the state tile
 //    [dk_pad x 16 columns] lives in LDS and the per-token vectors are read
 //    from the prepared chunk in global memory.
@@ -38,8 +50,11 @@ constexpr int kThreads = 256;
 constexpr int kChunkTokens = 1024;   // reference kGatedDeltaNet2PrepareTokens (gated_deltanet2.h:11)
 constexpr int kRegKeyLimit = 256;    // reference kGatedDeltaNet2RegisterKeyLimit (gated_deltanet2.h:10)
 constexpr int kMaxLdsKeys = 2048;    // LDS-state path: dk_pad * 16 columns * 4 B <= 128 KiB
-constexpr int kTB = 8;               // tokens per staged block in the register path
 constexpr float kL2Eps = 1.0e-6f;    // reference kL2NormEps (gated_deltanet2_fwd.cu:14)
+
+// Prepared row of one (b,h,t): [khat | beta*khat*d | qhat*d | d], kp floats
+// each; qhat.khat of the row goes to a separate per-(b,h,t) array (p.prep_qk).
+__host__ __device__ constexpr int PrepRow(int kp) { return 4 * kp; }
 
 // ---------------------------------------------------------------------------
 // Preparation
@@ -72,19 +87,26 @@ __global__ __launch_bounds__(kThreads) void Gdn2PrepKernel(GatedDeltaNet2Params 
         q_mul *= rsqrtf(WaveSum64(qs) + kL2Eps);
         k_mul = rsqrtf(WaveSum64(ks) + kL2Eps);
     }
-    float *dst = p.prepared + (static_cast<size_t>(bh) * p.chunk_cap + tl) * 4 * static_cast<size_t>(kp);
+    float *dst = p.prepared + (static_cast<size_t>(bh) * p.chunk_cap + tl) * static_cast<size_t>(PrepRow(kp));
+    float qk = 0.0f;
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
         const int kd = lane + 64 * j;
         if (kd < kp) {
             const bool ok = kd < dk;
-            const float kn = k[j] * k_mul;
-            dst[kd] = ok ? kn : 0.0f;                                  // khat
-            dst[kp + kd] = ok ? q[j] * q_mul : 0.0f;                   // qhat
-            dst[2 * kp + kd] = ok ? expf(p.g[src + kd]) : 0.0f;        // exp(g)
-            dst[3 * kp + kd] = ok ? p.beta[src + kd] * kn : 0.0f;      // beta * khat
+            const float kn = ok ? k[j] * k_mul : 0.0f;                 // khat
+            const float qn = ok ? q[j] * q_mul : 0.0f;                 // qhat
+            const float d = ok ? expf(p.g[src + kd]) : 0.0f;           // exp(g)
+            const float bk = ok ? p.beta[src + kd] * kn : 0.0f;        // beta * khat
+            dst[kd] = kn;
+            dst[kp + kd] = bk * d;
+            dst[2 * kp + kd] = qn * d;
+            dst[3 * kp + kd] = d;
+            qk = fmaf(qn, kn, qk);
         }
     }
+    qk = WaveSum64(qk);
+    if (lane == 0) p.prep_qk[static_cast<size_t>(bh) * p.chunk_cap + tl] = qk;
 }
 
 // ---------------------------------------------------------------------------
@@ -110,18 +132,48 @@ __device__ __forceinline__ void LoadKeys(const float *src, float (&x)[KT]) {
     }
 }
 
+// LDS layout of one staged token for KT keys per lane: each of the 4 vectors
+// occupies KPS floats.  gfx950 serves a ds_read_b128 16 lanes at a time from
+// 64 four-byte banks, so the 16 key groups of a wave are conflict-free when
+// their 16-byte chunks land on distinct (address/16) mod 16 slots.  KT = 4
+// (contiguous) and KT = 12 (stride 3 chunks) already do; KT = 8 and 16 would
+// alias 2- and 4-way, so key i is stored at i + 4*(i/64) (16 bytes of
+// padding per 256 bytes) for them.
+template <int KT>
+struct Swz {
+    static constexpr int KP = 16 * KT;
+    static constexpr bool PAD = KT == 8 || KT == 16;
+    static constexpr int KPS = PAD ? KP + 4 * ((KP - 1) / 64) : KP;
+    static constexpr int RS = 4 * KPS;
+    __device__ static constexpr int Pos(int i) { return PAD ? i + 4 * (i / 64) : i; }
+};
+
+// Tokens per staged block: 8, or 4 when two 8-token buffers would exceed the
+// 64 KiB of statically declared LDS.
+template <int KT>
+__host__ __device__ constexpr int TokensPerBlock() {
+    return 2 * 8 * Swz<KT>::RS * 4 <= 60 * 1024 ? 8 : 4;
+}
+
 template <int KT, int CL>
 __global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params p, int t0, int tc) {
-    constexpr int KP = 16 * KT;               // padded keys (== p.dk_pad)
-    constexpr int VEC = 4 * KP;               // floats per token: khat, qhat, decay, beta*khat
+    using S_ = Swz<KT>;
+    constexpr int KP = S_::KP;                // padded keys (== p.dk_pad)
+    constexpr int KPS = S_::KPS;
+    constexpr int RS = S_::RS;
+    constexpr int TB = TokensPerBlock<KT>();
+    constexpr int ROW = PrepRow(KP);          // floats per prepared token row
     constexpr int COLS = 16 * CL;             // value columns per workgroup
-    constexpr int VEC4 = kTB * VEC / 4;       // float4 per staged block
+    constexpr int ROW4 = ROW / 4;
+    constexpr int VEC4 = TB * ROW4;           // float4 per staged block
     constexpr int VPT = (VEC4 + kThreads - 1) / kThreads;
-    constexpr int WVPT = (kTB * COLS + kThreads - 1) / kThreads;
+    constexpr int WVPT = (TB * COLS + kThreads - 1) / kThreads;
 
-    __shared__ __attribute__((aligned(16))) float sVec[kTB * VEC];
-    __shared__ float sWV[kTB * COLS];
-    __shared__ float sOut[kTB * COLS];
+    // Double-buffered staging: block i is written while the other waves may
+    // still read block i-1, so one barrier per block suffices.
+    __shared__ __attribute__((aligned(16))) float sVec[2][TB * RS];
+    __shared__ float sWV[2][TB * COLS];
+    __shared__ float sQK[2][TB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
@@ -149,89 +201,134 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params
         }
     }
 
-    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * VEC;
-    float4 vreg[VPT];
+    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * ROW;
+    const float *prep_qk = p.prep_qk + static_cast<size_t>(bh) * p.chunk_cap;
+    // staged as plain floats: float4 struct copies into a private array are
+    // lowered to memcpy and keep the array out of registers
+    float vreg[VPT][4];
     float wreg[WVPT], vvreg[WVPT];
-    auto load_block = [&](int tb0) {
-        const int nt = min(kTB, tc - tb0);
-        const float4 *src = reinterpret_cast<const float4 *>(prep + static_cast<size_t>(tb0) * VEC);
+    float qkreg = 0.0f;
+    auto load_block = [&](int tb0) __attribute__((always_inline)) {
+        const int nt = min(TB, tc - tb0);
+        const float4 *src = reinterpret_cast<const float4 *>(prep + static_cast<size_t>(tb0) * ROW);
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
-            const int i = tid + k * kThreads;
-            if (i < VEC4 && i < nt * (VEC / 4)) vreg[k] = src[i];
-            else vreg[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int i = min(tid + k * kThreads, nt * ROW4 - 1);   // clamped: no branch around the load
+            const float4 x = src[i];
+            vreg[k][0] = x.x; vreg[k][1] = x.y; vreg[k][2] = x.z; vreg[k][3] = x.w;
         }
+        qkreg = prep_qk[tb0 + min(tid, nt - 1)];
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
             const int i = tid + k * kThreads;
-            const int tt = i / COLS, cc = i % COLS;
-            const int col = v0 + cc;
-            wreg[k] = 0.0f;
-            vvreg[k] = 0.0f;
-            if (i < kTB * COLS && tt < nt && col < dv) {
-                const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
-                wreg[k] = p.w[idx];
-                vvreg[k] = p.v[idx];
-            }
+            const int tt = min(i / COLS, nt - 1), col = min(v0 + i % COLS, dv - 1);
+            const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
+            const bool ok = i < TB * COLS && i / COLS < nt && v0 + i % COLS < dv;
+            const float wv = p.w[idx], vv = p.v[idx];
+            wreg[k] = ok ? wv : 0.0f;
+            vvreg[k] = ok ? vv : 0.0f;
         }
     };
-
-    load_block(0);
-    for (int tb0 = 0; tb0 < tc; tb0 += kTB) {
-        const int nt = min(kTB, tc - tb0);
+    // Tokens past the end of a short block are staged as identity tokens
+    // (khat = beta*khat*d = qhat*d = 0, d = 1, w*v = 0): they leave a finite
+    // state exactly unchanged, so every block runs the same unrolled body.
+    auto stage = [&](int buf, int nt) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
             const int i = tid + k * kThreads;
-            if (i < VEC4) reinterpret_cast<float4 *>(sVec)[i] = vreg[k];
+            if (i < VEC4) {
+                const int tt = i / ROW4, ch = i % ROW4;     // ch: float4 chunk within the row
+                const int vec = ch / (KP / 4), c4 = ch % (KP / 4);
+                const bool live = tt < nt;
+                const float pad = vec == 3 ? 1.0f : 0.0f;
+                *reinterpret_cast<float4 *>(&sVec[buf][tt * RS + vec * KPS + S_::Pos(4 * c4)]) =
+                    make_float4(live ? vreg[k][0] : pad, live ? vreg[k][1] : pad,
+                                live ? vreg[k][2] : pad, live ? vreg[k][3] : pad);
+            }
         }
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
             const int i = tid + k * kThreads;
-            if (i < kTB * COLS) sWV[i] = wreg[k] * vvreg[k];   // w * v (reference :120)
+            if (i < TB * COLS) sWV[buf][i] = wreg[k] * vvreg[k];   // w * v (reference :120)
         }
-        __syncthreads();
-        if (tb0 + kTB < tc) load_block(tb0 + kTB);
+        if (tid < TB) sQK[buf][tid] = tid < nt ? qkreg : 0.0f;
+    };
 
-        for (int tt = 0; tt < nt; ++tt) {
-            const float *vt = sVec + tt * VEC + kg * KT;
-            float kn[KT], qn[KT], dec[KT], bk[KT];
-            LoadKeys<KT>(vt, kn);
-            LoadKeys<KT>(vt + KP, qn);
-            LoadKeys<KT>(vt + 2 * KP, dec);
-            LoadKeys<KT>(vt + 3 * KP, bk);
+    // lane's keys [kg*KT, kg*KT + KT) start at this LDS offset within a vector
+    const int kpos = S_::Pos(kg * KT);
+
+    load_block(0);
+    int buf = 0;
+    for (int tb0 = 0; tb0 < tc; tb0 += TB, buf ^= 1) {
+        const int nt = min(TB, tc - tb0);
+        stage(buf, nt);
+        __syncthreads();
+        if (tb0 + TB < tc) load_block(tb0 + TB);
+
+        // Lane kg keeps the output of token kg of the block for its columns.
+        float oreg[CL];
+#pragma unroll
+        for (int c = 0; c < CL; ++c) oreg[c] = 0.0f;
+        // Token tt+1's vectors are read from LDS while token tt computes.
+        const float *vb_ = &sVec[buf][kpos];
+        float cur[4][KT], nxt[4][KT];
+        float cwv[CL], nwv[CL];
+        float cqk, nqk;
+        auto read_token = [&](int tt, float (&x)[4][KT], float (&wv)[CL], float &qk) __attribute__((always_inline)) {
+            const float *vt = vb_ + tt * RS;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) LoadKeys<KT>(vt + m * KPS, x[m]);
+#pragma unroll
+            for (int c = 0; c < CL; ++c) wv[c] = sWV[buf][tt * COLS + (w * 4 + cg) * CL + c];
+            qk = sQK[buf][tt];
+        };
+        read_token(0, cur, cwv, cqk);
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt) {
+            if (tt + 1 < TB) read_token(tt + 1, nxt, nwv, nqk);
+            const float (&kn)[KT] = cur[0];
+            const float (&bkd)[KT] = cur[1];
+            const float (&qd)[KT] = cur[2];
+            const float (&dec)[KT] = cur[3];
 #pragma unroll
             for (int c = 0; c < CL; ++c) {
-                const int cl = (w * 4 + cg) * CL + c;
-                float e = 0.0f;
+                // two accumulators per sum shorten the dependent chains
+                float e0 = 0.0f, e1 = 0.0f, r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
-                for (int j = 0; j < KT; ++j) {
-                    S[c][j] *= dec[j];
-                    e = fmaf(bk[j], S[c][j], e);
+                for (int j = 0; j < KT; j += 2) {
+                    e0 = fmaf(bkd[j], S[c][j], e0);
+                    r0 = fmaf(qd[j], S[c][j], r0);
+                    if (j + 1 < KT) {
+                        e1 = fmaf(bkd[j + 1], S[c][j + 1], e1);
+                        r1 = fmaf(qd[j + 1], S[c][j + 1], r1);
+                    }
                 }
-                e = RowSum16(e);
-                const float u = sWV[tt * COLS + cl] - e;
-                float o = 0.0f;
+                const float e = RowSum16(e0 + e1);
+                const float r = RowSum16(r0 + r1);
+                const float u = cwv[c] - e;
+                const float o = fmaf(cqk, u, r);
 #pragma unroll
-                for (int j = 0; j < KT; ++j) {
-                    S[c][j] = fmaf(kn[j], u, S[c][j]);
-                    o = fmaf(qn[j], S[c][j], o);
-                }
-                o = RowSum16(o);
-                if (kg == 0) sOut[tt * COLS + cl] = o;
+                for (int j = 0; j < KT; ++j) S[c][j] = fmaf(kn[j], u, S[c][j] * dec[j]);
+                oreg[c] = kg == tt ? o : oreg[c];
+            }
+            if (tt + 1 < TB) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int j = 0; j < KT; ++j) cur[m][j] = nxt[m][j];
+#pragma unroll
+                for (int c = 0; c < CL; ++c) cwv[c] = nwv[c];
+                cqk = nqk;
             }
         }
-        __syncthreads();
-        // Coalesced store of the block's outputs (COLS contiguous floats per token).
-        for (int i = tid; i < nt * COLS; i += kThreads) {
-            const int tt = i / COLS, cc = i % COLS;
-            const int col = v0 + cc;
-            if (col < dv) {
-                const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
-                p.out[idx] = sOut[i];
+        if (kg < nt) {
+            const size_t obase = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + kg) * p.nheads + h) * dv;
+#pragma unroll
+            for (int c = 0; c < CL; ++c) {
+                const int col = v0 + (w * 4 + cg) * CL + c;
+                if (col < dv) p.out[obase + col] = oreg[c];
             }
         }
-        // The next iteration rewrites sVec/sWV (last read before the barrier
-        // above) and sOut only after its own barrier, so none is needed here.
     }
 
     if (t0 + tc < p.seqlen) {
@@ -266,6 +363,7 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
     const int kt = kp / 16;                     // keys per lane (multiple of 4)
     const int col = vb * 16 + cl;
     const bool col_ok = col < dv;
+    const int row = PrepRow(kp);
 
     const float *sinit = nullptr;
     if (t0 > 0) sinit = p.state;
@@ -277,38 +375,38 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
     }
     // Each lane touches only its own (key, column) cells: no barrier needed.
 
-    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * 4 * static_cast<size_t>(kp);
+    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * static_cast<size_t>(row);
     for (int tt = 0; tt < tc; ++tt) {
-        const float *vt = prep + static_cast<size_t>(tt) * 4 * kp + kg * kt;
-        const size_t vidx = ((static_cast<size_t>(b) * p.seqlen + t0 + tt) * p.nheads + h) * dv + col;
+        const float *vt = prep + static_cast<size_t>(tt) * row + kg * kt;
+        const size_t vidx = ((static_cast<size_t>(b) * p.seqlen + t0 + tt) * p.nheads + h) * dv + min(col, dv - 1);
         const float wv = col_ok ? p.w[vidx] * p.v[vidx] : 0.0f;
-        float e = 0.0f;
+        const float qk = p.prep_qk[static_cast<size_t>(bh) * p.chunk_cap + tt];
+        float e = 0.0f, r = 0.0f;
         for (int j = 0; j < kt; j += 4) {
-            const float4 d4 = *reinterpret_cast<const float4 *>(vt + 2 * kp + j);
-            const float4 b4 = *reinterpret_cast<const float4 *>(vt + 3 * kp + j);
-            const float dd[4] = {d4.x, d4.y, d4.z, d4.w}, bb[4] = {b4.x, b4.y, b4.z, b4.w};
+            const float4 b4 = *reinterpret_cast<const float4 *>(vt + kp + j);
+            const float4 q4 = *reinterpret_cast<const float4 *>(vt + 2 * kp + j);
+            const float bb[4] = {b4.x, b4.y, b4.z, b4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
-                float &s = sS[((j + x) * 16 + cl) * 16 + kg];
-                s *= dd[x];
+                const float s = sS[((j + x) * 16 + cl) * 16 + kg];
                 e = fmaf(bb[x], s, e);
+                r = fmaf(qq[x], s, r);
             }
         }
         e = RowSum16(e);
+        r = RowSum16(r);
         const float u = wv - e;
-        float o = 0.0f;
+        const float o = fmaf(qk, u, r);
         for (int j = 0; j < kt; j += 4) {
             const float4 k4 = *reinterpret_cast<const float4 *>(vt + j);
-            const float4 q4 = *reinterpret_cast<const float4 *>(vt + kp + j);
-            const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w};
+            const float4 d4 = *reinterpret_cast<const float4 *>(vt + 3 * kp + j);
+            const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, dd[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 float &s = sS[((j + x) * 16 + cl) * 16 + kg];
-                s = fmaf(kk[x], u, s);
-                o = fmaf(qq[x], s, o);
+                s = fmaf(kk[x], u, s * dd[x]);
             }
         }
-        o = RowSum16(o);
         if (kg == 0 && col_ok) p.out[vidx] = o;
     }
     if (t0 + tc < p.seqlen) {
@@ -322,6 +420,8 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+size_t Align256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
 int KeyTile(int dk) {
     // keys per lane for the 16-lane rows of the register kernel
     const int kt = (dk + 15) / 16;
@@ -379,10 +479,11 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
 
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
     const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
-    const size_t prepared = static_cast<size_t>(batch) * nheads * cap * 4 * PadKeys(dk);
+    const size_t rows = static_cast<size_t>(batch) * nheads * cap;
     const size_t state = seqlen > kChunkTokens ? static_cast<size_t>(batch) * nheads * dk * dv : 0;
-    // 256-byte alignment of the second region
-    return (prepared * sizeof(float) + 255) / 256 * 256 + state * sizeof(float);
+    // regions: prepared vectors | qhat.khat per row | carried state, each 256-byte aligned
+    return Align256(rows * PrepRow(PadKeys(dk)) * sizeof(float)) + Align256(rows * sizeof(float)) +
+           state * sizeof(float);
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
@@ -391,11 +492,13 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");
     p.dk_pad = PadKeys(p.dk);
     p.chunk_cap = std::min(p.seqlen, kChunkTokens);
-    const size_t prepared = static_cast<size_t>(p.batch) * p.nheads * p.chunk_cap * 4 * p.dk_pad;
-    p.prepared = static_cast<float *>(scratch);
-    p.state = p.seqlen > kChunkTokens
-                  ? reinterpret_cast<float *>(static_cast<char *>(scratch) + (prepared * sizeof(float) + 255) / 256 * 256)
-                  : nullptr;
+    const size_t rows = static_cast<size_t>(p.batch) * p.nheads * p.chunk_cap;
+    char *base = static_cast<char *>(scratch);
+    p.prepared = reinterpret_cast<float *>(base);
+    base += Align256(rows * PrepRow(p.dk_pad) * sizeof(float));
+    p.prep_qk = reinterpret_cast<float *>(base);
+    base += Align256(rows * sizeof(float));
+    p.state = p.seqlen > kChunkTokens ? reinterpret_cast<float *>(base) : nullptr;
     const long long bh = static_cast<long long>(p.batch) * p.nheads;
     if (bh * ((p.dv + 15) / 16) > 2147483647LL || bh * kChunkTokens / 4 > 2147483647LL)
         throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");

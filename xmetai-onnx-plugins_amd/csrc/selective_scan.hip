@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
 
     // ---- tile loads (global -> registers) ----------------------------------
     F4 ureg[IPT], dreg[IPT], bcreg[BCPT];
-    auto load_full = [&](int t0) {        // FAST, whole tile in range: no guards
+    auto load_full = [&](int t0) __attribute__((always_inline)) {        // FAST, whole tile in range: no guards
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
             const int it = min(tid + k * kThreads, ITEMS - 1);   // spare lanes re-read a valid item
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
             }
         }
     };
-    auto load_guarded = [&](int t0) {     // any tile: clamped addresses, zero past the ends
+    auto load_guarded = [&](int t0) __attribute__((always_inline)) {     // any tile: clamped addresses, zero past the ends
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
             const int it = tid + k * kThreads;
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
 
     // ---- phase 1: bias, softplus, delta*u into LDS; keep D*u ----------------
     F4 skip[IPT];
-    auto phase1 = [&](int t0, bool full) {
+    auto phase1 = [&](int t0, bool full) __attribute__((always_inline)) {
         // delta' = softplus?(delta + bias): one uniform branch per tile
         if (p.delta_softplus) {
 #pragma unroll
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
     };
 
     // ---- phase 2: the recurrence over one tile ------------------------------
-    auto phase2 = [&]() {
+    auto phase2 = [&]() __attribute__((always_inline)) {
         const float *rDl = sDl + lc * kRow;
         const float *rDu = sDu + lc * kRow;
         float *rY = sY + lc * kRow;
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
     };
 
     // ---- phase 3: add D*u, store y -------------------------------------------
-    auto phase3 = [&](int t0, bool full) {
+    auto phase3 = [&](int t0, bool full) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
             const int it = tid + k * kThreads;

@@ -34,7 +34,8 @@ struct GatedDeltaNet2Params {
     const float *initial_state;     // [batch, nheads, dk, dv] or nullptr
     float *out;                     // [batch, seqlen, nheads, dv]
     float *state;                   // carry between token chunks, [batch, nheads, dk, dv]
-    float *prepared;                // [batch*nheads, chunk_cap, 4, dk_pad]: khat, qhat, exp(g), beta*khat
+    float *prepared;                // [batch*nheads, chunk_cap, 4, dk_pad]: khat, beta*khat*d, qhat*d, d (d = exp(g))
+    float *prep_qk;                 // [batch*nheads, chunk_cap]: qhat . khat
     int batch, seqlen, nheads, dk, dv;
     int dk_pad;                     // dk rounded up to the recurrence's key tiling
     int chunk_cap;                  // tokens per preparation chunk (<= 1024)
