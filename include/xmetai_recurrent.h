@@ -152,6 +152,18 @@ int xm_gated_deltanet2_forward(const xm_tensor_t *inputs, size_t n_inputs,
                                const xm_gated_deltanet2_attrs_t *attrs, float *out, void *stream,
                                const xm_allocator_t *alloc, char *errbuf, size_t errlen);
 
+/* ---- SoftmaxCPU (CPU execution provider) ------------------------------------
+ * Softmax of a HOST fp32 tensor of any rank along `axis` (ONNX attribute
+ * "axis", int, default -1; negative values count from the last dimension).
+ * Per line: subtract the maximum, exp, sum in axis order, multiply by
+ * (sum > 0 ? 1/sum : 0).  An empty tensor returns XM_OK without checking the
+ * axis; otherwise an axis outside [-rank, rank) fails with "SoftmaxCPU axis
+ * out of range".  `out` has the input's shape and may not alias `in`.
+ * Reference: csrc/softmax_cpu/softmax_cpu_ort.cpp:20-114 (kernel), :79-88
+ * (axis attribute). */
+int xm_softmax_cpu(const float *in, const int64_t *shape, int32_t rank, int64_t axis, float *out,
+                   char *errbuf, size_t errlen);
+
 /* ---- Library ---------------------------------------------------------------
  * Version string and a description of the build (target, kernel variants). */
 const char *xm_version(void);

@@ -126,3 +126,20 @@ def _setup_signatures():
         fn.restype = None
         fn = getattr(L, "xmo_mamba3_siso" + sfx)
         fn.restype = None
+
+
+def softmax_cpu(x, axis=-1, dtype=np.float32):
+    """See xmo_softmax_cpu in xm_oracle.c (fp32: the reference's operations and order)."""
+    a = np.asarray(x, np.float32, order="C")
+    ax = axis + a.ndim if axis < 0 else axis
+    if not 0 <= ax < a.ndim:
+        raise ValueError("axis out of range")
+    outer = int(np.prod(a.shape[:ax], dtype=np.int64))
+    inner = int(np.prod(a.shape[ax + 1:], dtype=np.int64))
+    o, op = _out(a.shape, dtype)
+    if a.size == 0:
+        return o
+    fn = getattr(lib(), "xmo_softmax_cpu" + _sfx(dtype))
+    fn.restype = None
+    fn(a.ctypes.data_as(_f32p), ctypes.c_size_t(outer), ctypes.c_size_t(a.shape[ax]), ctypes.c_size_t(inner), op)
+    return o

@@ -296,3 +296,30 @@ void XMO_NAME(xmo_mamba3_siso)(const float *Q, const float *K, const float *V, c
         free(S); free(th); free(qv); free(kv);
     }
 }
+
+/* ---------------------------------------------------------------------------
+ * SoftmaxCPU, softmax_cpu_ort.cpp:38-77: one line at a time along the axis,
+ * max, then e = exp(x - max) summed in axis order, then e * inv_sum with
+ * inv_sum = sum > 0 ? 1 / sum : 0 (:75).  In the fp32 build every operation
+ * is the reference's fp32 operation in the reference's order.
+ * ------------------------------------------------------------------------- */
+void XMO_NAME(xmo_softmax_cpu)(const float *in, size_t outer, size_t axis_dim, size_t inner, real *out) {
+    for (size_t o = 0; o < outer; ++o) {
+        for (size_t i = 0; i < inner; ++i) {
+            const size_t base = o * axis_dim * inner + i;
+            real mx = -(real)INFINITY;
+            for (size_t a = 0; a < axis_dim; ++a) {
+                const real x = (real)in[base + a * inner];
+                mx = x > mx ? x : mx;   /* std::max(max, x): keeps max unless x is larger */
+            }
+            real sum = 0;
+            for (size_t a = 0; a < axis_dim; ++a) {
+                const real e = r_exp((real)in[base + a * inner] - mx);
+                out[base + a * inner] = e;
+                sum += e;
+            }
+            const real inv = sum > 0 ? (real)1 / sum : (real)0;
+            for (size_t a = 0; a < axis_dim; ++a) out[base + a * inner] *= inv;
+        }
+    }
+}

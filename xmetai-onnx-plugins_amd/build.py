@@ -47,6 +47,7 @@ SOURCES = [
     "selective_scan_host.cpp",
     "gated_deltanet2_host.cpp",
     "mamba3_siso_host.cpp",
+    "softmax_cpu.cpp",
 ]
 
 ORT_SOURCES = [

@@ -179,8 +179,10 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params
     const int lane = tid & 63, w = tid >> 6;
     const int kg = lane & 15, cg = lane >> 4;
     const int nvb = (p.dv + COLS - 1) / COLS;
-    const int vb = blockIdx.x % nvb;
-    const int bh = blockIdx.x / nvb;
+    // the nvb workgroups of one (b,h) read the same token vectors: keep them on one XCD
+    const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int vb = wg % nvb;
+    const int bh = wg / nvb;
     const int b = bh / p.nheads, h = bh % p.nheads;
     const int dk = p.dk, dv = p.dv;
     const int v0 = vb * COLS;
@@ -356,8 +358,9 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
     const int kg = lane & 15, cg = lane >> 4;
     const int cl = w * 4 + cg;                  // column within the workgroup (16 per workgroup)
     const int nvb = (p.dv + 15) / 16;
-    const int vb = blockIdx.x % nvb;
-    const int bh = blockIdx.x / nvb;
+    const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int vb = wg % nvb;
+    const int bh = wg / nvb;
     const int b = bh / p.nheads, h = bh % p.nheads;
     const int dk = p.dk, dv = p.dv, kp = p.dk_pad;
     const int kt = kp / 16;                     // keys per lane (multiple of 4)

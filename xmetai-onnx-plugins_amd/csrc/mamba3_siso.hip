@@ -56,8 +56,10 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     const int lane = tid & 63, w = tid >> 6;
     const int T = p.seqlen, N = p.n, P = p.p, A = p.a;
     const int nrb = (P + RB - 1) / RB;
-    const int rb = blockIdx.x % nrb;
-    const int bh = blockIdx.x / nrb;
+    // the nrb workgroups of one (b,h) read the same token vectors: keep them on one XCD
+    const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int rb = wg % nrb;
+    const int bh = wg / nrb;
     const int b = bh / p.nheads, h = bh % p.nheads;
     const int gq = h / (p.nheads / p.nheads_qk);
     const int r0 = rb * RB;

@@ -58,4 +58,17 @@ __device__ __forceinline__ double WaveSum64d(double x) {
     return x;
 }
 
+// MI355X deals the workgroups of a launch round-robin to its 8 XCDs
+// (workgroup x runs on XCD x % 8), and each XCD has its own L2.  This maps
+// the hardware index to a logical one under which XCD j owns one contiguous
+// range of logical indices, so workgroups that read the same data (adjacent
+// logical indices) share an L2 instead of fetching it once per XCD.  It is a
+// bijection on [0, n) for any n.
+constexpr int kNumXcds = 8;
+__device__ __forceinline__ int XcdLocalBlock(int x, int n) {
+    const int per = n / kNumXcds, rem = n % kNumXcds;
+    const int xcd = x % kNumXcds, slot = x / kNumXcds;
+    return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
 }  // namespace xm

@@ -28,13 +28,14 @@ from ._capi import (XM_ERR_ALLOC, XM_ERR_DEVICE, XM_ERR_INVALID_ARGUMENT, XM_ERR
                     EXPORTED_SYMBOLS, LIB_PATH)
 
 __all__ = [
-    "XmError", "lib", "version", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn",
+    "XmError", "lib", "version", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn", "softmax_cpu",
     "validate", "TorchAllocator", "EXPORTED_SYMBOLS", "LIB_PATH",
     "XM_OK", "XM_ERR_INVALID_ARGUMENT", "XM_ERR_UNSUPPORTED", "XM_ERR_DEVICE", "XM_ERR_ALLOC",
 ]
 
 DOMAIN = "xmetai_plugins"
-OP_NAMES = ("SelectiveScanFn", "Mamba3SisoFn", "GatedDeltaNet2Fn")
+# registration order of the reference (register_op.cpp:24-39)
+OP_NAMES = ("SelectiveScanFn", "Mamba3SisoFn", "GatedDeltaNet2Fn", "SoftmaxCPU")
 
 _lib = None
 
@@ -246,3 +247,18 @@ def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, us
                 scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
                 output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
                 has_cu_seqlens=int(bool(has_cu_seqlens)), state_v_first=int(bool(state_v_first)))
+
+
+def softmax_cpu(x, axis: int = -1):
+    """SoftmaxCPU (CPU execution provider): softmax of a host fp32 array along
+    ``axis`` (reference: softmax_cpu_ort.cpp:20-114).  Returns a new float32
+    NumPy array of the input's shape."""
+    import numpy as np
+    a = np.asarray(x, dtype=np.float32, order="C")   # keeps rank 0 (ascontiguousarray would not)
+    out = np.empty_like(a)
+    shape = (ctypes.c_int64 * max(1, a.ndim))(*a.shape)
+    err = ctypes.create_string_buffer(512)
+    st = lib().xm_softmax_cpu(a.ctypes.data if a.size else None, shape, a.ndim, int(axis),
+                              out.ctypes.data if out.size else None, err, len(err))
+    _check(st, err)
+    return out

@@ -79,7 +79,7 @@ OPS = {
 # Every symbol include/xmetai_recurrent.h declares.
 EXPORTED_SYMBOLS = [
     f"xm_{op}_{fn}" for op in OPS for fn in ("attrs_default", "check_attrs", "validate", "forward")
-] + ["xm_version"]
+] + ["xm_softmax_cpu", "xm_version"]
 
 
 def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
@@ -100,6 +100,9 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(XmAllocator),
                       ctypes.c_char_p, ctypes.c_size_t]
         f.restype = ctypes.c_int
+    lib.xm_softmax_cpu.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int64,
+                                   ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    lib.xm_softmax_cpu.restype = ctypes.c_int
     lib.xm_version.argtypes = []
     lib.xm_version.restype = ctypes.c_char_p
     return lib
