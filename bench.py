@@ -169,64 +169,68 @@ def cpu_baseline(op, inputs, budget_s):
     if name == "selective_scan":
         full_units = s.batch * s.dim
 
-        def run(nch):
+        def run(n):
+            # n (batch, channel) pairs: channels of batch 0, or whole batches
+            nb = -(-n // s.dim)
+            nch = n if nb == 1 else s.dim
             sub = {k: inputs[k] for k in op["keys"]}
             for k in ("u", "delta"):
-                sub[k] = np.ascontiguousarray(inputs[k][:1, :nch])
+                sub[k] = np.ascontiguousarray(inputs[k][:nb, :nch])
             for k in ("A", "D", "delta_bias"):
                 sub[k] = np.ascontiguousarray(inputs[k][:nch])
-            sub["B"] = np.ascontiguousarray(inputs["B"][:1])
-            sub["C"] = np.ascontiguousarray(inputs["C"][:1])
+            sub["B"] = np.ascontiguousarray(inputs["B"][:nb])
+            sub["C"] = np.ascontiguousarray(inputs["C"][:nb])
             sub["z"] = None
             t = time.perf_counter()
             numpy_ref.selective_scan(**sub, delta_softplus=True, dtype=np.float32)
-            return time.perf_counter() - t
+            return time.perf_counter() - t, nb * nch
 
-        unit = "channels"
-        sample_fmt = "batch 1 x {n} of {d} channels x {L} tokens, dstate {N} (NumPy fp32 oracle), scaled by channel count"
-        fmt_args = dict(d=s.dim, L=s.seqlen, N=s.dstate)
-        max_units = s.dim
+        unit = "(batch, channel) pairs"
+        sample_fmt = ("{n} of {full} (batch, channel) pairs x {L} tokens, dstate {N} (NumPy fp32 oracle), "
+                      "scaled by pair count")
+        fmt_args = dict(L=s.seqlen, N=s.dstate)
     else:
         full_units = s.batch * s.nheads
 
-        def run(nh):
+        def run(n):
+            # n (batch, head) pairs: heads of batch 0, or whole batches
+            nb = -(-n // s.nheads)
+            nh = n if nb == 1 else s.nheads
             sub = {}
             for k in op["keys"]:
                 v = inputs[k]
                 if v is None:
                     sub[k] = None
                 elif k in ("ADT", "DT", "Trap", "initial_state"):
-                    sub[k] = np.ascontiguousarray(v[:1, :nh])
+                    sub[k] = np.ascontiguousarray(v[:nb, :nh])
                 elif k in ("Q_bias", "K_bias", "D"):
                     sub[k] = np.ascontiguousarray(v[:nh])
                 else:
-                    sub[k] = np.ascontiguousarray(v[:1, :, :nh])
+                    sub[k] = np.ascontiguousarray(v[:nb, :, :nh])
             t = time.perf_counter()
             if name == "gated_deltanet2":
                 numpy_ref.gated_deltanet2(*(sub[k] for k in op["keys"]), scale=s.scale, dtype=np.float32)
             else:
                 numpy_ref.mamba3_siso(*(sub[k] for k in op["keys"]), dtype=np.float32)
-            return time.perf_counter() - t
+            return time.perf_counter() - t, nb * nh
 
-        unit = "heads"
-        sample_fmt = "batch 1 x {n} of {h} heads x {T} tokens (NumPy fp32 oracle), scaled by (batch, head) count"
-        fmt_args = dict(h=s.nheads, T=s.seqlen)
-        max_units = s.nheads
+        unit = "(batch, head) pairs"
+        sample_fmt = "{n} of {full} (batch, head) pairs x {T} tokens (NumPy fp32 oracle), scaled by pair count"
+        fmt_args = dict(T=s.seqlen)
+    max_units = full_units
 
     # calibrate on growing slices until one takes >= 0.5 s, then size the
     # measured slice to the budget
     n = 1
-    t = run(n)
+    t, n = run(n)
     while t < 0.5 and n < max_units:
-        n = min(max_units, n * 4)
-        t = run(n)
+        t, n = run(min(max_units, n * 4))
     if t < budget_s * 0.8 and n < max_units:
-        n = min(max_units, max(n + 1, int(n * budget_s / max(t, 1e-3))))
-        t = run(n)
+        t, n = run(min(max_units, max(n + 1, int(n * budget_s / max(t, 1e-3)))))
     t_full = t * full_units / n
     tokens = op["tokens"]
     return dict(value=tokens / t_full, unit="tokens/s", cores=1, kind="port",
-                sample=sample_fmt.format(n=n, **fmt_args), sample_seconds=round(t, 3),
+                sample=sample_fmt.format(n=n, full=full_units, **fmt_args), sample_seconds=round(t, 3),
                 sampled_units=n, unit_axis=unit, **cpu_env())
 
 
@@ -246,7 +250,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ops", default="selective_scan,gated_deltanet2,mamba3_siso")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget for the headline op")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline budget per op (seconds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", default="bench",
                     help="bench | copy | profile-selective_scan | profile-gated_deltanet2 | profile-mamba3_siso")
@@ -308,7 +312,7 @@ def main():
                  achieved_GBps=round(gbps, 1), frac_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
         log(f"{name}: {med_ms:.3f} ms/call, {r['tokens_per_s']:.4g} tokens/s, {gbps:.0f} GB/s")
         if not args.no_cpu_baseline:
-            budget = args.cpu_seconds if name == "selective_scan" else args.cpu_seconds / 2
+            budget = args.cpu_seconds
             log(f"{name}: CPU baseline (~{budget:.0f} s)")
             r["cpu_baseline"] = cpu_baseline(op, host, budget)
             log(f"{name}: CPU {r['cpu_baseline']['value']:.4g} tokens/s ({r['cpu_baseline']['sample']})")

@@ -265,3 +265,61 @@ def test_m3_head_divisibility_and_odd_dim():
     shapes = m3_shapes(N=15, A=4)
     with pytest.raises(XmError, match="positive even headdim_qk"):
         validate("mamba3_siso", shapes, has_d=1, has_z=0)
+
+
+# ---------------------------------------------------------------------------
+# ONNX Runtime layer (compiled only where ORT headers exist; its contract with
+# the reference is checked on the sources here)
+# ---------------------------------------------------------------------------
+
+ORT_DIR = os.path.join(ROOT, "xmetai-onnx-plugins_amd", "csrc", "ort")
+
+
+def _src(name):
+    with open(os.path.join(ORT_DIR, name)) as f:
+        return f.read()
+
+
+def test_ort_header_declares_register_custom_ops():
+    with open(os.path.join(ROOT, "include", "xmetai_onnx_plugins_ort.h")) as f:
+        h = f.read()
+    assert "OrtStatus *ORT_API_CALL RegisterCustomOps(OrtSessionOptions *options, const OrtApiBase *api_base);" in h
+
+
+def test_ort_registration_domain_and_order():
+    # reference register_op.cpp:20-40: domain xmetai_plugins, ops in this order
+    reg = _src("register_op.cpp")
+    assert 'extern "C" OrtStatus *ORT_API_CALL RegisterCustomOps' in reg
+    assert 'kDomain = "xmetai_plugins"' in _src("ort_glue.h")
+    order = ["XmAddSelectiveScanFnOp", "XmAddMamba3SisoFnOp", "XmAddGatedDeltaNet2FnOp", "XmAddSoftmaxCpuOp"]
+    line = [l for l in reg.splitlines() if "const AddFn adds[]" in l][0]
+    assert [line.index(n) for n in order] == sorted(line.index(n) for n in order)
+
+
+def test_ort_descriptors_match_reference_contract():
+    ops = _src("ops_ort.cpp")
+    for name, n_in in (("SelectiveScanFn", 8), ("Mamba3SisoFn", 11), ("GatedDeltaNet2Fn", 7)):
+        block = ops[ops.index(f'return "{name}";') - 400:ops.index(f'return "{name}";') + 600]
+        assert f"GetInputTypeCount() const {{ return {n_in}; }}" in block
+        assert "GetOutputTypeCount() const { return 1; }" in block
+        assert "GetExecutionProviderType() const { return XM_ORT_GPU_EP; }" in block
+    for attr in ("delta_softplus", "return_last_state", "chunk_size", "has_d", "has_z", "return_final_states",
+                 "has_input_states", "has_cu_seqlens", "scale", "use_qk_l2norm_in_kernel", "output_final_state",
+                 "use_gate_in_kernel", "state_v_first"):
+        assert f'"{attr}"' in ops
+    sm = _src("softmax_cpu_ort.cpp")
+    assert 'return "SoftmaxCPU";' in sm and '"CPUExecutionProvider"' in sm and '"axis", -1' in sm
+    assert '#define XM_ORT_GPU_EP "ROCMExecutionProvider"' in _src("ort_glue.h")
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(os.environ.get("ORT_INCLUDE_DIR", "/nonexistent"),
+                                                    "onnxruntime_c_api.h")),
+                    reason="ONNX Runtime headers are not installed (set ORT_INCLUDE_DIR)")
+def test_ort_library_builds_and_exports_register_custom_ops():
+    import ctypes
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("xm_build", os.path.join(ROOT, "xmetai-onnx-plugins_amd", "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    mod.build(ort_include=os.environ["ORT_INCLUDE_DIR"])
+    assert hasattr(ctypes.CDLL(mod.ORT_LIB), "RegisterCustomOps")

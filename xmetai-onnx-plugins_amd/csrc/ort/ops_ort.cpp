@@ -1,0 +1,129 @@
+// ONNX Runtime descriptors and kernels of the three device operators.
+//
+// Names, input counts, element types and attribute names/defaults are the
+// reference's (selective_scan_fn_ort.cpp:48-56, :235-246;
+// mamba3_siso_fn_ort.cpp:41-59, :235-246; gated_deltanet2_fn_ort.cpp:44-64,
+// :226-237); the execution provider is ROCm.  Attribute checks run in the
+// kernel constructor (session creation), shape checks in Compute (Run), both
+// through the C ABI, which carries the reference's messages.
+#include "ort_glue.h"
+
+namespace {
+
+using xm_ort::Check;
+using xm_ort::ComputeDeviceOp;
+using xm_ort::FloatAttr;
+using xm_ort::IntAttr;
+
+// ---- SelectiveScanFn -------------------------------------------------------
+class SelectiveScanKernel {
+public:
+    SelectiveScanKernel(const OrtApi &api, const OrtKernelInfo *info) : api_(api) {
+        xm_selective_scan_attrs_default(&attrs_);
+        attrs_.delta_softplus = IntAttr(api, info, "delta_softplus", attrs_.delta_softplus);
+        attrs_.return_last_state = IntAttr(api, info, "return_last_state", attrs_.return_last_state);
+        char err[512];
+        Check(xm_selective_scan_check_attrs(&attrs_, err, sizeof(err)), err);
+    }
+    void Compute(OrtKernelContext *ctx) {
+        ComputeDeviceOp(api_, ctx, 8, attrs_, xm_selective_scan_validate, xm_selective_scan_forward);
+    }
+
+private:
+    const OrtApi &api_;
+    xm_selective_scan_attrs_t attrs_{};
+};
+
+struct SelectiveScanOp : Ort::CustomOpBase<SelectiveScanOp, SelectiveScanKernel> {
+    void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new SelectiveScanKernel(api, info); }
+    const char *GetName() const { return "SelectiveScanFn"; }
+    const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
+    size_t GetInputTypeCount() const { return 8; }
+    ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    size_t GetOutputTypeCount() const { return 1; }
+    ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+};
+
+// ---- Mamba3SisoFn ----------------------------------------------------------
+class Mamba3SisoKernel {
+public:
+    Mamba3SisoKernel(const OrtApi &api, const OrtKernelInfo *info) : api_(api) {
+        xm_mamba3_siso_attrs_default(&attrs_);
+        attrs_.chunk_size = IntAttr(api, info, "chunk_size", attrs_.chunk_size);
+        attrs_.has_d = IntAttr(api, info, "has_d", attrs_.has_d);
+        attrs_.has_z = IntAttr(api, info, "has_z", attrs_.has_z);
+        attrs_.return_final_states = IntAttr(api, info, "return_final_states", attrs_.return_final_states);
+        attrs_.has_input_states = IntAttr(api, info, "has_input_states", attrs_.has_input_states);
+        attrs_.has_cu_seqlens = IntAttr(api, info, "has_cu_seqlens", attrs_.has_cu_seqlens);
+        char err[512];
+        Check(xm_mamba3_siso_check_attrs(&attrs_, err, sizeof(err)), err);
+    }
+    void Compute(OrtKernelContext *ctx) {
+        ComputeDeviceOp(api_, ctx, 11, attrs_, xm_mamba3_siso_validate, xm_mamba3_siso_forward);
+    }
+
+private:
+    const OrtApi &api_;
+    xm_mamba3_siso_attrs_t attrs_{};
+};
+
+struct Mamba3SisoOp : Ort::CustomOpBase<Mamba3SisoOp, Mamba3SisoKernel> {
+    void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new Mamba3SisoKernel(api, info); }
+    const char *GetName() const { return "Mamba3SisoFn"; }
+    const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
+    size_t GetInputTypeCount() const { return 11; }
+    ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    size_t GetOutputTypeCount() const { return 1; }
+    ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+};
+
+// ---- GatedDeltaNet2Fn ------------------------------------------------------
+class GatedDeltaNet2Kernel {
+public:
+    GatedDeltaNet2Kernel(const OrtApi &api, const OrtKernelInfo *info) : api_(api) {
+        xm_gated_deltanet2_attrs_default(&attrs_);
+        attrs_.scale = FloatAttr(api, info, "scale", attrs_.scale);
+        attrs_.use_qk_l2norm_in_kernel = IntAttr(api, info, "use_qk_l2norm_in_kernel", attrs_.use_qk_l2norm_in_kernel);
+        attrs_.output_final_state = IntAttr(api, info, "output_final_state", attrs_.output_final_state);
+        attrs_.use_gate_in_kernel = IntAttr(api, info, "use_gate_in_kernel", attrs_.use_gate_in_kernel);
+        attrs_.has_cu_seqlens = IntAttr(api, info, "has_cu_seqlens", attrs_.has_cu_seqlens);
+        attrs_.state_v_first = IntAttr(api, info, "state_v_first", attrs_.state_v_first);
+        char err[512];
+        Check(xm_gated_deltanet2_check_attrs(&attrs_, err, sizeof(err)), err);
+    }
+    void Compute(OrtKernelContext *ctx) {
+        ComputeDeviceOp(api_, ctx, 7, attrs_, xm_gated_deltanet2_validate, xm_gated_deltanet2_forward);
+    }
+
+private:
+    const OrtApi &api_;
+    xm_gated_deltanet2_attrs_t attrs_{};
+};
+
+struct GatedDeltaNet2Op : Ort::CustomOpBase<GatedDeltaNet2Op, GatedDeltaNet2Kernel> {
+    void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new GatedDeltaNet2Kernel(api, info); }
+    const char *GetName() const { return "GatedDeltaNet2Fn"; }
+    const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
+    size_t GetInputTypeCount() const { return 7; }
+    ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    size_t GetOutputTypeCount() const { return 1; }
+    ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+};
+
+// Descriptors live for the whole process: the domain that references them is
+// never released.
+SelectiveScanOp g_selective_scan_op;
+Mamba3SisoOp g_mamba3_siso_op;
+GatedDeltaNet2Op g_gated_deltanet2_op;
+
+}  // namespace
+
+OrtStatus *XmAddSelectiveScanFnOp(const OrtApi &api, OrtCustomOpDomain *domain) {
+    return api.CustomOpDomain_Add(domain, &g_selective_scan_op);
+}
+OrtStatus *XmAddMamba3SisoFnOp(const OrtApi &api, OrtCustomOpDomain *domain) {
+    return api.CustomOpDomain_Add(domain, &g_mamba3_siso_op);
+}
+OrtStatus *XmAddGatedDeltaNet2FnOp(const OrtApi &api, OrtCustomOpDomain *domain) {
+    return api.CustomOpDomain_Add(domain, &g_gated_deltanet2_op);
+}

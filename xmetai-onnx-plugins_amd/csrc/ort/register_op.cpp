@@ -1,0 +1,29 @@
+// RegisterCustomOps: the symbol ONNX Runtime looks up when a session loads
+// this library.  Reference: csrc/register_op.cpp:11-41 — domain
+// "xmetai_plugins", operators added in the order SelectiveScanFn,
+// Mamba3SisoFn, GatedDeltaNet2Fn, SoftmaxCPU, first failing status returned.
+#include "ort_glue.h"
+#include "xmetai_onnx_plugins_ort.h"
+
+OrtStatus *XmAddSelectiveScanFnOp(const OrtApi &api, OrtCustomOpDomain *domain);
+OrtStatus *XmAddMamba3SisoFnOp(const OrtApi &api, OrtCustomOpDomain *domain);
+OrtStatus *XmAddGatedDeltaNet2FnOp(const OrtApi &api, OrtCustomOpDomain *domain);
+OrtStatus *XmAddSoftmaxCpuOp(const OrtApi &api, OrtCustomOpDomain *domain);
+
+extern "C" OrtStatus *ORT_API_CALL RegisterCustomOps(OrtSessionOptions *options, const OrtApiBase *api_base) {
+    if (api_base == nullptr) return nullptr;
+    const OrtApi *api = api_base->GetApi(ORT_API_VERSION);
+    if (api == nullptr) return nullptr;   // the runtime is older than the headers this library was built with
+    Ort::InitApi(api);                    // ORT_API_MANUAL_INIT: the C++ wrapper uses the runtime's table
+    if (options == nullptr) return api->CreateStatus(ORT_INVALID_ARGUMENT, "RegisterCustomOps received null session options");
+    OrtCustomOpDomain *domain = nullptr;
+    OrtStatus *st = api->CreateCustomOpDomain(xm_ort::kDomain, &domain);
+    if (st != nullptr) return st;
+    using AddFn = OrtStatus *(*)(const OrtApi &, OrtCustomOpDomain *);
+    const AddFn adds[] = {XmAddSelectiveScanFnOp, XmAddMamba3SisoFnOp, XmAddGatedDeltaNet2FnOp, XmAddSoftmaxCpuOp};
+    for (AddFn add : adds) {
+        st = add(*api, domain);
+        if (st != nullptr) return st;
+    }
+    return api->AddCustomOpDomain(options, domain);
+}
