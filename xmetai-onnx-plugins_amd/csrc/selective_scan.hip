@@ -57,6 +57,29 @@ __device__ __forceinline__ float LaneGroupSum(float x) {
     return x;
 }
 
+// Sums of four values (tokens 0..3) over the 8 lanes {c, c+8, ..., c+56} of
+// one channel c = lane % 8, with the gfx950 lane-swap instructions:
+// permlane32_swap(a, b) yields [a.lo32, b.lo32] and [a.hi32, b.hi32], and
+// permlane16_swap(a, b) yields [a.r0, b.r0, a.r2, b.r2] and [a.r1, b.r1, a.r3,
+// b.r3] (r = 16-lane row), so adding the two halves of each swap halves the
+// number of lanes and of values at once.  Seven instructions instead of the
+// twelve of four separate 3-step reductions.  On return every lane of row r
+// holds the channel sum of token {0, 2, 1, 3}[r] (see SwapReducedToken).
+__device__ __forceinline__ float SwapReduce8x4(const float (&y)[4]) {
+    const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[0]), __float_as_uint(y[1]), false, false);
+    const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[2]), __float_as_uint(y[3]), false, false);
+    const float y01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);   // lanes 0-31: y0, 32-63: y1
+    const float y23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);   // lanes 0-31: y2, 32-63: y3
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(y01), __float_as_uint(y23), false, false);
+    const float z = __uint_as_float(q[0]) + __uint_as_float(q[1]);         // rows: y0, y2, y1, y3
+    return z + DppF<0x128>(z);                                             // lanes c and c+8 of a row
+}
+
+__device__ __forceinline__ int SwapReducedToken(int lane) {
+    const int r = lane >> 4;
+    return ((r & 1) << 1) | (r >> 1);
+}
+
 struct F4 {
     float v[4];
 };
@@ -150,8 +173,13 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
         CVAR ? p.C + (static_cast<size_t>(b) * p.groups_c + (BVAR ? g : 0)) * static_cast<size_t>(N) * L : nullptr;
 
     // ---- per-lane recurrence constants ------------------------------------
-    const int lc = tid / LPC;   // channel of this lane within the workgroup
-    const int lq = tid % LPC;   // which block of SPL states
+    // channel of this lane within the workgroup, and which block of SPL states
+    // it holds.  With 8 lanes per channel the lanes of channel c of a wave are
+    // c, c+8, ..., c+56 (the layout SwapReduce8x4 reduces over).
+    constexpr bool kSwap = LPC == 8;
+    const int lane = tid & 63;
+    const int lc = kSwap ? (tid >> 6) * 8 + (lane & 7) : tid / LPC;
+    const int lq = kSwap ? lane >> 3 : tid % LPC;
     const bool lane_ok = lc < nvalid;
     const int dl = cbase + lc;
     float A2[SPL], h[SPL], bco[SPL], cco[SPL];
@@ -307,14 +335,20 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
                     y[e] = fmaf(h[j], cc, y[e]);              // out += h * C
                 }
             }
+            if constexpr (kSwap) {
+                float z = SwapReduce8x4(y);
+                asm volatile("" : "+v"(z));   // keep the reduction ahead of the branch
+                if ((lane & 8) == 0) rY[q4 * 4 + SwapReducedToken(lane)] = z;
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                y[e] = LaneGroupSum<LPC>(y[e]);
-                // keep the whole reduction ahead of the branch below, so every
-                // step folds into one v_add_f32_dpp (no instruction emitted)
-                asm volatile("" : "+v"(y[e]));
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = LaneGroupSum<LPC>(y[e]);
+                    // keep the whole reduction ahead of the branch below, so every
+                    // step folds into one v_add_f32_dpp (no instruction emitted)
+                    asm volatile("" : "+v"(y[e]));
+                }
+                if (lq == 0) *reinterpret_cast<float4 *>(rY + q4 * 4) = make_float4(y[0], y[1], y[2], y[3]);
             }
-            if (lq == 0) *reinterpret_cast<float4 *>(rY + q4 * 4) = make_float4(y[0], y[1], y[2], y[3]);
         }
     };
 
