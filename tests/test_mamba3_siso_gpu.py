@@ -52,12 +52,14 @@ def test_mamba3_parity(name):
     check(f"mamba3_siso/{name}", run_gpu(inp), run_ref(inp), TOL_M3)
 
 
-@pytest.mark.parametrize("rpt", ["1", "2", "4"])
-def test_mamba3_row_layouts_agree(rpt, monkeypatch):
-    s = M(1, 60, 3, 64, 64, has_z=True)
+@pytest.mark.parametrize("shape", [(2, 33, 2, 65, 64), (1, 17, 2, 100, 256), (1, 64, 2, 32, 128),
+                                   (1, 47, 3, 97, 192), (2, 31, 2, 3, 32)])
+def test_mamba3_row_blocks_and_ragged_token_blocks(shape):
+    """Several 32-row workgroups per head with a partial last one, token counts
+    that end inside a block (32-token blocks for N <= 128, 16 above), Z present."""
+    s = M(*shape, has_z=True)
     inp = W.mamba3_siso_inputs(s, seed=4)
-    monkeypatch.setenv("XM_M3_RPT", rpt)
-    check(f"mamba3_siso/rpt{rpt}", run_gpu(inp), run_ref(inp), TOL_M3)
+    check("mamba3_siso/rows_" + "_".join(map(str, shape)), run_gpu(inp), run_ref(inp), TOL_M3)
 
 
 def test_mamba3_long_angle_accumulation():

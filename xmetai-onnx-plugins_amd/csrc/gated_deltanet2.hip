@@ -112,26 +112,6 @@ __global__ __launch_bounds__(kThreads) void Gdn2PrepKernel(GatedDeltaNet2Params 
 // ---------------------------------------------------------------------------
 // Register-state recurrence (dk <= 256)
 // ---------------------------------------------------------------------------
-template <int KT>
-__device__ __forceinline__ void LoadKeys(const float *src, float (&x)[KT]) {
-    if constexpr (KT % 4 == 0) {
-#pragma unroll
-        for (int j = 0; j < KT; j += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + j);
-            x[j] = v.x; x[j + 1] = v.y; x[j + 2] = v.z; x[j + 3] = v.w;
-        }
-    } else if constexpr (KT % 2 == 0) {
-#pragma unroll
-        for (int j = 0; j < KT; j += 2) {
-            const float2 v = *reinterpret_cast<const float2 *>(src + j);
-            x[j] = v.x; x[j + 1] = v.y;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < KT; ++j) x[j] = src[j];
-    }
-}
-
 // LDS layout of one staged token for KT keys per lane: each of the 4 vectors
 // occupies KPS floats.  gfx950 serves a ds_read_b128 16 lanes at a time from
 // 64 four-byte banks, so the 16 key groups of a wave are conflict-free when

@@ -8,17 +8,30 @@
 //   gamma = DT_t sigmoid(Trap_t); look = DT_{t+1} (1 - sigmoid(Trap_{t+1})) (0 at t = T-1)
 //   S *= exp(ADT_t);  y = q_rot.S + (D + qk gamma) V_t  (* silu(Z_t));  S += V_t (x) k_rot (gamma + look)
 //
-// One fused kernel; a workgroup owns one (b,h) and a block of 16*RPT state
-// rows, and walks the sequence in blocks of kTB tokens:
-//   A) angle scan: tanh(Angles)*DT*pi for every (token, pair) in parallel,
-//      then one lane per pair accumulates in fp64 and wraps, so the angle
-//      state carries no fp32 round-off from step to step;
-//   B) one wave per token: bias add, q.k (wave reduction), rotation,
-//      trapezoid coefficients, decay and diagonal term -> LDS;
-//   C) recurrence: lane (row group, key group) holds RPT rows x KPT keys of
-//      S in VGPRs; the readout over keys is a 4-step DPP row sum;
-//   D) y = readout + diag*V (* silu(Z)), stored with coalesced rows.
-// Pairs >= A are not rotated (reference :109).
+// One fused kernel.  A workgroup of 512 threads owns one (b,h) and 32 state
+// rows (P), so the usual P = 64 takes two workgroups per head and a 4 x 32
+// head workload fills the 256 CUs with one workgroup each.  The sequence is
+// walked in blocks of TB tokens; the per-token vectors of block j+1 are
+// prepared while block j's recurrence runs, in double-buffered LDS, with two
+// barriers per block:
+//   prep A (per wave: SEG = TB/8 consecutive tokens x every pair): angle
+//     increments tanh(Angles) * DT * pi in fp64 and their running sum over
+//     the wave's tokens;
+//   prep B: each wave adds the block carry and the sums of the earlier waves,
+//     wraps with the reference's period 2 * (float)pi, rotates q/k with the
+//     hardware sine/cosine of the wrapped angle (v_sin/v_cos take revolutions;
+//     the revolutions are formed in fp64), writes rotated q and k to LDS, sums
+//     q.k over the pairs, and one lane per token forms decay, gamma + look and
+//     the diagonal D + qk gamma;
+//   recurrence: lane (row group rg, key group kg) holds KPT keys of one row
+//     of S in VGPRs; the readout over keys is a 4-step DPP row sum; token
+//     tt+1's vectors are read from LDS while token tt computes; lane kg keeps
+//     the output of tokens kg and kg+16 and stores them after the block.
+// Summing the angle increments first and wrapping once per token equals the
+// reference's wrap after every step in exact arithmetic; fp64 keeps the
+// difference far below fp32 resolution.  Pairs >= A are not rotated (:109).
+// Tokens past the end of the last block are identity tokens (decay 1, zero
+// k scale, zero v): they leave the state unchanged and are not stored.
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -29,229 +42,310 @@
 namespace xm {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTB = 16;                 // tokens per block
-constexpr float kPiF = 3.14159265358979323846f;      // reference kPi (mamba3_siso_fwd.cu:15)
-constexpr double kTwoPiD = 2.0 * static_cast<double>(kPiF);  // reference kTwoPi = 2 * kPi
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRows = kThreads / 16;     // state rows per workgroup (one per 16-lane row group)
+constexpr float kPiF = 3.14159265358979323846f;                     // reference kPi (mamba3_siso_fwd.cu:15)
+constexpr double kTwoPiF = 2.0 * static_cast<double>(kPiF);         // reference kTwoPi = 2 * kPi: the wrap period
+constexpr double kRevPerRad = 0.15915494309189533577;               // 1 / (2 pi): radians -> revolutions
 
-__device__ __forceinline__ float Sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+template <int KPT>
+struct M3Layout {
+    static constexpr int NP = 16 * KPT;                 // padded headdim_qk
+    static constexpr int PAIRS = NP / 2;
+    static constexpr int PB = (PAIRS + 63) / 64;        // pairs per lane in the preparation
+    static constexpr int TB = KPT >= 12 ? 16 : 32;      // tokens per block
+    static constexpr int SEG = TB / kWaves;             // tokens per wave in the preparation
+    static constexpr int TVP = (TB * kRows + kThreads - 1) / kThreads;   // V values per thread per block
+    // gfx950 serves ds_read_b128 16 lanes at a time from 64 banks: for 8 and
+    // 16 keys per lane, 16 bytes of padding per 256 bytes keep the 16 key
+    // groups of a row on distinct banks.
+    static constexpr bool PAD = KPT == 8 || KPT == 16;
+    static constexpr int NPS = PAD ? NP + 4 * ((NP - 1) / 64) : NP;   // floats per token row of sQ / sK
+    __host__ __device__ static constexpr int Pos(int i) { return PAD ? i + 4 * (i / 64) : i; }
+    // dynamic LDS (bytes), doubles first
+    static constexpr size_t kSeg = 0;                                          // double [kWaves][PAIRS]
+    static constexpr size_t kCarry = kSeg + sizeof(double) * kWaves * PAIRS;   // double [2][PAIRS]
+    static constexpr size_t kQ = kCarry + sizeof(double) * 2 * PAIRS;          // float [2][TB][NPS]
+    static constexpr size_t kK = kQ + sizeof(float) * 2 * TB * NPS;            // float [2][TB][NPS]
+    static constexpr size_t kV = kK + sizeof(float) * 2 * TB * NPS;            // float [2][TB][kRows]
+    static constexpr size_t kScal = kV + sizeof(float) * 2 * TB * kRows;       // float [2][3][TB]
+    static constexpr size_t kBytes = kScal + sizeof(float) * 2 * 3 * TB;
+    static_assert(kQ % 16 == 0 && kK % 16 == 0 && kV % 16 == 0, "LDS regions must stay 16-byte aligned");
+    static_assert(kBytes <= 160 * 1024, "LDS budget");
+};
 
-template <int KPT, int RPT>
+__device__ __forceinline__ float FastSigmoid(float x) { return __fdividef(1.0f, 1.0f + __expf(-x)); }
+
+template <int KPT>
 __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) {
-    constexpr int NP = 16 * KPT;        // padded headdim_qk
-    constexpr int PAIRS = NP / 2;
-    constexpr int RB = 16 * RPT;        // state rows per workgroup
+    using L = M3Layout<KPT>;
+    constexpr int PAIRS = L::PAIRS, PB = L::PB, TB = L::TB, SEG = L::SEG, NPS = L::NPS, TVP = L::TVP;
 
-    __shared__ __attribute__((aligned(16))) float sQ[kTB * NP];   // rotated q
-    __shared__ __attribute__((aligned(16))) float sK[kTB * NP];   // rotated k * (gamma + look)
-    __shared__ float sV[kTB * RB];
-    __shared__ float sZ[kTB * RB];
-    __shared__ float sY[kTB * RB];
-    __shared__ float sDecay[kTB], sDiag[kTB];
-    __shared__ float sTh[kTB * PAIRS];      // wrapped angle per (token, pair)
-    __shared__ double sDelta[kTB * PAIRS];  // angle increments
-    __shared__ double sCarry[PAIRS];        // angle state at the end of the previous block
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    double *sSeg = reinterpret_cast<double *>(smem + L::kSeg);
+    double *sCarry = reinterpret_cast<double *>(smem + L::kCarry);
+    float *sQ = reinterpret_cast<float *>(smem + L::kQ);
+    float *sK = reinterpret_cast<float *>(smem + L::kK);
+    float *sV = reinterpret_cast<float *>(smem + L::kV);
+    float *sScal = reinterpret_cast<float *>(smem + L::kScal);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
-    const int T = p.seqlen, N = p.n, P = p.p, A = p.a;
-    const int nrb = (P + RB - 1) / RB;
-    // the nrb workgroups of one (b,h) read the same token vectors: keep them on one XCD
+    const int T = p.seqlen, N = p.n, P = p.p, A = p.a, H = p.nheads;
+    const int half_n = N / 2;
+    const int nrb = (P + kRows - 1) / kRows;
+    // the nrb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
     const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
     const int rb = wg % nrb;
     const int bh = wg / nrb;
-    const int b = bh / p.nheads, h = bh % p.nheads;
-    const int gq = h / (p.nheads / p.nheads_qk);
-    const int r0 = rb * RB;
-    const bool has_z = p.Z != nullptr;
+    const int b = bh / H, h = bh % H;
+    const int gq = h / (H / p.nheads_qk);
+    const int r0 = rb * kRows;
     const float dval = p.D ? p.D[h] : 0.0f;
-
     const float *dtr = p.DT + static_cast<size_t>(bh) * T;
     const float *trr = p.Trap + static_cast<size_t>(bh) * T;
     const float *adr = p.ADT + static_cast<size_t>(bh) * T;
 
-    // Recurrence lane layout: kg = key group (16 lanes of a DPP row), rg = row group.
-    const int kg = tid & 15, rg = tid >> 4;
-    float S[RPT][KPT];
+    // ---- preparation state: lane handles pairs lane + 64*x, tokens w*SEG + s
+    float2 qbias[PB], kbias[PB];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
+    for (int x = 0; x < PB; ++x) {
+        const int pr = lane + 64 * x;
+        const int pc = min(pr, half_n - 1);
+        const float2 qb = *reinterpret_cast<const float2 *>(p.Q_bias + static_cast<size_t>(h) * N + 2 * pc);
+        const float2 kb = *reinterpret_cast<const float2 *>(p.K_bias + static_cast<size_t>(h) * N + 2 * pc);
+        const bool ok = pr < half_n;
+        qbias[x] = ok ? qb : make_float2(0.0f, 0.0f);
+        kbias[x] = ok ? kb : make_float2(0.0f, 0.0f);
+    }
+    float ang[PB][SEG], dts[SEG];
+    float2 qv[PB][SEG], kv[PB][SEG];
+    float vreg[TVP];
+    float tdt = 0.0f, ttrap = 0.0f, tadt = 0.0f, tdt1 = 0.0f, ttrap1 = 0.0f;   // token scalars (lane < SEG)
+    double pre[PB][SEG];
+
+    // global -> registers for the block at t0 (clamped addresses, zero outside)
+    auto load_prep = [&](int t0) __attribute__((always_inline)) {
+        const int nt = min(TB, T - t0);
 #pragma unroll
-        for (int j = 0; j < KPT; ++j) S[i][j] = 0.0f;
-    for (int i = tid; i < PAIRS; i += kThreads) sCarry[i] = 0.0;
-
-    for (int t0 = 0; t0 < T; t0 += kTB) {
-        const int nt = min(kTB, T - t0);
-
-        // ---- A1: angle increments tanh(angle) * dt * pi (fp32 tanh, fp64 products)
-        for (int i = tid; i < kTB * PAIRS; i += kThreads) {
-            const int tt = i / PAIRS, pr = i % PAIRS;
-            double dlt = 0.0;
-            if (tt < nt && pr < A) {
-                const int t = t0 + tt;
-                const float ang = p.Angles[((static_cast<size_t>(b) * T + t) * p.nheads + h) * A + pr];
-                dlt = static_cast<double>(tanhf(ang)) * static_cast<double>(dtr[t]) * static_cast<double>(kPiF);
-            }
-            sDelta[i] = dlt;
-        }
-        // V and Z rows of this block (coalesced: RB contiguous floats per token).
-        for (int i = tid; i < kTB * RB; i += kThreads) {
-            const int tt = i / RB, r = r0 + i % RB;
-            float vv = 0.0f, zz = 0.0f;
-            if (tt < nt && r < P) {
-                const size_t idx = ((static_cast<size_t>(b) * T + t0 + tt) * p.nheads + h) * P + r;
-                vv = p.V[idx];
-                if (has_z) zz = p.Z[idx];
-            }
-            sV[i] = vv;
-            sZ[i] = zz;
-        }
-        __syncthreads();
-
-        // ---- A2: sequential wrap per pair, in fp64 (reference :82-86, :26-28)
-        for (int pr = tid; pr < A; pr += kThreads) {
-            double th = sCarry[pr];
-            for (int tt = 0; tt < nt; ++tt) {
-                th += sDelta[tt * PAIRS + pr];
-                th -= kTwoPiD * floor(th * (1.0 / kTwoPiD));
-                sTh[tt * PAIRS + pr] = static_cast<float>(th);
-            }
-            sCarry[pr] = th;
-        }
-        __syncthreads();
-
-        // ---- B: per-token vectors, one wave per token
-        for (int tt = w; tt < nt; tt += kThreads / 64) {
-            const int t = t0 + tt;
+        for (int s = 0; s < SEG; ++s) {
+            const int tt = w * SEG + s;
+            const bool ok = tt < nt;
+            const int t = min(t0 + tt, T - 1);
+            const float d = dtr[t];
+            dts[s] = ok ? d : 0.0f;
             const size_t qrow = ((static_cast<size_t>(b) * T + t) * p.nheads_qk + gq) * N;
-            float qk = 0.0f;
-            float2 qv[(PAIRS + 63) / 64], kv[(PAIRS + 63) / 64];
+            const size_t arow = ((static_cast<size_t>(b) * T + t) * H + h) * A;
 #pragma unroll
-            for (int x = 0; x < (PAIRS + 63) / 64; ++x) {
+            for (int x = 0; x < PB; ++x) {
                 const int pr = lane + 64 * x;
-                float2 qq = make_float2(0.0f, 0.0f), kk = make_float2(0.0f, 0.0f);
-                if (pr < N / 2) {
-                    const float2 q2 = *reinterpret_cast<const float2 *>(p.Q + qrow + 2 * pr);
-                    const float2 k2 = *reinterpret_cast<const float2 *>(p.K + qrow + 2 * pr);
-                    const float2 qb = *reinterpret_cast<const float2 *>(p.Q_bias + static_cast<size_t>(h) * N + 2 * pr);
-                    const float2 kb = *reinterpret_cast<const float2 *>(p.K_bias + static_cast<size_t>(h) * N + 2 * pr);
-                    qq = make_float2(q2.x + qb.x, q2.y + qb.y);
-                    kk = make_float2(k2.x + kb.x, k2.y + kb.y);
-                    qk = fmaf(qq.x, kk.x, qk);
-                    qk = fmaf(qq.y, kk.y, qk);
-                }
-                qv[x] = qq;
-                kv[x] = kk;
-            }
-            qk = WaveSum64(qk);   // unrotated q.k (reference :89-106)
-            const float dt = dtr[t];
-            const float gamma = dt * Sigmoid(trr[t]);
-            float look = 0.0f;
-            if (t + 1 < T) look = dtr[t + 1] * (1.0f - Sigmoid(trr[t + 1]));
-            const float kscale = gamma + look;
-#pragma unroll
-            for (int x = 0; x < (PAIRS + 63) / 64; ++x) {
-                const int pr = lane + 64 * x;
-                if (pr < PAIRS) {
-                    float c = 1.0f, s = 0.0f;
-                    if (pr < A) sincosf(sTh[tt * PAIRS + pr], &s, &c);
-                    const float2 qq = qv[x], kk = kv[x];
-                    sQ[tt * NP + 2 * pr] = qq.x * c - qq.y * s;
-                    sQ[tt * NP + 2 * pr + 1] = qq.x * s + qq.y * c;
-                    sK[tt * NP + 2 * pr] = (kk.x * c - kk.y * s) * kscale;
-                    sK[tt * NP + 2 * pr + 1] = (kk.x * s + kk.y * c) * kscale;
-                }
-            }
-            if (lane == 0) {
-                sDecay[tt] = expf(adr[t]);
-                sDiag[tt] = dval + qk * gamma;
+                const float a = p.Angles[arow + min(pr, A - 1)];
+                ang[x][s] = (ok && pr < A) ? a : 0.0f;
+                const int pc = min(pr, half_n - 1);
+                const float2 q2 = *reinterpret_cast<const float2 *>(p.Q + qrow + 2 * pc);
+                const float2 k2 = *reinterpret_cast<const float2 *>(p.K + qrow + 2 * pc);
+                const bool okp = ok && pr < half_n;
+                qv[x][s] = okp ? make_float2(q2.x + qbias[x].x, q2.y + qbias[x].y) : make_float2(0.0f, 0.0f);
+                kv[x][s] = okp ? make_float2(k2.x + kbias[x].x, k2.y + kbias[x].y) : make_float2(0.0f, 0.0f);
             }
         }
-        __syncthreads();
+        {
+            const int t = min(t0 + w * SEG + min(lane, SEG - 1), T - 1);
+            const int t1 = min(t + 1, T - 1);
+            tdt = dtr[t];
+            ttrap = trr[t];
+            tadt = adr[t];
+            tdt1 = dtr[t1];
+            ttrap1 = trr[t1];
+        }
+#pragma unroll
+        for (int k = 0; k < TVP; ++k) {
+            const int i = tid + k * kThreads;
+            const int tt = i / kRows, r = r0 + i % kRows;
+            const bool ok = i < TB * kRows && tt < nt && r < P;
+            const int t = min(t0 + tt, T - 1);
+            const float v = p.V[((static_cast<size_t>(b) * T + t) * H + h) * P + min(r, P - 1)];
+            vreg[k] = ok ? v : 0.0f;
+        }
+    };
 
-        // ---- C: recurrence over the block
-        for (int tt = 0; tt < nt; ++tt) {
-            const float dec = sDecay[tt];
-            float q[KPT], k[KPT];
+    // prep A: fp64 angle increments and their running sum over the wave's tokens
+    auto prep_a = [&]() __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < KPT; j += 4) {
-                const float4 a = *reinterpret_cast<const float4 *>(&sQ[tt * NP + kg * KPT + j]);
-                const float4 c = *reinterpret_cast<const float4 *>(&sK[tt * NP + kg * KPT + j]);
-                q[j] = a.x; q[j + 1] = a.y; q[j + 2] = a.z; q[j + 3] = a.w;
-                k[j] = c.x; k[j + 1] = c.y; k[j + 2] = c.z; k[j + 3] = c.w;
+        for (int x = 0; x < PB; ++x) {
+            double acc = 0.0;
+#pragma unroll
+            for (int s = 0; s < SEG; ++s) {
+                acc += static_cast<double>(tanhf(ang[x][s])) * static_cast<double>(dts[s]) * static_cast<double>(kPiF);
+                pre[x][s] = acc;
             }
-#pragma unroll
-            for (int i = 0; i < RPT; ++i) {
-                const int rl = rg * RPT + i;
-                const float vv = sV[tt * RB + rl];
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KPT; ++j) {
-                    S[i][j] *= dec;
-                    acc = fmaf(q[j], S[i][j], acc);
-                }
-                acc = RowSum16(acc);
-#pragma unroll
-                for (int j = 0; j < KPT; ++j) S[i][j] = fmaf(vv, k[j], S[i][j]);
-                if (kg == 0) sY[tt * RB + rl] = acc;
-            }
+            const int pr = lane + 64 * x;
+            if (pr < PAIRS) sSeg[w * PAIRS + pr] = acc;
         }
-        __syncthreads();
+    };
 
-        // ---- D: y = readout + diag * V, optional silu(Z) gate; coalesced store
-        for (int i = tid; i < nt * RB; i += kThreads) {
-            const int tt = i / RB, r = r0 + i % RB;
-            if (r < P) {
-                float y = sY[i] + sDiag[tt] * sV[i];
-                if (has_z) {
-                    const float z = sZ[i];
-                    y *= z * Sigmoid(z);
+    // prep B: wrapped angles, rotation, q.k and per-token scalars into buffer nb
+    auto prep_b = [&](int t0, int nb, int cb) __attribute__((always_inline)) {
+        const int nt = min(TB, T - t0);
+        float qk[SEG];
+#pragma unroll
+        for (int s = 0; s < SEG; ++s) qk[s] = 0.0f;
+#pragma unroll
+        for (int x = 0; x < PB; ++x) {
+            const int pr = lane + 64 * x;
+            if (pr < PAIRS) {
+                double carry = sCarry[cb * PAIRS + pr];
+                for (int w2 = 0; w2 < w; ++w2) carry += sSeg[w2 * PAIRS + pr];
+                const bool rot = pr < A;
+                double th = 0.0;
+#pragma unroll
+                for (int s = 0; s < SEG; ++s) {
+                    const int tt = w * SEG + s;
+                    th = carry + pre[x][s];
+                    th -= kTwoPiF * floor(th / kTwoPiF);     // wrap_two_pi (reference :26-28)
+                    float c = 1.0f, sn = 0.0f;
+                    if (rot) {
+                        const float rev = static_cast<float>(th * kRevPerRad);
+                        sn = __builtin_amdgcn_sinf(rev);
+                        c = __builtin_amdgcn_cosf(rev);
+                    }
+                    const float2 q = qv[x][s], k = kv[x][s];
+                    qk[s] = fmaf(q.x, k.x, fmaf(q.y, k.y, qk[s]));   // unrotated q.k (reference :89-106)
+                    const int o = (nb * TB + tt) * NPS + L::Pos(2 * pr);
+                    *reinterpret_cast<float2 *>(&sQ[o]) = make_float2(q.x * c - q.y * sn, q.x * sn + q.y * c);
+                    *reinterpret_cast<float2 *>(&sK[o]) = make_float2(k.x * c - k.y * sn, k.x * sn + k.y * c);
                 }
-                p.out[((static_cast<size_t>(b) * T + t0 + tt) * p.nheads + h) * P + r] = y;
+                if (w == kWaves - 1) sCarry[(cb ^ 1) * PAIRS + pr] = rot ? th : 0.0;
             }
         }
-        // Next block's phase A writes sDelta/sV/sZ (last read before the
-        // barrier above) and sTh/sQ/sK/sY only after further barriers.
+        float myqk = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SEG; ++s) {
+            const float v = WaveSum64(qk[s]);
+            myqk = lane == s ? v : myqk;
+        }
+        if (lane < SEG) {
+            const int tt = w * SEG + lane;
+            const int t = t0 + tt;
+            const bool ok = tt < nt;
+            const float gamma = tdt * FastSigmoid(ttrap);
+            const float look = t + 1 < T ? tdt1 * (1.0f - FastSigmoid(ttrap1)) : 0.0f;
+            float *sc = sScal + nb * 3 * TB;
+            sc[tt] = ok ? __expf(tadt) : 1.0f;                // decay
+            sc[TB + tt] = ok ? gamma + look : 0.0f;            // k scale
+            sc[2 * TB + tt] = ok ? fmaf(myqk, gamma, dval) : 0.0f;   // D + qk * gamma
+        }
+#pragma unroll
+        for (int k = 0; k < TVP; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < TB * kRows) sV[nb * TB * kRows + i] = vreg[k];
+        }
+    };
+
+    // ---- recurrence
+    const int kg = tid & 15, rg = tid >> 4;
+    const int row = r0 + rg;
+    const int kpos = L::Pos(kg * KPT);
+    float S[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) S[j] = 0.0f;
+
+    auto recur = [&](int t0, int buf) __attribute__((always_inline)) {
+        const int nt = min(TB, T - t0);
+        const float *qb = sQ + buf * TB * NPS + kpos;
+        const float *kb = sK + buf * TB * NPS + kpos;
+        const float *sc = sScal + buf * 3 * TB;
+        const float *vr = sV + buf * TB * kRows + rg;
+        float oreg[TB / 16];
+#pragma unroll
+        for (int u = 0; u < TB / 16; ++u) oreg[u] = 0.0f;
+        float cq[KPT], ck[KPT], nq[KPT], nk[KPT];
+        float cdec, cks, cdiag, cv, ndec = 1.0f, nks = 0.0f, ndiag = 0.0f, nv = 0.0f;
+        LoadKeys<KPT>(qb, cq);
+        LoadKeys<KPT>(kb, ck);
+        cdec = sc[0]; cks = sc[TB]; cdiag = sc[2 * TB]; cv = vr[0];
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt) {
+            if (tt + 1 < TB) {
+                LoadKeys<KPT>(qb + (tt + 1) * NPS, nq);
+                LoadKeys<KPT>(kb + (tt + 1) * NPS, nk);
+                ndec = sc[tt + 1]; nks = sc[TB + tt + 1]; ndiag = sc[2 * TB + tt + 1]; nv = vr[(tt + 1) * kRows];
+            }
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KPT; j += 2) {
+                S[j] *= cdec;                       // decay before the readout (reference :140-143)
+                a0 = fmaf(cq[j], S[j], a0);
+                if (j + 1 < KPT) {
+                    S[j + 1] *= cdec;
+                    a1 = fmaf(cq[j + 1], S[j + 1], a1);
+                }
+            }
+            const float y = fmaf(cdiag, cv, RowSum16(a0 + a1));
+            const float vk = cv * cks;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j) S[j] = fmaf(vk, ck[j], S[j]);   // S += V (x) k_rot (gamma + look)
+            oreg[tt / 16] = kg == (tt & 15) ? y : oreg[tt / 16];
+            if (tt + 1 < TB) {
+#pragma unroll
+                for (int j = 0; j < KPT; ++j) { cq[j] = nq[j]; ck[j] = nk[j]; }
+                cdec = ndec; cks = nks; cdiag = ndiag; cv = nv;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < TB / 16; ++u) {
+            const int tt = u * 16 + kg;
+            if (tt < nt && row < P) {
+                const size_t idx = ((static_cast<size_t>(b) * T + t0 + tt) * H + h) * P + row;
+                float y = oreg[u];
+                if (p.Z) {
+                    const float z = p.Z[idx];
+                    y *= z * FastSigmoid(z);                 // silu gate (reference :155-158)
+                }
+                p.out[idx] = y;
+            }
+        }
+    };
+
+    if (tid < PAIRS) sCarry[tid] = 0.0;
+    const int nblk = (T + TB - 1) / TB;
+    load_prep(0);
+    prep_a();
+    __syncthreads();
+    prep_b(0, 0, 0);
+    __syncthreads();
+    for (int j = 0; j < nblk; ++j) {
+        const int buf = j & 1;
+        const bool next = j + 1 < nblk;
+        if (next) load_prep((j + 1) * TB);
+        recur(j * TB, buf);
+        if (next) prep_a();
+        __syncthreads();
+        if (next) prep_b((j + 1) * TB, buf ^ 1, (j + 1) & 1);
         __syncthreads();
     }
 }
 
 template <int KPT>
-void LaunchKPT(const Mamba3SisoParams &p, int rpt, hipStream_t stream) {
-    if (KPT >= 12 && rpt == 4) rpt = 2;
-    const int rb = 16 * rpt;
-    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + rb - 1) / rb);
+void LaunchKPT(const Mamba3SisoParams &p, hipStream_t stream) {
+    using L = M3Layout<KPT>;
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    const dim3 grid(static_cast<unsigned>(blocks));
-    if (rpt == 1) {
-        hipLaunchKernelGGL((Mamba3FwdKernel<KPT, 1>), grid, dim3(kThreads), 0, stream, p);
-    } else if (rpt == 2 || KPT >= 12) {
-        // 4 rows per lane would exceed 64 KiB of LDS for headdim_qk > 128
-        hipLaunchKernelGGL((Mamba3FwdKernel<KPT, 2>), grid, dim3(kThreads), 0, stream, p);
-    } else {
-        if constexpr (KPT < 12) hipLaunchKernelGGL((Mamba3FwdKernel<KPT, 4>), grid, dim3(kThreads), 0, stream, p);
-    }
-}
-
-// Rows per lane (16 rows per workgroup per row per lane).  XM_M3_RPT (1, 2
-// or 4) overrides, for tuning.
-int RowsPerLane(const Mamba3SisoParams &p) {
-    const char *env = std::getenv("XM_M3_RPT");
-    const int forced = env ? std::atoi(env) : 0;
-    if (forced == 1 || forced == 2 || forced == 4) return forced;
-    (void)p;
-    return 1;   // measured fastest at 4 x 4096 x 32 heads, P = 64, N = 128
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3FwdKernel<KPT>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
+    hipLaunchKernelGGL((Mamba3FwdKernel<KPT>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), L::kBytes, stream, p);
 }
 
 }  // namespace
 
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream_v) {
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
-    const int rpt = RowsPerLane(p);
     const int kpt = (p.n + 15) / 16;
-    if (kpt <= 4) LaunchKPT<4>(p, rpt, stream);
-    else if (kpt <= 8) LaunchKPT<8>(p, rpt, stream);
-    else if (kpt <= 12) LaunchKPT<12>(p, rpt, stream);
-    else LaunchKPT<16>(p, rpt, stream);
+    if (kpt <= 4) LaunchKPT<4>(p, stream);
+    else if (kpt <= 8) LaunchKPT<8>(p, stream);
+    else if (kpt <= 12) LaunchKPT<12>(p, stream);
+    else LaunchKPT<16>(p, stream);
     XM_LAUNCH_CHECK("Mamba3SisoFn");
 }
 

@@ -58,6 +58,27 @@ __device__ __forceinline__ double WaveSum64d(double x) {
     return x;
 }
 
+// KT consecutive floats of LDS into registers, 16 or 8 bytes at a time.
+template <int KT>
+__device__ __forceinline__ void LoadKeys(const float *src, float (&x)[KT]) {
+    if constexpr (KT % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < KT; j += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + j);
+            x[j] = v.x; x[j + 1] = v.y; x[j + 2] = v.z; x[j + 3] = v.w;
+        }
+    } else if constexpr (KT % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < KT; j += 2) {
+            const float2 v = *reinterpret_cast<const float2 *>(src + j);
+            x[j] = v.x; x[j + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KT; ++j) x[j] = src[j];
+    }
+}
+
 // MI355X deals the workgroups of a launch round-robin to its 8 XCDs
 // (workgroup x runs on XCD x % 8), and each XCD has its own L2.  This maps
 // the hardware index to a logical one under which XCD j owns one contiguous
