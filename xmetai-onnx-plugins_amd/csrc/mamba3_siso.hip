@@ -119,35 +119,41 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         qbias[x] = ok ? qb : make_float2(0.0f, 0.0f);
         kbias[x] = ok ? kb : make_float2(0.0f, 0.0f);
     }
+    // Per-token row bases and strides (elements); token t of this (b,h) is at base + t * stride.
+    const size_t q_stride = static_cast<size_t>(p.nheads_qk) * N;
+    const float *qbase = p.Q + (static_cast<size_t>(b) * T * p.nheads_qk + gq) * N;
+    const float *kbase = p.K + (static_cast<size_t>(b) * T * p.nheads_qk + gq) * N;
+    const size_t a_stride = static_cast<size_t>(H) * A;
+    const float *abase = p.Angles + (static_cast<size_t>(b) * T * H + h) * A;
+    const size_t v_stride = static_cast<size_t>(H) * P;
+    const size_t vbase = (static_cast<size_t>(b) * T * H + h) * P;   // also the output / Z base
+
+    // Raw prefetched values.  The loads use clamped addresses and nothing
+    // selects on them until they are consumed after the recurrence: a select
+    // next to the load lets the compiler sink the load into a branch and
+    // wait for it on the spot, which would serialise the prefetch.
     float ang[PB][SEG], dts[SEG];
     float2 qv[PB][SEG], kv[PB][SEG];
     float vreg[TVP];
     float tdt = 0.0f, ttrap = 0.0f, tadt = 0.0f, tdt1 = 0.0f, ttrap1 = 0.0f;   // token scalars (lane < SEG)
     double pre[PB][SEG];
 
-    // global -> registers for the block at t0 (clamped addresses, zero outside)
+    // global -> registers for the block at t0
     auto load_prep = [&](int t0) __attribute__((always_inline)) {
-        const int nt = min(TB, T - t0);
 #pragma unroll
         for (int s = 0; s < SEG; ++s) {
-            const int tt = w * SEG + s;
-            const bool ok = tt < nt;
-            const int t = min(t0 + tt, T - 1);
-            const float d = dtr[t];
-            dts[s] = ok ? d : 0.0f;
-            const size_t qrow = ((static_cast<size_t>(b) * T + t) * p.nheads_qk + gq) * N;
-            const size_t arow = ((static_cast<size_t>(b) * T + t) * H + h) * A;
+            const int t = min(t0 + w * SEG + s, T - 1);
+            dts[s] = dtr[t];
+            const float *qr = qbase + static_cast<size_t>(t) * q_stride;
+            const float *kr = kbase + static_cast<size_t>(t) * q_stride;
+            const float *ar = abase + static_cast<size_t>(t) * a_stride;
 #pragma unroll
             for (int x = 0; x < PB; ++x) {
                 const int pr = lane + 64 * x;
-                const float a = p.Angles[arow + min(pr, A - 1)];
-                ang[x][s] = (ok && pr < A) ? a : 0.0f;
+                ang[x][s] = ar[min(pr, A - 1)];
                 const int pc = min(pr, half_n - 1);
-                const float2 q2 = *reinterpret_cast<const float2 *>(p.Q + qrow + 2 * pc);
-                const float2 k2 = *reinterpret_cast<const float2 *>(p.K + qrow + 2 * pc);
-                const bool okp = ok && pr < half_n;
-                qv[x][s] = okp ? make_float2(q2.x + qbias[x].x, q2.y + qbias[x].y) : make_float2(0.0f, 0.0f);
-                kv[x][s] = okp ? make_float2(k2.x + kbias[x].x, k2.y + kbias[x].y) : make_float2(0.0f, 0.0f);
+                qv[x][s] = *reinterpret_cast<const float2 *>(qr + 2 * pc);
+                kv[x][s] = *reinterpret_cast<const float2 *>(kr + 2 * pc);
             }
         }
         {
@@ -162,22 +168,23 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 #pragma unroll
         for (int k = 0; k < TVP; ++k) {
             const int i = tid + k * kThreads;
-            const int tt = i / kRows, r = r0 + i % kRows;
-            const bool ok = i < TB * kRows && tt < nt && r < P;
-            const int t = min(t0 + tt, T - 1);
-            const float v = p.V[((static_cast<size_t>(b) * T + t) * H + h) * P + min(r, P - 1)];
-            vreg[k] = ok ? v : 0.0f;
+            const int t = min(t0 + i / kRows, T - 1);
+            vreg[k] = p.V[vbase + static_cast<size_t>(t) * v_stride + min(r0 + i % kRows, P - 1)];
         }
     };
 
     // prep A: fp64 angle increments and their running sum over the wave's tokens
-    auto prep_a = [&]() __attribute__((always_inline)) {
+    auto prep_a = [&](int t0) __attribute__((always_inline)) {
+        const int nt = min(TB, T - t0);
 #pragma unroll
         for (int x = 0; x < PB; ++x) {
+            const bool rot = lane + 64 * x < A;
             double acc = 0.0;
 #pragma unroll
             for (int s = 0; s < SEG; ++s) {
-                acc += static_cast<double>(tanhf(ang[x][s])) * static_cast<double>(dts[s]) * static_cast<double>(kPiF);
+                const bool ok = rot && w * SEG + s < nt;
+                const float a = ok ? ang[x][s] : 0.0f, d = ok ? dts[s] : 0.0f;
+                acc += static_cast<double>(tanhf(a)) * static_cast<double>(d) * static_cast<double>(kPiF);
                 pre[x][s] = acc;
             }
             const int pr = lane + 64 * x;
@@ -210,7 +217,11 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
                         sn = __builtin_amdgcn_sinf(rev);
                         c = __builtin_amdgcn_cosf(rev);
                     }
-                    const float2 q = qv[x][s], k = kv[x][s];
+                    const bool okp = w * SEG + s < nt && pr < half_n;
+                    const float2 q = okp ? make_float2(qv[x][s].x + qbias[x].x, qv[x][s].y + qbias[x].y)
+                                         : make_float2(0.0f, 0.0f);
+                    const float2 k = okp ? make_float2(kv[x][s].x + kbias[x].x, kv[x][s].y + kbias[x].y)
+                                         : make_float2(0.0f, 0.0f);
                     qk[s] = fmaf(q.x, k.x, fmaf(q.y, k.y, qk[s]));   // unrotated q.k (reference :89-106)
                     const int o = (nb * TB + tt) * NPS + L::Pos(2 * pr);
                     *reinterpret_cast<float2 *>(&sQ[o]) = make_float2(q.x * c - q.y * sn, q.x * sn + q.y * c);
@@ -239,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 #pragma unroll
         for (int k = 0; k < TVP; ++k) {
             const int i = tid + k * kThreads;
-            if (i < TB * kRows) sV[nb * TB * kRows + i] = vreg[k];
+            if (i < TB * kRows) sV[nb * TB * kRows + i] = (i / kRows < nt && r0 + i % kRows < P) ? vreg[k] : 0.0f;
         }
     };
 
@@ -297,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         for (int u = 0; u < TB / 16; ++u) {
             const int tt = u * 16 + kg;
             if (tt < nt && row < P) {
-                const size_t idx = ((static_cast<size_t>(b) * T + t0 + tt) * H + h) * P + row;
+                const size_t idx = vbase + static_cast<size_t>(t0 + tt) * v_stride + row;
                 float y = oreg[u];
                 if (p.Z) {
                     const float z = p.Z[idx];
@@ -311,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     if (tid < PAIRS) sCarry[tid] = 0.0;
     const int nblk = (T + TB - 1) / TB;
     load_prep(0);
-    prep_a();
+    prep_a(0);
     __syncthreads();
     prep_b(0, 0, 0);
     __syncthreads();
@@ -320,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         const bool next = j + 1 < nblk;
         if (next) load_prep((j + 1) * TB);
         recur(j * TB, buf);
-        if (next) prep_a();
+        if (next) prep_a((j + 1) * TB);
         __syncthreads();
         if (next) prep_b((j + 1) * TB, buf ^ 1, (j + 1) & 1);
         __syncthreads();
