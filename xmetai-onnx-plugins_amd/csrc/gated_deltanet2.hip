@@ -200,15 +200,15 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params
             vreg[k][0] = x.x; vreg[k][1] = x.y; vreg[k][2] = x.z; vreg[k][3] = x.w;
         }
         qkreg = prep_qk[tb0 + min(tid, nt - 1)];
+        // raw values: the validity select happens at staging time, so the
+        // compiler cannot sink these loads into a branch and wait on them here
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
             const int i = tid + k * kThreads;
             const int tt = min(i / COLS, nt - 1), col = min(v0 + i % COLS, dv - 1);
             const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
-            const bool ok = i < TB * COLS && i / COLS < nt && v0 + i % COLS < dv;
-            const float wv = p.w[idx], vv = p.v[idx];
-            wreg[k] = ok ? wv : 0.0f;
-            vvreg[k] = ok ? vv : 0.0f;
+            wreg[k] = p.w[idx];
+            vvreg[k] = p.v[idx];
         }
     };
     // Tokens past the end of a short block are staged as identity tokens
@@ -231,7 +231,8 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
             const int i = tid + k * kThreads;
-            if (i < TB * COLS) sWV[buf][i] = wreg[k] * vvreg[k];   // w * v (reference :120)
+            const bool ok = i / COLS < nt && v0 + i % COLS < dv;
+            if (i < TB * COLS) sWV[buf][i] = ok ? wreg[k] * vvreg[k] : 0.0f;   // w * v (reference :120)
         }
         if (tid < TB) sQK[buf][tid] = tid < nt ? qkreg : 0.0f;
     };
