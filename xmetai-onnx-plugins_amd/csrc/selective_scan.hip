@@ -75,6 +75,17 @@ __device__ __forceinline__ float SwapReduce8x4(const float (&y)[4]) {
     return z + DppF<0x128>(z);                                             // lanes c and c+8 of a row
 }
 
+// The same for 4 lanes per channel, {c, c+16, c+32, c+48} with c = lane % 16:
+// the two swap stages alone reduce over the 4 lanes (six instructions).
+__device__ __forceinline__ float SwapReduce4x4(const float (&y)[4]) {
+    const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[0]), __float_as_uint(y[1]), false, false);
+    const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[2]), __float_as_uint(y[3]), false, false);
+    const float y01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);
+    const float y23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(y01), __float_as_uint(y23), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 __device__ __forceinline__ int SwapReducedToken(int lane) {
     const int r = lane >> 4;
     return ((r & 1) << 1) | (r >> 1);
@@ -176,10 +187,12 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
     // channel of this lane within the workgroup, and which block of SPL states
     // it holds.  With 8 lanes per channel the lanes of channel c of a wave are
     // c, c+8, ..., c+56 (the layout SwapReduce8x4 reduces over).
-    constexpr bool kSwap = LPC == 8;
+    // With 4 lanes per channel they are c, c+16, c+32, c+48.
+    constexpr bool kSwap = LPC == 8 || LPC == 4;
+    constexpr int kCpWave = 64 / LPC;    // channels per wave
     const int lane = tid & 63;
-    const int lc = kSwap ? (tid >> 6) * 8 + (lane & 7) : tid / LPC;
-    const int lq = kSwap ? lane >> 3 : tid % LPC;
+    const int lc = kSwap ? (tid >> 6) * kCpWave + lane % kCpWave : tid / LPC;
+    const int lq = kSwap ? lane / kCpWave : tid % LPC;
     const bool lane_ok = lc < nvalid;
     const int dl = cbase + lc;
     float A2[SPL], h[SPL], bco[SPL], cco[SPL];
@@ -335,10 +348,12 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
                     y[e] = fmaf(h[j], cc, y[e]);              // out += h * C
                 }
             }
-            if constexpr (kSwap) {
+            if constexpr (LPC == 8) {
                 float z = SwapReduce8x4(y);
                 asm volatile("" : "+v"(z));   // keep the reduction ahead of the branch
                 if ((lane & 8) == 0) rY[q4 * 4 + SwapReducedToken(lane)] = z;
+            } else if constexpr (LPC == 4) {
+                rY[q4 * 4 + SwapReducedToken(lane)] = SwapReduce4x4(y);   // every lane: a distinct (channel, token)
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
