@@ -62,6 +62,26 @@ def test_mamba3_row_blocks_and_ragged_token_blocks(shape):
     check("mamba3_siso/rows_" + "_".join(map(str, shape)), run_gpu(inp), run_ref(inp), TOL_M3)
 
 
+@pytest.mark.parametrize("pattern", ["mild", "mixed", "steep", "growth"])
+def test_mamba3_scaled_and_unscaled_blocks(pattern):
+    """Token blocks whose accumulated decay stays within e^+-40 run on the scaled
+    state; steeper ones (|sum ADT| > 40 within a block) take the per-token decay
+    loop.  Both, and blocks switching between them, must match the oracle."""
+    s = M(2, 150, 2, 24, 64, has_z=pattern == "mixed")
+    inp = W.mamba3_siso_inputs(s, seed=11)
+    t = np.arange(s.seqlen)
+    if pattern == "mild":
+        adt = np.full(s.seqlen, -0.3)
+    elif pattern == "mixed":
+        adt = np.where((t // 32) % 2 == 0, -0.2, -5.0)          # alternating scaled / unscaled blocks
+    elif pattern == "steep":
+        adt = np.where(t % 7 == 3, -100.0, -2.0)                # underflowing decays
+    else:
+        adt = np.where(t % 2 == 0, 0.9, -0.5)                   # growth within the bound
+    inp["ADT"] = np.broadcast_to(adt.astype(np.float32), inp["ADT"].shape).copy()
+    check(f"mamba3_siso/decay_{pattern}", run_gpu(inp), run_ref(inp), TOL_M3)
+
+
 def test_mamba3_long_angle_accumulation():
     """4096 steps with large angle increments: the wrapped angle state must not
     drift from the fp64 oracle (the device accumulates it in fp64)."""

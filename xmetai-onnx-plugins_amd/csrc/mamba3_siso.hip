@@ -202,8 +202,13 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         for (int x = 0; x < PB; ++x) {
             const int pr = lane + 64 * x;
             if (pr < PAIRS) {
+                // earlier waves' sums: all reads issued at once, summed in wave order
                 double carry = sCarry[cb * PAIRS + pr];
-                for (int w2 = 0; w2 < w; ++w2) carry += sSeg[w2 * PAIRS + pr];
+#pragma unroll
+                for (int w2 = 0; w2 < kWaves - 1; ++w2) {
+                    const double v = sSeg[w2 * PAIRS + pr];
+                    carry = w2 < w ? carry + v : carry;
+                }
                 const bool rot = pr < A;
                 double th = 0.0;
 #pragma unroll
