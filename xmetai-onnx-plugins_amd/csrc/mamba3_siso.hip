@@ -48,6 +48,7 @@ constexpr int kRows = kThreads / 16;     // state rows per workgroup (one per 16
 constexpr float kPiF = 3.14159265358979323846f;                     // reference kPi (mamba3_siso_fwd.cu:15)
 constexpr double kTwoPiF = 2.0 * static_cast<double>(kPiF);         // reference kTwoPi = 2 * kPi: the wrap period
 constexpr double kRevPerRad = 0.15915494309189533577;               // 1 / (2 pi): radians -> revolutions
+constexpr double kInvTwoPiF = 1.0 / kTwoPiF;
 
 template <int KPT>
 struct M3Layout {
@@ -76,6 +77,20 @@ struct M3Layout {
 };
 
 __device__ __forceinline__ float FastSigmoid(float x) { return __fdividef(1.0f, 1.0f + __expf(-x)); }
+
+// tanh without branches: the odd Taylor series to x^9 below |x| = 0.25
+// (truncation < 1e-8 relative), above it 1 - 2 / (e^{2|x|} + 1) with the
+// hardware exp2 and reciprocal (about 5e-7 relative near 0.25, less above).
+__device__ __forceinline__ float TanhF(float x) {
+    const float ax = fabsf(x), x2 = ax * ax;
+    float p = fmaf(x2, 62.0f / 2835.0f, -17.0f / 315.0f);
+    p = fmaf(x2, p, 2.0f / 15.0f);
+    p = fmaf(x2, p, -1.0f / 3.0f);
+    const float small = fmaf(ax, x2 * p, ax);
+    const float e = __builtin_amdgcn_exp2f(fminf(ax * (2.0f * kLog2eF), 126.0f));
+    const float big = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+    return copysignf(ax < 0.25f ? small : big, x);
+}
 
 template <int KPT>
 __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) {
@@ -184,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
             for (int s = 0; s < SEG; ++s) {
                 const bool ok = rot && w * SEG + s < nt;
                 const float a = ok ? ang[x][s] : 0.0f, d = ok ? dts[s] : 0.0f;
-                acc += static_cast<double>(tanhf(a)) * static_cast<double>(d) * static_cast<double>(kPiF);
+                acc += static_cast<double>(TanhF(a)) * static_cast<double>(d) * static_cast<double>(kPiF);
                 pre[x][s] = acc;
             }
             const int pr = lane + 64 * x;
@@ -215,7 +230,9 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
                 for (int s = 0; s < SEG; ++s) {
                     const int tt = w * SEG + s;
                     th = carry + pre[x][s];
-                    th -= kTwoPiF * floor(th / kTwoPiF);     // wrap_two_pi (reference :26-28)
+                    // wrap_two_pi (reference :26-28); the reciprocal can move a wrap by one
+                    // period only within an ulp of a multiple, where sin/cos agree
+                    th -= kTwoPiF * floor(th * kInvTwoPiF);
                     float c = 1.0f, sn = 0.0f;
                     if (rot) {
                         const float rev = static_cast<float>(th * kRevPerRad);
