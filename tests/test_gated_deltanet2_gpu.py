@@ -58,19 +58,22 @@ def test_gdn2_parity(name):
     check(f"gated_deltanet2/{name}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
 
 
-@pytest.mark.parametrize("cl", ["1", "2"])
-def test_gdn2_column_layouts_agree(cl, monkeypatch):
-    s = S(2, 70, 2, 128, 96)
+@pytest.mark.parametrize("shape", [(8, 40, 32, 64, 32), (2, 70, 2, 128, 96), (1, 19, 2, 256, 200)])
+def test_gdn2_workgroup_shapes(shape):
+    """Workgroups of 8 waves (32 columns, 8-token blocks) on large (b,h) grids
+    and of 4 waves (16 columns, 4-token blocks) on small ones; partial column
+    blocks and token counts that end inside a block."""
+    s = S(*shape)
     inp = W.gated_deltanet2_inputs(s, seed=3)
-    monkeypatch.setenv("XM_GDN2_CL", cl)
-    check(f"gated_deltanet2/cl{cl}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
+    check("gated_deltanet2/wg_" + "_".join(map(str, shape)), run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
 
 
 def test_gdn2_torch_allocator_and_overlapping_streams():
-    """Two calls in flight on two streams with scratch from torch's caching
-    allocator: each matches its own oracle result."""
+    """Two calls in flight on two streams, one on the fused path (no scratch)
+    and one on the large-key path with scratch from torch's caching allocator
+    (1100 tokens: two preparation chunks): each matches its own oracle result."""
     import torch
-    s1, s2 = S(2, 1100, 2, 64, 32), S(1, 700, 3, 128, 40)
+    s1, s2 = S(1, 1100, 2, 300, 24), S(1, 700, 3, 128, 40)
     i1, i2 = W.gated_deltanet2_inputs(s1, seed=5), W.gated_deltanet2_inputs(s2, seed=6)
     d1 = [to_dev(i1[k]) for k in KEYS]
     d2 = [to_dev(i2[k]) for k in KEYS]

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void Gdn2PrepKernel(GatedDeltaNet2Params 
 }
 
 // ---------------------------------------------------------------------------
-// Register-state recurrence (dk <= 256)
+// Fused register-state kernel (dk <= 256): preparation + recurrence
 // ---------------------------------------------------------------------------
 // LDS layout of one staged token for KT keys per lane: each of the 4 vectors
 // occupies KPS floats.  gfx950 serves a ds_read_b128 16 lanes at a time from
@@ -128,202 +128,210 @@ struct Swz {
     __device__ static constexpr int Pos(int i) { return PAD ? i + 4 * (i / 64) : i; }
 };
 
-// Tokens per staged block: 8, or 4 when two 8-token buffers would exceed the
-// 64 KiB of statically declared LDS.
-template <int KT>
-__host__ __device__ constexpr int TokensPerBlock() {
-    return 2 * 8 * Swz<KT>::RS * 4 <= 60 * 1024 ? 8 : 4;
-}
+// NW waves per workgroup, 4*NW value columns (one per 16-lane row), blocks
+// of NW tokens (wave w prepares token w of the block).
+template <int KT, int NW>
+struct FusedLayout {
+    static constexpr int KP = Swz<KT>::KP;
+    static constexpr int RS = Swz<KT>::RS;                 // floats per staged token
+    static constexpr int TB = NW;                          // tokens per block
+    static constexpr int THREADS = 64 * NW;
+    static constexpr int COLS = 4 * NW;                    // value columns per workgroup
+    static constexpr int KPL = KP <= 64 ? 1 : KP / 64;     // keys per lane in the preparation
+    static constexpr int WVPT = (TB * COLS + THREADS - 1) / THREADS;
+    static constexpr size_t kVec = 0;                                   // float [2][TB][RS]
+    static constexpr size_t kWV = kVec + sizeof(float) * 2 * TB * RS;   // float [2][TB][COLS]
+    static constexpr size_t kQK = kWV + sizeof(float) * 2 * TB * COLS;  // float [2][TB]
+    static constexpr size_t kBytes = kQK + sizeof(float) * 2 * TB;
+    static_assert(kBytes <= 160 * 1024, "LDS budget");
+};
 
-template <int KT, int CL>
-__global__ __launch_bounds__(kThreads) void Gdn2RecurKernel(GatedDeltaNet2Params p, int t0, int tc) {
+template <int KT, int NW>
+__global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params p) {
+    using L = FusedLayout<KT, NW>;
     using S_ = Swz<KT>;
-    constexpr int KP = S_::KP;                // padded keys (== p.dk_pad)
-    constexpr int KPS = S_::KPS;
-    constexpr int RS = S_::RS;
-    constexpr int TB = TokensPerBlock<KT>();
-    constexpr int ROW = PrepRow(KP);          // floats per prepared token row
-    constexpr int COLS = 16 * CL;             // value columns per workgroup
-    constexpr int ROW4 = ROW / 4;
-    constexpr int VEC4 = TB * ROW4;           // float4 per staged block
-    constexpr int VPT = (VEC4 + kThreads - 1) / kThreads;
-    constexpr int WVPT = (TB * COLS + kThreads - 1) / kThreads;
+    constexpr int KP = L::KP, KPS = S_::KPS, RS = L::RS, TB = L::TB, COLS = L::COLS;
+    constexpr int KPL = L::KPL, THREADS = L::THREADS, WVPT = L::WVPT;
 
-    // Double-buffered staging: block i is written while the other waves may
-    // still read block i-1, so one barrier per block suffices.
-    __shared__ __attribute__((aligned(16))) float sVec[2][TB * RS];
-    __shared__ float sWV[2][TB * COLS];
-    __shared__ float sQK[2][TB];
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    float *sVec = reinterpret_cast<float *>(smem + L::kVec);
+    float *sWV = reinterpret_cast<float *>(smem + L::kWV);
+    float *sQK = reinterpret_cast<float *>(smem + L::kQK);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int kg = lane & 15, cg = lane >> 4;
-    const int nvb = (p.dv + COLS - 1) / COLS;
-    // the nvb workgroups of one (b,h) read the same token vectors: keep them on one XCD
+    const int T = p.seqlen, H = p.nheads, dk = p.dk, dv = p.dv;
+    const int nvb = (dv + COLS - 1) / COLS;
+    // the nvb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
     const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
     const int vb = wg % nvb;
     const int bh = wg / nvb;
-    const int b = bh / p.nheads, h = bh % p.nheads;
-    const int dk = p.dk, dv = p.dv;
+    const int b = bh / H, h = bh % H;
     const int v0 = vb * COLS;
+    const int col = v0 + w * 4 + cg;              // this lane's value column
 
-    // State init: initial_state for the first chunk, else the carried state.
-    float S[CL][KT];
-    const float *sinit = nullptr;
-    if (t0 > 0) sinit = p.state;
-    else if (p.initial_state) sinit = p.initial_state;
+    float S[KT];
     const size_t sbase = static_cast<size_t>(bh) * dk * dv;
 #pragma unroll
-    for (int c = 0; c < CL; ++c) {
-        const int col = v0 + (w * 4 + cg) * CL + c;
-#pragma unroll
-        for (int j = 0; j < KT; ++j) {
-            const int kd = kg * KT + j;
-            S[c][j] = (sinit && kd < dk && col < dv) ? sinit[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
-        }
+    for (int j = 0; j < KT; ++j) {
+        const int kd = kg * KT + j;
+        S[j] = (p.initial_state && kd < dk && col < dv) ? p.initial_state[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
     }
 
-    const float *prep = p.prepared + static_cast<size_t>(bh) * p.chunk_cap * ROW;
-    const float *prep_qk = p.prep_qk + static_cast<size_t>(bh) * p.chunk_cap;
-    // staged as plain floats: float4 struct copies into a private array are
-    // lowered to memcpy and keep the array out of registers
-    float vreg[VPT][4];
-    float wreg[WVPT], vvreg[WVPT];
-    float qkreg = 0.0f;
-    auto load_block = [&](int tb0) __attribute__((always_inline)) {
-        const int nt = min(TB, tc - tb0);
-        const float4 *src = reinterpret_cast<const float4 *>(prep + static_cast<size_t>(tb0) * ROW);
+    // token t of (b,h): q/k/g/beta row at kbase + t*kstride, v/w/out row at vbase + t*vstride
+    const size_t kstride = static_cast<size_t>(H) * dk, vstride = static_cast<size_t>(H) * dv;
+    const size_t kbase = (static_cast<size_t>(b) * T * H + h) * dk;
+    const size_t vbase = (static_cast<size_t>(b) * T * H + h) * dv;
+    auto key = [&](int x) __attribute__((always_inline)) { return KP <= 64 ? lane : lane * KPL + x; };
+
+    // Raw rows of the next block, loaded before the current block's recurrence
+    // and consumed after it.  Clamped addresses, no selects here: a select
+    // next to a load lets the compiler sink the load and wait on the spot.
+    float rq[KPL], rk[KPL], rgd[KPL], rbt[KPL], rw[WVPT], rv[WVPT];
+    auto load_block = [&](int t0) __attribute__((always_inline)) {
+        const size_t base = kbase + static_cast<size_t>(min(t0 + w, T - 1)) * kstride;
 #pragma unroll
-        for (int k = 0; k < VPT; ++k) {
-            const int i = min(tid + k * kThreads, nt * ROW4 - 1);   // clamped: no branch around the load
-            const float4 x = src[i];
-            vreg[k][0] = x.x; vreg[k][1] = x.y; vreg[k][2] = x.z; vreg[k][3] = x.w;
+        for (int x = 0; x < KPL; ++x) {
+            const int kc = min(key(x), dk - 1);
+            rq[x] = p.q[base + kc];
+            rk[x] = p.k[base + kc];
+            rgd[x] = p.g[base + kc];
+            rbt[x] = p.beta[base + kc];
         }
-        qkreg = prep_qk[tb0 + min(tid, nt - 1)];
-        // raw values: the validity select happens at staging time, so the
-        // compiler cannot sink these loads into a branch and wait on them here
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
-            const int i = tid + k * kThreads;
-            const int tt = min(i / COLS, nt - 1), col = min(v0 + i % COLS, dv - 1);
-            const size_t idx = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + tt) * p.nheads + h) * dv + col;
-            wreg[k] = p.w[idx];
-            vvreg[k] = p.v[idx];
+            const int i = tid + k * THREADS;
+            const int t = min(t0 + min(i / COLS, TB - 1), T - 1);
+            const size_t idx = vbase + static_cast<size_t>(t) * vstride + min(v0 + i % COLS, dv - 1);
+            rw[k] = p.w[idx];
+            rv[k] = p.v[idx];
         }
     };
-    // Tokens past the end of a short block are staged as identity tokens
-    // (khat = beta*khat*d = qhat*d = 0, d = 1, w*v = 0): they leave a finite
-    // state exactly unchanged, so every block runs the same unrolled body.
-    auto stage = [&](int buf, int nt) __attribute__((always_inline)) {
+
+    // Preparation of one block into LDS buffer `buf` (reference :39-76):
+    // qhat = q*scale*rsqrt(|q|^2+eps), khat = k*rsqrt(|k|^2+eps), d = exp(g), and
+    // the staged vectors [khat | beta*khat*d | qhat*d | d] plus qhat.khat and w*v.
+    // Tokens past the end are identity tokens (zero vectors, d = 1, w*v = 0):
+    // they leave a finite state exactly unchanged.
+    auto prep_block = [&](int t0, int buf) __attribute__((always_inline)) {
+        const int nt = min(TB, T - t0);
+        const bool live = w < nt;                 // wave-uniform
+        float q[KPL], k[KPL];
+        float qs = 0.0f, ks = 0.0f;
 #pragma unroll
-        for (int k = 0; k < VPT; ++k) {
-            const int i = tid + k * kThreads;
-            if (i < VEC4) {
-                const int tt = i / ROW4, ch = i % ROW4;     // ch: float4 chunk within the row
-                const int vec = ch / (KP / 4), c4 = ch % (KP / 4);
-                const bool live = tt < nt;
-                const float pad = vec == 3 ? 1.0f : 0.0f;
-                *reinterpret_cast<float4 *>(&sVec[buf][tt * RS + vec * KPS + S_::Pos(4 * c4)]) =
-                    make_float4(live ? vreg[k][0] : pad, live ? vreg[k][1] : pad,
-                                live ? vreg[k][2] : pad, live ? vreg[k][3] : pad);
+        for (int x = 0; x < KPL; ++x) {
+            const bool ok = live && key(x) < dk;
+            q[x] = ok ? rq[x] : 0.0f;
+            k[x] = ok ? rk[x] : 0.0f;
+            qs = fmaf(q[x], q[x], qs);
+            ks = fmaf(k[x], k[x], ks);
+        }
+        float q_mul = p.scale, k_mul = 1.0f;
+        if (p.l2norm) {
+            // reference :58-62: q_mul = scale * rsqrt(sum + eps); k_mul = rsqrt(sum + eps)
+            q_mul *= rsqrtf(WaveSum64(qs) + kL2Eps);
+            k_mul = rsqrtf(WaveSum64(ks) + kL2Eps);
+        }
+        float *vt = sVec + (buf * TB + w) * RS;
+        float qk = 0.0f;
+#pragma unroll
+        for (int x = 0; x < KPL; ++x) {
+            const int kd = key(x);
+            if (kd < KP) {
+                const bool ok = live && kd < dk;
+                const float kn = k[x] * k_mul;                         // khat
+                const float qn = q[x] * q_mul;                         // qhat
+                const float d = ok ? __expf(rgd[x]) : (live ? 0.0f : 1.0f);   // exp(g), hardware exp2 (the reference is built with fast math)
+                const float bk = ok ? rbt[x] * kn : 0.0f;              // beta * khat
+                const int pos = S_::Pos(kd);
+                vt[pos] = kn;
+                vt[KPS + pos] = bk * d;
+                vt[2 * KPS + pos] = qn * d;
+                vt[3 * KPS + pos] = d;
+                qk = fmaf(qn, kn, qk);
             }
         }
+        qk = WaveSum64(qk);
+        if (lane == 0) sQK[buf * TB + w] = qk;
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
-            const int i = tid + k * kThreads;
+            const int i = tid + k * THREADS;
             const bool ok = i / COLS < nt && v0 + i % COLS < dv;
-            if (i < TB * COLS) sWV[buf][i] = ok ? wreg[k] * vvreg[k] : 0.0f;   // w * v (reference :120)
+            if (i < TB * COLS) sWV[buf * TB * COLS + i] = ok ? rw[k] * rv[k] : 0.0f;   // w * v (reference :120)
         }
-        if (tid < TB) sQK[buf][tid] = tid < nt ? qkreg : 0.0f;
     };
 
     // lane's keys [kg*KT, kg*KT + KT) start at this LDS offset within a vector
     const int kpos = S_::Pos(kg * KT);
+    const int cl = w * 4 + cg;                    // column within the workgroup
 
-    load_block(0);
-    int buf = 0;
-    for (int tb0 = 0; tb0 < tc; tb0 += TB, buf ^= 1) {
-        const int nt = min(TB, tc - tb0);
-        stage(buf, nt);
-        __syncthreads();
-        if (tb0 + TB < tc) load_block(tb0 + TB);
-
-        // Lane kg keeps the output of token kg of the block for its columns.
-        float oreg[CL];
-#pragma unroll
-        for (int c = 0; c < CL; ++c) oreg[c] = 0.0f;
-        // Token tt+1's vectors are read from LDS while token tt computes.
-        const float *vb_ = &sVec[buf][kpos];
+    // Recurrence over one block (reference :82-140, one-phase form above).
+    auto recur_block = [&](int t0, int buf) __attribute__((always_inline)) {
+        const float *vb_ = sVec + buf * TB * RS + kpos;
+        const float *wvb = sWV + buf * TB * COLS + cl;
+        const float *qkb = sQK + buf * TB;
         float cur[4][KT], nxt[4][KT];
-        float cwv[CL], nwv[CL];
-        float cqk, nqk;
-        auto read_token = [&](int tt, float (&x)[4][KT], float (&wv)[CL], float &qk) __attribute__((always_inline)) {
-            const float *vt = vb_ + tt * RS;
+        float cwv, nwv = 0.0f, cqk, nqk = 0.0f;
 #pragma unroll
-            for (int m = 0; m < 4; ++m) LoadKeys<KT>(vt + m * KPS, x[m]);
-#pragma unroll
-            for (int c = 0; c < CL; ++c) wv[c] = sWV[buf][tt * COLS + (w * 4 + cg) * CL + c];
-            qk = sQK[buf][tt];
-        };
-        read_token(0, cur, cwv, cqk);
+        for (int m = 0; m < 4; ++m) LoadKeys<KT>(vb_ + m * KPS, cur[m]);
+        cwv = wvb[0];
+        cqk = qkb[0];
+        float oreg = 0.0f;
 #pragma unroll
         for (int tt = 0; tt < TB; ++tt) {
-            if (tt + 1 < TB) read_token(tt + 1, nxt, nwv, nqk);
+            if (tt + 1 < TB) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) LoadKeys<KT>(vb_ + (tt + 1) * RS + m * KPS, nxt[m]);
+                nwv = wvb[(tt + 1) * COLS];
+                nqk = qkb[tt + 1];
+            }
             const float (&kn)[KT] = cur[0];
             const float (&bkd)[KT] = cur[1];
             const float (&qd)[KT] = cur[2];
             const float (&dec)[KT] = cur[3];
+            // two accumulators per sum shorten the dependent chains
+            float e0 = 0.0f, e1 = 0.0f, r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
-            for (int c = 0; c < CL; ++c) {
-                // two accumulators per sum shorten the dependent chains
-                float e0 = 0.0f, e1 = 0.0f, r0 = 0.0f, r1 = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KT; j += 2) {
-                    e0 = fmaf(bkd[j], S[c][j], e0);
-                    r0 = fmaf(qd[j], S[c][j], r0);
-                    if (j + 1 < KT) {
-                        e1 = fmaf(bkd[j + 1], S[c][j + 1], e1);
-                        r1 = fmaf(qd[j + 1], S[c][j + 1], r1);
-                    }
+            for (int j = 0; j < KT; j += 2) {
+                e0 = fmaf(bkd[j], S[j], e0);
+                r0 = fmaf(qd[j], S[j], r0);
+                if (j + 1 < KT) {
+                    e1 = fmaf(bkd[j + 1], S[j + 1], e1);
+                    r1 = fmaf(qd[j + 1], S[j + 1], r1);
                 }
-                const float e = RowSum16(e0 + e1);
-                const float r = RowSum16(r0 + r1);
-                const float u = cwv[c] - e;
-                const float o = fmaf(cqk, u, r);
-#pragma unroll
-                for (int j = 0; j < KT; ++j) S[c][j] = fmaf(kn[j], u, S[c][j] * dec[j]);
-                oreg[c] = kg == tt ? o : oreg[c];
             }
+            const float e = RowSum16(e0 + e1);
+            const float r = RowSum16(r0 + r1);
+            const float u = cwv - e;
+            const float o = fmaf(cqk, u, r);
+#pragma unroll
+            for (int j = 0; j < KT; ++j) S[j] = fmaf(kn[j], u, S[j] * dec[j]);
+            oreg = kg == tt ? o : oreg;
             if (tt + 1 < TB) {
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
 #pragma unroll
                     for (int j = 0; j < KT; ++j) cur[m][j] = nxt[m][j];
-#pragma unroll
-                for (int c = 0; c < CL; ++c) cwv[c] = nwv[c];
+                cwv = nwv;
                 cqk = nqk;
             }
         }
-        if (kg < nt) {
-            const size_t obase = ((static_cast<size_t>(b) * p.seqlen + t0 + tb0 + kg) * p.nheads + h) * dv;
-#pragma unroll
-            for (int c = 0; c < CL; ++c) {
-                const int col = v0 + (w * 4 + cg) * CL + c;
-                if (col < dv) p.out[obase + col] = oreg[c];
-            }
-        }
-    }
+        // lane kg holds the output of token kg of the block
+        if (kg < min(TB, T - t0) && col < dv) p.out[vbase + static_cast<size_t>(t0 + kg) * vstride + col] = oreg;
+    };
 
-    if (t0 + tc < p.seqlen) {
-#pragma unroll
-        for (int c = 0; c < CL; ++c) {
-            const int col = v0 + (w * 4 + cg) * CL + c;
-#pragma unroll
-            for (int j = 0; j < KT; ++j) {
-                const int kd = kg * KT + j;
-                if (kd < dk && col < dv) p.state[sbase + static_cast<size_t>(kd) * dv + col] = S[c][j];
-            }
-        }
+    load_block(0);
+    prep_block(0, 0);
+    __syncthreads();
+    const int nblk = (T + TB - 1) / TB;
+    for (int j = 0; j < nblk; ++j) {
+        const int buf = j & 1;
+        const bool next = j + 1 < nblk;
+        if (next) load_block((j + 1) * TB);
+        recur_block(j * TB, buf);
+        if (next) prep_block((j + 1) * TB, buf ^ 1);
+        __syncthreads();
     }
 }
 
@@ -417,29 +425,26 @@ int KeyTile(int dk) {
     return 16;
 }
 
-int PadKeys(int dk) {
-    if (dk <= kRegKeyLimit) return 16 * KeyTile(dk);
-    return (dk + 63) / 64 * 64;
-}
+int PadKeysLds(int dk) { return (dk + 63) / 64 * 64; }
 
-int ColumnsPerLane(int batch, int nheads, int dv) {
-    const char *env = std::getenv("XM_GDN2_CL");
-    const int forced = env ? std::atoi(env) : 0;
-    if (forced == 1 || forced == 2) return forced;
-    (void)batch; (void)nheads; (void)dv;
-    return 1;   // measured faster than 2 columns per lane at 4 x 4096 x 16 x 128 x 128
-}
-
-template <int KT, int CL>
-void LaunchRecur(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
-    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.dv + 16 * CL - 1) / (16 * CL));
-    hipLaunchKernelGGL((Gdn2RecurKernel<KT, CL>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, p, t0, tc);
+template <int KT, int NW>
+void LaunchFused(const GatedDeltaNet2Params &p, hipStream_t stream) {
+    using L = FusedLayout<KT, NW>;
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.dv + L::COLS - 1) / L::COLS);
+    if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2FusedKernel<KT, NW>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
+    hipLaunchKernelGGL((Gdn2FusedKernel<KT, NW>), dim3(static_cast<unsigned>(blocks)), dim3(L::THREADS), L::kBytes,
+                       stream, p);
 }
 
 template <int KT>
-void LaunchRecurKT(const GatedDeltaNet2Params &p, int cl, int t0, int tc, hipStream_t stream) {
-    if (cl == 2) LaunchRecur<KT, 2>(p, t0, tc, stream);
-    else LaunchRecur<KT, 1>(p, t0, tc, stream);
+void LaunchFusedKT(const GatedDeltaNet2Params &p, hipStream_t stream) {
+    // 8 waves (32 columns) per workgroup when that still gives one workgroup
+    // per CU, else 4 (16 columns) for more workgroups on small problems.
+    const long long wgs8 = static_cast<long long>(p.batch) * p.nheads * ((p.dv + 31) / 32);
+    if (wgs8 >= 256) LaunchFused<KT, 8>(p, stream);
+    else LaunchFused<KT, 4>(p, stream);
 }
 
 template <int KPL>
@@ -451,9 +456,7 @@ void LaunchPrep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t strea
 
 void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
     const int kpl = (p.dk_pad + 63) / 64;
-    if (kpl <= 1) LaunchPrep<1>(p, t0, tc, stream);
-    else if (kpl <= 2) LaunchPrep<2>(p, t0, tc, stream);
-    else if (kpl <= 4) LaunchPrep<4>(p, t0, tc, stream);
+    if (kpl <= 4) LaunchPrep<4>(p, t0, tc, stream);
     else if (kpl <= 8) LaunchPrep<8>(p, t0, tc, stream);
     else if (kpl <= 16) LaunchPrep<16>(p, t0, tc, stream);
     else LaunchPrep<32>(p, t0, tc, stream);
@@ -462,11 +465,12 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
 }  // namespace
 
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
+    if (dk <= kRegKeyLimit) return 0;   // fused kernel: no scratch
     const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
     const size_t rows = static_cast<size_t>(batch) * nheads * cap;
     const size_t state = seqlen > kChunkTokens ? static_cast<size_t>(batch) * nheads * dk * dv : 0;
     // regions: prepared vectors | qhat.khat per row | carried state, each 256-byte aligned
-    return Align256(rows * PrepRow(PadKeys(dk)) * sizeof(float)) + Align256(rows * sizeof(float)) +
+    return Align256(rows * PrepRow(PadKeysLds(dk)) * sizeof(float)) + Align256(rows * sizeof(float)) +
            state * sizeof(float);
 }
 
@@ -474,7 +478,20 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v)
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.dk > kMaxLdsKeys)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");
-    p.dk_pad = PadKeys(p.dk);
+    if (p.dk <= kRegKeyLimit) {
+        switch (KeyTile(p.dk)) {
+            case 1: LaunchFusedKT<1>(p, stream); break;
+            case 2: LaunchFusedKT<2>(p, stream); break;
+            case 4: LaunchFusedKT<4>(p, stream); break;
+            case 8: LaunchFusedKT<8>(p, stream); break;
+            case 12: LaunchFusedKT<12>(p, stream); break;
+            default: LaunchFusedKT<16>(p, stream); break;
+        }
+        XM_LAUNCH_CHECK("GatedDeltaNet2Fn");
+        return;
+    }
+    // dk > 256: preparation in token chunks, state in LDS, carried through scratch
+    p.dk_pad = PadKeysLds(p.dk);
     p.chunk_cap = std::min(p.seqlen, kChunkTokens);
     const size_t rows = static_cast<size_t>(p.batch) * p.nheads * p.chunk_cap;
     char *base = static_cast<char *>(scratch);
@@ -486,31 +503,15 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v)
     const long long bh = static_cast<long long>(p.batch) * p.nheads;
     if (bh * ((p.dv + 15) / 16) > 2147483647LL || bh * kChunkTokens / 4 > 2147483647LL)
         throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-    const int cl = ColumnsPerLane(p.batch, p.nheads, p.dv);
-    const int kt = KeyTile(p.dk);
-    if (p.dk > kRegKeyLimit) {
-        const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
-        XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    }
+    const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
     for (int t0 = 0; t0 < p.seqlen; t0 += p.chunk_cap) {
         const int tc = std::min(p.chunk_cap, p.seqlen - t0);
         Prep(p, t0, tc, stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn preparation");
-        if (p.dk > kRegKeyLimit) {
-            const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
-            const long long blocks = bh * ((p.dv + 15) / 16);
-            hipLaunchKernelGGL(Gdn2RecurLdsKernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, p, t0, tc);
-        } else {
-            switch (kt) {
-                case 1: LaunchRecurKT<1>(p, cl, t0, tc, stream); break;
-                case 2: LaunchRecurKT<2>(p, cl, t0, tc, stream); break;
-                case 4: LaunchRecurKT<4>(p, cl, t0, tc, stream); break;
-                case 8: LaunchRecurKT<8>(p, cl, t0, tc, stream); break;
-                case 12: LaunchRecurKT<12>(p, cl, t0, tc, stream); break;
-                default: LaunchRecurKT<16>(p, cl, t0, tc, stream); break;
-            }
-        }
+        const long long blocks = bh * ((p.dv + 15) / 16);
+        hipLaunchKernelGGL(Gdn2RecurLdsKernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, p, t0, tc);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn recurrence");
     }
 }

@@ -43,13 +43,16 @@ __device__ __forceinline__ float RowSum16(float x) {
     return x;
 }
 
-// Sum over 64 lanes, result in every lane (a row sum, then the two cross-row
-// steps through __shfl_xor).
+// Sum over 64 lanes, result in every lane.  After the row sum every lane of
+// row r holds that row's sum; the GFX9 broadcast DPP controls then add row 0
+// into row 1 and row 2 into row 3 (row_bcast:15, rows 1 and 3 enabled), and
+// lane 31 (rows 0+1) into rows 2 and 3 (row_bcast:31), so lane 63 holds the
+// total, which readlane returns to every lane.  No LDS traffic.
 __device__ __forceinline__ float WaveSum64(float x) {
     x = RowSum16(x);
-    x += __shfl_xor(x, 16);
-    x += __shfl_xor(x, 32);
-    return x;
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
 __device__ __forceinline__ double WaveSum64d(double x) {
