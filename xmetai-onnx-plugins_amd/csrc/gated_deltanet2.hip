@@ -290,19 +290,15 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
             const float (&bkd)[KT] = cur[1];
             const float (&qd)[KT] = cur[2];
             const float (&dec)[KT] = cur[3];
-            // two accumulators per sum shorten the dependent chains
-            float e0 = 0.0f, e1 = 0.0f, r0 = 0.0f, r1 = 0.0f;
+            // e and r are two independent chains; the other wave of the SIMD covers their latency
+            float e = 0.0f, r = 0.0f;
 #pragma unroll
-            for (int j = 0; j < KT; j += 2) {
-                e0 = fmaf(bkd[j], S[j], e0);
-                r0 = fmaf(qd[j], S[j], r0);
-                if (j + 1 < KT) {
-                    e1 = fmaf(bkd[j + 1], S[j + 1], e1);
-                    r1 = fmaf(qd[j + 1], S[j + 1], r1);
-                }
+            for (int j = 0; j < KT; ++j) {
+                e = fmaf(bkd[j], S[j], e);
+                r = fmaf(qd[j], S[j], r);
             }
-            const float e = RowSum16(e0 + e1);
-            const float r = RowSum16(r0 + r1);
+            e = RowSum16(e);
+            r = RowSum16(r);
             const float u = cwv - e;
             const float o = fmaf(cqk, u, r);
 #pragma unroll
