@@ -18,23 +18,18 @@
 // the reference only in the association of their products.
 //
 // Kernels:
-//  * Gdn2PrepKernel: one wave per (b,t,h) row of a token chunk (<= 1024
-//    tokens, so scratch does not grow with seqlen).  Writes khat, beta*khat*d,
-//    qhat*d, d (each zero-padded to dk_pad) and qhat.khat, head-major so that
-//    one (b,h)'s token stream is contiguous.
-//  * Gdn2RecurKernel (dk <= 256): the state lives in VGPRs.  A wave is 4 rows
-//    of 16 lanes; the 16 lanes of a row split the keys (KT each) of CL value
-//    columns, so the reduction over keys is a 4-step DPP row sum with no
-//    barrier.  The 4 waves of a workgroup (16*CL columns of one (b,h)) share
-//    the per-token vectors, staged through LDS a block of tokens at a time
-//    with coalesced 16-byte loads prefetched one block ahead; the LDS copy
-//    inserts 4 floats every 32 keys so the key-sliced 16-byte reads of a row
-//    hit distinct banks.
-//  * Gdn2RecurLdsKernel (dk > 256): same lane layout, the state tile
-//    [dk_pad x 16 columns] lives in LDS and the per-token vectors are read
-//    from the prepared chunk in global memory.
-// The fp32 state crosses chunk boundaries through the state scratch buffer
-// (reference :101-102, :133-139).
+//  * Gdn2FusedKernel (dk <= 256): one launch for the whole sequence, no
+//    scratch.  A workgroup of NW waves owns 4*NW value columns of one (b,h);
+//    each 16-lane row owns one column and its lanes split the keys (KT each),
+//    so the reduction over keys is a 4-step DPP row sum.  The state lives in
+//    VGPRs.  Tokens run in blocks of NW: wave w prepares token w of the next
+//    block (L2 norms, exp(g), the four vectors, qhat.khat, w*v) into
+//    double-buffered LDS while the current block's recurrence runs.
+//  * Gdn2PrepKernel + Gdn2RecurLdsKernel (dk > 256): the preparation writes
+//    khat, beta*khat*d, qhat*d, d and qhat.khat for a chunk of <= 1024 tokens
+//    to scratch; the recurrence keeps the [dk_pad x 16 columns] state tile in
+//    LDS and carries the fp32 state across chunks through scratch
+//    (reference :101-102, :133-139).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
