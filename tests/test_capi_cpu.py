@@ -186,17 +186,17 @@ def gdn_shapes(B=2, T=5, H=3, K=16, V=8, s0=True):
 def test_gdn2_valid_and_scratch():
     out, scratch = validate("gated_deltanet2", gdn_shapes(), scale=0.25)
     assert out == (2, 5, 3, 8)
-    # headdim_k <= 256: one fused kernel, no scratch at any length
+    # headdim_k <= 512: one fused kernel, no scratch at any length
     assert scratch == 0
-    assert validate("gated_deltanet2", gdn_shapes(T=3000, K=256, V=64))[1] == 0
-    # headdim_k > 256: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded
+    assert validate("gated_deltanet2", gdn_shapes(T=3000, K=512, V=64))[1] == 0
+    # headdim_k > 512: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded
     # to 64) + one q.k float per row, plus the carried state when T > 1024
     a256 = lambda n: (n + 255) // 256 * 256
-    _, s_short = validate("gated_deltanet2", gdn_shapes(T=100, K=300, V=64))
-    assert s_short == a256(2 * 3 * 100 * 4 * 320 * 4) + a256(2 * 3 * 100 * 4)
-    _, s_long = validate("gated_deltanet2", gdn_shapes(T=3000, K=300, V=64))
+    _, s_short = validate("gated_deltanet2", gdn_shapes(T=100, K=600, V=64))
+    assert s_short == a256(2 * 3 * 100 * 4 * 640 * 4) + a256(2 * 3 * 100 * 4)
+    _, s_long = validate("gated_deltanet2", gdn_shapes(T=3000, K=600, V=64))
     rows = 2 * 3 * 1024
-    assert s_long == a256(rows * 4 * 320 * 4) + a256(rows * 4) + 2 * 3 * 300 * 64 * 4
+    assert s_long == a256(rows * 4 * 640 * 4) + a256(rows * 4) + 2 * 3 * 600 * 64 * 4
 
 
 @pytest.mark.parametrize("idx,shape,msg", [

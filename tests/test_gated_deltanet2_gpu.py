@@ -40,14 +40,17 @@ CASES = {
     "k128_v65_partial_wave": S(2, 64, 4, 128, 65),
     "k200_v40": S(1, 17, 2, 200, 40),
     "k256_v256": S(1, 48, 2, 256, 256),
-    "k257_lds_path": S(1, 21, 2, 257, 20),
-    "k320_v64_lds_path": S(2, 40, 2, 320, 64),
-    "k512_v7_lds_path": S(1, 12, 1, 512, 7, per_key_gates=True),
+    "k257_two_rows": S(1, 21, 2, 257, 20),
+    "k320_v64": S(2, 40, 2, 320, 64),
+    "k512_v7_perkey": S(1, 12, 1, 512, 7, per_key_gates=True),
+    "k513_lds_path": S(1, 21, 2, 513, 20),
+    "k600_v33_lds_path": S(2, 40, 2, 600, 33),
+    "k1024_lds_path_perkey": S(1, 12, 1, 1024, 7, per_key_gates=True),
     "t1023": S(1, 1023, 2, 32, 16),
     "t1024": S(1, 1024, 2, 32, 16),
     "t1025_chunk_carry": S(1, 1025, 2, 32, 16),
     "t2100_two_carries": S(2, 2100, 1, 64, 32, per_key_gates=True),
-    "t1500_lds_carry": S(1, 1500, 1, 300, 16),
+    "t1500_lds_carry": S(1, 1500, 1, 600, 16),
 }
 
 
@@ -58,14 +61,26 @@ def test_gdn2_parity(name):
     check(f"gated_deltanet2/{name}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
 
 
-@pytest.mark.parametrize("shape", [(8, 40, 32, 64, 32), (2, 70, 2, 128, 96), (1, 19, 2, 256, 200)])
+@pytest.mark.parametrize("shape", [(8, 40, 32, 64, 32), (4, 30, 16, 64, 96), (2, 20, 16, 400, 128),
+                                   (2, 70, 2, 128, 96), (1, 19, 2, 256, 200)])
 def test_gdn2_workgroup_shapes(shape):
-    """Workgroups of 8 waves (32 columns, 8-token blocks) on large (b,h) grids
-    and of 4 waves (16 columns, 4-token blocks) on small ones; partial column
-    blocks and token counts that end inside a block."""
+    """The automatic choice: 1, 2 or 4 rows of 16 lanes per value column (2
+    rows for dk = 400), 8- or 4-wave workgroups, partial column blocks and
+    token counts that end inside a block."""
     s = S(*shape)
     inp = W.gated_deltanet2_inputs(s, seed=3)
     check("gated_deltanet2/wg_" + "_".join(map(str, shape)), run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
+
+
+@pytest.mark.parametrize("rows", ["1", "2", "4"])
+@pytest.mark.parametrize("shape", [(2, 37, 3, 64, 40), (1, 45, 2, 200, 24)])
+def test_gdn2_rows_per_column_agree(rows, shape, monkeypatch):
+    """Every column layout (forced through XM_GDN2_ROWS where the keys fit)
+    matches the oracle on the same inputs."""
+    s = S(*shape)
+    inp = W.gated_deltanet2_inputs(s, seed=7)
+    monkeypatch.setenv("XM_GDN2_ROWS", rows)
+    check(f"gated_deltanet2/rows{rows}_" + "_".join(map(str, shape)), run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
 
 
 def test_gdn2_torch_allocator_and_overlapping_streams():
@@ -73,7 +88,7 @@ def test_gdn2_torch_allocator_and_overlapping_streams():
     and one on the large-key path with scratch from torch's caching allocator
     (1100 tokens: two preparation chunks): each matches its own oracle result."""
     import torch
-    s1, s2 = S(1, 1100, 2, 300, 24), S(1, 700, 3, 128, 40)
+    s1, s2 = S(1, 1100, 2, 600, 24), S(1, 700, 3, 128, 40)
     i1, i2 = W.gated_deltanet2_inputs(s1, seed=5), W.gated_deltanet2_inputs(s2, seed=6)
     d1 = [to_dev(i1[k]) for k in KEYS]
     d2 = [to_dev(i2[k]) for k in KEYS]

@@ -18,14 +18,14 @@
 // the reference only in the association of their products.
 //
 // Kernels:
-//  * Gdn2FusedKernel (dk <= 256): one launch for the whole sequence, no
-//    scratch.  A workgroup of NW waves owns 4*NW value columns of one (b,h);
-//    each 16-lane row owns one column and its lanes split the keys (KT each),
-//    so the reduction over keys is a 4-step DPP row sum.  The state lives in
-//    VGPRs.  Tokens run in blocks of NW: wave w prepares token w of the next
+//  * Gdn2FusedKernel (dk <= 512): one launch for the whole sequence, no
+//    scratch.  A workgroup of NW waves owns 4*NW/R value columns of one
+//    (b,h); a column spans R = 1, 2 or 4 rows of 16 lanes that split its keys
+//    (KT each), so the reduction over keys is a 4-step DPP row sum plus one
+//    or two lane swaps.  The state lives in VGPRs.  Tokens run in blocks of NW: wave w prepares token w of the next
 //    block (L2 norms, exp(g), the four vectors, qhat.khat, w*v) into
 //    double-buffered LDS while the current block's recurrence runs.
-//  * Gdn2PrepKernel + Gdn2RecurLdsKernel (dk > 256): the preparation writes
+//  * Gdn2PrepKernel + Gdn2RecurLdsKernel (dk > 512): the preparation writes
 //    khat, beta*khat*d, qhat*d, d and qhat.khat for a chunk of <= 1024 tokens
 //    to scratch; the recurrence keeps the [dk_pad x 16 columns] state tile in
 //    LDS and carries the fp32 state across chunks through scratch
@@ -43,7 +43,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kChunkTokens = 1024;   // reference kGatedDeltaNet2PrepareTokens (gated_deltanet2.h:11)
-constexpr int kRegKeyLimit = 256;    // reference kGatedDeltaNet2RegisterKeyLimit (gated_deltanet2.h:10)
+constexpr int kFusedKeyLimit = 512;  // register-state kernel: up to 4 rows x 16 lanes x 8 keys per column
+                                     // (the reference's register path stops at 256, gated_deltanet2.h:10)
 constexpr int kMaxLdsKeys = 2048;    // LDS-state path: dk_pad * 16 columns * 4 B <= 128 KiB
 constexpr float kL2Eps = 1.0e-6f;    // reference kL2NormEps (gated_deltanet2_fwd.cu:14)
 
@@ -105,34 +106,40 @@ __global__ __launch_bounds__(kThreads) void Gdn2PrepKernel(GatedDeltaNet2Params 
 }
 
 // ---------------------------------------------------------------------------
-// Fused register-state kernel (dk <= 256): preparation + recurrence
+// Fused register-state kernel (dk <= 512): preparation + recurrence
 // ---------------------------------------------------------------------------
-// LDS layout of one staged token for KT keys per lane: each of the 4 vectors
-// occupies KPS floats.  gfx950 serves a ds_read_b128 16 lanes at a time from
-// 64 four-byte banks, so the 16 key groups of a wave are conflict-free when
-// their 16-byte chunks land on distinct (address/16) mod 16 slots.  KT = 4
-// (contiguous) and KT = 12 (stride 3 chunks) already do; KT = 8 and 16 would
-// alias 2- and 4-way, so key i is stored at i + 4*(i/64) (16 bytes of
-// padding per 256 bytes) for them.
-template <int KT>
+// LDS layout of one staged token for KT keys per lane and R rows of 16 lanes
+// per value column: each of the 4 vectors occupies KPS floats.  gfx950 serves
+// a ds_read_b128 16 lanes (one row) at a time from 64 four-byte banks, so the
+// 16 key groups of a row are conflict-free when their 16-byte chunks land on
+// distinct (address/16) mod 16 slots.  KT = 4 (contiguous) and KT = 12
+// (stride 3 chunks) already do, as do the 8-byte reads of KT = 2 and 6; KT =
+// 8 and 16 would alias 2- and 4-way, so key i is stored at i + 4*(i/64) (16
+// bytes of padding per 256 bytes) for them.
+template <int KT, int R>
 struct Swz {
-    static constexpr int KP = 16 * KT;
+    static constexpr int KP = 16 * R * KT;
     static constexpr bool PAD = KT == 8 || KT == 16;
     static constexpr int KPS = PAD ? KP + 4 * ((KP - 1) / 64) : KP;
     static constexpr int RS = 4 * KPS;
     __device__ static constexpr int Pos(int i) { return PAD ? i + 4 * (i / 64) : i; }
 };
 
-// NW waves per workgroup, 4*NW value columns (one per 16-lane row), blocks
-// of NW tokens (wave w prepares token w of the block).
-template <int KT, int NW>
+// NW waves per workgroup; a value column spans R rows of 16 lanes (R = 1,
+// 2 or 4, all in one wave), so a workgroup has 4*NW/R columns.  Blocks of
+// TB = NW * TPW tokens: wave w prepares tokens w*TPW .. w*TPW + TPW - 1.  The
+// 4-wave workgroups (small problems) take two tokens per wave where the
+// double-buffered staging fits in LDS: measured 4% faster there (longer blocks
+// hide the next block's HBM prefetch), 1% slower with 8 waves.
+template <int KT, int NW, int R>
 struct FusedLayout {
-    static constexpr int KP = Swz<KT>::KP;
-    static constexpr int RS = Swz<KT>::RS;                 // floats per staged token
-    static constexpr int TB = NW;                          // tokens per block
+    static constexpr int KP = Swz<KT, R>::KP;
+    static constexpr int RS = Swz<KT, R>::RS;              // floats per staged token
+    static constexpr int TPW = NW == 4 && 2 * 2 * NW * RS * sizeof(float) <= 150 * 1024 ? 2 : 1;
+    static constexpr int TB = NW * TPW;                    // tokens per block (<= 16)
     static constexpr int THREADS = 64 * NW;
-    static constexpr int COLS = 4 * NW;                    // value columns per workgroup
-    static constexpr int KPL = KP <= 64 ? 1 : KP / 64;     // keys per lane in the preparation
+    static constexpr int COLS = 4 * NW / R;                // value columns per workgroup
+    static constexpr int KPL = (KP + 63) / 64;             // keys per lane in the preparation
     static constexpr int WVPT = (TB * COLS + THREADS - 1) / THREADS;
     static constexpr size_t kVec = 0;                                   // float [2][TB][RS]
     static constexpr size_t kWV = kVec + sizeof(float) * 2 * TB * RS;   // float [2][TB][COLS]
@@ -141,12 +148,30 @@ struct FusedLayout {
     static_assert(kBytes <= 160 * 1024, "LDS budget");
 };
 
-template <int KT, int NW>
+// Sum over the R*16 lanes of one value column (rows 2c.. or all 4 rows), in
+// every lane of the column: the row sum, then the gfx950 lane swaps
+// (permlane16_swap pairs rows 0-1 and 2-3, permlane32_swap the two halves).
+template <int R>
+__device__ __forceinline__ float ColumnSum(float x) {
+    x = RowSum16(x);
+    if constexpr (R >= 2) {
+        const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    }
+    if constexpr (R == 4) {
+        const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    }
+    return x;
+}
+
+template <int KT, int NW, int R>
 __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params p) {
-    using L = FusedLayout<KT, NW>;
-    using S_ = Swz<KT>;
+    using L = FusedLayout<KT, NW, R>;
+    using S_ = Swz<KT, R>;
     constexpr int KP = L::KP, KPS = S_::KPS, RS = L::RS, TB = L::TB, COLS = L::COLS;
-    constexpr int KPL = L::KPL, THREADS = L::THREADS, WVPT = L::WVPT;
+    constexpr int KPL = L::KPL, THREADS = L::THREADS, WVPT = L::WVPT, TPW = L::TPW;
+    static_assert(TB <= 16, "lane kg keeps the output of token kg of a block");
 
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     float *sVec = reinterpret_cast<float *>(smem + L::kVec);
@@ -155,7 +180,11 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
-    const int kg = lane & 15, cg = lane >> 4;
+    const int kg = lane & 15;
+    const int grow = w * 4 + (lane >> 4);         // 16-lane row within the workgroup
+    const int cl = grow / R;                      // column within the workgroup
+    const int rho = grow % R;                     // row within the column
+    const int kb = (rho * 16 + kg) * KT;          // first of this lane's KT keys
     const int T = p.seqlen, H = p.nheads, dk = p.dk, dv = p.dv;
     const int nvb = (dv + COLS - 1) / COLS;
     // the nvb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
@@ -164,13 +193,13 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
     const int bh = wg / nvb;
     const int b = bh / H, h = bh % H;
     const int v0 = vb * COLS;
-    const int col = v0 + w * 4 + cg;              // this lane's value column
+    const int col = v0 + cl;                      // this lane's value column
 
     float S[KT];
     const size_t sbase = static_cast<size_t>(bh) * dk * dv;
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-        const int kd = kg * KT + j;
+        const int kd = kb + j;
         S[j] = (p.initial_state && kd < dk && col < dv) ? p.initial_state[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
     }
 
@@ -178,21 +207,24 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
     const size_t kstride = static_cast<size_t>(H) * dk, vstride = static_cast<size_t>(H) * dv;
     const size_t kbase = (static_cast<size_t>(b) * T * H + h) * dk;
     const size_t vbase = (static_cast<size_t>(b) * T * H + h) * dv;
-    auto key = [&](int x) __attribute__((always_inline)) { return KP <= 64 ? lane : lane * KPL + x; };
+    auto key = [&](int x) __attribute__((always_inline)) { return lane * KPL + x; };
 
     // Raw rows of the next block, loaded before the current block's recurrence
     // and consumed after it.  Clamped addresses, no selects here: a select
     // next to a load lets the compiler sink the load and wait on the spot.
-    float rq[KPL], rk[KPL], rgd[KPL], rbt[KPL], rw[WVPT], rv[WVPT];
+    float rq[TPW][KPL], rk[TPW][KPL], rgd[TPW][KPL], rbt[TPW][KPL], rw[WVPT], rv[WVPT];
     auto load_block = [&](int t0) __attribute__((always_inline)) {
-        const size_t base = kbase + static_cast<size_t>(min(t0 + w, T - 1)) * kstride;
 #pragma unroll
-        for (int x = 0; x < KPL; ++x) {
-            const int kc = min(key(x), dk - 1);
-            rq[x] = p.q[base + kc];
-            rk[x] = p.k[base + kc];
-            rgd[x] = p.g[base + kc];
-            rbt[x] = p.beta[base + kc];
+        for (int i = 0; i < TPW; ++i) {
+            const size_t base = kbase + static_cast<size_t>(min(t0 + w * TPW + i, T - 1)) * kstride;
+#pragma unroll
+            for (int x = 0; x < KPL; ++x) {
+                const int kc = min(key(x), dk - 1);
+                rq[i][x] = p.q[base + kc];
+                rk[i][x] = p.k[base + kc];
+                rgd[i][x] = p.g[base + kc];
+                rbt[i][x] = p.beta[base + kc];
+            }
         }
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
@@ -211,44 +243,49 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
     // they leave a finite state exactly unchanged.
     auto prep_block = [&](int t0, int buf) __attribute__((always_inline)) {
         const int nt = min(TB, T - t0);
-        const bool live = w < nt;                 // wave-uniform
-        float q[KPL], k[KPL];
-        float qs = 0.0f, ks = 0.0f;
 #pragma unroll
-        for (int x = 0; x < KPL; ++x) {
-            const bool ok = live && key(x) < dk;
-            q[x] = ok ? rq[x] : 0.0f;
-            k[x] = ok ? rk[x] : 0.0f;
-            qs = fmaf(q[x], q[x], qs);
-            ks = fmaf(k[x], k[x], ks);
-        }
-        float q_mul = p.scale, k_mul = 1.0f;
-        if (p.l2norm) {
-            // reference :58-62: q_mul = scale * rsqrt(sum + eps); k_mul = rsqrt(sum + eps)
-            q_mul *= rsqrtf(WaveSum64(qs) + kL2Eps);
-            k_mul = rsqrtf(WaveSum64(ks) + kL2Eps);
-        }
-        float *vt = sVec + (buf * TB + w) * RS;
-        float qk = 0.0f;
+        for (int i = 0; i < TPW; ++i) {
+            const int tt = w * TPW + i;
+            const bool live = tt < nt;                // wave-uniform
+            float q[KPL], k[KPL];
+            float qs = 0.0f, ks = 0.0f;
 #pragma unroll
-        for (int x = 0; x < KPL; ++x) {
-            const int kd = key(x);
-            if (kd < KP) {
-                const bool ok = live && kd < dk;
-                const float kn = k[x] * k_mul;                         // khat
-                const float qn = q[x] * q_mul;                         // qhat
-                const float d = ok ? __expf(rgd[x]) : (live ? 0.0f : 1.0f);   // exp(g), hardware exp2 (the reference is built with fast math)
-                const float bk = ok ? rbt[x] * kn : 0.0f;              // beta * khat
-                const int pos = S_::Pos(kd);
-                vt[pos] = kn;
-                vt[KPS + pos] = bk * d;
-                vt[2 * KPS + pos] = qn * d;
-                vt[3 * KPS + pos] = d;
-                qk = fmaf(qn, kn, qk);
+            for (int x = 0; x < KPL; ++x) {
+                const bool ok = live && key(x) < dk;
+                q[x] = ok ? rq[i][x] : 0.0f;
+                k[x] = ok ? rk[i][x] : 0.0f;
+                qs = fmaf(q[x], q[x], qs);
+                ks = fmaf(k[x], k[x], ks);
             }
+            float q_mul = p.scale, k_mul = 1.0f;
+            if (p.l2norm) {
+                // reference :58-62: q_mul = scale * rsqrt(sum + eps); k_mul = rsqrt(sum + eps)
+                q_mul *= rsqrtf(WaveSum64(qs) + kL2Eps);
+                k_mul = rsqrtf(WaveSum64(ks) + kL2Eps);
+            }
+            float *vt = sVec + (buf * TB + tt) * RS;
+            float qk = 0.0f;
+#pragma unroll
+            for (int x = 0; x < KPL; ++x) {
+                const int kd = key(x);
+                if (kd < KP) {
+                    const bool ok = live && kd < dk;
+                    const float kn = k[x] * k_mul;                         // khat
+                    const float qn = q[x] * q_mul;                         // qhat
+                    // exp(g), hardware exp2 (the reference is built with fast math)
+                    const float d = ok ? __expf(rgd[i][x]) : (live ? 0.0f : 1.0f);
+                    const float bk = ok ? rbt[i][x] * kn : 0.0f;           // beta * khat
+                    const int pos = S_::Pos(kd);
+                    vt[pos] = kn;
+                    vt[KPS + pos] = bk * d;
+                    vt[2 * KPS + pos] = qn * d;
+                    vt[3 * KPS + pos] = d;
+                    qk = fmaf(qn, kn, qk);
+                }
+            }
+            qk = WaveSum64(qk);
+            if (lane == 0) sQK[buf * TB + tt] = qk;
         }
-        qk = WaveSum64(qk);
-        if (lane == 0) sQK[buf * TB + w] = qk;
 #pragma unroll
         for (int k = 0; k < WVPT; ++k) {
             const int i = tid + k * THREADS;
@@ -257,9 +294,8 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
         }
     };
 
-    // lane's keys [kg*KT, kg*KT + KT) start at this LDS offset within a vector
-    const int kpos = S_::Pos(kg * KT);
-    const int cl = w * 4 + cg;                    // column within the workgroup
+    // lane's keys [kb, kb + KT) start at this LDS offset within a vector
+    const int kpos = S_::Pos(kb);
 
     // Recurrence over one block (reference :82-140, one-phase form above).
     auto recur_block = [&](int t0, int buf) __attribute__((always_inline)) {
@@ -292,8 +328,8 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
                 e = fmaf(bkd[j], S[j], e);
                 r = fmaf(qd[j], S[j], r);
             }
-            e = RowSum16(e);
-            r = RowSum16(r);
+            e = ColumnSum<R>(e);
+            r = ColumnSum<R>(r);
             const float u = cwv - e;
             const float o = fmaf(cqk, u, r);
 #pragma unroll
@@ -308,8 +344,8 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
                 cqk = nqk;
             }
         }
-        // lane kg holds the output of token kg of the block
-        if (kg < min(TB, T - t0) && col < dv) p.out[vbase + static_cast<size_t>(t0 + kg) * vstride + col] = oreg;
+        // lane kg of the column's first row holds the output of token kg of the block
+        if (rho == 0 && kg < min(TB, T - t0) && col < dv) p.out[vbase + static_cast<size_t>(t0 + kg) * vstride + col] = oreg;
     };
 
     load_block(0);
@@ -327,7 +363,7 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
 }
 
 // ---------------------------------------------------------------------------
-// LDS-state recurrence (dk > 256)
+// LDS-state recurrence (dk > 512)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Params p, int t0, int tc) {
     // State tile: key kd = kg*kt + j of column cl lives at (j*16 + cl)*16 + kg, so
@@ -405,37 +441,78 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
 // ---------------------------------------------------------------------------
 size_t Align256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
-int KeyTile(int dk) {
-    // keys per lane for the 16-lane rows of the register kernel
-    const int kt = (dk + 15) / 16;
-    if (kt <= 1) return 1;
-    if (kt <= 2) return 2;
-    if (kt <= 4) return 4;
-    if (kt <= 8) return 8;
-    if (kt <= 12) return 12;
-    return 16;
+// Keys per lane for a column of R rows of 16 lanes.
+int KeyTile(int dk, int r) {
+    const int kt = (dk + 16 * r - 1) / (16 * r);
+    for (int c : {1, 2, 4, 6, 8, 12, 16})
+        if (kt <= c) return c;
+    return 0;
 }
 
 int PadKeysLds(int dk) { return (dk + 63) / 64 * 64; }
 
-template <int KT, int NW>
+struct FusedConfig {
+    int kt, r, nw;
+};
+
+// Rows per column (1, 2 or 4): more rows mean fewer keys per lane and more
+// waves, at the price of one or two more reduction steps per sum.  Measured:
+// one row wins from one wave per SIMD (1024 waves) up, two rows only from two
+// waves per SIMD (2048), else four (at most 8 keys per lane).  8-wave
+// workgroups when they still give one workgroup per CU, else 4-wave ones.
+// XM_GDN2_ROWS (1, 2 or 4) forces the rows per column where the keys fit, for
+// tuning and tests.
+FusedConfig ChooseFused(const GatedDeltaNet2Params &p) {
+    const long long cols = static_cast<long long>(p.batch) * p.nheads * p.dv;
+    const char *env = std::getenv("XM_GDN2_ROWS");
+    const int forced = env ? std::atoi(env) : 0;
+    FusedConfig best{0, 0, 8};
+    for (int r : {1, 2, 4}) {
+        const int kt = KeyTile(p.dk, r);
+        if (kt == 0 || (r == 4 && kt > 8)) continue;
+        best.kt = kt;
+        best.r = r;
+        if (r == forced) break;
+        if (forced == 0 && cols * r / 4 >= (r == 1 ? 1024 : 2048)) break;
+    }
+    const long long wgs8 = static_cast<long long>(p.batch) * p.nheads * ((p.dv + 32 / best.r - 1) / (32 / best.r));
+    best.nw = wgs8 >= 256 ? 8 : 4;
+    return best;
+}
+
+template <int KT, int NW, int R>
 void LaunchFused(const GatedDeltaNet2Params &p, hipStream_t stream) {
-    using L = FusedLayout<KT, NW>;
+    using L = FusedLayout<KT, NW, R>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.dv + L::COLS - 1) / L::COLS);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2FusedKernel<KT, NW>),
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2FusedKernel<KT, NW, R>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
-    hipLaunchKernelGGL((Gdn2FusedKernel<KT, NW>), dim3(static_cast<unsigned>(blocks)), dim3(L::THREADS), L::kBytes,
+    hipLaunchKernelGGL((Gdn2FusedKernel<KT, NW, R>), dim3(static_cast<unsigned>(blocks)), dim3(L::THREADS), L::kBytes,
                        stream, p);
 }
 
-template <int KT>
-void LaunchFusedKT(const GatedDeltaNet2Params &p, hipStream_t stream) {
-    // 8 waves (32 columns) per workgroup when that still gives one workgroup
-    // per CU, else 4 (16 columns) for more workgroups on small problems.
-    const long long wgs8 = static_cast<long long>(p.batch) * p.nheads * ((p.dv + 31) / 32);
-    if (wgs8 >= 256) LaunchFused<KT, 8>(p, stream);
-    else LaunchFused<KT, 4>(p, stream);
+template <int NW, int R>
+void LaunchFusedNR(const GatedDeltaNet2Params &p, int kt, hipStream_t stream) {
+    switch (kt) {
+        case 1: LaunchFused<1, NW, R>(p, stream); break;
+        case 2: LaunchFused<2, NW, R>(p, stream); break;
+        case 4: LaunchFused<4, NW, R>(p, stream); break;
+        case 6: LaunchFused<6, NW, R>(p, stream); break;
+        case 8: LaunchFused<8, NW, R>(p, stream); break;
+        default:
+            if constexpr (R < 4) {
+                if (kt == 12) LaunchFused<12, NW, R>(p, stream);
+                else LaunchFused<16, NW, R>(p, stream);
+            }
+            break;
+    }
+}
+
+template <int NW>
+void LaunchFusedN(const GatedDeltaNet2Params &p, const FusedConfig &c, hipStream_t stream) {
+    if (c.r == 1) LaunchFusedNR<NW, 1>(p, c.kt, stream);
+    else if (c.r == 2) LaunchFusedNR<NW, 2>(p, c.kt, stream);
+    else LaunchFusedNR<NW, 4>(p, c.kt, stream);
 }
 
 template <int KPL>
@@ -456,7 +533,7 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
 }  // namespace
 
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
-    if (dk <= kRegKeyLimit) return 0;   // fused kernel: no scratch
+    if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch
     const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
     const size_t rows = static_cast<size_t>(batch) * nheads * cap;
     const size_t state = seqlen > kChunkTokens ? static_cast<size_t>(batch) * nheads * dk * dv : 0;
@@ -469,19 +546,14 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v)
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.dk > kMaxLdsKeys)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");
-    if (p.dk <= kRegKeyLimit) {
-        switch (KeyTile(p.dk)) {
-            case 1: LaunchFusedKT<1>(p, stream); break;
-            case 2: LaunchFusedKT<2>(p, stream); break;
-            case 4: LaunchFusedKT<4>(p, stream); break;
-            case 8: LaunchFusedKT<8>(p, stream); break;
-            case 12: LaunchFusedKT<12>(p, stream); break;
-            default: LaunchFusedKT<16>(p, stream); break;
-        }
+    if (p.dk <= kFusedKeyLimit) {
+        const FusedConfig c = ChooseFused(p);
+        if (c.nw == 8) LaunchFusedN<8>(p, c, stream);
+        else LaunchFusedN<4>(p, c, stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn");
         return;
     }
-    // dk > 256: preparation in token chunks, state in LDS, carried through scratch
+    // dk > 512: preparation in token chunks, state in LDS, carried through scratch
     p.dk_pad = PadKeysLds(p.dk);
     p.chunk_cap = std::min(p.seqlen, kChunkTokens);
     const size_t rows = static_cast<size_t>(p.batch) * p.nheads * p.chunk_cap;
