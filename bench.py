@@ -236,6 +236,38 @@ def cpu_baseline(op, inputs, budget_s):
 
 # ---------------------------------------------------------------------------
 
+def time_extra_configs(dev, steps):
+    """The reference's other configurations (CPU-sized selective scan, GDN-2
+    dispatch boundaries): device time only, same inputs and timing as above."""
+    import torch
+    from xmetai_onnx_plugins import workloads as W
+    import xmetai_onnx_plugins as xp
+    out = {}
+    for name in ("selective_scan_b1_d256_l512_n16", "gated_deltanet2_b1_t16384_h8_k256_v256",
+                 "gated_deltanet2_b2_t2048_h4_k320_v64", "gated_deltanet2_b4_t4096_h16_k128_v65"):
+        s = W.NAMED[name]
+        if name.startswith("selective_scan"):
+            keys = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+            inp = W.selective_scan_inputs(s, seed=0)
+            call = lambda d, s=s, keys=keys: xp.selective_scan_fn(*(d[k] for k in keys), delta_softplus=s.delta_softplus)
+            nbytes = W.selective_scan_bytes(s)
+        else:
+            keys = ("q", "k", "v", "g", "beta", "w", "initial_state")
+            inp = W.gated_deltanet2_inputs(s, seed=0)
+            call = lambda d, s=s, keys=keys: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale)
+            nbytes = W.gated_deltanet2_bytes(s)
+        d = to_device(inp, dev)
+        _, per = time_op(dict(call=call), d, steps, 2)
+        ms = statistics.median(per)
+        tokens = s.batch * s.seqlen
+        out[name] = dict(ms_per_call_median=round(ms, 4), tokens_per_s=tokens / (ms / 1e3),
+                         achieved_GBps=round(nbytes / (ms / 1e3) / 1e9, 1), algorithmic_bytes=nbytes)
+        log(f"{name}: {ms:.3f} ms/call")
+        del d, inp
+        torch.cuda.empty_cache()
+    return out
+
+
 def traffic_from_profiles(workload):
     path = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
     if not os.path.exists(path):
@@ -252,6 +284,8 @@ def main():
     ap.add_argument("--ops", default="selective_scan,gated_deltanet2,mamba3_siso")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline budget per op (seconds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip timing the other reference configurations (reported under 'configs')")
     ap.add_argument("--mode", default="bench",
                     help="bench | copy | profile-selective_scan | profile-gated_deltanet2 | profile-mamba3_siso")
     args = ap.parse_args()
@@ -322,6 +356,8 @@ def main():
         del d, host
         torch.cuda.empty_cache()
 
+    extra = {} if args.no_extra_configs else time_extra_configs(dev, min(args.steps, 10))
+
     log("achievable HBM: 2 GiB device copy")
     ach = achievable_hbm(dev)
     for r in results.values():
@@ -362,6 +398,7 @@ def main():
         "cpu_baseline": ss.get("cpu_baseline"),
         "achievable_hbm_GBps": round(ach, 1),
         "ops": results,
+        "configs": extra,
     }
     print(json.dumps(line), flush=True)
 

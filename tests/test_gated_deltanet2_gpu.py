@@ -31,6 +31,9 @@ def run_ref(inp, s):
 S = W.GatedDeltaNet2Shape
 CASES = {
     "k1_v1": S(1, 9, 2, 1, 1),
+    "t1_single_token": S(2, 1, 3, 64, 32),
+    "t3_shorter_than_block": S(1, 3, 2, 128, 40, per_key_gates=True),
+    "t9_big_grid_one_block_plus_one": S(8, 9, 16, 64, 64),
     "k16_v16": S(2, 33, 3, 16, 16),
     "k17_v15_partial": S(2, 20, 2, 17, 15),
     "k32_v33_nos0": S(1, 40, 2, 32, 33, initial_state=False),
