@@ -29,7 +29,7 @@
  *    the null stream).  Scratch comes from `alloc` in stream order; when
  *    `alloc` is NULL the library uses its own stream-ordered pool
  *    (hipMallocFromPoolAsync / hipFreeAsync on `stream`).
- *  - No host-visible side effects besides the output tensor.
+ *  - No host-visible side effects besides the output tensors.
  */
 #ifndef XMETAI_RECURRENT_H_
 #define XMETAI_RECURRENT_H_
@@ -77,7 +77,9 @@ typedef struct xm_allocator {
  * (reference: selective_scan_fwd_kernel.cuh:272-281; z only feeds a discarded
  * buffer there, :283-301, so y never depends on z).
  * Attributes (reference: selective_scan_fn_ort.cpp:50-56): delta_softplus
- * (int, default 0), return_last_state (int, default 0; non-zero rejected).  */
+ * (int, default 0), return_last_state (int, default 0; the reference rejects
+ * non-zero, here it selects the last-state output of
+ * xm_selective_scan_forward_states).  */
 typedef struct xm_selective_scan_attrs {
     int64_t delta_softplus;
     int64_t return_last_state;
@@ -92,10 +94,21 @@ int xm_selective_scan_check_attrs(const xm_selective_scan_attrs_t *attrs, char *
 int xm_selective_scan_validate(const xm_tensor_t *inputs, size_t n_inputs,
                                const xm_selective_scan_attrs_t *attrs, int64_t *out_shape,
                                int32_t *out_rank, size_t *scratch_bytes, char *errbuf, size_t errlen);
-/* Validate and enqueue.  `out` is a device buffer of prod(out_shape) floats. */
+/* Validate and enqueue.  `out` is a device buffer of prod(out_shape) floats.
+ * With return_last_state != 0 this entry point fails (use the one below). */
 int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs,
                               const xm_selective_scan_attrs_t *attrs, float *out, void *stream,
                               const xm_allocator_t *alloc, char *errbuf, size_t errlen);
+/* As above; with return_last_state != 0 it also writes the scan state after
+ * the last token to `last_state`, a device buffer [B, D, N] (zeros when L = 0).
+ * The reference rejects return_last_state != 0 (selective_scan_fn_ort.cpp:52-55);
+ * this is a widening with no counterpart there: the state is the `last_state`
+ * of the Mamba selective_scan_fn interface.  `last_state` is ignored (may be
+ * NULL) when return_last_state == 0. */
+int xm_selective_scan_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
+                                     const xm_selective_scan_attrs_t *attrs, float *out, float *last_state,
+                                     void *stream, const xm_allocator_t *alloc, char *errbuf,
+                                     size_t errlen);
 
 /* ---- Mamba3SisoFn ---------------------------------------------------------
  * Inputs: 0 Q [B,T,Hq,N]; 1 K [B,T,Hq,N]; 2 V [B,T,H,P]; 3 ADT [B,H,T];
@@ -130,9 +143,10 @@ int xm_mamba3_siso_forward(const xm_tensor_t *inputs, size_t n_inputs,
  * 6 initial_state [B,H,K,V] or empty.  Output 0: [B,T,H,V]
  * (reference: gated_deltanet2_fn_ort.cpp:66-142, :187-219).
  * Attributes (reference: :46-64): scale (float, default 1.0, positive and
- * finite), use_qk_l2norm_in_kernel (default 1), output_final_state,
- * use_gate_in_kernel, has_cu_seqlens, state_v_first (default 0; non-zero
- * rejected).  */
+ * finite), use_qk_l2norm_in_kernel (default 1), output_final_state (default
+ * 0; the reference rejects non-zero, here it selects the final-state output
+ * of xm_gated_deltanet2_forward_states), use_gate_in_kernel, has_cu_seqlens,
+ * state_v_first (default 0; non-zero rejected).  */
 typedef struct xm_gated_deltanet2_attrs {
     float scale;
     int64_t use_qk_l2norm_in_kernel;
@@ -151,6 +165,16 @@ int xm_gated_deltanet2_validate(const xm_tensor_t *inputs, size_t n_inputs,
 int xm_gated_deltanet2_forward(const xm_tensor_t *inputs, size_t n_inputs,
                                const xm_gated_deltanet2_attrs_t *attrs, float *out, void *stream,
                                const xm_allocator_t *alloc, char *errbuf, size_t errlen);
+/* As above; with output_final_state != 0 it also writes the state after the
+ * last token to `final_state`, a device buffer [B, H, K, V] (initial_state's
+ * layout, so a later call can continue from it).  A widening with no
+ * counterpart in the reference, which rejects output_final_state != 0
+ * (gated_deltanet2_fn_ort.cpp:49-51).  `final_state` is ignored (may be NULL)
+ * when output_final_state == 0. */
+int xm_gated_deltanet2_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
+                                      const xm_gated_deltanet2_attrs_t *attrs, float *out,
+                                      float *final_state, void *stream, const xm_allocator_t *alloc,
+                                      char *errbuf, size_t errlen);
 
 /* ---- SoftmaxCPU (CPU execution provider) ------------------------------------
  * Softmax of a HOST fp32 tensor of any rank along `axis` (ONNX attribute

@@ -63,12 +63,13 @@ def _sfx(dtype):
 
 
 def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
-                   delta_softplus=False, dtype=np.float64):
-    """See xmo_selective_scan in xm_oracle.c.  ``z`` is ignored (dead input)."""
+                   delta_softplus=False, dtype=np.float64, return_state=False):
+    """See xmo_selective_scan in xm_oracle.c.  ``z`` is ignored (dead input).
+    With ``return_state`` returns ``(y, last_state)``, last_state [B,D,N]."""
     u_, up = _fp(u); d_, dp = _fp(delta); A_, Ap = _fp(A)
     B_ = np.asarray(B, np.float32); C_ = np.asarray(C, np.float32)
-    batch, dim, seqlen = u_.shape
-    dstate = A_.shape[1]
+    batch, dim, seqlen = np.shape(u)
+    dstate = np.shape(A)[1]
     if B_.ndim == 3:
         B_ = B_[:, None]
     if C_.ndim == 3:
@@ -79,25 +80,28 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
     B_, Bp = _fp(B_); C_, Cp = _fp(C_)
     D_, Dp = _fp(D); bi_, bp = _fp(delta_bias)
     out, op = _out((batch, dim, seqlen), dtype)
+    st, sp = _out((batch, dim, dstate), dtype) if return_state else (None, None)
     getattr(lib(), "xmo_selective_scan" + _sfx(dtype))(
         up, dp, Ap, Bp, Cp, Dp, bp, batch, dim, seqlen, dstate, b_var, c_var, gb, gc,
-        int(bool(delta_softplus)), op)
-    return out
+        int(bool(delta_softplus)), op, sp)
+    return (out, st) if return_state else out
 
 
 def gated_deltanet2(q, k, v, g, beta, w, initial_state=None, scale=1.0,
-                    use_qk_l2norm=True, dtype=np.float64):
-    """See xmo_gated_deltanet2 in xm_oracle.c."""
+                    use_qk_l2norm=True, dtype=np.float64, return_state=False):
+    """See xmo_gated_deltanet2 in xm_oracle.c.  With ``return_state`` returns
+    ``(o, final_state)``, final_state [B,H,K,V]."""
     q_, qp = _fp(q); k_, kp = _fp(k); v_, vp = _fp(v)
     g_, gp = _fp(g); b_, bp = _fp(beta); w_, wp = _fp(w)
     s_, sp = _fp(initial_state)
     batch, seqlen, nheads, dk = q_.shape
     dv = v_.shape[3]
     out, op = _out((batch, seqlen, nheads, dv), dtype)
+    st, stp = _out((batch, nheads, dk, dv), dtype) if return_state else (None, None)
     getattr(lib(), "xmo_gated_deltanet2" + _sfx(dtype))(
         qp, kp, vp, gp, bp, wp, sp, batch, seqlen, nheads, dk, dv,
-        ctypes.c_float(float(scale)), int(bool(use_qk_l2norm)), op)
-    return out
+        ctypes.c_float(float(scale)), int(bool(use_qk_l2norm)), op, stp)
+    return (out, st) if return_state else out
 
 
 def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,

@@ -40,7 +40,7 @@ def _present(x) -> bool:
 # ---------------------------------------------------------------------------
 
 def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
-                   delta_softplus=False, dtype=np.float64):
+                   delta_softplus=False, dtype=np.float64, return_state=False):
     """Output 0 of SelectiveScanFn.
 
     Follows selective_scan_fwd_kernel.cuh:114-127 (D, delta_bias), :150-163
@@ -52,7 +52,9 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
     (selective_scan_fwd_kernel.cuh:280 vs :296-299).
 
     Shapes: u, delta [Bt,D,L]; A [D,N]; B, C [D,N] or [Bt,N,L] or [Bt,G,N,L];
-    D, delta_bias [D] or absent.  Returns y [Bt,D,L] in ``dtype``.
+    D, delta_bias [D] or absent.  Returns y [Bt,D,L] in ``dtype``; with
+    ``return_state`` returns ``(y, h)``, h [Bt,D,N] the scan state after the
+    last token (the Mamba selective_scan_fn's last_state; zeros when L = 0).
     """
     u = _as(u, dtype); delta = _as(delta, dtype)
     A = _as(A, dtype); B = _as(B, dtype); C = _as(C, dtype)
@@ -110,7 +112,7 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         for n in range(dstate):
             acc = acc + h[:, :, n] * cval[..., n]
         out[:, :, t] = acc
-    return out
+    return (out, h) if return_state else out
 
 
 # ---------------------------------------------------------------------------
@@ -141,14 +143,16 @@ def gdn2_prepare(q, k, g, beta, scale, use_qk_l2norm, dtype=np.float64):
 
 
 def gated_deltanet2(q, k, v, g, beta, w, initial_state=None, scale=1.0,
-                    use_qk_l2norm=True, dtype=np.float64):
+                    use_qk_l2norm=True, dtype=np.float64, return_state=False):
     """Output of GatedDeltaNet2Fn.
 
     Recurrence of gated_deltanet2_fwd.cu:82-140 (register path) and :142-233
     (generic path), identical math: per token, S[i,:] *= exp(g_i); erase_j =
     sum_i beta_i khat_i S[i,j]; write_j = w_j v_j - erase_j; S[i,j] += khat_i
     write_j; o_j = sum_i qhat_i S[i,j].  Shapes: q, k, g, beta [B,T,H,K];
-    v, w [B,T,H,V]; initial_state [B,H,K,V] or absent.  Returns [B,T,H,V].
+    v, w [B,T,H,V]; initial_state [B,H,K,V] or absent.  Returns [B,T,H,V];
+    with ``return_state`` returns ``(o, S)``, S [B,H,K,V] the state after the
+    last token.
     """
     qn, kn, dec, bk = gdn2_prepare(q, k, g, beta, scale, use_qk_l2norm, dtype)
     v = _as(v, dtype); w = _as(w, dtype)
@@ -165,7 +169,7 @@ def gated_deltanet2(q, k, v, g, beta, w, initial_state=None, scale=1.0,
         write = w[:, t] * v[:, t] - erase
         S += kn[:, t, :, :, None] * write[:, :, None, :]
         out[:, t] = np.einsum("bhk,bhkv->bhv", qn[:, t], S)
-    return out
+    return (out, S) if return_state else out
 
 
 # ---------------------------------------------------------------------------

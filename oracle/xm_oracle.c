@@ -57,6 +57,9 @@ static real r_cos(real x) { return IS_F32 ? (real)cosf((float)x) : (real)cos((do
  *   B: b_var ? [batch, groups_b, dstate, seqlen] : [dim, dstate]
  *   C: c_var ? [batch, groups_c, dstate, seqlen] : [dim, dstate]
  *   D, delta_bias: [dim] or NULL.
+ *   last_state: [batch, dim, dstate] or NULL; receives h after the last token
+ *   (zeros when seqlen == 0), the state the scan carries (the Mamba
+ *   selective_scan_fn's last_state).
  * Restates selective_scan_fwd_kernel.cuh:114-127, :150-163, :166-270,
  * :272-281 and selective_scan_fn_ort.cpp:107-117 (n_groups comes from B; when B
  * is constant the group index is 0 for every channel, so a variable C reads
@@ -65,7 +68,7 @@ static real r_cos(real x) { return IS_F32 ? (real)cosf((float)x) : (real)cos((do
 void XMO_NAME(xmo_selective_scan)(const float *u, const float *delta, const float *A, const float *B,
                                   const float *C, const float *D, const float *delta_bias, int batch,
                                   int dim, int seqlen, int dstate, int b_var, int c_var, int groups_b,
-                                  int groups_c, int delta_softplus, real *out) {
+                                  int groups_c, int delta_softplus, real *out, real *last_state) {
     const int ngroups = b_var ? groups_b : 1;
     const int ratio = dim / ngroups;
     const long long nbd = (long long)batch * dim;
@@ -113,6 +116,7 @@ void XMO_NAME(xmo_selective_scan)(const float *u, const float *delta, const floa
                     else cv = b_var ? cconst : bc;
                     yr[t] += h * cv;
                 }
+                if (last_state) last_state[(size_t)bd * dstate + n] = h;
             }
         }
         free(dl);
@@ -126,7 +130,9 @@ void XMO_NAME(xmo_selective_scan)(const float *u, const float *delta, const floa
 
 /*
  * Output of GatedDeltaNet2Fn.  q, k, g, beta: [batch, seqlen, nheads, dk];
- * v, w: [batch, seqlen, nheads, dv]; s0: [batch, nheads, dk, dv] or NULL.
+ * v, w: [batch, seqlen, nheads, dv]; s0: [batch, nheads, dk, dv] or NULL;
+ * final_state: [batch, nheads, dk, dv] or NULL, receives S after the last
+ * token (s0, or zeros, when seqlen == 0).
  * Preparation restates gated_deltanet2_fwd.cu:39-76 (q_mul = scale *
  * rsqrt(sum q^2 + 1e-6), k_mul = rsqrt(sum k^2 + 1e-6), exp(g), beta * khat);
  * the recurrence restates :82-140 (decay, erase, write = w*v - erase, update,
@@ -135,7 +141,7 @@ void XMO_NAME(xmo_selective_scan)(const float *u, const float *delta, const floa
 void XMO_NAME(xmo_gated_deltanet2)(const float *q, const float *k, const float *v, const float *g,
                                    const float *beta, const float *w, const float *s0, int batch,
                                    int seqlen, int nheads, int dk, int dv, float scale, int l2norm,
-                                   real *out) {
+                                   real *out, real *final_state) {
     const int nbh = batch * nheads;
 #pragma omp parallel
     {
@@ -199,6 +205,8 @@ void XMO_NAME(xmo_gated_deltanet2)(const float *q, const float *k, const float *
                 real *orow = out + row * dv;
                 for (int j = 0; j < dv; ++j) orow[j] = ov[j];
             }
+            if (final_state)
+                for (size_t i = 0; i < (size_t)dk * dv; ++i) final_state[(size_t)bh * dk * dv + i] = S[i];
         }
         free(S); free(qn); free(kn); free(dec); free(bk); free(er); free(ov);
     }

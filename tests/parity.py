@@ -23,7 +23,7 @@ def to_dev(x, device="cuda"):
     import torch
     if x is None:
         return None
-    return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+    return torch.from_numpy(np.require(x, requirements=["C", "W"])).to(device)
 
 
 def errors(got, ref):

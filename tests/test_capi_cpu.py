@@ -66,12 +66,10 @@ def test_attribute_defaults_match_reference():
 
 
 @pytest.mark.parametrize("op,kw,msg,status", [
-    ("selective_scan", dict(return_last_state=1), "SelectiveScanFn does not support return_last_state=1 in ORT kernel", xp.XM_ERR_UNSUPPORTED),
     ("mamba3_siso", dict(chunk_size=0), "Mamba3SisoFn requires chunk_size > 0", xp.XM_ERR_INVALID_ARGUMENT),
     ("mamba3_siso", dict(return_final_states=1), "Mamba3SisoFn v1 does not support return_final_states", xp.XM_ERR_UNSUPPORTED),
     ("mamba3_siso", dict(has_input_states=1), "Mamba3SisoFn v1 does not support input states", xp.XM_ERR_UNSUPPORTED),
     ("mamba3_siso", dict(has_cu_seqlens=1), "Mamba3SisoFn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
-    ("gated_deltanet2", dict(output_final_state=1), "GatedDeltaNet2Fn v1 does not support output_final_state", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(use_gate_in_kernel=1), "GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(has_cu_seqlens=1), "GatedDeltaNet2Fn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(state_v_first=1), "GatedDeltaNet2Fn v1 expects state layout (batch, head, key, value)", xp.XM_ERR_UNSUPPORTED),
@@ -88,9 +86,58 @@ def test_attribute_rejections(op, kw, msg, status):
 
 
 def test_attribute_check_order_matches_reference():
-    # The GDN-2 constructor checks output_final_state before the scale.
-    with pytest.raises(XmError, match="output_final_state"):
-        check_attrs("gated_deltanet2", output_final_state=1, scale=-1.0)
+    # The GDN-2 constructor checks use_gate_in_kernel, cu_seqlens and the
+    # state layout before the scale (gated_deltanet2_fn_ort.cpp:49-63).
+    with pytest.raises(XmError, match="use_gate_in_kernel"):
+        check_attrs("gated_deltanet2", use_gate_in_kernel=1, scale=-1.0)
+    with pytest.raises(XmError, match="state layout"):
+        check_attrs("gated_deltanet2", state_v_first=1, scale=float("nan"))
+
+
+def test_state_attributes_are_accepted():
+    # Widening: the reference rejects these two; here they select the state
+    # output of the *_forward_states entry points.  Mamba-3's stays rejected.
+    check_attrs("selective_scan", return_last_state=1, delta_softplus=1)
+    check_attrs("gated_deltanet2", output_final_state=1, scale=0.5)
+    with pytest.raises(XmError, match="return_final_states"):
+        check_attrs("mamba3_siso", return_final_states=1)
+
+
+def _forward_host_error(op, shapes, entry, state_ptr=None, **attrs):
+    """Calls a forward entry point on shape-only descriptors with a host-side
+    error expected before any device work; returns (status, message)."""
+    _, n = xp._capi.OPS[op]
+    arr = (xp._capi.XmTensor * n)(*[xp._desc_from_shape(sh if sh is not None else (0,)) for sh in shapes])
+    a = xp._attrs(op, **attrs)
+    err = ctypes.create_string_buffer(512)
+    fn = getattr(xp.lib(), f"xm_{op}_{entry}")
+    out = ctypes.c_void_p(16)   # never dereferenced: every call below fails on the host first
+    if entry == "forward":
+        st = fn(arr, n, ctypes.byref(a), out, None, None, err, len(err))
+    else:
+        st = fn(arr, n, ctypes.byref(a), out, state_ptr, None, None, err, len(err))
+    return st, err.value.decode()
+
+
+def test_plain_forward_refuses_a_state_request():
+    st, msg = _forward_host_error("selective_scan", ss_shapes(), "forward", return_last_state=1)
+    assert st == xp.XM_ERR_INVALID_ARGUMENT and "xm_selective_scan_forward_states" in msg
+    st, msg = _forward_host_error("gated_deltanet2", gdn_shapes(), "forward", output_final_state=1)
+    assert st == xp.XM_ERR_INVALID_ARGUMENT and "xm_gated_deltanet2_forward_states" in msg
+
+
+def test_states_entry_needs_a_state_buffer():
+    st, msg = _forward_host_error("selective_scan", ss_shapes(), "forward_states", None, return_last_state=1)
+    assert (st, msg) == (xp.XM_ERR_INVALID_ARGUMENT, "return_last_state=1 needs a last_state buffer")
+    st, msg = _forward_host_error("gated_deltanet2", gdn_shapes(), "forward_states", None, output_final_state=1)
+    assert (st, msg) == (xp.XM_ERR_INVALID_ARGUMENT, "output_final_state=1 needs a final_state buffer")
+
+
+def test_states_entry_validates_shapes_first():
+    bad = ss_shapes()
+    bad[1] = (2, 8, 15)
+    st, msg = _forward_host_error("selective_scan", bad, "forward_states", None, return_last_state=1)
+    assert st == xp.XM_ERR_INVALID_ARGUMENT and "needs a last_state buffer" not in msg
 
 
 # ---------------------------------------------------------------------------
@@ -302,10 +349,12 @@ def test_ort_registration_domain_and_order():
 
 def test_ort_descriptors_match_reference_contract():
     ops = _src("ops_ort.cpp")
-    for name, n_in in (("SelectiveScanFn", 8), ("Mamba3SisoFn", 11), ("GatedDeltaNet2Fn", 7)):
+    # output 1 (optional) is the state after the last token where the op has one
+    for name, n_in, n_out in (("SelectiveScanFn", 8, 2), ("Mamba3SisoFn", 11, 1), ("GatedDeltaNet2Fn", 7, 2)):
         block = ops[ops.index(f'return "{name}";') - 400:ops.index(f'return "{name}";') + 600]
         assert f"GetInputTypeCount() const {{ return {n_in}; }}" in block
-        assert "GetOutputTypeCount() const { return 1; }" in block
+        assert f"GetOutputTypeCount() const {{ return {n_out}; }}" in block
+        assert ("INPUT_OUTPUT_OPTIONAL" in block) == (n_out == 2)
         assert "GetExecutionProviderType() const { return XM_ORT_GPU_EP; }" in block
     for attr in ("delta_softplus", "return_last_state", "chunk_size", "has_d", "has_z", "return_final_states",
                  "has_input_states", "has_cu_seqlens", "scale", "use_qk_l2norm_in_kernel", "output_final_state",

@@ -108,6 +108,65 @@ def test_ss_matches_closed_form(impl, groups, softplus):
     np.testing.assert_allclose(y, ref, rtol=1e-10, atol=1e-11)
 
 
+def ss_state_closed_form(u, delta, A, B, bias, softplus, groups=1):
+    """h_n(L) = sum_s exp(A_n sum_{r=s+1..L} delta'_r) B[n,s] delta'_s u_s (explicit sums)."""
+    u = u.astype(F64); A = A.astype(F64); B = B.astype(F64)
+    Bt, Dm, L = u.shape
+    N = A.shape[1]
+    dl = delta.astype(F64) + (0 if bias is None else bias.astype(F64)[None, :, None])
+    if softplus:
+        dl = softplus64(dl)
+    tail = dl.sum(-1, keepdims=True) - np.cumsum(dl, axis=-1)      # sum_{r>s}
+    h = np.zeros((Bt, Dm, N))
+    ratio = Dm // groups
+    for d in range(Dm):
+        src = B[:, d // ratio] * (dl[:, d] * u[:, d])[:, None, :]   # [Bt,N,L]
+        h[:, d] = (np.exp(A[d][None, :, None] * tail[:, d][:, None, :]) * src).sum(-1)
+    return h
+
+
+@pytest.mark.parametrize("groups", [1, 2])
+def test_ss_last_state_matches_closed_form(impl, groups):
+    rng = np.random.default_rng(30 + groups)
+    Bt, Dm, L, N = 2, 4, 17, 5
+    u = rnd(rng, Bt, Dm, L); delta = rnd(rng, Bt, Dm, L, scale=0.5)
+    A = (-np.exp(rng.uniform(0, np.log(8), (Dm, N)))).astype(np.float32)
+    Bv = rnd(rng, Bt, groups, N, L); Cv = rnd(rng, Bt, groups, N, L); D = rnd(rng, Dm)
+    bias = rng.uniform(-3, -1, Dm).astype(np.float32)
+    Bin = Bv[:, 0] if groups == 1 else Bv
+    Cin = Cv[:, 0] if groups == 1 else Cv
+    y, h = impl.selective_scan(u, delta, A, Bin, Cin, D, None, bias, delta_softplus=True, dtype=F64,
+                               return_state=True)
+    np.testing.assert_allclose(h, ss_state_closed_form(u, delta, A, Bv, bias, True, groups), rtol=1e-11, atol=1e-12)
+    # the output of the call is the one without the state
+    np.testing.assert_array_equal(y, impl.selective_scan(u, delta, A, Bin, Cin, D, None, bias, delta_softplus=True,
+                                                         dtype=F64))
+
+
+def test_ss_last_state_is_the_readout_of_a_one_hot_c(impl):
+    # With C = e_n (variable, one-hot on state n) and D = 0, y at the last
+    # token is exactly h_n(L): the state's n index and layout [B,D,N] are pinned.
+    rng = np.random.default_rng(33)
+    Bt, Dm, L, N = 2, 3, 9, 4
+    u = rnd(rng, Bt, Dm, L); delta = np.abs(rnd(rng, Bt, Dm, L, scale=0.5))
+    A = (-np.exp(rng.uniform(0, 2, (Dm, N)))).astype(np.float32)
+    B = rnd(rng, Bt, N, L)
+    _, h = impl.selective_scan(u, delta, A, B, B, None, None, None, dtype=F64, return_state=True)
+    for n in range(N):
+        C = np.zeros((Bt, N, L), np.float32); C[:, n] = 1.0
+        y = impl.selective_scan(u, delta, A, B, C, None, None, None, dtype=F64)
+        np.testing.assert_allclose(h[:, :, n], y[:, :, -1], rtol=1e-13, atol=1e-14)
+
+
+def test_ss_last_state_of_an_empty_sequence_is_zero(impl):
+    u = np.zeros((2, 3, 0), np.float32)
+    A = -np.ones((3, 4), np.float32)
+    B = np.zeros((2, 4, 0), np.float32)
+    y, h = impl.selective_scan(u, u, A, B, B, None, None, None, dtype=F64, return_state=True)
+    assert y.shape == (2, 3, 0) and h.shape == (2, 3, 4)
+    np.testing.assert_array_equal(h, 0.0)
+
+
 def test_ss_constant_bc_equal_broadcast_variable(impl):
     # One channel per group, so a per-(group) variable B equals a per-channel constant B.
     rng = np.random.default_rng(5)
@@ -200,12 +259,13 @@ def gdn2_normalise(q, k, scale, l2):
     return qn, kn
 
 
-def gdn2_matrix_form(q, k, v, g, beta, w, s0, scale, l2):
+def gdn2_matrix_form(q, k, v, g, beta, w, s0, scale, l2, return_state=False):
     """S_t = (I - khat (beta*khat)^T) diag(exp g) S_{t-1} + khat (w*v)^T;  o_t = qhat^T S_t."""
     qn, kn = gdn2_normalise(q, k, float(np.float32(scale)), l2)
     Bt, T, H, K = q.shape
     V = v.shape[-1]
     out = np.zeros((Bt, T, H, V))
+    final = np.zeros((Bt, H, K, V))
     for b in range(Bt):
         for h in range(H):
             S = np.zeros((K, V)) if s0 is None else s0[b, h].astype(F64)
@@ -215,7 +275,8 @@ def gdn2_matrix_form(q, k, v, g, beta, w, s0, scale, l2):
                 M = np.eye(K) - kk @ bk.T
                 S = M @ (np.exp(g[b, t, h].astype(F64))[:, None] * S) + kk @ (w[b, t, h].astype(F64) * v[b, t, h])[None, :]
                 out[b, t, h] = qn[b, t, h] @ S
-    return out
+            final[b, h] = S
+    return (out, final) if return_state else out
 
 
 def gdn2_rand(rng, Bt, T, H, K, V, s0=True, per_key=True):
@@ -237,6 +298,34 @@ def test_gdn2_matches_matrix_form(impl, l2):
     o = impl.gated_deltanet2(q, k, v, g, beta, w, S0, scale=0.7, use_qk_l2norm=l2, dtype=F64)
     ref = gdn2_matrix_form(q, k, v, g, beta, w, S0, 0.7, l2)
     np.testing.assert_allclose(o, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_gdn2_final_state_matches_matrix_form(impl):
+    rng = np.random.default_rng(18)
+    q, k, v, g, beta, w, S0 = gdn2_rand(rng, 2, 7, 2, 5, 3)
+    o, S = impl.gated_deltanet2(q, k, v, g, beta, w, S0, scale=0.6, dtype=F64, return_state=True)
+    ref_o, ref_S = gdn2_matrix_form(q, k, v, g, beta, w, S0, 0.6, True, return_state=True)
+    assert S.shape == (2, 2, 5, 3)
+    np.testing.assert_allclose(S, ref_S, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(o, ref_o, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("split", [1, 6, 10])
+def test_gdn2_final_state_chains(impl, split):
+    # Running tokens [0, split) and then [split, T) from the first call's final
+    # state equals one run over [0, T): the state is the whole carry, in
+    # initial_state's [B,H,K,V] layout (K != V, so a transposed layout fails).
+    rng = np.random.default_rng(19)
+    q, k, v, g, beta, w, S0 = gdn2_rand(rng, 2, 11, 3, 6, 4)
+    o, S = impl.gated_deltanet2(q, k, v, g, beta, w, S0, scale=0.8, dtype=F64, return_state=True)
+    cut = lambda x, a, b: np.ascontiguousarray(x[:, a:b])
+    o1, S1 = impl.gated_deltanet2(*(cut(x, 0, split) for x in (q, k, v, g, beta, w)), S0, scale=0.8, dtype=F64,
+                                  return_state=True)
+    o2, S2 = impl.gated_deltanet2(*(cut(x, split, 11) for x in (q, k, v, g, beta, w)), S1.astype(np.float32),
+                                  scale=0.8, dtype=F64, return_state=True)
+    # S1 passes through fp32 (the operator's input type), hence the tolerance
+    np.testing.assert_allclose(np.concatenate([o1, o2], axis=1), o, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(S2, S, rtol=2e-6, atol=2e-6)
 
 
 def test_gdn2_linear_attention_special_case(impl):
@@ -319,9 +408,10 @@ def test_gdn2_numpy_and_c_agree():
     rng = np.random.default_rng(17)
     args = dict(zip(("q", "k", "v", "g", "beta", "w", "initial_state"), gdn2_rand(rng, 2, 40, 3, 16, 12)))
     for dt, tol in ((F64, 1e-12), (np.float32, 1e-5)):
-        a = numpy_ref.gated_deltanet2(**args, scale=0.25, dtype=dt)
-        b = cref.gated_deltanet2(**args, scale=0.25, dtype=dt)
+        a, sa = numpy_ref.gated_deltanet2(**args, scale=0.25, dtype=dt, return_state=True)
+        b, sb = cref.gated_deltanet2(**args, scale=0.25, dtype=dt, return_state=True)
         np.testing.assert_allclose(a, b, rtol=tol, atol=tol)
+        np.testing.assert_allclose(sa, sb, rtol=tol, atol=tol)
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,172 @@
+"""State outputs on the GPU vs the fp64 oracle, through the C ABI.
+
+SelectiveScanFn with return_last_state=1 writes the scan state after the last
+token, [B,D,N]; GatedDeltaNet2Fn with output_final_state=1 writes the state
+after the last token, [B,H,K,V] (initial_state's layout).  Both attributes
+are rejected by the reference's ORT kernels (selective_scan_fn_ort.cpp:52-55,
+gated_deltanet2_fn_ort.cpp:49-51); here they are a widening served by the
+``*_forward_states`` entry points.  Checked: the state against the oracle's,
+output 0 unchanged bit for bit by the extra write, every kernel variant
+(lane layouts, key tiles, rows per column, the LDS-state path with its chunk
+carry), empty sequences, and chaining (two calls joined through the state
+equal one call).
+"""
+
+import numpy as np
+import pytest
+
+from oracle import cref
+from parity import TOL_GDN2, TOL_SS, check, to_dev
+from xmetai_onnx_plugins import gated_deltanet2_fn, selective_scan_fn, workloads as W
+
+pytestmark = pytest.mark.gpu
+
+SS_KEYS = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+GDN_KEYS = ("q", "k", "v", "g", "beta", "w", "initial_state")
+
+
+# ---------------------------------------------------------------------------
+# SelectiveScanFn last_state
+# ---------------------------------------------------------------------------
+
+def ss_gpu(inp, softplus=True, state=True):
+    import torch
+    r = selective_scan_fn(*(to_dev(inp[k]) for k in SS_KEYS), delta_softplus=softplus, return_last_state=state)
+    torch.cuda.synchronize()
+    if state:
+        return r[0].cpu().numpy(), r[1].cpu().numpy()
+    return r.cpu().numpy()
+
+
+def ss_ref(inp, softplus=True):
+    return cref.selective_scan(*(inp[k] for k in SS_KEYS), delta_softplus=softplus, dtype=np.float64,
+                               return_state=True)
+
+
+SS_CASES = {
+    "n1": W.SelectiveScanShape(2, 40, 64, 1),
+    "n3_ragged_l37": W.SelectiveScanShape(2, 33, 37, 3),
+    "n16_groups2": W.SelectiveScanShape(2, 96, 64, 16, groups=2),
+    "n16_const_bc": W.SelectiveScanShape(1, 70, 48, 16, b_var=False, c_var=False),
+    "n16_l1": W.SelectiveScanShape(3, 64, 1, 16),
+    "n16_l2050": W.SelectiveScanShape(1, 16, 2050, 16),
+    "n64_groups4": W.SelectiveScanShape(2, 64, 40, 64, groups=4),
+    "n100": W.SelectiveScanShape(1, 20, 33, 100),
+    "n256": W.SelectiveScanShape(1, 17, 24, 256),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SS_CASES))
+def test_ss_last_state_parity(name):
+    s = SS_CASES[name]
+    inp = W.selective_scan_inputs(s, seed=4)
+    y, h = ss_gpu(inp)
+    ref_y, ref_h = ss_ref(inp)
+    assert h.shape == (s.batch, s.dim, s.dstate)
+    check(f"selective_scan_state/{name}/y", y, ref_y, TOL_SS)
+    check(f"selective_scan_state/{name}/h", h, ref_h, TOL_SS)
+    np.testing.assert_array_equal(y, ss_gpu(inp, state=False))   # the state write leaves y alone
+
+
+@pytest.mark.parametrize("lpc", ["4", "8", "16"])
+def test_ss_last_state_lane_layouts(lpc, monkeypatch):
+    s = W.SelectiveScanShape(2, 70, 45, 16)
+    inp = W.selective_scan_inputs(s, seed=5)
+    monkeypatch.setenv("XM_SS_LPC", lpc)
+    y, h = ss_gpu(inp)
+    ref_y, ref_h = ss_ref(inp)
+    check(f"selective_scan_state/lpc{lpc}/y", y, ref_y, TOL_SS)
+    check(f"selective_scan_state/lpc{lpc}/h", h, ref_h, TOL_SS)
+
+
+def test_ss_last_state_of_an_empty_sequence_is_zero():
+    import torch
+    s = W.SelectiveScanShape(2, 8, 0, 4)
+    inp = W.selective_scan_inputs(s, seed=0)
+    args = [to_dev(inp[k]) for k in SS_KEYS]
+    args[0] = torch.zeros((2, 8, 0), device="cuda")
+    args[1] = torch.zeros((2, 8, 0), device="cuda")
+    y, h = selective_scan_fn(*args, delta_softplus=True, return_last_state=True)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 8, 0) and h.shape == (2, 8, 4)
+    assert torch.count_nonzero(h).item() == 0
+
+
+# ---------------------------------------------------------------------------
+# GatedDeltaNet2Fn final_state
+# ---------------------------------------------------------------------------
+
+def gdn_gpu(inp, s, state=True):
+    import torch
+    r = gated_deltanet2_fn(*(to_dev(inp[k]) for k in GDN_KEYS), scale=s.scale, use_qk_l2norm_in_kernel=s.l2norm,
+                           output_final_state=state)
+    torch.cuda.synchronize()
+    if state:
+        return r[0].cpu().numpy(), r[1].cpu().numpy()
+    return r.cpu().numpy()
+
+
+def gdn_ref(inp, s):
+    return cref.gated_deltanet2(*(inp[k] for k in GDN_KEYS), scale=s.scale, use_qk_l2norm=s.l2norm,
+                                dtype=np.float64, return_state=True)
+
+
+S = W.GatedDeltaNet2Shape
+GDN_CASES = {
+    "k1_v1": S(1, 9, 2, 1, 1),
+    "t1_single_token": S(2, 1, 3, 64, 32),
+    "t3_shorter_than_block": S(1, 3, 2, 128, 40, per_key_gates=True),
+    "k17_v15_partial": S(2, 20, 2, 17, 15),
+    "k32_v33_nos0": S(1, 40, 2, 32, 33, initial_state=False),
+    "k128_v65_partial_wave": S(2, 64, 4, 128, 65),
+    "k200_v40": S(1, 17, 2, 200, 40),
+    "k257_two_rows": S(1, 21, 2, 257, 20),
+    "k512_v7_perkey": S(1, 12, 1, 512, 7, per_key_gates=True),
+    "k600_v33_lds_path": S(2, 40, 2, 600, 33),
+    "t1500_lds_carry": S(1, 1500, 1, 600, 16),
+    "k1024_lds_path_perkey": S(1, 12, 1, 1024, 7, per_key_gates=True),
+}
+
+
+@pytest.mark.parametrize("name", sorted(GDN_CASES))
+def test_gdn2_final_state_parity(name):
+    s = GDN_CASES[name]
+    inp = W.gated_deltanet2_inputs(s, seed=6)
+    o, st = gdn_gpu(inp, s)
+    ref_o, ref_st = gdn_ref(inp, s)
+    assert st.shape == (s.batch, s.nheads, s.dk, s.dv)
+    check(f"gated_deltanet2_state/{name}/o", o, ref_o, TOL_GDN2)
+    check(f"gated_deltanet2_state/{name}/S", st, ref_st, TOL_GDN2)
+    np.testing.assert_array_equal(o, gdn_gpu(inp, s, state=False))   # the state write leaves o alone
+
+
+@pytest.mark.parametrize("rows", ["1", "2", "4"])
+def test_gdn2_final_state_rows_per_column(rows, monkeypatch):
+    s = S(2, 37, 3, 64, 40)
+    inp = W.gated_deltanet2_inputs(s, seed=7)
+    monkeypatch.setenv("XM_GDN2_ROWS", rows)
+    o, st = gdn_gpu(inp, s)
+    ref_o, ref_st = gdn_ref(inp, s)
+    check(f"gated_deltanet2_state/rows{rows}/o", o, ref_o, TOL_GDN2)
+    check(f"gated_deltanet2_state/rows{rows}/S", st, ref_st, TOL_GDN2)
+
+
+@pytest.mark.parametrize("shape,split", [((2, 300, 4, 128, 128), 123), ((1, 1100, 2, 600, 24), 1030)])
+def test_gdn2_final_state_chains(shape, split):
+    """Tokens [0, split) then [split, T) started from the first call's final
+    state give the outputs and final state of one call over [0, T)."""
+    import torch
+    s = S(*shape)
+    inp = W.gated_deltanet2_inputs(s, seed=8)
+    dev = {k: to_dev(v) for k, v in inp.items()}
+    kw = dict(scale=s.scale, use_qk_l2norm_in_kernel=s.l2norm, output_final_state=True)
+    o, st = gated_deltanet2_fn(*(dev[k] for k in GDN_KEYS), **kw)
+    part = lambda a, b: [dev[k][:, a:b].contiguous() for k in GDN_KEYS[:-1]]
+    o1, st1 = gated_deltanet2_fn(*part(0, split), dev["initial_state"], **kw)
+    o2, st2 = gated_deltanet2_fn(*part(split, s.seqlen), st1, **kw)
+    torch.cuda.synchronize()
+    whole = o.cpu().numpy()
+    chained = torch.cat([o1, o2], dim=1).cpu().numpy()
+    # the same arithmetic in the same order, with the state passing through fp32 memory
+    check(f"gated_deltanet2_state/chain_{split}/o", chained, whole, 1e-5)
+    check(f"gated_deltanet2_state/chain_{split}/S", st2.cpu().numpy(), st.cpu().numpy(), 1e-5)

@@ -360,6 +360,14 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
         if (next) prep_block((j + 1) * TB, buf ^ 1);
         __syncthreads();
     }
+    // State after the last token (identity tokens of a short last block keep it unchanged).
+    if (p.final_state != nullptr && col < dv) {
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+            const int kd = kb + j;
+            if (kd < dk) p.final_state[sbase + static_cast<size_t>(kd) * dv + col] = S[j];
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -428,10 +436,12 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
         }
         if (kg == 0 && col_ok) p.out[vidx] = o;
     }
-    if (t0 + tc < p.seqlen) {
+    // carry to the next chunk, or the final state after the last one
+    float *dst = t0 + tc < p.seqlen ? p.state : p.final_state;
+    if (dst != nullptr) {
         for (int j = 0; j < kt; ++j) {
             const int kd = kg * kt + j;
-            if (kd < dk && col_ok) p.state[sbase + static_cast<size_t>(kd) * dv + col] = sS[(j * 16 + cl) * 16 + kg];
+            if (kd < dk && col_ok) dst[sbase + static_cast<size_t>(kd) * dv + col] = sS[(j * 16 + cl) * 16 + kg];
         }
     }
 }

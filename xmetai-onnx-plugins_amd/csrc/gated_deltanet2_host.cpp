@@ -3,9 +3,15 @@
 // (constructor checks in the same order, ValidateInputs and its messages,
 // ToIntDim, output shape = v.shape).
 //
-// Scratch (requested from the caller's allocator, reference :86-111): the
-// prepared per-token vectors of one <=1024-token chunk, and the fp32 state
-// carried between chunks when seqlen > 1024.
+// Scratch (requested from the caller's allocator, reference :86-111): none for
+// headdim_k <= 512 (one fused kernel); above that, the prepared per-token
+// vectors of one <=1024-token chunk and the fp32 state carried between chunks
+// when seqlen > 1024.
+//
+// Widening: output_final_state = 1, which the reference rejects (:49-51), is
+// accepted through xm_gated_deltanet2_forward_states, which also writes the
+// state after the last token, [batch, nheads, headdim_k, headdim_v] (the
+// layout initial_state takes, so a call can continue where another stopped).
 #include <cmath>
 
 #include "xm_common.h"
@@ -17,7 +23,6 @@ namespace {
 constexpr size_t kNumInputs = 7;
 
 void CheckAttrs(const xm_gated_deltanet2_attrs_t &a) {
-    if (a.output_final_state != 0) Unsupported("GatedDeltaNet2Fn v1 does not support output_final_state");
     if (a.use_gate_in_kernel != 0)
         Unsupported("GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel");
     if (a.has_cu_seqlens != 0) Unsupported("GatedDeltaNet2Fn v1 does not support cu_seqlens");
@@ -74,6 +79,21 @@ Plan Validate(const std::vector<View> &in, const xm_gated_deltanet2_attrs_t &att
     return plan;
 }
 
+void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t &attrs, float *out,
+             float *final_state, void *stream, const xm_allocator_t *alloc) {
+    CheckAttrs(attrs);
+    auto views = MakeViews(inputs, n_inputs, kNumInputs, "GatedDeltaNet2Fn");
+    Plan plan = Validate(views, attrs);
+    if (out == nullptr) Invalid("output pointer is null");
+    const bool want_state = attrs.output_final_state != 0;
+    if (want_state && final_state == nullptr) Invalid("output_final_state=1 needs a final_state buffer");
+    plan.params.out = out;
+    plan.params.final_state = want_state ? final_state : nullptr;
+    Scratch scratch(alloc, stream);
+    void *buf = scratch.Get(plan.scratch);
+    LaunchGatedDeltaNet2(plan.params, buf, stream);
+}
+
 }  // namespace
 }  // namespace xm
 
@@ -113,14 +133,19 @@ int xm_gated_deltanet2_forward(const xm_tensor_t *inputs, size_t n_inputs, const
                                float *out, void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
-        xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "GatedDeltaNet2Fn");
-        xm::Plan plan = xm::Validate(views, *attrs);
-        if (out == nullptr) xm::Invalid("output pointer is null");
-        plan.params.out = out;
-        xm::Scratch scratch(alloc, stream);
-        void *buf = scratch.Get(plan.scratch);
-        xm::LaunchGatedDeltaNet2(plan.params, buf, stream);
+        if (attrs->output_final_state != 0)
+            xm::Invalid("GatedDeltaNet2Fn with output_final_state=1 needs a final_state output "
+                        "(xm_gated_deltanet2_forward_states)");
+        xm::Forward(inputs, n_inputs, *attrs, out, nullptr, stream, alloc);
+    });
+}
+
+int xm_gated_deltanet2_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
+                                      const xm_gated_deltanet2_attrs_t *attrs, float *out, float *final_state,
+                                      void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
+    return xm::Guard(errbuf, errlen, [&] {
+        if (attrs == nullptr) xm::Invalid("attrs is null");
+        xm::Forward(inputs, n_inputs, *attrs, out, final_state, stream, alloc);
     });
 }
 

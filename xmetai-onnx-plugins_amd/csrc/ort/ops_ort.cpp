@@ -6,6 +6,11 @@
 // :226-237); the execution provider is ROCm.  Attribute checks run in the
 // kernel constructor (session creation), shape checks in Compute (Run), both
 // through the C ABI, which carries the reference's messages.
+//
+// Widening: SelectiveScanFn with return_last_state=1 and GatedDeltaNet2Fn
+// with output_final_state=1, which the reference rejects, fill an optional
+// output 1 with the state after the last token ([B,D,N] and [B,H,K,V]).
+// Mamba3SisoFn keeps one output.
 #include "ort_glue.h"
 
 namespace {
@@ -14,6 +19,8 @@ using xm_ort::Check;
 using xm_ort::ComputeDeviceOp;
 using xm_ort::FloatAttr;
 using xm_ort::IntAttr;
+using xm_ort::StateOutput;
+
 
 // ---- SelectiveScanFn -------------------------------------------------------
 class SelectiveScanKernel {
@@ -26,7 +33,19 @@ public:
         Check(xm_selective_scan_check_attrs(&attrs_, err, sizeof(err)), err);
     }
     void Compute(OrtKernelContext *ctx) {
-        ComputeDeviceOp(api_, ctx, 8, attrs_, xm_selective_scan_validate, xm_selective_scan_forward);
+        const bool want = attrs_.return_last_state != 0;
+        auto state = [want](const xm_tensor_t *in) {
+            StateOutput so;
+            so.what = "return_last_state";
+            if (want) {   // [B, D, N]: u is [B, D, L] and A is [D, N] (validated)
+                so.rank = 3;
+                so.shape[0] = in[0].shape[0];
+                so.shape[1] = in[0].shape[1];
+                so.shape[2] = in[2].shape[1];
+            }
+            return so;
+        };
+        ComputeDeviceOp(api_, ctx, 8, attrs_, xm_selective_scan_validate, state, xm_selective_scan_forward_states);
     }
 
 private:
@@ -40,8 +59,11 @@ struct SelectiveScanOp : Ort::CustomOpBase<SelectiveScanOp, SelectiveScanKernel>
     const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
     size_t GetInputTypeCount() const { return 8; }
     ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
-    size_t GetOutputTypeCount() const { return 1; }
+    size_t GetOutputTypeCount() const { return 2; }
     ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    OrtCustomOpInputOutputCharacteristic GetOutputCharacteristic(size_t i) const {
+        return i == 0 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
+    }
 };
 
 // ---- Mamba3SisoFn ----------------------------------------------------------
@@ -59,7 +81,16 @@ public:
         Check(xm_mamba3_siso_check_attrs(&attrs_, err, sizeof(err)), err);
     }
     void Compute(OrtKernelContext *ctx) {
-        ComputeDeviceOp(api_, ctx, 11, attrs_, xm_mamba3_siso_validate, xm_mamba3_siso_forward);
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_mamba3_siso_attrs_t *a, float *out, float *,
+                         void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
+            return xm_mamba3_siso_forward(in, n, a, out, stream, alloc, err, errlen);
+        };
+        auto state = [](const xm_tensor_t *) {
+            StateOutput so;
+            so.what = "return_final_states";
+            return so;
+        };
+        ComputeDeviceOp(api_, ctx, 11, attrs_, xm_mamba3_siso_validate, state, launch);
     }
 
 private:
@@ -92,7 +123,20 @@ public:
         Check(xm_gated_deltanet2_check_attrs(&attrs_, err, sizeof(err)), err);
     }
     void Compute(OrtKernelContext *ctx) {
-        ComputeDeviceOp(api_, ctx, 7, attrs_, xm_gated_deltanet2_validate, xm_gated_deltanet2_forward);
+        const bool want = attrs_.output_final_state != 0;
+        auto state = [want](const xm_tensor_t *in) {
+            StateOutput so;
+            so.what = "output_final_state";
+            if (want) {   // [B, H, K, V]: q is [B, T, H, K] and v is [B, T, H, V] (validated)
+                so.rank = 4;
+                so.shape[0] = in[0].shape[0];
+                so.shape[1] = in[0].shape[2];
+                so.shape[2] = in[0].shape[3];
+                so.shape[3] = in[2].shape[3];
+            }
+            return so;
+        };
+        ComputeDeviceOp(api_, ctx, 7, attrs_, xm_gated_deltanet2_validate, state, xm_gated_deltanet2_forward_states);
     }
 
 private:
@@ -106,8 +150,11 @@ struct GatedDeltaNet2Op : Ort::CustomOpBase<GatedDeltaNet2Op, GatedDeltaNet2Kern
     const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
     size_t GetInputTypeCount() const { return 7; }
     ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
-    size_t GetOutputTypeCount() const { return 1; }
+    size_t GetOutputTypeCount() const { return 2; }
     ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    OrtCustomOpInputOutputCharacteristic GetOutputCharacteristic(size_t i) const {
+        return i == 0 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
+    }
 };
 
 // Descriptors live for the whole process: the domain that references them is

@@ -112,13 +112,24 @@ struct ScratchAdapter {
     }
 };
 
+// Optional output 1 of an operator: the recurrent state after the last token.
+// rank == 0 means the node's attributes do not ask for it.
+struct StateOutput {
+    int32_t rank = 0;
+    int64_t shape[XM_MAX_RANK] = {};
+    const char *what = "";   // attribute that asks for it, for error messages
+};
+
 // Compute of a device operator: describe the inputs, validate (the C ABI
-// writes the output shape and the scratch size), allocate the output, take
-// the execution provider's compute stream, enqueue.  Nothing synchronises the
-// host and nothing is cached on the kernel object.
-template <typename Attrs, typename Validate, typename Forward>
+// writes the output shape and the scratch size), allocate output 0 (and
+// output 1 when the attributes ask for the state), take the execution
+// provider's compute stream, enqueue.  Nothing synchronises the host and
+// nothing is cached on the kernel object.
+//   state(in) -> StateOutput
+//   launch(in, n, &attrs, out, state_or_null, stream, alloc, err, errlen) -> status
+template <typename Attrs, typename Validate, typename State, typename Launch>
 void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t n_inputs, const Attrs &attrs,
-                     Validate validate, Forward forward) {
+                     Validate validate, State state, Launch launch) {
     size_t count = 0;
     ThrowIfFailed(api, api.KernelContext_GetInputCount(ctx, &count));
     if (count != n_inputs) throw std::runtime_error("unexpected number of inputs");
@@ -137,6 +148,20 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t n_inputs, 
     ThrowIfFailed(api, api.KernelContext_GetOutput(ctx, 0, out_shape, static_cast<size_t>(out_rank), &out));
     void *out_data = nullptr;
     ThrowIfFailed(api, api.GetTensorMutableData(out, &out_data));
+
+    size_t n_outputs = 0;
+    ThrowIfFailed(api, api.KernelContext_GetOutputCount(ctx, &n_outputs));
+    const StateOutput so = state(in.data());
+    void *state_data = nullptr;
+    if (so.rank > 0) {
+        if (n_outputs < 2) throw std::runtime_error(std::string(so.what) + "=1 needs a second output (the state)");
+        OrtValue *sv = nullptr;
+        ThrowIfFailed(api, api.KernelContext_GetOutput(ctx, 1, so.shape, static_cast<size_t>(so.rank), &sv));
+        ThrowIfFailed(api, api.GetTensorMutableData(sv, &state_data));
+    } else if (n_outputs > 1) {
+        throw std::runtime_error(std::string("output 1 (the state) needs ") + so.what + "=1");
+    }
+
     void *stream = nullptr;
     ThrowIfFailed(api, api.KernelContext_GetGPUComputeStream(ctx, &stream));
 
@@ -152,8 +177,8 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t n_inputs, 
         ThrowIfFailed(api, api.KernelContext_GetAllocator(ctx, s.mem, &s.allocator));
         ap = &alloc;
     }
-    const int st = forward(in.data(), n_inputs, &attrs, static_cast<float *>(out_data), stream, ap, err,
-                           sizeof(err));
+    const int st = launch(in.data(), n_inputs, &attrs, static_cast<float *>(out_data),
+                          static_cast<float *>(state_data), stream, ap, err, sizeof(err));
     if (s.allocator != nullptr) api.ReleaseAllocator(s.allocator);
     Check(st, err);
 }

@@ -408,6 +408,14 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
         __syncthreads();
         phase3(t0, false);
     }
+    // Scan state after the last token (tokens past the end kept it unchanged).
+    if (p.last_state != nullptr && lane_ok) {
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const int n = lq * SPL + j;
+            if (n < N) p.last_state[(static_cast<size_t>(b) * p.dim + dl) * N + n] = h[j];
+        }
+    }
 }
 
 struct Config {

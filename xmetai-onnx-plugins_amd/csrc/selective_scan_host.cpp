@@ -11,6 +11,11 @@
 // No scratch is needed: the reference's per-chunk state buffer `x` is written
 // and never read, and its gated `out_z` buffer is discarded (kernel.cuh:256,
 // :296-299), so this implementation computes neither.
+//
+// Widening: return_last_state = 1, which the reference rejects (:52-55), is
+// accepted through xm_selective_scan_forward_states, which also writes the
+// scan state after the last token, [batch, dim, dstate] (the `last_state` of
+// the Mamba selective_scan_fn interface).
 #include "xm_common.h"
 #include "xm_params.h"
 
@@ -19,9 +24,12 @@ namespace {
 
 constexpr size_t kNumInputs = 8;
 
-void CheckAttrs(const xm_selective_scan_attrs_t &a) {
+void CheckAttrs(const xm_selective_scan_attrs_t &) {}
+
+void RequireStateEntry(const xm_selective_scan_attrs_t &a) {
     if (a.return_last_state != 0)
-        Unsupported("SelectiveScanFn does not support return_last_state=1 in ORT kernel");
+        Invalid("SelectiveScanFn with return_last_state=1 needs a last_state output "
+                "(xm_selective_scan_forward_states)");
 }
 
 // rearrange(B, "b dstate l -> b 1 dstate l") when rank 3 (reference :26-31, :77-78).
@@ -106,6 +114,25 @@ Plan Validate(const std::vector<View> &in, const xm_selective_scan_attrs_t &attr
     return plan;
 }
 
+void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_selective_scan_attrs_t &attrs, float *out,
+             float *last_state, void *stream) {
+    CheckAttrs(attrs);
+    auto views = MakeViews(inputs, n_inputs, kNumInputs, "SelectiveScanFn");
+    Plan plan = Validate(views, attrs);
+    const bool want_state = attrs.return_last_state != 0;
+    if (want_state && last_state == nullptr) Invalid("return_last_state=1 needs a last_state buffer");
+    plan.params.last_state = want_state ? last_state : nullptr;
+    if (plan.empty) {
+        // no tokens: the state is the zero initial state
+        const size_t state_elems = static_cast<size_t>(plan.params.batch) * plan.params.dim * plan.params.dstate;
+        if (want_state) LaunchFillZeros(last_state, state_elems, stream);
+        return;
+    }
+    if (out == nullptr) Invalid("output pointer is null");
+    plan.params.out = out;
+    LaunchSelectiveScan(plan.params, stream);
+}
+
 }  // namespace
 }  // namespace xm
 
@@ -142,13 +169,18 @@ int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs, const 
     (void)alloc;
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
-        xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "SelectiveScanFn");
-        xm::Plan plan = xm::Validate(views, *attrs);
-        if (plan.empty) return;
-        if (out == nullptr) xm::Invalid("output pointer is null");
-        plan.params.out = out;
-        xm::LaunchSelectiveScan(plan.params, stream);
+        xm::RequireStateEntry(*attrs);
+        xm::Forward(inputs, n_inputs, *attrs, out, nullptr, stream);
+    });
+}
+
+int xm_selective_scan_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
+                                     const xm_selective_scan_attrs_t *attrs, float *out, float *last_state,
+                                     void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
+    (void)alloc;
+    return xm::Guard(errbuf, errlen, [&] {
+        if (attrs == nullptr) xm::Invalid("attrs is null");
+        xm::Forward(inputs, n_inputs, *attrs, out, last_state, stream);
     });
 }
 

@@ -19,6 +19,7 @@ struct SelectiveScanParams {
     const float *D;          // [dim] or nullptr
     const float *delta_bias; // [dim] or nullptr
     float *out;              // [batch, dim, seqlen]
+    float *last_state;       // [batch, dim, dstate]: h after the last token, or nullptr
     int batch, dim, seqlen, dstate;
     int b_var, c_var;
     int groups_b;            // n_groups (from B; 1 when B is constant)
@@ -33,6 +34,7 @@ struct GatedDeltaNet2Params {
     const float *v, *w;             // [batch, seqlen, nheads, dv]
     const float *initial_state;     // [batch, nheads, dk, dv] or nullptr
     float *out;                     // [batch, seqlen, nheads, dv]
+    float *final_state;             // [batch, nheads, dk, dv]: S after the last token, or nullptr
     float *state;                   // carry between token chunks, [batch, nheads, dk, dv]
     float *prepared;                // [batch*nheads, chunk_cap, 4, dk_pad]: khat, beta*khat*d, qhat*d, d (d = exp(g))
     float *prep_qk;                 // [batch*nheads, chunk_cap]: qhat . khat
@@ -62,5 +64,7 @@ void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
+// Enqueues a kernel that writes `count` zeros (no memset node in a captured graph).
+void LaunchFillZeros(float *dst, size_t count, void *stream);
 
 }  // namespace xm

@@ -2,6 +2,7 @@
 // the version string.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
 
@@ -46,6 +47,21 @@ void *DefaultAlloc(size_t bytes, void *stream) {
 
 void DefaultFree(void *ptr, void *stream) {
     if (ptr != nullptr) (void)hipFreeAsync(ptr, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+__global__ __launch_bounds__(256) void FillZerosKernel(float *dst, size_t count) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) dst[i] = 0.0f;
+}
+}  // namespace
+
+void LaunchFillZeros(float *dst, size_t count, void *stream) {
+    if (count == 0) return;
+    const size_t blocks = std::min<size_t>((count + 255) / 256, 4096);
+    hipLaunchKernelGGL(FillZerosKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), dst, count);
+    XM_LAUNCH_CHECK("zero fill");
 }
 
 }  // namespace xm

@@ -192,7 +192,10 @@ class TorchAllocator:
 # operators
 # ---------------------------------------------------------------------------
 
-def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocator], stream, **attrs):
+def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocator], stream,
+         state_shape=None, **attrs):
+    """Validates and enqueues one operator call.  With ``state_shape`` set it
+    calls the op's ``_forward_states`` entry point and returns ``(out, state)``."""
     import torch
     _, n = _capi.OPS[op]
     descs = [_desc_from_tensor(x) for x in inputs]
@@ -209,18 +212,35 @@ def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocato
     if stream is None:
         stream = torch.cuda.current_stream(ref.device)
     alloc_ptr = ctypes.byref(allocator.struct) if allocator is not None else None
+    out_ptr = ctypes.c_void_p(out.data_ptr() if out.numel() else None)
     with torch.cuda.device(ref.device):
-        st = getattr(lib(), f"xm_{op}_forward")(arr, n, ctypes.byref(a), ctypes.c_void_p(out.data_ptr() if out.numel() else None),
-                                                ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
+        if state_shape is None:
+            st = getattr(lib(), f"xm_{op}_forward")(arr, n, ctypes.byref(a), out_ptr,
+                                                    ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
+            _check(st, err)
+            return out
+        state = torch.empty(tuple(int(d) for d in state_shape), dtype=torch.float32, device=ref.device)
+        st = getattr(lib(), f"xm_{op}_forward_states")(
+            arr, n, ctypes.byref(a), out_ptr, ctypes.c_void_p(state.data_ptr() if state.numel() else None),
+            ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
     _check(st, err)
-    return out
+    return out, state
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, delta_softplus=False,
                       return_last_state=False, allocator=None, stream=None):
     """SelectiveScanFn: returns y [B,D,L] (the un-gated scan output; z is
-    validated and otherwise unused, as in selective_scan_fwd_kernel.cuh:272-301)."""
+    validated and otherwise unused, as in selective_scan_fwd_kernel.cuh:272-301).
+
+    With ``return_last_state=True`` (rejected by the reference's ORT kernel,
+    selective_scan_fn_ort.cpp:52-55; accepted here as a widening) it returns
+    ``(y, last_state)``, last_state [B,D,N] being the scan state after the
+    last token (zeros when L = 0)."""
+    state_shape = None   # shapes of other ranks fail validation before the launch
+    if return_last_state and u.dim() == 3 and A.dim() == 2:
+        state_shape = (u.shape[0], u.shape[1], A.shape[1])
     return _run("selective_scan", [u, delta, A, B, C, D, z, delta_bias], 0, allocator, stream,
+                state_shape=state_shape,
                 delta_softplus=int(bool(delta_softplus)), return_last_state=int(bool(return_last_state)))
 
 
@@ -242,8 +262,17 @@ def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=Non
 def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, use_qk_l2norm_in_kernel=True,
                        output_final_state=False, use_gate_in_kernel=False, has_cu_seqlens=False,
                        state_v_first=False, allocator=None, stream=None):
-    """GatedDeltaNet2Fn: returns [B,T,H,V]."""
+    """GatedDeltaNet2Fn: returns [B,T,H,V].
+
+    With ``output_final_state=True`` (rejected by the reference,
+    gated_deltanet2_fn_ort.cpp:49-51; accepted here as a widening) it returns
+    ``(o, final_state)``, final_state [B,H,K,V] being the state after the last
+    token in initial_state's layout."""
+    state_shape = None   # shapes of other ranks fail validation before the launch
+    if output_final_state and q.dim() == 4 and v.dim() == 4:
+        state_shape = (q.shape[0], q.shape[2], q.shape[3], v.shape[3])
     return _run("gated_deltanet2", [q, k, v, g, beta, w, initial_state], 2, allocator, stream,
+                state_shape=state_shape,
                 scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
                 output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
                 has_cu_seqlens=int(bool(has_cu_seqlens)), state_v_first=int(bool(state_v_first)))

@@ -76,10 +76,14 @@ OPS = {
     "gated_deltanet2": (GatedDeltaNet2Attrs, 7),
 }
 
+# Ops with a second entry point that also writes the recurrent state after the
+# last token: op prefix -> the attribute that asks for it.
+STATE_OUTPUTS = {"selective_scan": "return_last_state", "gated_deltanet2": "output_final_state"}
+
 # Every symbol include/xmetai_recurrent.h declares.
 EXPORTED_SYMBOLS = [
     f"xm_{op}_{fn}" for op in OPS for fn in ("attrs_default", "check_attrs", "validate", "forward")
-] + ["xm_softmax_cpu", "xm_version"]
+] + [f"xm_{op}_forward_states" for op in STATE_OUTPUTS] + ["xm_softmax_cpu", "xm_version"]
 
 
 def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
@@ -100,6 +104,11 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(XmAllocator),
                       ctypes.c_char_p, ctypes.c_size_t]
         f.restype = ctypes.c_int
+        if op in STATE_OUTPUTS:
+            f = getattr(lib, f"xm_{op}_forward_states")
+            f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                          ctypes.POINTER(XmAllocator), ctypes.c_char_p, ctypes.c_size_t]
+            f.restype = ctypes.c_int
     lib.xm_softmax_cpu.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
     lib.xm_softmax_cpu.restype = ctypes.c_int
