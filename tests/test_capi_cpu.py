@@ -233,12 +233,31 @@ def gdn_shapes(B=2, T=5, H=3, K=16, V=8, s0=True):
 def test_gdn2_valid_and_scratch():
     out, scratch = validate("gated_deltanet2", gdn_shapes(), scale=0.25)
     assert out == (2, 5, 3, 8)
-    # headdim_k <= 512: one fused kernel, no scratch at any length
-    assert scratch == 0
+    a256 = lambda n: (n + 255) // 256 * 256
+
+    # headdim_k <= 256 (chunked path): per (b,h) and 16-token chunk of a window
+    # of up to 128 chunks, E, R, Ut tiles (256 floats per 16 keys each), G_15
+    # (16 per 16 keys), T and M T (256 each), q and k multipliers (16 each);
+    # keys padded to 16 * kpw * ks;
+    # plus the state carried between windows when there is more than one
+    def chunk_scratch(B, T, H, K, V):
+        kq = -(-K // 16)
+        kpw = 2 if kq >= 2 else 1
+        ks = 1
+        while ks * kpw < kq:
+            ks *= 2
+        kq = kpw * ks
+        block = 3 * kq * 256 + 16 * kq + 512 + 32
+        nch = -(-T // 16)
+        win = min(nch, 128)
+        return a256(B * H * win * block * 4) + (a256(B * H * K * V * 4) if nch > 128 else 0)
+    assert scratch == chunk_scratch(2, 5, 3, 16, 8)
+    for T, K, V in ((100, 128, 64), (3000, 128, 128), (17, 100, 7), (2049, 256, 16), (2048, 33, 40)):
+        assert validate("gated_deltanet2", gdn_shapes(T=T, K=K, V=V))[1] == chunk_scratch(2, T, 3, K, V), (T, K, V)
+    # 256 < headdim_k <= 512: one fused kernel, no scratch at any length
     assert validate("gated_deltanet2", gdn_shapes(T=3000, K=512, V=64))[1] == 0
     # headdim_k > 512: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded
     # to 64) + one q.k float per row, plus the carried state when T > 1024
-    a256 = lambda n: (n + 255) // 256 * 256
     _, s_short = validate("gated_deltanet2", gdn_shapes(T=100, K=600, V=64))
     assert s_short == a256(2 * 3 * 100 * 4 * 640 * 4) + a256(2 * 3 * 100 * 4)
     _, s_long = validate("gated_deltanet2", gdn_shapes(T=3000, K=600, V=64))

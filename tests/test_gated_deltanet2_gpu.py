@@ -3,7 +3,14 @@ the C ABI.  Covers the reference's dispatch boundaries: key dimensions on
 both sides of 256 (VGPR-state and LDS-state paths), partial waves (value
 dims that are not multiples of the column tiling), initial states, Q/K
 normalisation on and off, several batches, token counts around the
-1024-token preparation chunk, and overlapping calls on one device."""
+1024-token preparation chunk, and overlapping calls on one device.
+
+Three device paths: the chunked fp32-MFMA kernel (dk <= 256, the default
+there), the token-sequential register kernel (dk <= 512; forced for
+dk <= 256 with XM_GDN2_PATH=seq) and the LDS-state kernel (dk > 512).  The
+parity cases run on both paths where both apply; the chunked path's
+pairwise fallback (forced with XM_GDN2_PAIRWISE=1, or taken by chunks with
+extreme decays) has its own cases."""
 
 import numpy as np
 import pytest
@@ -57,11 +64,39 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("path", ["default", "seq"])
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_gdn2_parity(name):
+def test_gdn2_parity(name, path, monkeypatch):
     s = CASES[name]
+    if path == "seq":
+        if s.dk > 256:
+            pytest.skip("dk > 256 has one path")
+        monkeypatch.setenv("XM_GDN2_PATH", "seq")
     inp = W.gated_deltanet2_inputs(s, seed=0)
-    check(f"gated_deltanet2/{name}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
+    check(f"gated_deltanet2/{name}/{path}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
+
+
+@pytest.mark.parametrize("shape", [(1, 37, 2, 64, 40), (2, 50, 2, 128, 33), (1, 20, 1, 256, 16), (1, 9, 2, 5, 3)])
+def test_gdn2_chunk_pairwise_fallback(shape, monkeypatch):
+    """The chunked path with every chunk on the pairwise decay products."""
+    s = S(*shape, per_key_gates=True)
+    inp = W.gated_deltanet2_inputs(s, seed=9)
+    monkeypatch.setenv("XM_GDN2_PAIRWISE", "1")
+    check("gated_deltanet2/pairwise_" + "_".join(map(str, shape)), run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
+
+
+@pytest.mark.parametrize("g", [-30.0, -200.0, 3.0])
+def test_gdn2_chunk_extreme_decay(g):
+    """Chunks whose cumulative decay leaves [2^-60, 2^60] (a hard reset of some
+    keys, or growth) take the pairwise products; the others the fast form."""
+    s = S(2, 90, 2, 64, 24, per_key_gates=True)
+    inp = W.gated_deltanet2_inputs(s, seed=10)
+    inp["g"] = inp["g"].copy()
+    inp["g"][:, 20] = g                    # every key of token 20
+    inp["g"][1, 47, :, :9] = g             # some keys of one token
+    if g > 0:
+        inp["g"][:, 60:80] = g             # growth: e^48 over the chunk of tokens 64-79
+    check(f"gated_deltanet2/extreme_{g}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
 
 
 @pytest.mark.parametrize("shape", [(8, 40, 32, 64, 32), (4, 30, 16, 64, 96), (2, 20, 16, 400, 128),
@@ -82,6 +117,7 @@ def test_gdn2_rows_per_column_agree(rows, shape, monkeypatch):
     matches the oracle on the same inputs."""
     s = S(*shape)
     inp = W.gated_deltanet2_inputs(s, seed=7)
+    monkeypatch.setenv("XM_GDN2_PATH", "seq")
     monkeypatch.setenv("XM_GDN2_ROWS", rows)
     check(f"gated_deltanet2/rows{rows}_" + "_".join(map(str, shape)), run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)
 

@@ -125,6 +125,7 @@ GDN_CASES = {
     "k600_v33_lds_path": S(2, 40, 2, 600, 33),
     "t1500_lds_carry": S(1, 1500, 1, 600, 16),
     "k1024_lds_path_perkey": S(1, 12, 1, 1024, 7, per_key_gates=True),
+    "t4100_three_windows": S(1, 4100, 2, 64, 24),
 }
 
 

@@ -43,6 +43,7 @@ SOURCES = [
     "xm_runtime.hip",
     "selective_scan.hip",
     "gated_deltanet2.hip",
+    "gated_deltanet2_chunk.hip",
     "mamba3_siso.hip",
     "selective_scan_host.cpp",
     "gated_deltanet2_host.cpp",

@@ -543,6 +543,7 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
 }  // namespace
 
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
+    if (dk <= 256) return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv);   // chunked path
     if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch
     const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
     const size_t rows = static_cast<size_t>(batch) * nheads * cap;
@@ -553,6 +554,7 @@ size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
+    if (LaunchGatedDeltaNet2Chunked(p, scratch, stream_v)) return;   // dk <= 256: gated_deltanet2_chunk.hip
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.dk > kMaxLdsKeys)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");

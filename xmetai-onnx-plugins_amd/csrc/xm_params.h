@@ -43,6 +43,8 @@ struct GatedDeltaNet2Params {
     int chunk_cap;                  // tokens per preparation chunk (<= 1024)
     int l2norm;
     float scale;
+    int pairwise_only;              // chunked path: take the pairwise decay products in every chunk (test switch)
+    int vec4_keys;                  // chunked path: dk % 4 == 0 and q, k, g, beta 16-byte aligned
 };
 
 // Mamba3SisoFn (reference parameter block: mamba3_siso.h:10-36).
@@ -63,6 +65,12 @@ struct Mamba3SisoParams {
 void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
+// Chunked fp32-MFMA path (dk <= 256).  Returns false, launching nothing, when
+// the shape is not one it takes (or XM_GDN2_PATH=seq).  `scratch` holds
+// GatedDeltaNet2ChunkScratchBytes bytes: the prepared chunk vectors of one
+// window of up to 2048 tokens, and the state carried between windows.
+size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
+bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
 // Enqueues a kernel that writes `count` zeros (no memset node in a captured graph).
 void LaunchFillZeros(float *dst, size_t count, void *stream);
