@@ -201,8 +201,9 @@ __device__ __forceinline__ void PairSteps(std::integer_sequence<int, Ds...>, con
     (PairStep<Ds>(p, rowbase, live, kq, m16, g4, qm, km, dst), ...);
 }
 
-// A and M of a chunk whose decays leave the fast range (the whole wave calls it).
-__device__ __attribute__((noinline)) void PairwiseAM(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kq,
+// A and M of a chunk whose decays leave the fast range (the whole wave calls
+// it).  Inlined: a call would give every wave a stack frame and its traffic.
+__device__ __forceinline__ void PairwiseAM(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kq,
                                                      float qm, float km, float *dst) {
     const int lane = threadIdx.x & 63;
     PairSteps(std::make_integer_sequence<int, kC>{}, p, rowbase, live, kq, lane & 15, lane >> 4, qm, km, dst);
@@ -232,9 +233,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     float qs = 0.0f, kq2 = 0.0f;
     bool in_range = true;
     v4f al = {0.0f, 0.0f, 0.0f, 0.0f}, mu = al;
-    for (int kt = 0; kt < kq; ++kt) {
-        float q[4], k[4], g[4], bt[4];
-        LoadKeyTile(p, rowbase, live, kt, g4, q, k, g, bt);
+    // one key tile: operand-layout vectors to the block, A' and M' accumulated
+    auto tile = [&](int kt, const float (&q)[4], const float (&k)[4], const float (&g)[4], const float (&bt)[4])
+                    __attribute__((always_inline)) {
         v4f e, r, kb, g15;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -264,6 +265,16 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
             al = Mfma(e[ii], kb[ii], al);
             mu = Mfma(r[ii], kb[ii], mu);
         }
+    };
+    // key tiles in pairs, both loaded before either is used: the two halves of
+    // a 128-byte line of each token row are requested together
+    for (int kt = 0; kt < kq; kt += 2) {
+        float q0[4], k0[4], g0[4], b0[4], q1[4], k1[4], g1[4], b1[4];
+        const bool pair = kt + 1 < kq;   // kq is 1 or even
+        LoadKeyTile(p, rowbase, live, kt, g4, q0, k0, g0, b0);
+        if (pair) LoadKeyTile(p, rowbase, live, kt + 1, g4, q1, k1, g1, b1);
+        tile(kt, q0, k0, g0, b0);
+        if (pair) tile(kt + 1, q1, k1, g1, b1);
     }
     qs = RowsSum4(qs);
     kq2 = RowsSum4(kq2);
@@ -535,6 +546,11 @@ struct ChunkConfig {
     int kpw, ks, ct;
 };
 
+// Two key tiles (32 keys) per wave, ks = a power of two waves per column
+// tile (keys padded to 32 ks).  Fewer splits leave too few waves for the
+// chip (one wave per SIMD at best, and half the SIMDs idle for 4 x 16 heads
+// of 128 x 128); more add cross-wave exchanges.  Measured on 4 x 4096 x 16
+// heads, dk = dv = 128: ks = 1, 2, 4 -> 1.18, 0.97, 0.93 ms.
 ChunkConfig ChooseChunk(int batch, int nheads, int dk, int dv) {
     const int kq = (dk + 15) / 16;
     ChunkConfig c{kq >= 2 ? 2 : 1, 1, 1};
@@ -542,12 +558,16 @@ ChunkConfig ChooseChunk(int batch, int nheads, int dk, int dv) {
     while (c.ks < need) c.ks *= 2;
     const long long heads = static_cast<long long>(batch) * nheads;
     const int vt = (dv + 15) / 16;
-    for (int ct : {4, 2}) {
-        if (c.ks * ct <= 8 && ct <= vt && heads * ((vt + ct - 1) / ct) >= 256) {
-            c.ct = ct;
-            break;
-        }
+    const char *env = std::getenv("XM_GDN2_CT");   // column tiles per workgroup (test switch)
+    if (env != nullptr) {
+        const int f = std::atoi(env);
+        if ((f == 1 || f == 2 || f == 4) && c.ks * f <= 8) c.ct = f;
+        return c;
     }
+    // one column tile per workgroup when that gives two workgroups per CU
+    // (their phases drift apart and overlap); two otherwise, where the keys
+    // allow (4 x 16 heads: dv = 128 -> one, 0.93 ms; dv = 65 -> two, 0.85 ms)
+    if (heads * vt < 512 && vt >= 2 && c.ks * 2 <= 8) c.ct = 2;
     return c;
 }
 
@@ -580,13 +600,11 @@ void LaunchRecurCt(const GatedDeltaNet2Params &p, int ct, int c0, int wn, int kq
 
 void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0, int wn, int kq, const float *s_in,
                     float *s_out, hipStream_t stream) {
-    if (c.kpw == 1) return LaunchRecurCt<1, 1>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
-    switch (c.ks) {
-        case 1: return LaunchRecurCt<2, 1>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
-        case 2: return LaunchRecurCt<2, 2>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
-        case 4: return LaunchRecurCt<2, 4>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
-        default: return LaunchRecurCt<2, 8>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
-    }
+#define XM_GDN2_RECUR(KPW_, KS_) \
+    if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecurCt<KPW_, KS_>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
+    XM_GDN2_RECUR(1, 1) XM_GDN2_RECUR(2, 1) XM_GDN2_RECUR(2, 2) XM_GDN2_RECUR(2, 4) XM_GDN2_RECUR(2, 8)
+#undef XM_GDN2_RECUR
+    throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }
 
 }  // namespace
