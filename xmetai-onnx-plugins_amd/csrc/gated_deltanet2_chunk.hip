@@ -427,15 +427,20 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
             if (idx < L::F4) StF4(smem + buf * FB + idx * 4, st[j]);
         }
     };
-    float rw[2][4], rv[2][4];   // w, v of chunks by parity: tokens 4(l/16)+i, this lane's column
-    auto load_wv = [&](int cw, int par) __attribute__((always_inline)) {
+    // w, v of one chunk: tokens 4(l/16)+i, this lane's column.  Two sets in
+    // turn with compile-time roles (a runtime-indexed pair would make the
+    // consumer wait for the newest loads as well).
+    struct WV {
+        float w[4], v[4];
+    };
+    auto load_wv = [&](int cw, WV &x) __attribute__((always_inline)) {
         const int t0 = (c0 + cw) * kC;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = min(t0 + 4 * g4 + i, T - 1);
             const size_t idx = ((static_cast<size_t>(b) * T + t) * H + h) * dv + colc;
-            rw[par][i] = p.w[idx];
-            rv[par][i] = p.v[idx];
+            x.w[i] = p.w[idx];
+            x.v[i] = p.v[idx];
         }
     };
     // block offsets (floats)
@@ -456,18 +461,24 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
 
     load_block(0, stage0);
     store_block(0, stage0);
-    if (wn > 1) load_block(1, stage1);
-    if (wn > 2) load_block(2, stage0);
-    if (tile_live) load_wv(0, 0);
+    load_block(min(1, wn - 1), stage1);
+    load_block(min(2, wn - 1), stage0);
+    // Loads below are issued on every path (chunk indices clamped to the
+    // window, idle column tiles reading column 0): with a load count that
+    // depends on the path, the compiler's wait counts turn conservative and a
+    // consumer waits for the newest prefetches as well.
+    WV wv0, wv1;
+    load_wv(0, wv0);
     __syncthreads();
-    // one chunk; stage_nx holds chunk cw + 1 and then receives chunk cw + 3
-    auto step = [&](int cw, v4f (&stage_nx)[L::CP]) __attribute__((always_inline)) {
+    // one chunk; stage_nx holds chunk cw + 1 and then receives chunk cw + 3;
+    // wv_cur holds this chunk's w, v and wv_nx receives chunk cw + 1's
+    auto step = [&](int cw, v4f (&stage_nx)[L::CP], const WV &wv_cur, WV &wv_nx) __attribute__((always_inline)) {
         const int t0 = (c0 + cw) * kC;
+        load_wv(min(cw + 1, wn - 1), wv_nx);
         const float *const cur = smem + (cw & 1) * FB;
         const float *const prv = smem + ((cw + 1) & 1) * FB;   // chunk cw - 1 (until it is refilled below)
         if (tile_live) {
             if (cw > 0) update(prv);
-            if (cw + 1 < wn) load_wv(cw + 1, (cw + 1) & 1);
             v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
@@ -485,10 +496,8 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
         }
         __syncthreads();
         // chunk cw + 1 into the buffer of chunk cw - 1 (read only before the barrier)
-        if (cw + 1 < wn) {
-            store_block((cw + 1) & 1, stage_nx);
-            if (cw + 3 < wn) load_block(cw + 3, stage_nx);
-        }
+        if (cw + 1 < wn) store_block((cw + 1) & 1, stage_nx);
+        load_block(min(cw + 3, wn - 1), stage_nx);
         if (tile_live) {
             v4f xe = LdsF4(sXp + ((ct * KS) * 2 + 0) * 256 + lane * 4);
             v4f xr = LdsF4(sXp + ((ct * KS) * 2 + 1) * 256 + lane * 4);
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bool ok = col_ok && t0 + 4 * g4 + i < T;
-                y[i] = (ok ? rw[cw & 1][i] * rv[cw & 1][i] : 0.0f) - km[i] * xe[i];   // rows of E' S0 times k_mul
+                y[i] = (ok ? wv_cur.w[i] * wv_cur.v[i] : 0.0f) - km[i] * xe[i];   // rows of E' S0 times k_mul
             }
             const v4f ta = LdsF4(cur + oT + lane * 4);
             v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -528,8 +537,8 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
         __syncthreads();
     };
     for (int cw = 0; cw < wn; cw += 2) {
-        step(cw, stage1);
-        if (cw + 1 < wn) step(cw + 1, stage0);
+        step(cw, stage1, wv0, wv1);
+        if (cw + 1 < wn) step(cw + 1, stage0, wv1, wv0);
     }
     if (s_out != nullptr && col_ok) {
 #pragma unroll
