@@ -359,41 +359,43 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
 // ---------------------------------------------------------------------------
 // Recurrence over one window
 // ---------------------------------------------------------------------------
-template <int KPW, int KS, int CT>
-struct RecurLayout {
-    static constexpr int NW = KS * CT;
-    static constexpr int THREADS = 64 * NW;
-    static constexpr int KQ = KPW * KS;
-    static constexpr int FB = BlockFloats(KQ);              // one prepared chunk block
-    static constexpr int F4 = FB / 4;
-    static constexpr int CP = (F4 + THREADS - 1) / THREADS;  // 16-byte copies per thread per block
-    // LDS, in floats: [2][FB] staged blocks | [NW][2][256] partial E' S0, R' S0
-    static constexpr int oXp = 2 * FB;
-    static constexpr int kFloats = oXp + NW * 512;
-    static constexpr size_t kBytes = kFloats * sizeof(float);
+// The operands of one chunk that a wave needs, in MFMA lane order: its key
+// tiles of E', R', Ut' and G_15, T, M T, the row multipliers and this lane's
+// w, v (tokens 4(l/16)+i).
+template <int KPW>
+struct ChunkOperands {
+    v4f e[KPW], r[KPW], ut[KPW], g[KPW];
+    v4f t, mt, qm, km;
+    float w[4], v[4];
 };
 
-template <int KPW, int KS, int CT>
-__global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaNet2Params p, int c0, int wn,
-                                                                     const float *s_in, float *s_out) {
-    using L = RecurLayout<KPW, KS, CT>;
+template <int KPW, int KS>
+struct RecurLayout {
+    static constexpr int THREADS = 64 * KS;
+    static constexpr int KQ = KPW * KS;
+    static constexpr int FB = BlockFloats(KQ);   // one prepared chunk block
+    // LDS, in floats: [2 chunk parities][KS waves][E' S0, R' S0][256] partials
+    static constexpr int kFloats = KS > 1 ? 2 * KS * 512 : 1;
+};
+
+template <int KPW, int KS>
+__global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Params p, int c0, int wn,
+                                                                const float *s_in, float *s_out) {
+    using L = RecurLayout<KPW, KS>;
     constexpr int KQ = L::KQ, FB = L::FB;
-    extern __shared__ float smem[];
-    float *const sXp = smem + L::oXp;
+    constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oG = 3 * KQ * 256;   // block offsets (floats)
+    constexpr int oT = oG + 16 * KQ, oMT = oT + 256, oMul = oT + 512;
+    __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
 
     const int T = p.seqlen, H = p.nheads, dk = p.dk, dv = p.dv;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int ct = w / KS, ks = w % KS;
-    const int m16 = lane & 15, g4 = lane >> 4;
+    const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+    const int g4 = lane >> 4;
     const int VT = (dv + 15) / 16;
-    const int ncg = (VT + CT - 1) / CT;
     const int blk = XcdLocalBlock(blockIdx.x, gridDim.x);
-    const int bh = blk / ncg, cg = blk % ncg;
+    const int bh = blk / VT, vt = blk % VT;
     const int b = bh / H, h = bh % H;
-    const int vt = cg * CT + ct;
-    const bool tile_live = vt < VT;              // wave-uniform
-    const int col = vt * 16 + m16;
-    const bool col_ok = tile_live && col < dv;
+    const int col = vt * 16 + (lane & 15);
+    const bool col_ok = col < dv;
     const int colc = col_ok ? col : 0;
     const size_t sbase = static_cast<size_t>(bh) * dk * dv;
     const float *const prep0 = p.prepared + static_cast<size_t>(bh) * wn * FB;
@@ -409,136 +411,115 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
         }
     }
 
-    // prepared block of chunk cw: global -> registers (two chunks ahead, set
-    // cw % 2) -> LDS buffer cw % 2
-    v4f stage0[L::CP], stage1[L::CP];
-    auto load_block = [&](int cw, v4f (&st)[L::CP]) __attribute__((always_inline)) {
+    // Loads are issued on every path (chunk indices clamped to the window):
+    // with a load count that depends on the path, the compiler's wait counts
+    // turn conservative and a consumer waits for the newest prefetches too.
+    auto load_ops = [&](int cw, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
         const float *const bp = prep0 + static_cast<size_t>(cw) * FB;
 #pragma unroll
-        for (int j = 0; j < L::CP; ++j) {
-            const int idx = min(tid + j * L::THREADS, L::F4 - 1);
-            st[j] = LdgF4(bp + idx * 4);
+        for (int kt = 0; kt < KPW; ++kt) {
+            const int kg = ks * KPW + kt;
+            o.e[kt] = LdgF4(bp + oE + kg * 256 + lane * 4);
+            o.r[kt] = LdgF4(bp + oR + kg * 256 + lane * 4);
         }
-    };
-    auto store_block = [&](int buf, const v4f (&st)[L::CP]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < L::CP; ++j) {
-            const int idx = tid + j * L::THREADS;
-            if (idx < L::F4) StF4(smem + buf * FB + idx * 4, st[j]);
-        }
-    };
-    // w, v of one chunk: tokens 4(l/16)+i, this lane's column.  Two sets in
-    // turn with compile-time roles (a runtime-indexed pair would make the
-    // consumer wait for the newest loads as well).
-    struct WV {
-        float w[4], v[4];
-    };
-    auto load_wv = [&](int cw, WV &x) __attribute__((always_inline)) {
         const int t0 = (c0 + cw) * kC;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = min(t0 + 4 * g4 + i, T - 1);
             const size_t idx = ((static_cast<size_t>(b) * T + t) * H + h) * dv + colc;
-            x.w[i] = p.w[idx];
-            x.v[i] = p.v[idx];
+            o.w[i] = p.w[idx];
+            o.v[i] = p.v[idx];
         }
-    };
-    // block offsets (floats)
-    constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oG = 3 * KQ * 256;
-    constexpr int oT = oG + 16 * KQ, oMT = oT + 256, oMul = oT + 512;
-
-    v4f u_prev = {0.0f, 0.0f, 0.0f, 0.0f};   // k_mul o U of the previous chunk
-    auto update = [&](const float *blkl) __attribute__((always_inline)) {   // S = G_15 o S + Ut'^T u_prev
+        o.km = LdgF4(bp + oMul + 16 + 4 * g4);
+        o.t = LdgF4(bp + oT + lane * 4);
+        o.qm = LdgF4(bp + oMul + 4 * g4);
+        o.mt = LdgF4(bp + oMT + lane * 4);
 #pragma unroll
         for (int kt = 0; kt < KPW; ++kt) {
             const int kg = ks * KPW + kt;
-            S[kt] *= LdsF4(blkl + oG + kg * 16 + 4 * g4);
-            const v4f ua = LdsF4(blkl + oU + kg * 256 + lane * 4);
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(ua[ii], u_prev[ii], S[kt]);
+            o.g[kt] = LdgF4(bp + oG + kg * 16 + 4 * g4);
+            o.ut[kt] = LdgF4(bp + oU + kg * 256 + lane * 4);
         }
     };
 
-    load_block(0, stage0);
-    store_block(0, stage0);
-    load_block(min(1, wn - 1), stage1);
-    load_block(min(2, wn - 1), stage0);
-    // Loads below are issued on every path (chunk indices clamped to the
-    // window, idle column tiles reading column 0): with a load count that
-    // depends on the path, the compiler's wait counts turn conservative and a
-    // consumer waits for the newest prefetches as well.
-    WV wv0, wv1;
-    load_wv(0, wv0);
-    __syncthreads();
-    // one chunk; stage_nx holds chunk cw + 1 and then receives chunk cw + 3;
-    // wv_cur holds this chunk's w, v and wv_nx receives chunk cw + 1's
-    auto step = [&](int cw, v4f (&stage_nx)[L::CP], const WV &wv_cur, WV &wv_nx) __attribute__((always_inline)) {
+    // One chunk: partial E' S0, R' S0 over this wave's keys, summed across the
+    // KS waves (one barrier; the partial buffers alternate by chunk parity, so
+    // a wave that runs ahead writes the other buffer, and cannot run two
+    // chunks ahead past the next barrier); y = WV - km o E' S0; U = T y;
+    // O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut'^T (km o U).  The
+    // operand set then receives chunk cw + 2.
+    auto step = [&](int cw, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
         const int t0 = (c0 + cw) * kC;
-        load_wv(min(cw + 1, wn - 1), wv_nx);
-        const float *const cur = smem + (cw & 1) * FB;
-        const float *const prv = smem + ((cw + 1) & 1) * FB;   // chunk cw - 1 (until it is refilled below)
-        if (tile_live) {
-            if (cw > 0) update(prv);
-            v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
+        v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
 #pragma unroll
-            for (int kt = 0; kt < KPW; ++kt) {
-                const int kg = ks * KPW + kt;
-                const v4f ea = LdsF4(cur + oE + kg * 256 + lane * 4);
-                const v4f ra = LdsF4(cur + oR + kg * 256 + lane * 4);
+        for (int kt = 0; kt < KPW; ++kt) {
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    xe = Mfma(ea[ii], S[kt][ii], xe);
-                    xr = Mfma(ra[ii], S[kt][ii], xr);
-                }
+            for (int ii = 0; ii < 4; ++ii) {
+                xe = Mfma(o.e[kt][ii], S[kt][ii], xe);
+                xr = Mfma(o.r[kt][ii], S[kt][ii], xr);
             }
-            StF4(sXp + (w * 2 + 0) * 256 + lane * 4, xe);
-            StF4(sXp + (w * 2 + 1) * 256 + lane * 4, xr);
         }
-        __syncthreads();
-        // chunk cw + 1 into the buffer of chunk cw - 1 (read only before the barrier)
-        if (cw + 1 < wn) store_block((cw + 1) & 1, stage_nx);
-        load_block(min(cw + 3, wn - 1), stage_nx);
-        if (tile_live) {
-            v4f xe = LdsF4(sXp + ((ct * KS) * 2 + 0) * 256 + lane * 4);
-            v4f xr = LdsF4(sXp + ((ct * KS) * 2 + 1) * 256 + lane * 4);
+        if constexpr (KS > 1) {
+            float *const xp = sXp + (cw & 1) * (KS * 512);
+            StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
+            StF4(xp + (ks * 2 + 1) * 256 + lane * 4, xr);
+            __syncthreads();
+            // the same summation order in every wave: identical U everywhere
+            xe = LdsF4(xp + lane * 4);
 #pragma unroll
-            for (int z = 1; z < KS; ++z) {
-                xe += LdsF4(sXp + ((ct * KS + z) * 2 + 0) * 256 + lane * 4);
-                xr += LdsF4(sXp + ((ct * KS + z) * 2 + 1) * 256 + lane * 4);
-            }
-            const v4f qm = LdsF4(cur + oMul + 4 * g4);
-            const v4f km = LdsF4(cur + oMul + 16 + 4 * g4);
-            v4f y;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool ok = col_ok && t0 + 4 * g4 + i < T;
-                y[i] = (ok ? wv_cur.w[i] * wv_cur.v[i] : 0.0f) - km[i] * xe[i];   // rows of E' S0 times k_mul
-            }
-            const v4f ta = LdsF4(cur + oT + lane * 4);
-            v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) u = Mfma(ta[ii], y[ii], u);
-            u_prev = km * u;   // the update's Ut' is unnormalised
+            for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
             if (ks == 0) {
-                const v4f ma = LdsF4(cur + oMT + lane * 4);
-                v4f o = qm * xr;   // rows of R' S0 times q_mul
+                xr = LdsF4(xp + 256 + lane * 4);
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) o = Mfma(ma[ii], y[ii], o);
-                if (col_ok) {
+                for (int z = 1; z < KS; ++z) xr += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
+            }
+        }
+        v4f y;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int t = t0 + 4 * g4 + i;
-                        if (t < T) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] = o[i];
-                    }
+        for (int i = 0; i < 4; ++i) {
+            const bool ok = col_ok && t0 + 4 * g4 + i < T;
+            y[i] = (ok ? o.w[i] * o.v[i] : 0.0f) - o.km[i] * xe[i];   // rows of E' S0 times k_mul
+        }
+        v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
+        if (ks == 0) {
+            v4f out = o.qm * xr;   // rows of R' S0 times q_mul
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) out = Mfma(o.mt[ii], y[ii], out);
+            if (col_ok) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = t0 + 4 * g4 + i;
+                    if (t < T) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] = out[i];
                 }
             }
-            if (cw == wn - 1) update(cur);   // state after the window
         }
-        __syncthreads();
+        const v4f uk = o.km * u;   // the update's Ut' is unnormalised
+#pragma unroll
+        for (int kt = 0; kt < KPW; ++kt) {
+            S[kt] *= o.g[kt];
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], uk[ii], S[kt]);
+        }
+        load_ops(min(cw + 2, wn - 1), o);
     };
-    for (int cw = 0; cw < wn; cw += 2) {
-        step(cw, stage1, wv0, wv1);
-        if (cw + 1 < wn) step(cw + 1, stage0, wv1, wv0);
+
+    // two operand sets in turn, with compile-time roles
+    // (the sets' loads in the same order as in the loop: an interleaved
+    // prologue would set the loop's wait counts to its own, shorter distances)
+    ChunkOperands<KPW> opa, opb;
+    load_ops(0, opa);
+    __builtin_amdgcn_sched_barrier(0);
+    load_ops(min(1, wn - 1), opb);
+    // each step leaves the loop or goes on to the other set's step: a path
+    // from one set's step back to itself (no newer loads outstanding, to the
+    // compiler) would take its wait counts to zero
+    for (int cw = 0;; cw += 2) {
+        step(cw, opa);
+        if (cw + 1 >= wn) break;
+        step(cw + 1, opb);
+        if (cw + 2 >= wn) break;
     }
     if (s_out != nullptr && col_ok) {
 #pragma unroll
@@ -552,65 +533,36 @@ __global__ __launch_bounds__(64 * KS * CT) void Gdn2ChunkRecurKernel(GatedDeltaN
 }
 
 struct ChunkConfig {
-    int kpw, ks, ct;
+    int kpw, ks;
 };
 
 // Two key tiles (32 keys) per wave, ks = a power of two waves per column
 // tile (keys padded to 32 ks).  Fewer splits leave too few waves for the
 // chip (one wave per SIMD at best, and half the SIMDs idle for 4 x 16 heads
-// of 128 x 128); more add cross-wave exchanges.  Measured on 4 x 4096 x 16
-// heads, dk = dv = 128: ks = 1, 2, 4 -> 1.18, 0.97, 0.93 ms.
-ChunkConfig ChooseChunk(int batch, int nheads, int dk, int dv) {
+// of 128 x 128); more add cross-wave exchanges.
+ChunkConfig ChooseChunk(int dk) {
     const int kq = (dk + 15) / 16;
-    ChunkConfig c{kq >= 2 ? 2 : 1, 1, 1};
+    ChunkConfig c{kq >= 2 ? 2 : 1, 1};
     const int need = (kq + c.kpw - 1) / c.kpw;
     while (c.ks < need) c.ks *= 2;
-    const long long heads = static_cast<long long>(batch) * nheads;
-    const int vt = (dv + 15) / 16;
-    const char *env = std::getenv("XM_GDN2_CT");   // column tiles per workgroup (test switch)
-    if (env != nullptr) {
-        const int f = std::atoi(env);
-        if ((f == 1 || f == 2 || f == 4) && c.ks * f <= 8) c.ct = f;
-        return c;
-    }
-    // one column tile per workgroup when that gives two workgroups per CU
-    // (their phases drift apart and overlap); two otherwise, where the keys
-    // allow (4 x 16 heads: dv = 128 -> one, 0.93 ms; dv = 65 -> two, 0.85 ms)
-    if (heads * vt < 512 && vt >= 2 && c.ks * 2 <= 8) c.ct = 2;
     return c;
 }
 
-template <int KPW, int KS, int CT>
+template <int KPW, int KS>
 void LaunchRecur(const GatedDeltaNet2Params &p, int c0, int wn, int kq, const float *s_in, float *s_out,
                  hipStream_t stream) {
-    using L = RecurLayout<KPW, KS, CT>;
-    static_assert(L::kBytes <= 160 * 1024, "LDS budget");
-    if (kq != L::KQ) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
+    if (kq != RecurLayout<KPW, KS>::KQ) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
     const int vt = (p.dv + 15) / 16;
-    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((vt + CT - 1) / CT);
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * vt;
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2ChunkRecurKernel<KPW, KS, CT>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
-    hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, CT>), dim3(static_cast<unsigned>(blocks)), dim3(L::THREADS),
-                       L::kBytes, stream, p, c0, wn, s_in, s_out);
-}
-
-template <int KPW, int KS>
-void LaunchRecurCt(const GatedDeltaNet2Params &p, int ct, int c0, int wn, int kq, const float *s_in, float *s_out,
-                   hipStream_t stream) {
-    if constexpr (KS * 4 <= 8) {
-        if (ct == 4) return LaunchRecur<KPW, KS, 4>(p, c0, wn, kq, s_in, s_out, stream);
-    }
-    if constexpr (KS * 2 <= 8) {
-        if (ct == 2) return LaunchRecur<KPW, KS, 2>(p, c0, wn, kq, s_in, s_out, stream);
-    }
-    LaunchRecur<KPW, KS, 1>(p, c0, wn, kq, s_in, s_out, stream);
+    hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, stream,
+                       p, c0, wn, s_in, s_out);
 }
 
 void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0, int wn, int kq, const float *s_in,
                     float *s_out, hipStream_t stream) {
 #define XM_GDN2_RECUR(KPW_, KS_) \
-    if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecurCt<KPW_, KS_>(p, c.ct, c0, wn, kq, s_in, s_out, stream);
+    if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecur<KPW_, KS_>(p, c0, wn, kq, s_in, s_out, stream);
     XM_GDN2_RECUR(1, 1) XM_GDN2_RECUR(2, 1) XM_GDN2_RECUR(2, 2) XM_GDN2_RECUR(2, 4) XM_GDN2_RECUR(2, 8)
 #undef XM_GDN2_RECUR
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
@@ -620,7 +572,7 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
 
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
     if (dk > kChunkKeyLimit) return 0;
-    const ChunkConfig c = ChooseChunk(batch, nheads, dk, dv);
+    const ChunkConfig c = ChooseChunk(dk);
     const int kq = c.kpw * c.ks;
     const int nchunks = (seqlen + kC - 1) / kC;
     const int win = std::min(nchunks, kWindowChunks);
@@ -640,7 +592,7 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, v
     q.pairwise_only = pw != nullptr && std::atoi(pw) != 0;
     auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
     q.vec4_keys = p.dk % 4 == 0 && a16(p.q) && a16(p.k) && a16(p.g) && a16(p.beta);
-    const ChunkConfig c = ChooseChunk(p.batch, p.nheads, p.dk, p.dv);
+    const ChunkConfig c = ChooseChunk(p.dk);
     const int kq = c.kpw * c.ks;
     const int nchunks = (p.seqlen + kC - 1) / kC;
     const int win = std::min(nchunks, kWindowChunks);
