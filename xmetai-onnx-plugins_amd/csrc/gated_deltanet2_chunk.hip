@@ -66,6 +66,27 @@ __device__ __forceinline__ v4f Mfma(float a, float b, v4f c) {
 __device__ __forceinline__ v4f LdsF4(const float *p) { return *reinterpret_cast<const v4f *>(p); }
 __device__ __forceinline__ void StF4(float *p, v4f v) { *reinterpret_cast<v4f *>(p) = v; }
 
+// Raw buffer access: a wave-uniform descriptor (base address, size in bytes)
+// and per-lane byte offsets.  Loads at offsets at or beyond the size return
+// zeros and stores there are dropped, which masks tokens past the sequence
+// end and columns past dv with no branch.  Offsets that must be checked go in
+// the per-lane operand; the scalar operand only ever carries in-range bases.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kRawBufferWord3 = 0x00020000;                       // untyped 32-bit data format
+constexpr int kOutOfRange = static_cast<int>(0x80000000u);        // beyond any descriptor size used here
+__device__ __forceinline__ Rsrc MakeRsrc(const float *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), static_cast<short>(0), bytes, kRawBufferWord3);
+}
+__device__ __forceinline__ v4f BufF4(Rsrc r, int voff, int soff) {
+    return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ float BufF(Rsrc r, int voff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+__device__ __forceinline__ void BufStF(Rsrc r, int voff, float x) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, voff, 0, 0);
+}
+
 // Orders this wave's LDS accesses before and after (the LDS unit serves one
 // wave's operations in order; this stops the compiler from moving them).
 __device__ __forceinline__ void WaveSync() {
@@ -388,7 +409,7 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
     __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
 
     const int T = p.seqlen, H = p.nheads, dk = p.dk, dv = p.dv;
-    const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4;
     const int VT = (dv + 15) / 16;
     const int blk = XcdLocalBlock(blockIdx.x, gridDim.x);
@@ -396,9 +417,19 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
     const int b = bh / H, h = bh % H;
     const int col = vt * 16 + (lane & 15);
     const bool col_ok = col < dv;
-    const int colc = col_ok ? col : 0;
     const size_t sbase = static_cast<size_t>(bh) * dk * dv;
     const float *const prep0 = p.prepared + static_cast<size_t>(bh) * wn * FB;
+    const Rsrc rblk = MakeRsrc(prep0, wn * FB * 4);   // this head's prepared blocks of the window
+    // byte offsets, from a chunk's first token in [B,T,H,V], of this lane's
+    // tokens 4(l/16)+i in its column (out of range for columns past dv); the
+    // per-chunk descriptors of w, v and out end after the chunk's last valid
+    // token, so padded tokens read zeros and are not stored
+    const int HV = H * dv;
+    int vo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vo[i] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
+    auto rows_bytes = [&](int t0) { return ((min(T - t0, kC) - 1) * HV + dv) * 4; };
+    auto token_base = [&](const float *x, int t0) { return x + ((static_cast<size_t>(b) * T + t0) * H + h) * dv; };
 
     v4f S[KPW];
 #pragma unroll
@@ -414,31 +445,32 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
     // Loads are issued on every path (chunk indices clamped to the window):
     // with a load count that depends on the path, the compiler's wait counts
     // turn conservative and a consumer waits for the newest prefetches too.
+    const int lo = lane * 16, go = g4 * 16;   // a lane's 16 bytes of a tile; a lane group's of a row vector
     auto load_ops = [&](int cw, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
-        const float *const bp = prep0 + static_cast<size_t>(cw) * FB;
+        const int sb = cw * (FB * 4);
 #pragma unroll
         for (int kt = 0; kt < KPW; ++kt) {
             const int kg = ks * KPW + kt;
-            o.e[kt] = LdgF4(bp + oE + kg * 256 + lane * 4);
-            o.r[kt] = LdgF4(bp + oR + kg * 256 + lane * 4);
+            o.e[kt] = BufF4(rblk, lo, sb + (oE + kg * 256) * 4);
+            o.r[kt] = BufF4(rblk, lo, sb + (oR + kg * 256) * 4);
         }
         const int t0 = (c0 + cw) * kC;
+        const Rsrc rw = MakeRsrc(token_base(p.w, t0), rows_bytes(t0));
+        const Rsrc rv = MakeRsrc(token_base(p.v, t0), rows_bytes(t0));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = min(t0 + 4 * g4 + i, T - 1);
-            const size_t idx = ((static_cast<size_t>(b) * T + t) * H + h) * dv + colc;
-            o.w[i] = p.w[idx];
-            o.v[i] = p.v[idx];
+            o.w[i] = BufF(rw, vo[i]);
+            o.v[i] = BufF(rv, vo[i]);
         }
-        o.km = LdgF4(bp + oMul + 16 + 4 * g4);
-        o.t = LdgF4(bp + oT + lane * 4);
-        o.qm = LdgF4(bp + oMul + 4 * g4);
-        o.mt = LdgF4(bp + oMT + lane * 4);
+        o.km = BufF4(rblk, go, sb + (oMul + 16) * 4);
+        o.t = BufF4(rblk, lo, sb + oT * 4);
+        o.qm = BufF4(rblk, go, sb + oMul * 4);
+        o.mt = BufF4(rblk, lo, sb + oMT * 4);
 #pragma unroll
         for (int kt = 0; kt < KPW; ++kt) {
             const int kg = ks * KPW + kt;
-            o.g[kt] = LdgF4(bp + oG + kg * 16 + 4 * g4);
-            o.ut[kt] = LdgF4(bp + oU + kg * 256 + lane * 4);
+            o.g[kt] = BufF4(rblk, go, sb + (oG + kg * 16) * 4);
+            o.ut[kt] = BufF4(rblk, lo, sb + (oU + kg * 256) * 4);
         }
     };
 
@@ -474,12 +506,9 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
                 for (int z = 1; z < KS; ++z) xr += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
             }
         }
-        v4f y;
+        v4f y;   // w, v are zero past the sequence end and dv
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool ok = col_ok && t0 + 4 * g4 + i < T;
-            y[i] = (ok ? o.w[i] * o.v[i] : 0.0f) - o.km[i] * xe[i];   // rows of E' S0 times k_mul
-        }
+        for (int i = 0; i < 4; ++i) y[i] = o.w[i] * o.v[i] - o.km[i] * xe[i];   // rows of E' S0 times k_mul
         v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
@@ -487,13 +516,9 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
             v4f out = o.qm * xr;   // rows of R' S0 times q_mul
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) out = Mfma(o.mt[ii], y[ii], out);
-            if (col_ok) {
+            const Rsrc ro = MakeRsrc(token_base(p.out, t0), rows_bytes(t0));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = t0 + 4 * g4 + i;
-                    if (t < T) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] = out[i];
-                }
-            }
+            for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
         }
         const v4f uk = o.km * u;   // the update's Ut' is unnormalised
 #pragma unroll
@@ -586,6 +611,8 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, v
     const char *path = std::getenv("XM_GDN2_PATH");
     if (path != nullptr && std::strcmp(path, "seq") == 0) return false;
     if (p.dk > kChunkKeyLimit) return false;
+    // the recurrence's 32-bit buffer offsets span 16 tokens of [B,T,H,V]
+    if (static_cast<long long>(p.nheads) * p.dv >= (1LL << 25)) return false;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     GatedDeltaNet2Params q = p;
     const char *pw = std::getenv("XM_GDN2_PAIRWISE");
