@@ -480,6 +480,22 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
     // chunks ahead past the next barrier); y = WV - km o E' S0; U = T y;
     // O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut'^T (km o U).  The
     // operand set then receives chunk cw + 2.
+    // the output of a chunk, O = q_mul o R' S0 + (M T) Y, as this wave's
+    // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the 4
+    // with ii % KS == ks); published with the next chunk's E' S0 partials and summed
+    // by wave 0, so the output products are spread over the waves
+    v4f op = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto store_out = [&](int t0, const v4f &out) __attribute__((always_inline)) {
+        const Rsrc ro = MakeRsrc(token_base(p.out, t0), rows_bytes(t0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
+    };
+    auto sum_out = [&](const float *xp) __attribute__((always_inline)) -> v4f {
+        v4f out = LdsF4(xp + 256 + lane * 4);
+#pragma unroll
+        for (int z = 1; z < KS; ++z) out += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
+        return out;
+    };
     auto step = [&](int cw, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
         const int t0 = (c0 + cw) * kC;
         v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
@@ -494,17 +510,13 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
         if constexpr (KS > 1) {
             float *const xp = sXp + (cw & 1) * (KS * 512);
             StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
-            StF4(xp + (ks * 2 + 1) * 256 + lane * 4, xr);
+            StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);   // output partial of chunk cw - 1
             __syncthreads();
             // the same summation order in every wave: identical U everywhere
             xe = LdsF4(xp + lane * 4);
 #pragma unroll
             for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
-            if (ks == 0) {
-                xr = LdsF4(xp + 256 + lane * 4);
-#pragma unroll
-                for (int z = 1; z < KS; ++z) xr += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
-            }
+            if (ks == 0 && cw > 0) store_out(t0 - kC, sum_out(xp));
         }
         v4f y;   // w, v are zero past the sequence end and dv
 #pragma unroll
@@ -512,14 +524,11 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
         v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
-        if (ks == 0) {
-            v4f out = o.qm * xr;   // rows of R' S0 times q_mul
+        op = o.qm * xr;   // rows of R' S0 times q_mul
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) out = Mfma(o.mt[ii], y[ii], out);
-            const Rsrc ro = MakeRsrc(token_base(p.out, t0), rows_bytes(t0));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
-        }
+        for (int ii = 0; ii < 4; ++ii)
+            if (ii % KS == ks) op = Mfma(o.mt[ii], y[ii], op);   // wave-uniform
+        if constexpr (KS == 1) store_out(t0, op);
         const v4f uk = o.km * u;   // the update's Ut' is unnormalised
 #pragma unroll
         for (int kt = 0; kt < KPW; ++kt) {
@@ -545,6 +554,12 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
         if (cw + 1 >= wn) break;
         step(cw + 1, opb);
         if (cw + 2 >= wn) break;
+    }
+    if constexpr (KS > 1) {   // output of the last chunk
+        float *const xp = sXp + (wn & 1) * (KS * 512);
+        StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);
+        __syncthreads();
+        if (ks == 0) store_out((c0 + wn - 1) * kC, sum_out(xp));
     }
     if (s_out != nullptr && col_ok) {
 #pragma unroll
