@@ -1,15 +1,22 @@
 #!/usr/bin/env python3
 """Benchmark of the three recurrent operators on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--settle-ms S] [--gpus 1]
 
 A step is one SelectiveScanFn call over the Mamba-2.8B-layer workload
 (batch 8, d_inner 5120, seqlen 2048, dstate 16, variable B/C, softplus, D,
-delta_bias, z present), inputs resident in HBM.  W untimed steps, then K
-timed steps bracketed by torch.cuda.synchronize(); rank 0 prints one JSON
+delta_bias, z present), inputs resident in HBM.  Untimed calls of the same
+operator for S ms (clock settle), W untimed steps, then K timed steps
+bracketed by torch.cuda.synchronize(); rank 0 prints one JSON
 line on stdout (progress goes to stderr).  GatedDeltaNet2Fn (4 x 4096 x 16
 heads, dk = dv = 128, with initial state) and Mamba3SisoFn (4 x 4096 x 32
 heads, P = 64, N = 128) are timed the same way and reported under "ops".
+
+The settle phase is there because the GPU's power management reacts to a
+VALU-heavy load started from idle: the first calls run at ~0.36 ms, the
+next ~40 at up to 0.48 ms, and from about call 100 on the selective scan
+holds ~0.34 ms.  K steps taken right after W = 3 would time that transient
+rather than sustained throughput.
 
 Throughput is tokens/s = batch * seqlen / time; the roofline figures use the
 algorithmic bytes of xmetai_onnx_plugins.workloads (unique input bytes the
@@ -104,8 +111,13 @@ def to_device(inputs, dev):
     return {k: (None if v is None else torch.from_numpy(np.ascontiguousarray(v)).to(dev)) for k, v in inputs.items()}
 
 
-def time_op(op, dev_inputs, steps, warmup):
+def time_op(op, dev_inputs, steps, warmup, settle_ms=0.0):
     import torch
+    end = time.perf_counter() + settle_ms / 1e3
+    while time.perf_counter() < end:   # untimed: the clock settles under this load
+        for _ in range(8):
+            op["call"](dev_inputs)
+        torch.cuda.synchronize()
     for _ in range(warmup):
         op["call"](dev_inputs)
     torch.cuda.synchronize()
@@ -236,7 +248,7 @@ def cpu_baseline(op, inputs, budget_s):
 
 # ---------------------------------------------------------------------------
 
-def time_extra_configs(dev, steps):
+def time_extra_configs(dev, steps, settle_ms):
     """The reference's other configurations (CPU-sized selective scan, GDN-2
     dispatch boundaries): device time only, same inputs and timing as above."""
     import torch
@@ -257,7 +269,7 @@ def time_extra_configs(dev, steps):
             call = lambda d, s=s, keys=keys: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale)
             nbytes = W.gated_deltanet2_bytes(s)
         d = to_device(inp, dev)
-        _, per = time_op(dict(call=call), d, steps, 2)
+        _, per = time_op(dict(call=call), d, steps, 2, settle_ms)
         ms = statistics.median(per)
         tokens = s.batch * s.seqlen
         out[name] = dict(ms_per_call_median=round(ms, 4), tokens_per_s=tokens / (ms / 1e3),
@@ -279,8 +291,10 @@ def traffic_from_profiles(workload):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-ms", type=float, default=500.0,
+                    help="untimed calls of each operator for this long before its warmup steps")
     ap.add_argument("--ops", default="selective_scan,gated_deltanet2,mamba3_siso")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline budget per op (seconds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -318,7 +332,7 @@ def main():
         d = to_device(op["gen"](), dev)
         if "device_extra" in op:
             d.update(op["device_extra"](dev))
-        wall, per = time_op(op, d, args.steps, args.warmup)
+        wall, per = time_op(op, d, args.steps, args.warmup, args.settle_ms)
         log(f"{name}: {statistics.median(per):.3f} ms/call (median of {args.steps})")
         return
 
@@ -335,8 +349,8 @@ def main():
         if "device_extra" in op:
             d.update(op["device_extra"](dev))
         torch.cuda.synchronize()
-        log(f"{name}: timing {args.warmup} warmup + {args.steps} steps")
-        wall, per = time_op(op, d, args.steps, args.warmup)
+        log(f"{name}: timing {args.settle_ms:.0f} ms settle + {args.warmup} warmup + {args.steps} steps")
+        wall, per = time_op(op, d, args.steps, args.warmup, args.settle_ms)
         ev_ms = sum(per) / len(per)
         med_ms = statistics.median(per)
         gbps = op["nbytes"] / (med_ms / 1e3) / 1e9
@@ -356,7 +370,7 @@ def main():
         del d, host
         torch.cuda.empty_cache()
 
-    extra = {} if args.no_extra_configs else time_extra_configs(dev, min(args.steps, 10))
+    extra = {} if args.no_extra_configs else time_extra_configs(dev, min(args.steps, 20), min(args.settle_ms, 200.0))
 
     log("achievable HBM: 2 GiB device copy")
     ach = achievable_hbm(dev)
@@ -376,6 +390,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": wall * 1e3 / steps,
         "higher_is_better": True,
         "scaling": "weak",
