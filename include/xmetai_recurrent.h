@@ -117,8 +117,16 @@ int xm_selective_scan_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
  * Output 0: [B,T,H,P] (reference: mamba3_siso_fn_ort.cpp:61-111).
  * Attributes (reference: :43-59): chunk_size (default 64, must be > 0, not
  * otherwise used), has_d and has_z (default 1, must match the presence of D
- * and Z), return_final_states, has_input_states, has_cu_seqlens (default 0;
- * non-zero rejected).  */
+ * and Z), return_final_states and has_input_states (default 0; the reference
+ * rejects non-zero, here they select the states below), has_cu_seqlens
+ * (default 0; non-zero rejected).
+ * States (a widening with no counterpart in the reference, which rejects them
+ * at mamba3_siso_fn_ort.cpp:50-55): ssm [B,H,P,N], angle [B,H,A], k [B,H,N],
+ * v [B,H,P] -- the scan state and the angle state after the last token, that
+ * token's rotated k and its V.  With has_input_states != 0 they are inputs
+ * 11-14 (15 inputs) and the scan starts from ssm + v (x) k * DT_0 *
+ * (1 - sigmoid(Trap_0)) and angle, so that two calls chained through the
+ * states give the outputs and states of one call.  */
 typedef struct xm_mamba3_siso_attrs {
     int64_t chunk_size;
     int64_t has_d;
@@ -133,9 +141,19 @@ int xm_mamba3_siso_check_attrs(const xm_mamba3_siso_attrs_t *attrs, char *errbuf
 int xm_mamba3_siso_validate(const xm_tensor_t *inputs, size_t n_inputs,
                             const xm_mamba3_siso_attrs_t *attrs, int64_t *out_shape,
                             int32_t *out_rank, size_t *scratch_bytes, char *errbuf, size_t errlen);
+/* With return_final_states != 0 this entry point fails (use the one below). */
 int xm_mamba3_siso_forward(const xm_tensor_t *inputs, size_t n_inputs,
                            const xm_mamba3_siso_attrs_t *attrs, float *out, void *stream,
                            const xm_allocator_t *alloc, char *errbuf, size_t errlen);
+/* As above; with return_final_states != 0 it also writes the four states
+ * after the last token to device buffers ssm_state [B,H,P,N], angle_state
+ * [B,H,A], k_state [B,H,N] and v_state [B,H,P] (the layouts inputs 11-14
+ * take).  The buffers are ignored (may be NULL) when return_final_states == 0.
+ * A widening with no counterpart in the reference (mamba3_siso_fn_ort.cpp:50-52). */
+int xm_mamba3_siso_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
+                                  const xm_mamba3_siso_attrs_t *attrs, float *out, float *ssm_state,
+                                  float *angle_state, float *k_state, float *v_state, void *stream,
+                                  const xm_allocator_t *alloc, char *errbuf, size_t errlen);
 
 /* ---- GatedDeltaNet2Fn -----------------------------------------------------
  * Inputs: 0 q [B,T,H,K]; 1 k [B,T,H,K]; 2 v [B,T,H,V]; 3 g [B,T,H,K]

@@ -105,8 +105,10 @@ def gated_deltanet2(q, k, v, g, beta, w, initial_state=None, scale=1.0,
 
 
 def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
-                dtype=np.float64):
-    """See xmo_mamba3_siso in xm_oracle.c."""
+                dtype=np.float64, input_states=None, return_state=False):
+    """See xmo_mamba3_siso in xm_oracle.c.  ``input_states`` is ``(ssm [B,H,P,N],
+    angle [B,H,A], k [B,H,N], v [B,H,P])`` or None; with ``return_state``
+    returns ``(y, (ssm, angle, k, v))``, the same four after the last token."""
     Q_, Qp = _fp(Q); K_, Kp = _fp(K); V_, Vp = _fp(V)
     a_, ap = _fp(ADT); dt_, dtp = _fp(DT); tr_, trp = _fp(Trap)
     qb_, qbp = _fp(Q_bias); kb_, kbp = _fp(K_bias); an_, anp = _fp(Angles)
@@ -114,11 +116,18 @@ def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
     batch, seqlen, nheads_qk, n = Q_.shape
     nheads, p = V_.shape[2], V_.shape[3]
     a_dim = an_.shape[3]
+    ins = input_states if input_states is not None else (None, None, None, None)
+    (is_, isp), (ia_, iap), (ik_, ikp), (iv_, ivp) = (_fp(x) for x in ins)
     out, op = _out((batch, seqlen, nheads, p), dtype)
+    if return_state:
+        shapes = ((batch, nheads, p, n), (batch, nheads, a_dim), (batch, nheads, n), (batch, nheads, p))
+        fs = [_out(sh, dtype) for sh in shapes]
+    else:
+        fs = [(None, None)] * 4
     getattr(lib(), "xmo_mamba3_siso" + _sfx(dtype))(
         Qp, Kp, Vp, ap, dtp, trp, qbp, kbp, anp, Dp, Zp, batch, seqlen, nheads, nheads_qk,
-        n, p, a_dim, op)
-    return out
+        n, p, a_dim, isp, iap, ikp, ivp, op, *(x[1] for x in fs))
+    return (out, tuple(x[0] for x in fs)) if return_state else out
 
 
 def _setup_signatures():

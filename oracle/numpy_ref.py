@@ -187,7 +187,7 @@ def _sigmoid(x, dtype):
 
 
 def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
-                dtype=np.float64):
+                dtype=np.float64, input_states=None, return_state=False):
     """Output of Mamba3SisoFn (forward, no input/final state, no cu_seqlens).
 
     Follows mamba3_siso_fwd.cu:79-171: per step the angle state is advanced by
@@ -201,6 +201,12 @@ def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
 
     Shapes: Q, K [B,T,Hq,N]; V [B,T,H,P]; ADT, DT, Trap [B,H,T]; Q_bias,
     K_bias [H,N]; Angles [B,T,H,A]; D [H] or absent; Z [B,T,H,P] or absent.
+
+    States (a widening; the reference rejects them, mamba3_siso_fn_ort.cpp:50-55):
+    ``input_states`` = (ssm [B,H,P,N], angle [B,H,A], k [B,H,N], v [B,H,P]) starts
+    from S = ssm + v (x) k * DT_0 (1 - sigmoid(Trap_0)) (the previous call's last
+    token's look-ahead, :126-134) and theta = angle; ``return_state`` also
+    returns those four after the last token (its rotated k and its V).
     """
     Q = _as(Q, dtype); K = _as(K, dtype); V = _as(V, dtype)
     ADT = _as(ADT, dtype); DT = _as(DT, dtype); Trap = _as(Trap, dtype)
@@ -216,10 +222,17 @@ def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
     Zv = _as(Z, dtype) if has_z else None
     pi = dtype(PI_F32)
 
-    S = np.zeros((batch, nheads, p_dim, n), dtype)
-    theta = np.zeros((batch, nheads, a_dim), dtype)
     out = np.empty((batch, seqlen, nheads, p_dim), dtype)
     sig_trap = _sigmoid(Trap, dtype)                          # [B,H,T]
+    if input_states is not None:
+        s_in, a_in, k_in, v_in = (_as(x, dtype) for x in input_states)
+        look0 = DT[:, :, 0] * (dtype(1.0) - sig_trap[:, :, 0])   # [B,H]
+        S = s_in + v_in[..., :, None] * (k_in[..., None, :] * look0[..., None, None])
+        theta = a_in.copy()
+    else:
+        S = np.zeros((batch, nheads, p_dim, n), dtype)
+        theta = np.zeros((batch, nheads, a_dim), dtype)
+    k_rot = np.zeros((batch, nheads, n), dtype)
     for t in range(seqlen):
         dt = DT[:, :, t]                                       # [B,H]
         theta = _wrap_two_pi(theta + np.tanh(Ang[:, t]) * dt[..., None] * pi, dtype)
@@ -249,6 +262,8 @@ def mamba3_siso(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None,
             y = y * (zt * _sigmoid(zt, dtype))
         out[:, t] = y
         S += V[:, t][..., None] * k_scaled[:, :, None, :]
+    if return_state:
+        return out, (S, theta, k_rot, V[:, seqlen - 1].copy())
     return out
 
 

@@ -226,11 +226,24 @@ static real sigmoid_r(real x) { return (real)1 / ((real)1 + r_exp(-x)); }
  * per-step wrap of the angle state (:26-28, :82-86), the unrotated q.k diagonal
  * term (:89-106), rotation of pairs below A (:108-123), the trapezoid look-ahead
  * (:126-134), decay before readout (:140-161) and the update after it (:164-169).
+ *
+ * States (a widening: the reference rejects has_input_states and
+ * return_final_states, mamba3_siso_fn_ort.cpp:50-55).  The state after a call
+ * is (ssm [B,H,P,N], angle [B,H,A], k [B,H,N], v [B,H,P]): S and the angle
+ * state after the last token (whose look-ahead is 0, :126-134), and that
+ * token's rotated k and its v.  A call given these states starts from
+ * S = ssm + v (x) k * DT_0 (1 - sigmoid(Trap_0)), the last token's look-ahead
+ * now that its successor is known, and the angle state; so two calls chained
+ * through the states give the outputs and states of one call.  in_* may be
+ * NULL (zero state); f_* may be NULL (not written).
  */
 void XMO_NAME(xmo_mamba3_siso)(const float *Q, const float *K, const float *V, const float *ADT,
                                const float *DT, const float *Trap, const float *Qb, const float *Kb,
                                const float *Ang, const float *D, const float *Z, int batch, int seqlen,
-                               int nheads, int nheads_qk, int n, int p, int a_dim, real *out) {
+                               int nheads, int nheads_qk, int n, int p, int a_dim,
+                               const float *in_ssm, const float *in_ang, const float *in_k,
+                               const float *in_v, real *out, real *f_ssm, real *f_ang, real *f_k,
+                               real *f_v) {
     const int nbh = batch * nheads;
     const int grp = nheads / nheads_qk;
     const real pi = (real)kPiF;
@@ -246,9 +259,18 @@ void XMO_NAME(xmo_mamba3_siso)(const float *Q, const float *K, const float *V, c
             const int b = bh / nheads;
             const int h = bh % nheads;
             const int gq = h / grp;
-            memset(S, 0, sizeof(real) * (size_t)p * n);
-            for (int a = 0; a < a_dim; ++a) th[a] = 0;
             const float *dtr = DT + (size_t)bh * seqlen, *trr = Trap + (size_t)bh * seqlen, *adr = ADT + (size_t)bh * seqlen;
+            if (in_ssm) {
+                const real look0 = seqlen > 0 ? (real)dtr[0] * ((real)1 - sigmoid_r((real)trr[0])) : (real)0;
+                for (int r = 0; r < p; ++r)
+                    for (int i = 0; i < n; ++i)
+                        S[(size_t)r * n + i] = (real)in_ssm[((size_t)bh * p + r) * n + i] +
+                                               (real)in_v[(size_t)bh * p + r] * ((real)in_k[(size_t)bh * n + i] * look0);
+                for (int a = 0; a < a_dim; ++a) th[a] = (real)in_ang[(size_t)bh * a_dim + a];
+            } else {
+                memset(S, 0, sizeof(real) * (size_t)p * n);
+                for (int a = 0; a < a_dim; ++a) th[a] = 0;
+            }
             for (int t = 0; t < seqlen; ++t) {
                 const real dt = (real)dtr[t];
                 const float *angr = Ang + (((size_t)b * seqlen + t) * nheads + h) * a_dim;
@@ -300,6 +322,13 @@ void XMO_NAME(xmo_mamba3_siso)(const float *Q, const float *K, const float *V, c
                     for (int i = 0; i < n; ++i) Sr[i] += vv * (kv[i] * ksc);
                 }
             }
+            if (f_ssm) memcpy(f_ssm + (size_t)bh * p * n, S, sizeof(real) * (size_t)p * n);
+            if (f_ang)
+                for (int a = 0; a < a_dim; ++a) f_ang[(size_t)bh * a_dim + a] = th[a];
+            if (f_k && seqlen > 0)
+                for (int i = 0; i < n; ++i) f_k[(size_t)bh * n + i] = kv[i];   /* rotated k of the last token */
+            if (f_v && seqlen > 0)
+                for (int r = 0; r < p; ++r) f_v[(size_t)bh * p + r] = (real)V[(((size_t)b * seqlen + seqlen - 1) * nheads + h) * p + r];
         }
         free(S); free(th); free(qv); free(kv);
     }

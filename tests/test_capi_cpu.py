@@ -67,8 +67,6 @@ def test_attribute_defaults_match_reference():
 
 @pytest.mark.parametrize("op,kw,msg,status", [
     ("mamba3_siso", dict(chunk_size=0), "Mamba3SisoFn requires chunk_size > 0", xp.XM_ERR_INVALID_ARGUMENT),
-    ("mamba3_siso", dict(return_final_states=1), "Mamba3SisoFn v1 does not support return_final_states", xp.XM_ERR_UNSUPPORTED),
-    ("mamba3_siso", dict(has_input_states=1), "Mamba3SisoFn v1 does not support input states", xp.XM_ERR_UNSUPPORTED),
     ("mamba3_siso", dict(has_cu_seqlens=1), "Mamba3SisoFn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(use_gate_in_kernel=1), "GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(has_cu_seqlens=1), "GatedDeltaNet2Fn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
@@ -95,18 +93,17 @@ def test_attribute_check_order_matches_reference():
 
 
 def test_state_attributes_are_accepted():
-    # Widening: the reference rejects these two; here they select the state
-    # output of the *_forward_states entry points.  Mamba-3's stays rejected.
+    # Widening: the reference rejects these; here they select the state
+    # outputs of the *_forward_states entry points (and Mamba-3's state inputs).
     check_attrs("selective_scan", return_last_state=1, delta_softplus=1)
     check_attrs("gated_deltanet2", output_final_state=1, scale=0.5)
-    with pytest.raises(XmError, match="return_final_states"):
-        check_attrs("mamba3_siso", return_final_states=1)
+    check_attrs("mamba3_siso", return_final_states=1, has_input_states=1)
 
 
-def _forward_host_error(op, shapes, entry, state_ptr=None, **attrs):
+def _forward_host_error(op, shapes, entry, state_ptrs=(None,), **attrs):
     """Calls a forward entry point on shape-only descriptors with a host-side
     error expected before any device work; returns (status, message)."""
-    _, n = xp._capi.OPS[op]
+    n = len(shapes)
     arr = (xp._capi.XmTensor * n)(*[xp._desc_from_shape(sh if sh is not None else (0,)) for sh in shapes])
     a = xp._attrs(op, **attrs)
     err = ctypes.create_string_buffer(512)
@@ -115,7 +112,7 @@ def _forward_host_error(op, shapes, entry, state_ptr=None, **attrs):
     if entry == "forward":
         st = fn(arr, n, ctypes.byref(a), out, None, None, err, len(err))
     else:
-        st = fn(arr, n, ctypes.byref(a), out, state_ptr, None, None, err, len(err))
+        st = fn(arr, n, ctypes.byref(a), out, *state_ptrs, None, None, err, len(err))
     return st, err.value.decode()
 
 
@@ -124,19 +121,24 @@ def test_plain_forward_refuses_a_state_request():
     assert st == xp.XM_ERR_INVALID_ARGUMENT and "xm_selective_scan_forward_states" in msg
     st, msg = _forward_host_error("gated_deltanet2", gdn_shapes(), "forward", output_final_state=1)
     assert st == xp.XM_ERR_INVALID_ARGUMENT and "xm_gated_deltanet2_forward_states" in msg
+    st, msg = _forward_host_error("mamba3_siso", m3_shapes(), "forward", return_final_states=1, has_z=0)
+    assert st == xp.XM_ERR_INVALID_ARGUMENT and "xm_mamba3_siso_forward_states" in msg
 
 
 def test_states_entry_needs_a_state_buffer():
-    st, msg = _forward_host_error("selective_scan", ss_shapes(), "forward_states", None, return_last_state=1)
+    st, msg = _forward_host_error("selective_scan", ss_shapes(), "forward_states", (None,), return_last_state=1)
     assert (st, msg) == (xp.XM_ERR_INVALID_ARGUMENT, "return_last_state=1 needs a last_state buffer")
-    st, msg = _forward_host_error("gated_deltanet2", gdn_shapes(), "forward_states", None, output_final_state=1)
+    st, msg = _forward_host_error("gated_deltanet2", gdn_shapes(), "forward_states", (None,), output_final_state=1)
     assert (st, msg) == (xp.XM_ERR_INVALID_ARGUMENT, "output_final_state=1 needs a final_state buffer")
+    some = (ctypes.c_void_p(16), ctypes.c_void_p(16), None, ctypes.c_void_p(16))   # one of the four missing
+    st, msg = _forward_host_error("mamba3_siso", m3_shapes(), "forward_states", some, return_final_states=1, has_z=0)
+    assert (st, msg) == (xp.XM_ERR_INVALID_ARGUMENT, "return_final_states=1 needs four state buffers")
 
 
 def test_states_entry_validates_shapes_first():
     bad = ss_shapes()
     bad[1] = (2, 8, 15)
-    st, msg = _forward_host_error("selective_scan", bad, "forward_states", None, return_last_state=1)
+    st, msg = _forward_host_error("selective_scan", bad, "forward_states", (None,), return_last_state=1)
     assert st == xp.XM_ERR_INVALID_ARGUMENT and "needs a last_state buffer" not in msg
 
 
@@ -302,6 +304,36 @@ def m3_shapes(B=2, T=7, H=4, Hq=2, P=8, N=16, A=8, has_d=True, has_z=False):
             (B, T, H, A), (H,) if has_d else None, (B, T, H, P) if has_z else None]
 
 
+def m3_state_shapes(B=2, H=4, P=8, N=16, A=8):
+    return [(B, H, P, N), (B, H, A), (B, H, N), (B, H, P)]
+
+
+def test_m3_input_states_take_inputs_11_to_14():
+    # Widening: has_input_states=1 adds the four states as inputs 11-14.
+    out, scratch = validate("mamba3_siso", m3_shapes() + m3_state_shapes(), has_input_states=1, has_z=0)
+    assert out == (2, 7, 4, 8) and scratch == 0
+    with pytest.raises(XmError, match="expects 15 inputs, got 11"):
+        validate("mamba3_siso", m3_shapes(), has_input_states=1, has_z=0)
+    with pytest.raises(XmError, match="expects 11 inputs, got 15"):
+        validate("mamba3_siso", m3_shapes() + m3_state_shapes(), has_z=0)
+
+
+@pytest.mark.parametrize("i,shape,msg", [
+    (0, (2, 4, 16, 8), "ssm_state must have shape (batch, nheads, headdim_v, headdim_qk)"),
+    (0, (2, 4, 8), "ssm_state must have rank 4"),
+    (1, (2, 4, 7), "angle_state must have shape (batch, nheads, headdim_angles)"),
+    (2, (2, 2, 16), "k_state must have shape (batch, nheads, headdim_qk)"),
+    (3, (2, 4, 16), "v_state must have shape (batch, nheads, headdim_v)"),
+    (3, None, "v_state must have rank 3"),
+])
+def test_m3_input_state_shapes(i, shape, msg):
+    st = m3_state_shapes()
+    st[i] = shape
+    with pytest.raises(XmError) as e:
+        validate("mamba3_siso", m3_shapes() + st, has_input_states=1, has_z=0)
+    assert e.value.message == msg
+
+
 def test_m3_valid():
     out, scratch = validate("mamba3_siso", m3_shapes(), has_d=1, has_z=0)
     assert out == (2, 7, 4, 8) and scratch == 0
@@ -369,11 +401,13 @@ def test_ort_registration_domain_and_order():
 def test_ort_descriptors_match_reference_contract():
     ops = _src("ops_ort.cpp")
     # output 1 (optional) is the state after the last token where the op has one
-    for name, n_in, n_out in (("SelectiveScanFn", 8, 2), ("Mamba3SisoFn", 11, 1), ("GatedDeltaNet2Fn", 7, 2)):
-        block = ops[ops.index(f'return "{name}";') - 400:ops.index(f'return "{name}";') + 600]
+    # (Mamba-3: inputs 11-14 optional, the input states)
+    for name, n_in, n_out in (("SelectiveScanFn", 8, 2), ("Mamba3SisoFn", 15, 5), ("GatedDeltaNet2Fn", 7, 2)):
+        block = ops[ops.index(f'return "{name}";') - 400:ops.index(f'return "{name}";') + 800]
         assert f"GetInputTypeCount() const {{ return {n_in}; }}" in block
         assert f"GetOutputTypeCount() const {{ return {n_out}; }}" in block
-        assert ("INPUT_OUTPUT_OPTIONAL" in block) == (n_out == 2)
+        assert "return i == 0 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;" in block
+        assert ("GetInputCharacteristic" in block) == (name == "Mamba3SisoFn")
         assert "GetExecutionProviderType() const { return XM_ORT_GPU_EP; }" in block
     for attr in ("delta_softplus", "return_last_state", "chunk_size", "has_d", "has_z", "return_final_states",
                  "has_input_states", "has_cu_seqlens", "scale", "use_qk_l2norm_in_kernel", "output_final_state",

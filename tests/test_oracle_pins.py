@@ -540,6 +540,114 @@ def test_m3_numpy_and_c_agree():
         np.testing.assert_allclose(numpy_ref.mamba3_siso(**a, dtype=dt), cref.mamba3_siso(**a, dtype=dt), rtol=tol, atol=tol)
 
 
+# ---- Mamba-3 states (a widening: the reference rejects them) --------------
+
+def m3_states_closed_form(a, ins=None):
+    """Outputs and states (ssm, angle, k, v) in matrix form.  From
+    S0 = ssm + v (x) k * DT_0 (1 - sigmoid(Trap_0)) and theta_0 = angle:
+      y_t += e^{sum_{r<=t} ADT_r} (R_t q_t) . S0 (the decayed initial state),
+      S_T = e^{sum ADT} S0 + sum_s e^{sum_{r>s} ADT_r} (gamma_s + look_s) V_s (x) R_s k_s (look_{T-1} = 0),
+      angle_T = theta_{T-1}, k_T = R_{T-1} k_{T-1}, v_T = V_{T-1}."""
+    Q, K, V = a["Q"].astype(F64), a["K"].astype(F64), a["V"].astype(F64)
+    ADT, DT, Trap = a["ADT"].astype(F64), a["DT"].astype(F64), a["Trap"].astype(F64)
+    Qb, Kb, Ang = a["Q_bias"].astype(F64), a["K_bias"].astype(F64), a["Angles"].astype(F64)
+    D = a["D"]; Z = a["Z"]
+    Bt, T, Hq, N = Q.shape
+    H, P = V.shape[2], V.shape[3]
+    Adim = Ang.shape[3]
+    out = np.zeros((Bt, T, H, P))
+    fs = (np.zeros((Bt, H, P, N)), np.zeros((Bt, H, Adim)), np.zeros((Bt, H, N)), np.zeros((Bt, H, P)))
+    for b in range(Bt):
+        for h in range(H):
+            g = h // (H // Hq)
+            q = Q[b, :, g] + Qb[h]; k = K[b, :, g] + Kb[h]
+            look0 = DT[b, h, 0] * (1 - sig64(Trap[b, h, 0]))
+            if ins is None:
+                S0, th0 = np.zeros((P, N)), np.zeros(Adim)
+            else:
+                S0 = ins[0][b, h].astype(F64) + np.outer(ins[3][b, h].astype(F64), ins[2][b, h].astype(F64)) * look0
+                th0 = ins[1][b, h].astype(F64)
+            inc = np.tanh(Ang[b, :, h]) * DT[b, h][:, None] * PI_F
+            theta = np.mod(th0[None] + np.cumsum(inc, axis=0), TWO_PI_F)
+            def rot(x):
+                y = x.copy()
+                for p in range(Adim):
+                    c, s = np.cos(theta[:, p]), np.sin(theta[:, p])
+                    y[:, 2 * p] = c * x[:, 2 * p] - s * x[:, 2 * p + 1]
+                    y[:, 2 * p + 1] = s * x[:, 2 * p] + c * x[:, 2 * p + 1]
+                return y
+            qr, kr = rot(q), rot(k)
+            gam = DT[b, h] * sig64(Trap[b, h])
+            look = np.zeros(T); look[:-1] = DT[b, h, 1:] * (1 - sig64(Trap[b, h, 1:]))
+            cs = np.cumsum(ADT[b, h])
+            Dec = np.exp(cs[:, None] - cs[None, :]) * np.tril(np.ones((T, T)), -1)
+            y = ((qr @ kr.T) * Dec * (gam + look)[None, :]) @ V[b, :, h]
+            y += ((0 if D is None else float(D[h])) + (q * k).sum(1) * gam)[:, None] * V[b, :, h]
+            y += (qr * np.exp(cs)[:, None]) @ S0.T
+            if Z is not None:
+                zz = Z[b, :, h].astype(F64)
+                y = y * zz * sig64(zz)
+            out[b, :, h] = y
+            wts = np.exp(cs[-1] - cs) * (gam + look)
+            fs[0][b, h] = np.exp(cs[-1]) * S0 + (V[b, :, h] * wts[:, None]).T @ kr
+            fs[1][b, h] = theta[-1]
+            fs[2][b, h] = kr[-1]
+            fs[3][b, h] = V[b, -1, h]
+    return out, fs
+
+
+def m3_rand_states(rng, a):
+    Bt, _, _, N = a["Q"].shape
+    H, P, Adim = a["V"].shape[2], a["V"].shape[3], a["Angles"].shape[3]
+    return (rnd(rng, Bt, H, P, N, scale=0.3), rng.uniform(0, 6.28, (Bt, H, Adim)).astype(np.float32),
+            rnd(rng, Bt, H, N, scale=N ** -0.5), rnd(rng, Bt, H, P))
+
+
+@pytest.mark.parametrize("with_inputs", [False, True])
+def test_m3_states_match_closed_form(impl, with_inputs):
+    rng = np.random.default_rng(28)
+    a = m3_rand(rng, 2, 9, 2, 3, 8, 3, Hq=1, z=True)
+    ins = m3_rand_states(rng, a) if with_inputs else None
+    y, st = impl.mamba3_siso(**a, dtype=F64, input_states=ins, return_state=True)
+    ry, rst = m3_states_closed_form(a, ins)
+    np.testing.assert_allclose(y, ry, rtol=1e-9, atol=1e-11)
+    for got, want, name in zip(st, rst, ("ssm", "angle", "k", "v")):
+        np.testing.assert_allclose(got, want, rtol=1e-9, atol=1e-11, err_msg=name)
+
+
+@pytest.mark.parametrize("split", [1, 6, 12])
+def test_m3_chained_calls_equal_one_call(split):
+    """Tokens [0, split) then [split, T) continued from the first call's states
+    give the outputs and states of one call (the previous call's last token's
+    look-ahead is added with the next call's first DT and Trap)."""
+    rng = np.random.default_rng(29)
+    a = m3_rand(rng, 2, 13, 2, 3, 8, 3, z=True)
+    y, st = numpy_ref.mamba3_siso(**a, dtype=F64, return_state=True)
+    def part(lo, hi):
+        p = dict(a)
+        for k in ("Q", "K", "V", "Angles", "Z"):
+            p[k] = a[k][:, lo:hi]
+        for k in ("ADT", "DT", "Trap"):
+            p[k] = a[k][:, :, lo:hi]
+        return p
+    y1, s1 = numpy_ref.mamba3_siso(**part(0, split), dtype=F64, return_state=True)
+    y2, s2 = numpy_ref.mamba3_siso(**part(split, 13), dtype=F64, input_states=s1, return_state=True)
+    np.testing.assert_allclose(np.concatenate([y1, y2], axis=1), y, rtol=1e-12, atol=1e-13)
+    for got, want in zip(s2, st):
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-13)
+
+
+def test_m3_states_numpy_and_c_agree():
+    rng = np.random.default_rng(30)
+    a = m3_rand(rng, 2, 21, 3, 5, 8, 3, Hq=1, z=True)
+    ins = m3_rand_states(rng, a)
+    yn, sn = numpy_ref.mamba3_siso(**a, dtype=F64, input_states=ins, return_state=True)
+    yc, sc = cref.mamba3_siso(**a, dtype=F64, input_states=ins, return_state=True)
+    np.testing.assert_allclose(yn, yc, rtol=1e-12, atol=1e-12)
+    for x, z in zip(sn, sc):
+        np.testing.assert_allclose(x, z, rtol=1e-12, atol=1e-12)
+
+
 # ---------------------------------------------------------------------------
 # SoftmaxCPU
 # ---------------------------------------------------------------------------

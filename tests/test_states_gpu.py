@@ -1,4 +1,5 @@
-"""State outputs on the GPU vs the fp64 oracle, through the C ABI.
+"""State outputs (and Mamba-3's state inputs) on the GPU vs the fp64 oracle,
+through the C ABI.
 
 SelectiveScanFn with return_last_state=1 writes the scan state after the last
 token, [B,D,N]; GatedDeltaNet2Fn with output_final_state=1 writes the state
@@ -16,8 +17,8 @@ import numpy as np
 import pytest
 
 from oracle import cref
-from parity import TOL_GDN2, TOL_SS, check, to_dev
-from xmetai_onnx_plugins import gated_deltanet2_fn, selective_scan_fn, workloads as W
+from parity import TOL_GDN2, TOL_M3, TOL_SS, check, to_dev
+from xmetai_onnx_plugins import gated_deltanet2_fn, mamba3_siso_fn, selective_scan_fn, workloads as W
 
 pytestmark = pytest.mark.gpu
 
@@ -171,3 +172,100 @@ def test_gdn2_final_state_chains(shape, split):
     # the same arithmetic in the same order, with the state passing through fp32 memory
     check(f"gated_deltanet2_state/chain_{split}/o", chained, whole, 1e-5)
     check(f"gated_deltanet2_state/chain_{split}/S", st2.cpu().numpy(), st.cpu().numpy(), 1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Mamba3SisoFn states (ssm [B,H,P,N], angle [B,H,A], k [B,H,N], v [B,H,P])
+# ---------------------------------------------------------------------------
+
+M3_KEYS = ("Q", "K", "V", "ADT", "DT", "Trap", "Q_bias", "K_bias", "Angles", "D", "Z")
+M3 = W.Mamba3SisoShape
+M3_STATE_NAMES = ("ssm", "angle", "k", "v")
+
+
+def m3_states_for(s, seed):
+    rng = np.random.default_rng(seed)
+    B, H, P, N, A = s.batch, s.nheads, s.headdim, s.dstate, s.a
+    return ((0.3 * rng.standard_normal((B, H, P, N))).astype(np.float32),
+            rng.uniform(0.0, 6.28, (B, H, A)).astype(np.float32),
+            (rng.standard_normal((B, H, N)) * N ** -0.5).astype(np.float32),
+            rng.standard_normal((B, H, P)).astype(np.float32))
+
+
+def m3_gpu(inp, ins=None, state=True):
+    import torch
+    r = mamba3_siso_fn(*(to_dev(inp[k]) for k in M3_KEYS),
+                       input_states=None if ins is None else tuple(to_dev(x) for x in ins),
+                       return_final_states=state)
+    torch.cuda.synchronize()
+    if state:
+        return r[0].cpu().numpy(), [x.cpu().numpy() for x in r[1]]
+    return r.cpu().numpy()
+
+
+def m3_ref(inp, ins=None):
+    return cref.mamba3_siso(*(inp[k] for k in M3_KEYS), dtype=np.float64, input_states=ins, return_state=True)
+
+
+def check_m3_states(tag, got, ref, tol):
+    for g, r, nm in zip(got, ref, M3_STATE_NAMES):
+        if nm == "angle":   # compare on the circle: a wrap near 0 / 2 pi may fall either side
+            two_pi = 2.0 * float(np.float32(np.pi))
+            g = r + (np.mod(g - r + two_pi / 2, two_pi) - two_pi / 2)
+        check(f"{tag}/{nm}", g, r, tol)
+
+
+M3_CASES = {
+    "t1_n16": M3(2, 1, 2, 8, 16),
+    "n8_p7": M3(2, 17, 3, 7, 8),
+    "n64_p33_hq1_z": M3(1, 33, 4, 33, 64, nheads_qk=1, has_z=True),
+    "n128_a7": M3(1, 40, 2, 64, 128, angles=7),
+    "n130_padded": M3(1, 25, 2, 20, 130),
+    "n256": M3(1, 21, 2, 24, 256),
+    "p65_rowblocks_t70": M3(2, 70, 2, 65, 32),
+}
+
+
+@pytest.mark.parametrize("with_inputs", [False, True])
+@pytest.mark.parametrize("name", sorted(M3_CASES))
+def test_m3_states_parity(name, with_inputs):
+    s = M3_CASES[name]
+    inp = W.mamba3_siso_inputs(s, seed=9)
+    ins = m3_states_for(s, 10) if with_inputs else None
+    y, st = m3_gpu(inp, ins)
+    ry, rst = m3_ref(inp, ins)
+    assert [x.shape for x in st] == [x.shape for x in rst]
+    check(f"mamba3_state/{name}/{with_inputs}/y", y, ry, TOL_M3)
+    check_m3_states(f"mamba3_state/{name}/{with_inputs}", st, rst, TOL_M3)
+    np.testing.assert_array_equal(y, m3_gpu(inp, ins, state=False))   # the state writes leave y alone
+
+
+@pytest.mark.parametrize("shape,split", [((2, 100, 4, 16, 32), 37), ((1, 70, 2, 65, 128), 32),
+                                         ((1, 45, 2, 20, 256), 1)])
+def test_m3_states_chain(shape, split):
+    """Tokens [0, split) then [split, T) continued from the first call's states
+    give the outputs and states of one call over [0, T)."""
+    import torch
+    s = M3(*shape, has_z=True)
+    inp = W.mamba3_siso_inputs(s, seed=11)
+    dev = {k: to_dev(v) for k, v in inp.items() if v is not None}
+    T = s.seqlen
+
+    def part(a, b):
+        out = []
+        for k in M3_KEYS:
+            x = dev.get(k)
+            if x is None or k in ("Q_bias", "K_bias", "D"):
+                out.append(x)
+            elif k in ("ADT", "DT", "Trap"):
+                out.append(x[:, :, a:b].contiguous())
+            else:
+                out.append(x[:, a:b].contiguous())
+        return out
+
+    y, st = mamba3_siso_fn(*part(0, T), return_final_states=True)
+    y1, st1 = mamba3_siso_fn(*part(0, split), return_final_states=True)
+    y2, st2 = mamba3_siso_fn(*part(split, T), input_states=st1, return_final_states=True)
+    torch.cuda.synchronize()
+    check(f"mamba3_state/chain_{split}/y", torch.cat([y1, y2], dim=1).cpu().numpy(), y.cpu().numpy(), 1e-5)
+    check_m3_states(f"mamba3_state/chain_{split}", [x.cpu().numpy() for x in st2], [x.cpu().numpy() for x in st], 1e-5)

@@ -32,6 +32,14 @@
 // difference far below fp32 resolution.  Pairs >= A are not rotated (:109).
 // Tokens past the end of the last block are identity tokens (decay 1, zero
 // k scale, zero v): they leave the state unchanged and are not stored.
+//
+// States (a widening; the reference rejects has_input_states and
+// return_final_states, mamba3_siso_fn_ort.cpp:50-55): (ssm [P,N], angle [A],
+// k [N], v [P]) per (b,h).  The final ones are S and theta after the last
+// token (whose look-ahead is 0), its rotated k and its V; given as input they
+// start the scan from S = ssm + v (x) k * DT_0 (1 - sigmoid(Trap_0)), the
+// last token's look-ahead now that its successor is known, and theta = angle,
+// so two calls chained through the states equal one call.
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -283,6 +291,17 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     float S[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; ++j) S[j] = 0.0f;
+    if (p.in_ssm != nullptr && row < P) {
+        const float look0 = dtr[0] * (1.0f - FastSigmoid(trr[0]));
+        const float vl = p.in_v[static_cast<size_t>(bh) * P + row];
+        const float *srow = p.in_ssm + (static_cast<size_t>(bh) * P + row) * N;
+        const float *krow = p.in_k + static_cast<size_t>(bh) * N;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const int key = kg * KPT + j;
+            if (key < N) S[j] = fmaf(vl, krow[key] * look0, srow[key]);
+        }
+    }
 
     auto recur = [&](int t0, int buf) __attribute__((always_inline)) {
         const int nt = min(TB, T - t0);
@@ -341,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         }
     };
 
-    if (tid < PAIRS) sCarry[tid] = 0.0;
+    if (tid < PAIRS) sCarry[tid] = (p.in_angle != nullptr && tid < A) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + tid]) : 0.0;
     const int nblk = (T + TB - 1) / TB;
     load_prep(0);
     prep_a(0);
@@ -357,6 +376,25 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         __syncthreads();
         if (next) prep_b((j + 1) * TB, buf ^ 1, (j + 1) & 1);
         __syncthreads();
+    }
+    if (p.f_ssm != nullptr) {
+        // the last block's buffers are intact: sK holds its rotated k, the
+        // carry of parity nblk % 2 the wrapped angle after its last token
+        if (row < P) {
+            float *srow = p.f_ssm + (static_cast<size_t>(bh) * P + row) * N;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                if (kg * KPT + j < N) srow[kg * KPT + j] = S[j];
+        }
+        if (tid < kRows && r0 + tid < P)
+            p.f_v[static_cast<size_t>(bh) * P + r0 + tid] = p.V[vbase + static_cast<size_t>(T - 1) * v_stride + r0 + tid];
+        if (rb == 0) {
+            const int tl = (T - 1) - (nblk - 1) * TB;
+            const float *krow = sK + (((nblk - 1) & 1) * TB + tl) * NPS;
+            for (int i = tid; i < N; i += kThreads) p.f_k[static_cast<size_t>(bh) * N + i] = krow[L::Pos(i)];
+            for (int i = tid; i < A; i += kThreads)
+                p.f_angle[static_cast<size_t>(bh) * A + i] = static_cast<float>(sCarry[(nblk & 1) * PAIRS + i]);
+        }
     }
 }
 

@@ -5,6 +5,14 @@
 // The fused kernel keeps the state in VGPRs, so headdim_qk is limited to 256
 // (the reference's limit is its shared-memory budget, P*N + A + 4N + 128
 // floats).  No scratch.
+//
+// Widening: has_input_states = 1 and return_final_states = 1, which the
+// reference rejects (:50-55), are accepted.  The states are (ssm [B,H,P,N],
+// angle [B,H,A], k [B,H,N], v [B,H,P]): S and the angle state after the last
+// token, that token's rotated k and its V.  Input states come as inputs
+// 11-14 (15 inputs); final states go to the four buffers of
+// xm_mamba3_siso_forward_states.  Two calls chained through the states give
+// the outputs and states of one call.
 #include "xm_common.h"
 #include "xm_params.h"
 
@@ -12,12 +20,15 @@ namespace xm {
 namespace {
 
 constexpr size_t kNumInputs = 11;
+constexpr size_t kNumInputsWithStates = 15;
 
 void CheckAttrs(const xm_mamba3_siso_attrs_t &a) {
     if (a.chunk_size <= 0) Invalid("Mamba3SisoFn requires chunk_size > 0");
-    if (a.return_final_states != 0) Unsupported("Mamba3SisoFn v1 does not support return_final_states");
-    if (a.has_input_states != 0) Unsupported("Mamba3SisoFn v1 does not support input states");
     if (a.has_cu_seqlens != 0) Unsupported("Mamba3SisoFn v1 does not support cu_seqlens");
+}
+
+size_t ExpectedInputs(const xm_mamba3_siso_attrs_t &a) {
+    return a.has_input_states != 0 ? kNumInputsWithStates : kNumInputs;
 }
 
 struct Plan {
@@ -91,7 +102,44 @@ Plan Validate(const std::vector<View> &in, const xm_mamba3_siso_attrs_t &attrs) 
     p.Angles = Ang.data;
     p.D = has_d ? D.data : nullptr;
     p.Z = has_z ? Z.data : nullptr;
+    if (attrs.has_input_states != 0) {
+        const View &Ss = in[11], &As = in[12], &Ks = in[13], &Vs = in[14];
+        RequireRank(Ss, 4, "ssm_state");
+        RequireRank(As, 3, "angle_state");
+        RequireRank(Ks, 3, "k_state");
+        RequireRank(Vs, 3, "v_state");
+        if (Ss.shape != std::vector<int64_t>{batch, nheads, headdim_v, headdim_qk})
+            Invalid("ssm_state must have shape (batch, nheads, headdim_v, headdim_qk)");
+        if (As.shape != std::vector<int64_t>{batch, nheads, headdim_angles})
+            Invalid("angle_state must have shape (batch, nheads, headdim_angles)");
+        if (Ks.shape != std::vector<int64_t>{batch, nheads, headdim_qk})
+            Invalid("k_state must have shape (batch, nheads, headdim_qk)");
+        if (Vs.shape != std::vector<int64_t>{batch, nheads, headdim_v})
+            Invalid("v_state must have shape (batch, nheads, headdim_v)");
+        p.in_ssm = Ss.data;
+        p.in_angle = As.data;
+        p.in_k = Ks.data;
+        p.in_v = Vs.data;
+    }
     return plan;
+}
+
+void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_mamba3_siso_attrs_t &attrs, float *out,
+             float *const *states, void *stream) {
+    CheckAttrs(attrs);
+    auto views = MakeViews(inputs, n_inputs, ExpectedInputs(attrs), "Mamba3SisoFn");
+    Plan plan = Validate(views, attrs);
+    if (out == nullptr) Invalid("output pointer is null");
+    plan.params.out = out;
+    if (attrs.return_final_states != 0) {
+        for (int i = 0; i < 4; ++i)
+            if (states == nullptr || states[i] == nullptr) Invalid("return_final_states=1 needs four state buffers");
+        plan.params.f_ssm = states[0];
+        plan.params.f_angle = states[1];
+        plan.params.f_k = states[2];
+        plan.params.f_v = states[3];
+    }
+    LaunchMamba3Siso(plan.params, stream);
 }
 
 }  // namespace
@@ -122,7 +170,7 @@ int xm_mamba3_siso_validate(const xm_tensor_t *inputs, size_t n_inputs, const xm
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
         xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "Mamba3SisoFn");
+        auto views = xm::MakeViews(inputs, n_inputs, xm::ExpectedInputs(*attrs), "Mamba3SisoFn");
         xm::Plan plan = xm::Validate(views, *attrs);
         xm::WriteShape(plan.out_shape, out_shape, out_rank);
         if (scratch_bytes) *scratch_bytes = 0;
@@ -135,11 +183,21 @@ int xm_mamba3_siso_forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
         xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "Mamba3SisoFn");
-        xm::Plan plan = xm::Validate(views, *attrs);
-        if (out == nullptr) xm::Invalid("output pointer is null");
-        plan.params.out = out;
-        xm::LaunchMamba3Siso(plan.params, stream);
+        if (attrs->return_final_states != 0)
+            xm::Invalid("Mamba3SisoFn with return_final_states=1 needs final-state outputs "
+                        "(xm_mamba3_siso_forward_states)");
+        xm::Forward(inputs, n_inputs, *attrs, out, nullptr, stream);
+    });
+}
+
+int xm_mamba3_siso_forward_states(const xm_tensor_t *inputs, size_t n_inputs, const xm_mamba3_siso_attrs_t *attrs,
+                                  float *out, float *ssm_state, float *angle_state, float *k_state, float *v_state,
+                                  void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
+    (void)alloc;
+    return xm::Guard(errbuf, errlen, [&] {
+        if (attrs == nullptr) xm::Invalid("attrs is null");
+        float *const states[4] = {ssm_state, angle_state, k_state, v_state};
+        xm::Forward(inputs, n_inputs, *attrs, out, states, stream);
     });
 }
 

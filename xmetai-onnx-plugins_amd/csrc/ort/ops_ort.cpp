@@ -10,7 +10,9 @@
 // Widening: SelectiveScanFn with return_last_state=1 and GatedDeltaNet2Fn
 // with output_final_state=1, which the reference rejects, fill an optional
 // output 1 with the state after the last token ([B,D,N] and [B,H,K,V]).
-// Mamba3SisoFn keeps one output.
+// Mamba3SisoFn with return_final_states=1 fills optional outputs 1-4 (ssm
+// [B,H,P,N], angle [B,H,A], k [B,H,N], v [B,H,P]) and with has_input_states=1
+// takes the same four as optional inputs 11-14.
 #include "ort_glue.h"
 
 namespace {
@@ -19,7 +21,7 @@ using xm_ort::Check;
 using xm_ort::ComputeDeviceOp;
 using xm_ort::FloatAttr;
 using xm_ort::IntAttr;
-using xm_ort::StateOutput;
+using xm_ort::StateOutputs;
 
 
 // ---- SelectiveScanFn -------------------------------------------------------
@@ -35,17 +37,22 @@ public:
     void Compute(OrtKernelContext *ctx) {
         const bool want = attrs_.return_last_state != 0;
         auto state = [want](const xm_tensor_t *in) {
-            StateOutput so;
+            StateOutputs so;
             so.what = "return_last_state";
             if (want) {   // [B, D, N]: u is [B, D, L] and A is [D, N] (validated)
-                so.rank = 3;
-                so.shape[0] = in[0].shape[0];
-                so.shape[1] = in[0].shape[1];
-                so.shape[2] = in[2].shape[1];
+                so.count = 1;
+                so.rank[0] = 3;
+                so.shape[0][0] = in[0].shape[0];
+                so.shape[0][1] = in[0].shape[1];
+                so.shape[0][2] = in[2].shape[1];
             }
             return so;
         };
-        ComputeDeviceOp(api_, ctx, 8, attrs_, xm_selective_scan_validate, state, xm_selective_scan_forward_states);
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_selective_scan_attrs_t *a, float *out,
+                         float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
+            return xm_selective_scan_forward_states(in, n, a, out, states[0], stream, alloc, err, errlen);
+        };
+        ComputeDeviceOp(api_, ctx, 8, 8, attrs_, xm_selective_scan_validate, state, launch);
     }
 
 private:
@@ -81,16 +88,28 @@ public:
         Check(xm_mamba3_siso_check_attrs(&attrs_, err, sizeof(err)), err);
     }
     void Compute(OrtKernelContext *ctx) {
-        auto launch = [](const xm_tensor_t *in, size_t n, const xm_mamba3_siso_attrs_t *a, float *out, float *,
-                         void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
-            return xm_mamba3_siso_forward(in, n, a, out, stream, alloc, err, errlen);
-        };
-        auto state = [](const xm_tensor_t *) {
-            StateOutput so;
+        const bool want = attrs_.return_final_states != 0;
+        auto state = [want](const xm_tensor_t *in) {
+            StateOutputs so;
             so.what = "return_final_states";
+            if (want) {   // Q [B,T,Hq,N], V [B,T,H,P], Angles [B,T,H,A] (validated)
+                const int64_t b = in[0].shape[0], n = in[0].shape[3], h = in[2].shape[2], p = in[2].shape[3];
+                const int64_t a = in[8].shape[3];
+                const int64_t shapes[4][4] = {{b, h, p, n}, {b, h, a, 0}, {b, h, n, 0}, {b, h, p, 0}};
+                so.count = 4;
+                for (int i = 0; i < 4; ++i) {
+                    so.rank[i] = i == 0 ? 4 : 3;
+                    for (int d = 0; d < so.rank[i]; ++d) so.shape[i][d] = shapes[i][d];
+                }
+            }
             return so;
         };
-        ComputeDeviceOp(api_, ctx, 11, attrs_, xm_mamba3_siso_validate, state, launch);
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_mamba3_siso_attrs_t *a, float *out,
+                         float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
+            return xm_mamba3_siso_forward_states(in, n, a, out, states[0], states[1], states[2], states[3], stream,
+                                                 alloc, err, errlen);
+        };
+        ComputeDeviceOp(api_, ctx, 11, 15, attrs_, xm_mamba3_siso_validate, state, launch);
     }
 
 private:
@@ -102,10 +121,16 @@ struct Mamba3SisoOp : Ort::CustomOpBase<Mamba3SisoOp, Mamba3SisoKernel> {
     void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new Mamba3SisoKernel(api, info); }
     const char *GetName() const { return "Mamba3SisoFn"; }
     const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
-    size_t GetInputTypeCount() const { return 11; }
+    size_t GetInputTypeCount() const { return 15; }
     ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
-    size_t GetOutputTypeCount() const { return 1; }
+    OrtCustomOpInputOutputCharacteristic GetInputCharacteristic(size_t i) const {
+        return i < 11 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
+    }
+    size_t GetOutputTypeCount() const { return 5; }
     ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    OrtCustomOpInputOutputCharacteristic GetOutputCharacteristic(size_t i) const {
+        return i == 0 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
+    }
 };
 
 // ---- GatedDeltaNet2Fn ------------------------------------------------------
@@ -125,18 +150,23 @@ public:
     void Compute(OrtKernelContext *ctx) {
         const bool want = attrs_.output_final_state != 0;
         auto state = [want](const xm_tensor_t *in) {
-            StateOutput so;
+            StateOutputs so;
             so.what = "output_final_state";
             if (want) {   // [B, H, K, V]: q is [B, T, H, K] and v is [B, T, H, V] (validated)
-                so.rank = 4;
-                so.shape[0] = in[0].shape[0];
-                so.shape[1] = in[0].shape[2];
-                so.shape[2] = in[0].shape[3];
-                so.shape[3] = in[2].shape[3];
+                so.count = 1;
+                so.rank[0] = 4;
+                so.shape[0][0] = in[0].shape[0];
+                so.shape[0][1] = in[0].shape[2];
+                so.shape[0][2] = in[0].shape[3];
+                so.shape[0][3] = in[2].shape[3];
             }
             return so;
         };
-        ComputeDeviceOp(api_, ctx, 7, attrs_, xm_gated_deltanet2_validate, state, xm_gated_deltanet2_forward_states);
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_gated_deltanet2_attrs_t *a, float *out,
+                         float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
+            return xm_gated_deltanet2_forward_states(in, n, a, out, states[0], stream, alloc, err, errlen);
+        };
+        ComputeDeviceOp(api_, ctx, 7, 7, attrs_, xm_gated_deltanet2_validate, state, launch);
     }
 
 private:

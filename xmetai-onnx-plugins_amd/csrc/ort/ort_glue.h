@@ -112,31 +112,40 @@ struct ScratchAdapter {
     }
 };
 
-// Optional output 1 of an operator: the recurrent state after the last token.
-// rank == 0 means the node's attributes do not ask for it.
-struct StateOutput {
-    int32_t rank = 0;
-    int64_t shape[XM_MAX_RANK] = {};
+// Optional outputs 1..count of an operator: the recurrent state after the
+// last token.  count == 0 means the node's attributes do not ask for it.
+constexpr int kMaxStateOutputs = 4;
+struct StateOutputs {
+    int count = 0;
+    int32_t rank[kMaxStateOutputs] = {};
+    int64_t shape[kMaxStateOutputs][XM_MAX_RANK] = {};
     const char *what = "";   // attribute that asks for it, for error messages
 };
 
-// Compute of a device operator: describe the inputs, validate (the C ABI
-// writes the output shape and the scratch size), allocate output 0 (and
-// output 1 when the attributes ask for the state), take the execution
-// provider's compute stream, enqueue.  Nothing synchronises the host and
-// nothing is cached on the kernel object.
-//   state(in) -> StateOutput
-//   launch(in, n, &attrs, out, state_or_null, stream, alloc, err, errlen) -> status
+// Compute of a device operator: describe the inputs (between min_inputs and
+// max_inputs of them; an omitted optional input reads as an empty tensor),
+// validate (the C ABI writes the output shape and the scratch size), allocate
+// output 0 (and the state outputs when the attributes ask for them), take the
+// execution provider's compute stream, enqueue.  Nothing synchronises the
+// host and nothing is cached on the kernel object.
+//   state(in) -> StateOutputs
+//   launch(in, n, &attrs, out, float *states[kMaxStateOutputs], stream, alloc, err, errlen) -> status
 template <typename Attrs, typename Validate, typename State, typename Launch>
-void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t n_inputs, const Attrs &attrs,
-                     Validate validate, State state, Launch launch) {
-    size_t count = 0;
-    ThrowIfFailed(api, api.KernelContext_GetInputCount(ctx, &count));
-    if (count != n_inputs) throw std::runtime_error("unexpected number of inputs");
+void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t min_inputs, size_t max_inputs,
+                     const Attrs &attrs, Validate validate, State state, Launch launch) {
+    size_t n_inputs = 0;
+    ThrowIfFailed(api, api.KernelContext_GetInputCount(ctx, &n_inputs));
+    if (n_inputs < min_inputs || n_inputs > max_inputs) throw std::runtime_error("unexpected number of inputs");
     std::vector<xm_tensor_t> in(n_inputs);
     for (size_t i = 0; i < n_inputs; ++i) {
         const OrtValue *v = nullptr;
         ThrowIfFailed(api, api.KernelContext_GetInput(ctx, i, &v));
+        if (v == nullptr) {   // omitted optional input
+            in[i] = xm_tensor_t{};
+            in[i].rank = 1;
+            in[i].elem_type = XM_ELEM_FLOAT;
+            continue;
+        }
         in[i] = Describe(api, v);
     }
     char err[1024];
@@ -151,15 +160,21 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t n_inputs, 
 
     size_t n_outputs = 0;
     ThrowIfFailed(api, api.KernelContext_GetOutputCount(ctx, &n_outputs));
-    const StateOutput so = state(in.data());
-    void *state_data = nullptr;
-    if (so.rank > 0) {
-        if (n_outputs < 2) throw std::runtime_error(std::string(so.what) + "=1 needs a second output (the state)");
-        OrtValue *sv = nullptr;
-        ThrowIfFailed(api, api.KernelContext_GetOutput(ctx, 1, so.shape, static_cast<size_t>(so.rank), &sv));
-        ThrowIfFailed(api, api.GetTensorMutableData(sv, &state_data));
+    const StateOutputs so = state(in.data());
+    float *states[kMaxStateOutputs] = {};
+    if (so.count > 0) {
+        if (n_outputs < static_cast<size_t>(1 + so.count))
+            throw std::runtime_error(std::string(so.what) + "=1 needs " + std::to_string(so.count) +
+                                     " state output(s) after output 0");
+        for (int i = 0; i < so.count; ++i) {
+            OrtValue *sv = nullptr;
+            void *data = nullptr;
+            ThrowIfFailed(api, api.KernelContext_GetOutput(ctx, 1 + i, so.shape[i], static_cast<size_t>(so.rank[i]), &sv));
+            ThrowIfFailed(api, api.GetTensorMutableData(sv, &data));
+            states[i] = static_cast<float *>(data);
+        }
     } else if (n_outputs > 1) {
-        throw std::runtime_error(std::string("output 1 (the state) needs ") + so.what + "=1");
+        throw std::runtime_error(std::string("outputs after output 0 (the state) need ") + so.what + "=1");
     }
 
     void *stream = nullptr;
@@ -177,8 +192,8 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t n_inputs, 
         ThrowIfFailed(api, api.KernelContext_GetAllocator(ctx, s.mem, &s.allocator));
         ap = &alloc;
     }
-    const int st = launch(in.data(), n_inputs, &attrs, static_cast<float *>(out_data),
-                          static_cast<float *>(state_data), stream, ap, err, sizeof(err));
+    const int st = launch(in.data(), n_inputs, &attrs, static_cast<float *>(out_data), states, stream, ap, err,
+                          sizeof(err));
     if (s.allocator != nullptr) api.ReleaseAllocator(s.allocator);
     Check(st, err);
 }

@@ -57,6 +57,11 @@ struct Mamba3SisoParams {
     const float *D;                 // [nheads] or nullptr
     const float *Z;                 // [batch, seqlen, nheads, p] or nullptr
     float *out;                     // [batch, seqlen, nheads, p]
+    // States (widening): each set all null or all set.  in_*: the state
+    // before the first token (S = ssm + v (x) k * the first token's
+    // look-ahead); f_*: the state after the last token.
+    const float *in_ssm, *in_angle, *in_k, *in_v;   // [batch, nheads, p, n], [.., a], [.., n], [.., p]
+    float *f_ssm, *f_angle, *f_k, *f_v;
     int batch, seqlen, nheads, nheads_qk, n, p, a;
 };
 

@@ -129,8 +129,9 @@ def validate(op: str, shapes: Sequence[Optional[Sequence[int]]], **attrs):
     ``(output_shape, scratch_bytes)`` or raises :class:`XmError`.
     """
     _, n = _capi.OPS[op]
-    if len(shapes) != n:
+    if len(shapes) != n and not (op == "mamba3_siso" and len(shapes) == _capi.MAMBA3_INPUTS_WITH_STATES):
         raise TypeError(f"{op} takes {n} inputs")
+    n = len(shapes)
     arr = (_capi.XmTensor * n)(*[_desc_from_shape(s if s is not None else (0,)) for s in shapes])
     a = _attrs(op, **attrs)
     out_shape = (ctypes.c_int64 * _capi.XM_MAX_RANK)()
@@ -193,11 +194,12 @@ class TorchAllocator:
 # ---------------------------------------------------------------------------
 
 def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocator], stream,
-         state_shape=None, **attrs):
-    """Validates and enqueues one operator call.  With ``state_shape`` set it
-    calls the op's ``_forward_states`` entry point and returns ``(out, state)``."""
+         state_shapes=None, **attrs):
+    """Validates and enqueues one operator call.  With ``state_shapes`` (one
+    shape per state buffer) set it calls the op's ``_forward_states`` entry
+    point and returns ``(out, [state, ...])``."""
     import torch
-    _, n = _capi.OPS[op]
+    n = len(inputs)
     descs = [_desc_from_tensor(x) for x in inputs]
     arr = (_capi.XmTensor * n)(*descs)
     a = _attrs(op, **attrs)
@@ -214,17 +216,19 @@ def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocato
     alloc_ptr = ctypes.byref(allocator.struct) if allocator is not None else None
     out_ptr = ctypes.c_void_p(out.data_ptr() if out.numel() else None)
     with torch.cuda.device(ref.device):
-        if state_shape is None:
+        if state_shapes is None:
             st = getattr(lib(), f"xm_{op}_forward")(arr, n, ctypes.byref(a), out_ptr,
                                                     ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
             _check(st, err)
             return out
-        state = torch.empty(tuple(int(d) for d in state_shape), dtype=torch.float32, device=ref.device)
+        states = [torch.empty(tuple(int(d) for d in sh), dtype=torch.float32, device=ref.device)
+                  for sh in state_shapes]
         st = getattr(lib(), f"xm_{op}_forward_states")(
-            arr, n, ctypes.byref(a), out_ptr, ctypes.c_void_p(state.data_ptr() if state.numel() else None),
+            arr, n, ctypes.byref(a), out_ptr,
+            *(ctypes.c_void_p(x.data_ptr() if x.numel() else None) for x in states),
             ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
     _check(st, err)
-    return out, state
+    return out, states
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, delta_softplus=False,
@@ -236,27 +240,42 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, del
     selective_scan_fn_ort.cpp:52-55; accepted here as a widening) it returns
     ``(y, last_state)``, last_state [B,D,N] being the scan state after the
     last token (zeros when L = 0)."""
-    state_shape = None   # shapes of other ranks fail validation before the launch
+    shapes = None   # shapes of other ranks fail validation before the launch
     if return_last_state and u.dim() == 3 and A.dim() == 2:
-        state_shape = (u.shape[0], u.shape[1], A.shape[1])
-    return _run("selective_scan", [u, delta, A, B, C, D, z, delta_bias], 0, allocator, stream,
-                state_shape=state_shape,
-                delta_softplus=int(bool(delta_softplus)), return_last_state=int(bool(return_last_state)))
+        shapes = [(u.shape[0], u.shape[1], A.shape[1])]
+    r = _run("selective_scan", [u, delta, A, B, C, D, z, delta_bias], 0, allocator, stream,
+             state_shapes=shapes,
+             delta_softplus=int(bool(delta_softplus)), return_last_state=int(bool(return_last_state)))
+    return (r[0], r[1][0]) if shapes is not None else r
 
 
 def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None, *, chunk_size=64,
-                   has_d=None, has_z=None, return_final_states=False, has_input_states=False,
+                   has_d=None, has_z=None, input_states=None, return_final_states=False, has_input_states=None,
                    has_cu_seqlens=False, allocator=None, stream=None):
     """Mamba3SisoFn: returns [B,T,H,P].  ``has_d``/``has_z`` default to the
-    presence of D/Z (an exported graph sets them explicitly; default 1)."""
+    presence of D/Z (an exported graph sets them explicitly; default 1).
+
+    States (rejected by the reference, mamba3_siso_fn_ort.cpp:50-55; accepted
+    here as a widening): ``input_states`` = (ssm [B,H,P,N], angle [B,H,A],
+    k [B,H,N], v [B,H,P]) continues a previous call; ``return_final_states``
+    returns ``(y, (ssm, angle, k, v))`` after the last token."""
     def present(x):
         return x is not None and x.numel() > 0
     has_d = present(D) if has_d is None else has_d
     has_z = present(Z) if has_z is None else has_z
-    return _run("mamba3_siso", [Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z], 2, allocator, stream,
-                chunk_size=chunk_size, has_d=int(bool(has_d)), has_z=int(bool(has_z)),
-                return_final_states=int(bool(return_final_states)), has_input_states=int(bool(has_input_states)),
-                has_cu_seqlens=int(bool(has_cu_seqlens)))
+    has_input_states = input_states is not None if has_input_states is None else has_input_states
+    inputs = [Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z]
+    if has_input_states:
+        inputs += list(input_states)
+    shapes = None   # shapes of other ranks fail validation before the launch
+    if return_final_states and Q.dim() == 4 and V.dim() == 4 and Angles.dim() == 4:
+        b, h, pdim, n, a = Q.shape[0], V.shape[2], V.shape[3], Q.shape[3], Angles.shape[3]
+        shapes = [(b, h, pdim, n), (b, h, a), (b, h, n), (b, h, pdim)]
+    r = _run("mamba3_siso", inputs, 2, allocator, stream, state_shapes=shapes,
+             chunk_size=chunk_size, has_d=int(bool(has_d)), has_z=int(bool(has_z)),
+             return_final_states=int(bool(return_final_states)), has_input_states=int(bool(has_input_states)),
+             has_cu_seqlens=int(bool(has_cu_seqlens)))
+    return (r[0], tuple(r[1])) if shapes is not None else r
 
 
 def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, use_qk_l2norm_in_kernel=True,
@@ -268,14 +287,15 @@ def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, us
     gated_deltanet2_fn_ort.cpp:49-51; accepted here as a widening) it returns
     ``(o, final_state)``, final_state [B,H,K,V] being the state after the last
     token in initial_state's layout."""
-    state_shape = None   # shapes of other ranks fail validation before the launch
+    shapes = None   # shapes of other ranks fail validation before the launch
     if output_final_state and q.dim() == 4 and v.dim() == 4:
-        state_shape = (q.shape[0], q.shape[2], q.shape[3], v.shape[3])
-    return _run("gated_deltanet2", [q, k, v, g, beta, w, initial_state], 2, allocator, stream,
-                state_shape=state_shape,
-                scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
-                output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
-                has_cu_seqlens=int(bool(has_cu_seqlens)), state_v_first=int(bool(state_v_first)))
+        shapes = [(q.shape[0], q.shape[2], q.shape[3], v.shape[3])]
+    r = _run("gated_deltanet2", [q, k, v, g, beta, w, initial_state], 2, allocator, stream,
+             state_shapes=shapes,
+             scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
+             output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
+             has_cu_seqlens=int(bool(has_cu_seqlens)), state_v_first=int(bool(state_v_first)))
+    return (r[0], r[1][0]) if shapes is not None else r
 
 
 def softmax_cpu(x, axis: int = -1):

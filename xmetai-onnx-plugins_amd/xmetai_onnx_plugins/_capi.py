@@ -69,7 +69,7 @@ class GatedDeltaNet2Attrs(ctypes.Structure):
     ]
 
 
-# (op prefix, attrs struct, number of inputs)
+# (op prefix, attrs struct, number of inputs; Mamba3SisoFn takes 15 with has_input_states)
 OPS = {
     "selective_scan": (SelectiveScanAttrs, 8),
     "mamba3_siso": (Mamba3SisoAttrs, 11),
@@ -77,8 +77,10 @@ OPS = {
 }
 
 # Ops with a second entry point that also writes the recurrent state after the
-# last token: op prefix -> the attribute that asks for it.
-STATE_OUTPUTS = {"selective_scan": "return_last_state", "gated_deltanet2": "output_final_state"}
+# last token: op prefix -> (the attribute that asks for it, number of state buffers).
+STATE_OUTPUTS = {"selective_scan": ("return_last_state", 1), "gated_deltanet2": ("output_final_state", 1),
+                 "mamba3_siso": ("return_final_states", 4)}
+MAMBA3_INPUTS_WITH_STATES = 15
 
 # Every symbol include/xmetai_recurrent.h declares.
 EXPORTED_SYMBOLS = [
@@ -105,9 +107,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
                       ctypes.c_char_p, ctypes.c_size_t]
         f.restype = ctypes.c_int
         if op in STATE_OUTPUTS:
+            nstate = STATE_OUTPUTS[op][1]
             f = getattr(lib, f"xm_{op}_forward_states")
-            f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                          ctypes.POINTER(XmAllocator), ctypes.c_char_p, ctypes.c_size_t]
+            f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p] + [ctypes.c_void_p] * nstate + [
+                ctypes.c_void_p, ctypes.POINTER(XmAllocator), ctypes.c_char_p, ctypes.c_size_t]
             f.restype = ctypes.c_int
     lib.xm_softmax_cpu.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
