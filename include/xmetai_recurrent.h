@@ -43,6 +43,7 @@ extern "C" {
 
 #define XM_MAX_RANK 8
 #define XM_ELEM_FLOAT 1 /* ONNX TensorProto FLOAT */
+#define XM_ELEM_INT64 7 /* ONNX TensorProto INT64 (cu_seqlens) */
 
 typedef enum xm_status {
     XM_OK = 0,
@@ -119,14 +120,22 @@ int xm_selective_scan_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
  * otherwise used), has_d and has_z (default 1, must match the presence of D
  * and Z), return_final_states and has_input_states (default 0; the reference
  * rejects non-zero, here they select the states below), has_cu_seqlens
- * (default 0; non-zero rejected).
+ * (default 0; the reference rejects non-zero, here it selects packed
+ * sequences, below).
  * States (a widening with no counterpart in the reference, which rejects them
  * at mamba3_siso_fn_ort.cpp:50-55): ssm [B,H,P,N], angle [B,H,A], k [B,H,N],
  * v [B,H,P] -- the scan state and the angle state after the last token, that
  * token's rotated k and its V.  With has_input_states != 0 they are inputs
  * 11-14 (15 inputs) and the scan starts from ssm + v (x) k * DT_0 *
  * (1 - sigmoid(Trap_0)) and angle, so that two calls chained through the
- * states give the outputs and states of one call.  */
+ * states give the outputs and states of one call.
+ * Packed sequences (a widening; the reference rejects has_cu_seqlens at
+ * mamba3_siso_fn_ort.cpp:56-58): 16 inputs, input 15 cu_seqlens, int64
+ * (XM_ELEM_INT64) [N+1], the token offsets of N sequences packed along T
+ * (inputs 11-14 empty unless has_input_states != 0); the tensors have batch 1
+ * and the states are [N,H,...], one per sequence.  Offsets are read on the
+ * device: each is clamped into [0, T], a sequence ending before it starts is
+ * empty and passes its states through.  */
 typedef struct xm_mamba3_siso_attrs {
     int64_t chunk_size;
     int64_t has_d;
@@ -163,8 +172,17 @@ int xm_mamba3_siso_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
  * Attributes (reference: :46-64): scale (float, default 1.0, positive and
  * finite), use_qk_l2norm_in_kernel (default 1), output_final_state (default
  * 0; the reference rejects non-zero, here it selects the final-state output
- * of xm_gated_deltanet2_forward_states), use_gate_in_kernel, has_cu_seqlens,
- * state_v_first (default 0; non-zero rejected).  */
+ * of xm_gated_deltanet2_forward_states), has_cu_seqlens (default 0; the
+ * reference rejects non-zero, here it selects packed sequences, below),
+ * use_gate_in_kernel, state_v_first (default 0; non-zero rejected).
+ * Packed sequences (a widening with no counterpart in the reference, which
+ * rejects has_cu_seqlens at gated_deltanet2_fn_ort.cpp:55-57): with
+ * has_cu_seqlens != 0 input 7 is cu_seqlens, int64 (XM_ELEM_INT64) [N+1], the
+ * token offsets of N sequences packed along T; q..w are [1,T,H,.] and
+ * initial_state / final_state are [N,H,K,V], one state per sequence.  Offsets
+ * are read on the device: they should rise from 0 to T; each one is clamped
+ * into [0, T] and a sequence ending before it starts is empty (its state
+ * passes through).  head_k up to 512.  */
 typedef struct xm_gated_deltanet2_attrs {
     float scale;
     int64_t use_qk_l2norm_in_kernel;

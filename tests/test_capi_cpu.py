@@ -67,9 +67,7 @@ def test_attribute_defaults_match_reference():
 
 @pytest.mark.parametrize("op,kw,msg,status", [
     ("mamba3_siso", dict(chunk_size=0), "Mamba3SisoFn requires chunk_size > 0", xp.XM_ERR_INVALID_ARGUMENT),
-    ("mamba3_siso", dict(has_cu_seqlens=1), "Mamba3SisoFn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(use_gate_in_kernel=1), "GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel", xp.XM_ERR_UNSUPPORTED),
-    ("gated_deltanet2", dict(has_cu_seqlens=1), "GatedDeltaNet2Fn v1 does not support cu_seqlens", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(state_v_first=1), "GatedDeltaNet2Fn v1 expects state layout (batch, head, key, value)", xp.XM_ERR_UNSUPPORTED),
     ("gated_deltanet2", dict(scale=0.0), "GatedDeltaNet2Fn requires a positive finite scale", xp.XM_ERR_INVALID_ARGUMENT),
     ("gated_deltanet2", dict(scale=-1.0), "GatedDeltaNet2Fn requires a positive finite scale", xp.XM_ERR_INVALID_ARGUMENT),
@@ -98,6 +96,8 @@ def test_state_attributes_are_accepted():
     check_attrs("selective_scan", return_last_state=1, delta_softplus=1)
     check_attrs("gated_deltanet2", output_final_state=1, scale=0.5)
     check_attrs("mamba3_siso", return_final_states=1, has_input_states=1)
+    check_attrs("mamba3_siso", has_cu_seqlens=1)
+    check_attrs("gated_deltanet2", has_cu_seqlens=1)
 
 
 def _forward_host_error(op, shapes, entry, state_ptrs=(None,), **attrs):
@@ -290,6 +290,51 @@ def test_gdn2_zero_dims_rejected_like_reference():
         validate("gated_deltanet2", gdn_shapes(T=0))
 
 
+I64 = xp._capi.XM_ELEM_INT64
+
+
+def packed_gdn(N=3, T=20, H=3, K=16, V=8, s0=True, cu=None):
+    shapes = gdn_shapes(B=1, T=T, H=H, K=K, V=V, s0=False)
+    shapes[6] = (N, H, K, V) if s0 else None
+    return shapes + [cu or (N + 1,)], [1] * 7 + [I64]
+
+
+def test_gdn2_packed_sequences_valid_no_scratch():
+    # Widening: cu_seqlens (input 7, int64 [N+1]) packs N sequences; the
+    # fused kernel takes them (no scratch at any headdim_k up to 512).
+    for K in (16, 128, 256, 512):
+        shapes, types = packed_gdn(K=K)
+        assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1) == ((1, 20, 3, 8), 0)
+    shapes, types = packed_gdn(s0=False)
+    assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1)[0] == (1, 20, 3, 8)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda s, t: s.__setitem__(0, (2, 20, 3, 16)),
+     "GatedDeltaNet2Fn with cu_seqlens requires batch 1 (sequences packed along seqlen)"),
+    (lambda s, t: s.__setitem__(6, (1, 3, 16, 8)), "initial_state must have shape (sequences, head, headdim_k, headdim_v)"),
+    (lambda s, t: t.__setitem__(7, 1), "cu_seqlens must be an int64 tensor"),
+    (lambda s, t: s.__setitem__(7, (2, 2)), "cu_seqlens must have rank 1"),
+    (lambda s, t: s.__setitem__(7, (1,)), "cu_seqlens must hold at least two offsets"),
+])
+def test_gdn2_packed_sequences_rejections(mutate, msg):
+    shapes, types = packed_gdn()
+    mutate(shapes, types)
+    if shapes[0][0] == 2:   # the other q-shaped inputs follow q
+        shapes[1:6] = [(2,) + tuple(x[1:]) for x in shapes[1:6]]
+    with pytest.raises(XmError) as e:
+        validate("gated_deltanet2", shapes, types, has_cu_seqlens=1)
+    assert e.value.message == msg
+
+
+def test_gdn2_packed_sequences_limits():
+    shapes, types = packed_gdn(K=600)
+    with pytest.raises(XmError, match="with cu_seqlens supports headdim_k up to 512"):
+        validate("gated_deltanet2", shapes, types, has_cu_seqlens=1)
+    with pytest.raises(XmError, match="expects 8 inputs, got 7"):
+        validate("gated_deltanet2", gdn_shapes(B=1), has_cu_seqlens=1)
+
+
 def test_gdn2_absent_initial_state():
     out, _ = validate("gated_deltanet2", gdn_shapes(s0=False))
     assert out == (2, 5, 3, 8)
@@ -332,6 +377,27 @@ def test_m3_input_state_shapes(i, shape, msg):
     with pytest.raises(XmError) as e:
         validate("mamba3_siso", m3_shapes() + st, has_input_states=1, has_z=0)
     assert e.value.message == msg
+
+
+def test_m3_packed_sequences():
+    # Widening: cu_seqlens is input 15 (16 inputs; the state slots 11-14 stay
+    # empty without has_input_states).
+    base = m3_shapes(B=1, T=30)
+    types = [1] * 15 + [I64]
+    out, scratch = validate("mamba3_siso", base + [None] * 4 + [(4,)], types, has_cu_seqlens=1, has_z=0)
+    assert out == (1, 30, 4, 8) and scratch == 0
+    st = m3_state_shapes(B=3)
+    assert validate("mamba3_siso", base + st + [(4,)], types, has_cu_seqlens=1, has_input_states=1, has_z=0)[0] == \
+        (1, 30, 4, 8)
+    with pytest.raises(XmError, match="state inputs need has_input_states=1"):
+        validate("mamba3_siso", base + st + [(4,)], types, has_cu_seqlens=1, has_z=0)
+    with pytest.raises(XmError, match="ssm_state must have shape"):
+        validate("mamba3_siso", base + m3_state_shapes(B=1) + [(4,)], types, has_cu_seqlens=1, has_input_states=1,
+                 has_z=0)
+    with pytest.raises(XmError, match="requires batch 1"):
+        validate("mamba3_siso", m3_shapes(B=2) + [None] * 4 + [(4,)], types, has_cu_seqlens=1, has_z=0)
+    with pytest.raises(XmError, match="cu_seqlens must be an int64 tensor"):
+        validate("mamba3_siso", base + [None] * 4 + [(4,)], [1] * 16, has_cu_seqlens=1, has_z=0)
 
 
 def test_m3_valid():
@@ -401,13 +467,18 @@ def test_ort_registration_domain_and_order():
 def test_ort_descriptors_match_reference_contract():
     ops = _src("ops_ort.cpp")
     # output 1 (optional) is the state after the last token where the op has one
-    # (Mamba-3: inputs 11-14 optional, the input states)
-    for name, n_in, n_out in (("SelectiveScanFn", 8, 2), ("Mamba3SisoFn", 15, 5), ("GatedDeltaNet2Fn", 7, 2)):
-        block = ops[ops.index(f'return "{name}";') - 400:ops.index(f'return "{name}";') + 800]
+    # (Mamba-3: inputs 11-14 the input states, 15 cu_seqlens; GDN-2: 7 cu_seqlens; all optional)
+    for name, n_in, n_out, n_req in (("SelectiveScanFn", 8, 2, 8), ("Mamba3SisoFn", 16, 5, 11),
+                                     ("GatedDeltaNet2Fn", 8, 2, 7)):
+        block = ops[ops.index(f'return "{name}";') - 400:ops.index(f'return "{name}";') + 1000]
         assert f"GetInputTypeCount() const {{ return {n_in}; }}" in block
         assert f"GetOutputTypeCount() const {{ return {n_out}; }}" in block
         assert "return i == 0 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;" in block
-        assert ("GetInputCharacteristic" in block) == (name == "Mamba3SisoFn")
+        if n_req < n_in:
+            assert f"return i < {n_req} ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;" in block
+            assert f"return i == {n_in - 1} ? ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64" in block
+        else:
+            assert "GetInputCharacteristic" not in block
         assert "GetExecutionProviderType() const { return XM_ORT_GPU_EP; }" in block
     for attr in ("delta_softplus", "return_last_state", "chunk_size", "has_d", "has_z", "return_final_states",
                  "has_input_states", "has_cu_seqlens", "scale", "use_qk_l2norm_in_kernel", "output_final_state",

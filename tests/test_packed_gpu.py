@@ -1,0 +1,136 @@
+"""Packed sequences (cu_seqlens) on the GPU, through the C ABI.
+
+GatedDeltaNet2Fn and Mamba3SisoFn with has_cu_seqlens=1 (a widening: the
+reference rejects it, gated_deltanet2_fn_ort.cpp:55-57, mamba3_siso_fn_ort.cpp:
+56-58) take N sequences packed along one row of tokens, with one state per
+sequence.  Each packed call is checked against the fp64 oracle run on every
+sequence by itself, with that sequence's initial state: outputs and final
+states.  Covered: empty and one-token sequences, lengths that end inside a
+token block, every GDN-2 key layout up to headdim_k 512, Mamba-3 with and
+without input states.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import cref
+from parity import TOL_GDN2, TOL_M3, check, to_dev
+from xmetai_onnx_plugins import gated_deltanet2_fn, mamba3_siso_fn, workloads as W
+
+pytestmark = pytest.mark.gpu
+
+GDN_KEYS = ("q", "k", "v", "g", "beta", "w")
+M3_KEYS = ("Q", "K", "V", "ADT", "DT", "Trap", "Q_bias", "K_bias", "Angles", "D", "Z")
+
+
+def offsets(lengths):
+    return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+
+
+def cu_dev(lengths):
+    import torch
+    return torch.from_numpy(offsets(lengths)).to("cuda")
+
+
+# ---------------------------------------------------------------------------
+# GatedDeltaNet2Fn
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dk,dv", [(16, 8), (64, 40), (128, 65), (320, 24), (512, 16)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_gdn2_packed_matches_per_sequence(dk, dv, with_state):
+    import torch
+    lengths = [37, 0, 1, 16, 50]
+    T, H, N = sum(lengths), 2, len(lengths)
+    s = W.GatedDeltaNet2Shape(1, T, H, dk, dv, initial_state=False)
+    inp = W.gated_deltanet2_inputs(s, seed=12)
+    rng = np.random.default_rng(13)
+    s0 = (0.05 * rng.standard_normal((N, H, dk, dv))).astype(np.float32) if with_state else None
+    o, st = gated_deltanet2_fn(*(to_dev(inp[k]) for k in GDN_KEYS), None if s0 is None else to_dev(s0),
+                               scale=s.scale, use_qk_l2norm_in_kernel=s.l2norm, output_final_state=True,
+                               cu_seqlens=cu_dev(lengths))
+    torch.cuda.synchronize()
+    o, st = o.cpu().numpy(), st.cpu().numpy()
+    assert o.shape == (1, T, H, dv) and st.shape == (N, H, dk, dv)
+    cu = offsets(lengths)
+    for n in range(N):
+        lo, hi = cu[n], cu[n + 1]
+        init = s0[n:n + 1] if s0 is not None else np.zeros((1, H, dk, dv), np.float32)
+        if hi == lo:   # an empty sequence passes its state through
+            np.testing.assert_array_equal(st[n], init[0])
+            continue
+        part = [np.ascontiguousarray(inp[k][:, lo:hi]) for k in GDN_KEYS]
+        ro, rs = cref.gated_deltanet2(*part, init, scale=s.scale, use_qk_l2norm=s.l2norm, dtype=np.float64,
+                                      return_state=True)
+        check(f"gdn2_packed/{dk}x{dv}/seq{n}/o", o[:, lo:hi], ro, TOL_GDN2)
+        check(f"gdn2_packed/{dk}x{dv}/seq{n}/S", st[n:n + 1], rs, TOL_GDN2)
+
+
+def test_gdn2_packed_one_sequence_equals_unpacked():
+    """One sequence covering the whole row: the same outputs as the plain call
+    (which takes the chunked path at dk = 128) within the tolerance."""
+    import torch
+    s = W.GatedDeltaNet2Shape(1, 300, 4, 128, 128)
+    inp = W.gated_deltanet2_inputs(s, seed=14)
+    args = [to_dev(inp[k]) for k in GDN_KEYS] + [to_dev(inp["initial_state"])]
+    kw = dict(scale=s.scale, use_qk_l2norm_in_kernel=s.l2norm, output_final_state=True)
+    o1, s1 = gated_deltanet2_fn(*args, **kw)
+    o2, s2 = gated_deltanet2_fn(*args, cu_seqlens=cu_dev([300]), **kw)
+    torch.cuda.synchronize()
+    check("gdn2_packed/one/o", o2.cpu().numpy(), o1.cpu().numpy(), 1e-5)
+    check("gdn2_packed/one/S", s2.cpu().numpy(), s1.cpu().numpy(), 1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Mamba3SisoFn
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_qk,p_dim,hq", [(16, 8, 1), (64, 33, 2), (128, 64, 2), (256, 24, 2)])
+@pytest.mark.parametrize("with_states", [False, True])
+def test_m3_packed_matches_per_sequence(n_qk, p_dim, hq, with_states):
+    import torch
+    lengths = [45, 1, 0, 33, 70]
+    T, H, N = sum(lengths), 2, len(lengths)
+    s = W.Mamba3SisoShape(1, T, H, p_dim, n_qk, nheads_qk=hq, has_z=True)
+    inp = W.mamba3_siso_inputs(s, seed=15)
+    A = s.a
+    rng = np.random.default_rng(16)
+    ins = None
+    if with_states:
+        ins = ((0.3 * rng.standard_normal((N, H, p_dim, n_qk))).astype(np.float32),
+               rng.uniform(0, 6.28, (N, H, A)).astype(np.float32),
+               (rng.standard_normal((N, H, n_qk)) * n_qk ** -0.5).astype(np.float32),
+               rng.standard_normal((N, H, p_dim)).astype(np.float32))
+    y, st = mamba3_siso_fn(*(to_dev(inp[k]) for k in M3_KEYS),
+                           input_states=None if ins is None else tuple(to_dev(x) for x in ins),
+                           return_final_states=True, cu_seqlens=cu_dev(lengths))
+    torch.cuda.synchronize()
+    y, st = y.cpu().numpy(), [x.cpu().numpy() for x in st]
+    assert y.shape == (1, T, H, p_dim) and st[0].shape == (N, H, p_dim, n_qk)
+    cu = offsets(lengths)
+    two_pi = 2.0 * float(np.float32(np.pi))
+    for n in range(N):
+        lo, hi = cu[n], cu[n + 1]
+        init = tuple(x[n:n + 1] for x in ins) if ins is not None else None
+        if hi == lo:   # an empty sequence passes its states through (zeros without input states)
+            for got, x in zip(st, init or [None] * 4):
+                np.testing.assert_array_equal(got[n], x[0] if x is not None else 0.0)
+            continue
+        part = {}
+        for k in M3_KEYS:
+            x = inp[k]
+            if x is None or k in ("Q_bias", "K_bias", "D"):
+                part[k] = x
+            elif k in ("ADT", "DT", "Trap"):
+                part[k] = np.ascontiguousarray(x[:, :, lo:hi])
+            else:
+                part[k] = np.ascontiguousarray(x[:, lo:hi])
+        ry, rst = cref.mamba3_siso(*(part[k] for k in M3_KEYS), dtype=np.float64, input_states=init,
+                                   return_state=True)
+        tag = f"m3_packed/{n_qk}x{p_dim}/seq{n}"
+        check(f"{tag}/y", y[:, lo:hi], ry, TOL_M3)
+        for g, r, nm in zip(st, rst, ("ssm", "angle", "k", "v")):
+            g = g[n:n + 1]
+            if nm == "angle":
+                g = r + (np.mod(g - r + two_pi / 2, two_pi) - two_pi / 2)
+            check(f"{tag}/{nm}", g, r, TOL_M3)

@@ -185,13 +185,23 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
     const int cl = grow / R;                      // column within the workgroup
     const int rho = grow % R;                     // row within the column
     const int kb = (rho * 16 + kg) * KT;          // first of this lane's KT keys
-    const int T = p.seqlen, H = p.nheads, dk = p.dk, dv = p.dv;
+    const int H = p.nheads, dk = p.dk, dv = p.dv;
     const int nvb = (dv + COLS - 1) / COLS;
     // the nvb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
     const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
     const int vb = wg % nvb;
     const int bh = wg / nvb;
     const int b = bh / H, h = bh % H;
+    // tokens of sequence b: [tok0, tok0 + T) of the token axis (packed
+    // sequences: offsets clamped into [0, seqlen], an inverted range is empty)
+    int T = p.seqlen;
+    size_t tok0 = static_cast<size_t>(b) * T;
+    if (p.cu_seqlens != nullptr) {
+        const long long lo = min(max(p.cu_seqlens[b], 0LL), static_cast<long long>(p.seqlen));
+        const long long hi = min(max(p.cu_seqlens[b + 1], lo), static_cast<long long>(p.seqlen));
+        tok0 = static_cast<size_t>(lo);
+        T = static_cast<int>(hi - lo);
+    }
     const int v0 = vb * COLS;
     const int col = v0 + cl;                      // this lane's value column
 
@@ -205,8 +215,8 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
 
     // token t of (b,h): q/k/g/beta row at kbase + t*kstride, v/w/out row at vbase + t*vstride
     const size_t kstride = static_cast<size_t>(H) * dk, vstride = static_cast<size_t>(H) * dv;
-    const size_t kbase = (static_cast<size_t>(b) * T * H + h) * dk;
-    const size_t vbase = (static_cast<size_t>(b) * T * H + h) * dv;
+    const size_t kbase = (tok0 * H + h) * dk;
+    const size_t vbase = (tok0 * H + h) * dv;
     auto key = [&](int x) __attribute__((always_inline)) { return lane * KPL + x; };
 
     // Raw rows of the next block, loaded before the current block's recurrence
@@ -348,17 +358,19 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
         if (rho == 0 && kg < min(TB, T - t0) && col < dv) p.out[vbase + static_cast<size_t>(t0 + kg) * vstride + col] = oreg;
     };
 
-    load_block(0);
-    prep_block(0, 0);
-    __syncthreads();
-    const int nblk = (T + TB - 1) / TB;
-    for (int j = 0; j < nblk; ++j) {
-        const int buf = j & 1;
-        const bool next = j + 1 < nblk;
-        if (next) load_block((j + 1) * TB);
-        recur_block(j * TB, buf);
-        if (next) prep_block((j + 1) * TB, buf ^ 1);
+    if (T > 0) {   // workgroup-uniform: an empty sequence passes its state through
+        load_block(0);
+        prep_block(0, 0);
         __syncthreads();
+        const int nblk = (T + TB - 1) / TB;
+        for (int j = 0; j < nblk; ++j) {
+            const int buf = j & 1;
+            const bool next = j + 1 < nblk;
+            if (next) load_block((j + 1) * TB);
+            recur_block(j * TB, buf);
+            if (next) prep_block((j + 1) * TB, buf ^ 1);
+            __syncthreads();
+        }
     }
     // State after the last token (identity tokens of a short last block keep it unchanged).
     if (p.final_state != nullptr && col < dv) {
@@ -542,9 +554,9 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
 
 }  // namespace
 
-size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
-    if (dk <= 256) return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv);   // chunked path
-    if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed) {
+    if (dk <= 256 && !packed) return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv);   // chunked path
+    if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch (packed sequences always take it)
     const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
     const size_t rows = static_cast<size_t>(batch) * nheads * cap;
     const size_t state = seqlen > kChunkTokens ? static_cast<size_t>(batch) * nheads * dk * dv : 0;
@@ -554,10 +566,13 @@ size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
-    if (LaunchGatedDeltaNet2Chunked(p, scratch, stream_v)) return;   // dk <= 256: gated_deltanet2_chunk.hip
+    // dk <= 256: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
+    if (p.cu_seqlens == nullptr && LaunchGatedDeltaNet2Chunked(p, scratch, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.dk > kMaxLdsKeys)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");
+    if (p.cu_seqlens != nullptr && p.dk > kFusedKeyLimit)
+        throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn with cu_seqlens supports headdim_k up to 512");
     if (p.dk <= kFusedKeyLimit) {
         const FusedConfig c = ChooseFused(p);
         if (c.nw == 8) LaunchFusedN<8>(p, c, stream);

@@ -625,6 +625,7 @@ size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream_v) {
     const char *path = std::getenv("XM_GDN2_PATH");
     if (path != nullptr && std::strcmp(path, "seq") == 0) return false;
+    if (p.cu_seqlens != nullptr) return false;   // packed sequences: the fused kernel
     if (p.dk > kChunkKeyLimit) return false;
     // the recurrence's 32-bit buffer offsets span 16 tokens of [B,T,H,V]
     if (static_cast<long long>(p.nheads) * p.dv >= (1LL << 25)) return false;

@@ -12,6 +12,10 @@
 // accepted through xm_gated_deltanet2_forward_states, which also writes the
 // state after the last token, [batch, nheads, headdim_k, headdim_v] (the
 // layout initial_state takes, so a call can continue where another stopped).
+// Widening: has_cu_seqlens = 1 (rejected at :55-57) packs N sequences along
+// seqlen: input 7 is cu_seqlens (int64 [N+1]), the tensors have batch 1 and
+// the states are [N, nheads, headdim_k, headdim_v]; the fused kernel reads
+// each sequence's token range on the device (headdim_k up to 512).
 #include <cmath>
 
 #include "xm_common.h"
@@ -21,11 +25,11 @@ namespace xm {
 namespace {
 
 constexpr size_t kNumInputs = 7;
+constexpr size_t kNumInputsPacked = 8;   // + cu_seqlens
 
 void CheckAttrs(const xm_gated_deltanet2_attrs_t &a) {
     if (a.use_gate_in_kernel != 0)
         Unsupported("GatedDeltaNet2Fn v1 expects pre-applied gate tensors and does not support use_gate_in_kernel");
-    if (a.has_cu_seqlens != 0) Unsupported("GatedDeltaNet2Fn v1 does not support cu_seqlens");
     if (a.state_v_first != 0) Unsupported("GatedDeltaNet2Fn v1 expects state layout (batch, head, key, value)");
     if (!(a.scale > 0.0f) || !std::isfinite(a.scale)) Invalid("GatedDeltaNet2Fn requires a positive finite scale");
 }
@@ -36,7 +40,7 @@ struct Plan {
     size_t scratch = 0;
 };
 
-Plan Validate(const std::vector<View> &in, const xm_gated_deltanet2_attrs_t &attrs) {
+Plan Validate(const std::vector<View> &in, const IndexView *cu, const xm_gated_deltanet2_attrs_t &attrs) {
     const View &q = in[0], &k = in[1], &v = in[2], &g = in[3], &beta = in[4], &w = in[5], &s0 = in[6];
     // ValidateInputs (reference :187-219)
     RequireRank(q, 4, "q");
@@ -51,21 +55,28 @@ Plan Validate(const std::vector<View> &in, const xm_gated_deltanet2_attrs_t &att
     if (v.shape[0] != q.shape[0] || v.shape[1] != q.shape[1] || v.shape[2] != q.shape[2])
         Invalid("v batch/seqlen/head dimensions must match q");
     RequireSameShape(v, w, "v", "w");
+    // packed sequences: one row of tokens, one state per sequence
+    if (cu != nullptr && q.shape[0] != 1)
+        Invalid("GatedDeltaNet2Fn with cu_seqlens requires batch 1 (sequences packed along seqlen)");
+    const int64_t nstate = cu != nullptr ? cu->count - 1 : q.shape[0];
     if (s0.present()) {
         RequireRank(s0, 4, "initial_state");
-        if (s0.shape[0] != q.shape[0] || s0.shape[1] != q.shape[2] || s0.shape[2] != q.shape[3] ||
+        if (s0.shape[0] != nstate || s0.shape[1] != q.shape[2] || s0.shape[2] != q.shape[3] ||
             s0.shape[3] != v.shape[3])
-            Invalid("initial_state must have shape (batch, head, headdim_k, headdim_v)");
+            Invalid(cu != nullptr ? "initial_state must have shape (sequences, head, headdim_k, headdim_v)"
+                                  : "initial_state must have shape (batch, head, headdim_k, headdim_v)");
     }
     Plan plan;
     plan.out_shape = v.shape;
     GatedDeltaNet2Params &p = plan.params;
-    p.batch = ToIntDim(q.shape[0], "batch");
+    p.batch = ToIntDim(nstate, cu != nullptr ? "sequences" : "batch");
     p.seqlen = ToIntDim(q.shape[1], "seqlen");
     p.nheads = ToIntDim(q.shape[2], "nheads");
     p.dk = ToIntDim(q.shape[3], "headdim_k");
     p.dv = ToIntDim(v.shape[3], "headdim_v");
     if (p.dk > 2048) Unsupported("GatedDeltaNet2Fn supports headdim_k up to 2048");
+    if (cu != nullptr && p.dk > 512) Unsupported("GatedDeltaNet2Fn with cu_seqlens supports headdim_k up to 512");
+    p.cu_seqlens = cu != nullptr ? cu->data : nullptr;
     p.q = q.data;
     p.k = k.data;
     p.v = v.data;
@@ -75,15 +86,23 @@ Plan Validate(const std::vector<View> &in, const xm_gated_deltanet2_attrs_t &att
     p.initial_state = s0.present() ? s0.data : nullptr;
     p.l2norm = attrs.use_qk_l2norm_in_kernel != 0;
     p.scale = attrs.scale;
-    plan.scratch = GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv);
+    plan.scratch = GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv, cu != nullptr);
     return plan;
+}
+
+// The views (7 float inputs, plus cu_seqlens when packed) and the plan.
+Plan Prepare(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t &attrs) {
+    const bool packed = attrs.has_cu_seqlens != 0;
+    auto views = MakeViews(inputs, n_inputs, packed ? kNumInputsPacked : kNumInputs, "GatedDeltaNet2Fn", kNumInputs);
+    if (!packed) return Validate(views, nullptr, attrs);
+    const IndexView cu = MakeIndexView(inputs[kNumInputs], "cu_seqlens");
+    return Validate(views, &cu, attrs);
 }
 
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t &attrs, float *out,
              float *final_state, void *stream, const xm_allocator_t *alloc) {
     CheckAttrs(attrs);
-    auto views = MakeViews(inputs, n_inputs, kNumInputs, "GatedDeltaNet2Fn");
-    Plan plan = Validate(views, attrs);
+    Plan plan = Prepare(inputs, n_inputs, attrs);
     if (out == nullptr) Invalid("output pointer is null");
     const bool want_state = attrs.output_final_state != 0;
     if (want_state && final_state == nullptr) Invalid("output_final_state=1 needs a final_state buffer");
@@ -122,8 +141,7 @@ int xm_gated_deltanet2_validate(const xm_tensor_t *inputs, size_t n_inputs, cons
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
         xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "GatedDeltaNet2Fn");
-        xm::Plan plan = xm::Validate(views, *attrs);
+        xm::Plan plan = xm::Prepare(inputs, n_inputs, *attrs);
         xm::WriteShape(plan.out_shape, out_shape, out_rank);
         if (scratch_bytes) *scratch_bytes = plan.scratch;
     });

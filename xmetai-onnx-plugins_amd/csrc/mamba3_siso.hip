@@ -40,6 +40,11 @@
 // start the scan from S = ssm + v (x) k * DT_0 (1 - sigmoid(Trap_0)), the
 // last token's look-ahead now that its successor is known, and theta = angle,
 // so two calls chained through the states equal one call.
+//
+// Packed sequences (cu_seqlens, a widening): batch indexes sequences packed
+// along one row of seqlen tokens; a workgroup reads its sequence's offsets
+// (clamped into [0, seqlen]; an inverted range is empty, and an empty
+// sequence passes its states through, its pending look-ahead included).
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -115,7 +120,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
-    const int T = p.seqlen, N = p.n, P = p.p, A = p.a, H = p.nheads;
+    const int N = p.n, P = p.p, A = p.a, H = p.nheads;
     const int half_n = N / 2;
     const int nrb = (P + kRows - 1) / kRows;
     // the nrb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
@@ -126,9 +131,20 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     const int gq = h / (H / p.nheads_qk);
     const int r0 = rb * kRows;
     const float dval = p.D ? p.D[h] : 0.0f;
-    const float *dtr = p.DT + static_cast<size_t>(bh) * T;
-    const float *trr = p.Trap + static_cast<size_t>(bh) * T;
-    const float *adr = p.ADT + static_cast<size_t>(bh) * T;
+    // tokens of sequence b: [tok0, tok0 + T) of its token axis
+    int T = p.seqlen;
+    size_t tok0 = static_cast<size_t>(b) * T;    // in [B*T] for Q/K/V/Angles/Z
+    size_t sbase = static_cast<size_t>(bh) * T;  // in [B*H*T] for ADT/DT/Trap
+    if (p.cu_seqlens != nullptr) {
+        const long long lo = min(max(p.cu_seqlens[b], 0LL), static_cast<long long>(p.seqlen));
+        const long long hi = min(max(p.cu_seqlens[b + 1], lo), static_cast<long long>(p.seqlen));
+        tok0 = static_cast<size_t>(lo);
+        sbase = static_cast<size_t>(h) * p.seqlen + static_cast<size_t>(lo);
+        T = static_cast<int>(hi - lo);
+    }
+    const float *dtr = p.DT + sbase;
+    const float *trr = p.Trap + sbase;
+    const float *adr = p.ADT + sbase;
 
     // ---- preparation state: lane handles pairs lane + 64*x, tokens w*SEG + s
     float2 qbias[PB], kbias[PB];
@@ -144,12 +160,12 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     }
     // Per-token row bases and strides (elements); token t of this (b,h) is at base + t * stride.
     const size_t q_stride = static_cast<size_t>(p.nheads_qk) * N;
-    const float *qbase = p.Q + (static_cast<size_t>(b) * T * p.nheads_qk + gq) * N;
-    const float *kbase = p.K + (static_cast<size_t>(b) * T * p.nheads_qk + gq) * N;
+    const float *qbase = p.Q + (tok0 * p.nheads_qk + gq) * N;
+    const float *kbase = p.K + (tok0 * p.nheads_qk + gq) * N;
     const size_t a_stride = static_cast<size_t>(H) * A;
-    const float *abase = p.Angles + (static_cast<size_t>(b) * T * H + h) * A;
+    const float *abase = p.Angles + (tok0 * H + h) * A;
     const size_t v_stride = static_cast<size_t>(H) * P;
-    const size_t vbase = (static_cast<size_t>(b) * T * H + h) * P;   // also the output / Z base
+    const size_t vbase = (tok0 * H + h) * P;   // also the output / Z base
 
     // Raw prefetched values.  The loads use clamped addresses and nothing
     // selects on them until they are consumed after the recurrence: a select
@@ -292,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 #pragma unroll
     for (int j = 0; j < KPT; ++j) S[j] = 0.0f;
     if (p.in_ssm != nullptr && row < P) {
-        const float look0 = dtr[0] * (1.0f - FastSigmoid(trr[0]));
+        const float look0 = T > 0 ? dtr[0] * (1.0f - FastSigmoid(trr[0])) : 0.0f;   // stays pending when empty
         const float vl = p.in_v[static_cast<size_t>(bh) * P + row];
         const float *srow = p.in_ssm + (static_cast<size_t>(bh) * P + row) * N;
         const float *krow = p.in_k + static_cast<size_t>(bh) * N;
@@ -362,20 +378,24 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 
     if (tid < PAIRS) sCarry[tid] = (p.in_angle != nullptr && tid < A) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + tid]) : 0.0;
     const int nblk = (T + TB - 1) / TB;
-    load_prep(0);
-    prep_a(0);
-    __syncthreads();
-    prep_b(0, 0, 0);
-    __syncthreads();
-    for (int j = 0; j < nblk; ++j) {
-        const int buf = j & 1;
-        const bool next = j + 1 < nblk;
-        if (next) load_prep((j + 1) * TB);
-        recur(j * TB, buf);
-        if (next) prep_a((j + 1) * TB);
+    if (T > 0) {   // workgroup-uniform: an empty sequence passes its states through
+        load_prep(0);
+        prep_a(0);
         __syncthreads();
-        if (next) prep_b((j + 1) * TB, buf ^ 1, (j + 1) & 1);
+        prep_b(0, 0, 0);
         __syncthreads();
+        for (int j = 0; j < nblk; ++j) {
+            const int buf = j & 1;
+            const bool next = j + 1 < nblk;
+            if (next) load_prep((j + 1) * TB);
+            recur(j * TB, buf);
+            if (next) prep_a((j + 1) * TB);
+            __syncthreads();
+            if (next) prep_b((j + 1) * TB, buf ^ 1, (j + 1) & 1);
+            __syncthreads();
+        }
+    } else {
+        __syncthreads();   // the initial angle carry, read back below
     }
     if (p.f_ssm != nullptr) {
         // the last block's buffers are intact: sK holds its rotated k, the
@@ -386,12 +406,18 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
             for (int j = 0; j < KPT; ++j)
                 if (kg * KPT + j < N) srow[kg * KPT + j] = S[j];
         }
-        if (tid < kRows && r0 + tid < P)
-            p.f_v[static_cast<size_t>(bh) * P + r0 + tid] = p.V[vbase + static_cast<size_t>(T - 1) * v_stride + r0 + tid];
+        if (tid < kRows && r0 + tid < P) {
+            const size_t o = static_cast<size_t>(bh) * P + r0 + tid;
+            p.f_v[o] = T > 0 ? p.V[vbase + static_cast<size_t>(T - 1) * v_stride + r0 + tid]
+                             : (p.in_v != nullptr ? p.in_v[o] : 0.0f);
+        }
         if (rb == 0) {
-            const int tl = (T - 1) - (nblk - 1) * TB;
+            const int tl = T > 0 ? (T - 1) - (nblk - 1) * TB : 0;
             const float *krow = sK + (((nblk - 1) & 1) * TB + tl) * NPS;
-            for (int i = tid; i < N; i += kThreads) p.f_k[static_cast<size_t>(bh) * N + i] = krow[L::Pos(i)];
+            for (int i = tid; i < N; i += kThreads) {
+                const size_t o = static_cast<size_t>(bh) * N + i;
+                p.f_k[o] = T > 0 ? krow[L::Pos(i)] : (p.in_k != nullptr ? p.in_k[o] : 0.0f);
+            }
             for (int i = tid; i < A; i += kThreads)
                 p.f_angle[static_cast<size_t>(bh) * A + i] = static_cast<float>(sCarry[(nblk & 1) * PAIRS + i]);
         }

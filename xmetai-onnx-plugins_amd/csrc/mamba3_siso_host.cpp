@@ -13,6 +13,11 @@
 // 11-14 (15 inputs); final states go to the four buffers of
 // xm_mamba3_siso_forward_states.  Two calls chained through the states give
 // the outputs and states of one call.
+// Widening: has_cu_seqlens = 1 (rejected at :56-58) packs N sequences along
+// seqlen: input 15 is cu_seqlens (int64 [N+1]; 16 inputs, of which 11-14, the
+// states, are empty unless has_input_states = 1), the tensors have batch 1
+// and the states are [N, ...]; the kernel reads each sequence's token range
+// on the device.
 #include "xm_common.h"
 #include "xm_params.h"
 
@@ -21,13 +26,14 @@ namespace {
 
 constexpr size_t kNumInputs = 11;
 constexpr size_t kNumInputsWithStates = 15;
+constexpr size_t kNumInputsPacked = 16;   // cu_seqlens at 15, the state slots 11-14 before it
 
 void CheckAttrs(const xm_mamba3_siso_attrs_t &a) {
     if (a.chunk_size <= 0) Invalid("Mamba3SisoFn requires chunk_size > 0");
-    if (a.has_cu_seqlens != 0) Unsupported("Mamba3SisoFn v1 does not support cu_seqlens");
 }
 
 size_t ExpectedInputs(const xm_mamba3_siso_attrs_t &a) {
+    if (a.has_cu_seqlens != 0) return kNumInputsPacked;
     return a.has_input_states != 0 ? kNumInputsWithStates : kNumInputs;
 }
 
@@ -36,7 +42,7 @@ struct Plan {
     std::vector<int64_t> out_shape;
 };
 
-Plan Validate(const std::vector<View> &in, const xm_mamba3_siso_attrs_t &attrs) {
+Plan Validate(const std::vector<View> &in, const IndexView *cu, const xm_mamba3_siso_attrs_t &attrs) {
     const View &Q = in[0], &K = in[1], &V = in[2], &ADT = in[3], &DT = in[4], &Trap = in[5];
     const View &Qb = in[6], &Kb = in[7], &Ang = in[8], &D = in[9], &Z = in[10];
     // ValidateInputs (reference :146-227)
@@ -80,10 +86,15 @@ Plan Validate(const std::vector<View> &in, const xm_mamba3_siso_attrs_t &attrs) 
         if (Z.shape[0] != batch || Z.shape[1] != seqlen || Z.shape[2] != nheads || Z.shape[3] != headdim_v)
             Invalid("Z must have shape (batch, seqlen, nheads, headdim_v)");
     }
+    // packed sequences: one row of tokens, one state per sequence
+    if (cu != nullptr && batch != 1)
+        Invalid("Mamba3SisoFn with cu_seqlens requires batch 1 (sequences packed along seqlen)");
+    const int64_t nstate = cu != nullptr ? cu->count - 1 : batch;
     Plan plan;
     plan.out_shape = V.shape;
     Mamba3SisoParams &p = plan.params;
-    p.batch = ToIntDim(Q.shape[0], "batch");
+    p.batch = ToIntDim(nstate, cu != nullptr ? "sequences" : "batch");
+    p.cu_seqlens = cu != nullptr ? cu->data : nullptr;
     p.seqlen = ToIntDim(Q.shape[1], "seqlen");
     p.nheads_qk = ToIntDim(Q.shape[2], "nheads_qk");
     p.n = ToIntDim(Q.shape[3], "headdim_qk");
@@ -102,19 +113,22 @@ Plan Validate(const std::vector<View> &in, const xm_mamba3_siso_attrs_t &attrs) 
     p.Angles = Ang.data;
     p.D = has_d ? D.data : nullptr;
     p.Z = has_z ? Z.data : nullptr;
-    if (attrs.has_input_states != 0) {
+    if (attrs.has_input_states == 0) {
+        for (size_t i = kNumInputs; i < in.size(); ++i)
+            if (in[i].present()) Invalid("Mamba3SisoFn state inputs need has_input_states=1");
+    } else {
         const View &Ss = in[11], &As = in[12], &Ks = in[13], &Vs = in[14];
         RequireRank(Ss, 4, "ssm_state");
         RequireRank(As, 3, "angle_state");
         RequireRank(Ks, 3, "k_state");
         RequireRank(Vs, 3, "v_state");
-        if (Ss.shape != std::vector<int64_t>{batch, nheads, headdim_v, headdim_qk})
+        if (Ss.shape != std::vector<int64_t>{nstate, nheads, headdim_v, headdim_qk})
             Invalid("ssm_state must have shape (batch, nheads, headdim_v, headdim_qk)");
-        if (As.shape != std::vector<int64_t>{batch, nheads, headdim_angles})
+        if (As.shape != std::vector<int64_t>{nstate, nheads, headdim_angles})
             Invalid("angle_state must have shape (batch, nheads, headdim_angles)");
-        if (Ks.shape != std::vector<int64_t>{batch, nheads, headdim_qk})
+        if (Ks.shape != std::vector<int64_t>{nstate, nheads, headdim_qk})
             Invalid("k_state must have shape (batch, nheads, headdim_qk)");
-        if (Vs.shape != std::vector<int64_t>{batch, nheads, headdim_v})
+        if (Vs.shape != std::vector<int64_t>{nstate, nheads, headdim_v})
             Invalid("v_state must have shape (batch, nheads, headdim_v)");
         p.in_ssm = Ss.data;
         p.in_angle = As.data;
@@ -124,11 +138,20 @@ Plan Validate(const std::vector<View> &in, const xm_mamba3_siso_attrs_t &attrs) 
     return plan;
 }
 
+// The float views (and cu_seqlens, the last input, when packed) and the plan.
+Plan Prepare(const xm_tensor_t *inputs, size_t n_inputs, const xm_mamba3_siso_attrs_t &attrs) {
+    const size_t expected = ExpectedInputs(attrs);
+    const bool packed = attrs.has_cu_seqlens != 0;
+    auto views = MakeViews(inputs, n_inputs, expected, "Mamba3SisoFn", packed ? kNumInputsWithStates : expected);
+    if (!packed) return Validate(views, nullptr, attrs);
+    const IndexView cu = MakeIndexView(inputs[kNumInputsWithStates], "cu_seqlens");
+    return Validate(views, &cu, attrs);
+}
+
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_mamba3_siso_attrs_t &attrs, float *out,
              float *const *states, void *stream) {
     CheckAttrs(attrs);
-    auto views = MakeViews(inputs, n_inputs, ExpectedInputs(attrs), "Mamba3SisoFn");
-    Plan plan = Validate(views, attrs);
+    Plan plan = Prepare(inputs, n_inputs, attrs);
     if (out == nullptr) Invalid("output pointer is null");
     plan.params.out = out;
     if (attrs.return_final_states != 0) {
@@ -170,8 +193,7 @@ int xm_mamba3_siso_validate(const xm_tensor_t *inputs, size_t n_inputs, const xm
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
         xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::ExpectedInputs(*attrs), "Mamba3SisoFn");
-        xm::Plan plan = xm::Validate(views, *attrs);
+        xm::Plan plan = xm::Prepare(inputs, n_inputs, *attrs);
         xm::WriteShape(plan.out_shape, out_shape, out_rank);
         if (scratch_bytes) *scratch_bytes = 0;
     });

@@ -13,6 +13,9 @@
 // Mamba3SisoFn with return_final_states=1 fills optional outputs 1-4 (ssm
 // [B,H,P,N], angle [B,H,A], k [B,H,N], v [B,H,P]) and with has_input_states=1
 // takes the same four as optional inputs 11-14.
+// Widening: has_cu_seqlens=1 (GatedDeltaNet2Fn, Mamba3SisoFn) takes the
+// packed sequences' offsets as an optional int64 input (7 and 15); the
+// states then have one row per sequence.
 #include "ort_glue.h"
 
 namespace {
@@ -88,12 +91,13 @@ public:
         Check(xm_mamba3_siso_check_attrs(&attrs_, err, sizeof(err)), err);
     }
     void Compute(OrtKernelContext *ctx) {
-        const bool want = attrs_.return_final_states != 0;
-        auto state = [want](const xm_tensor_t *in) {
+        const bool want = attrs_.return_final_states != 0, packed = attrs_.has_cu_seqlens != 0;
+        auto state = [want, packed](const xm_tensor_t *in) {
             StateOutputs so;
             so.what = "return_final_states";
-            if (want) {   // Q [B,T,Hq,N], V [B,T,H,P], Angles [B,T,H,A] (validated)
-                const int64_t b = in[0].shape[0], n = in[0].shape[3], h = in[2].shape[2], p = in[2].shape[3];
+            if (want) {   // Q [B,T,Hq,N], V [B,T,H,P], Angles [B,T,H,A], cu_seqlens [N+1] (validated)
+                const int64_t b = packed ? in[15].shape[0] - 1 : in[0].shape[0];
+                const int64_t n = in[0].shape[3], h = in[2].shape[2], p = in[2].shape[3];
                 const int64_t a = in[8].shape[3];
                 const int64_t shapes[4][4] = {{b, h, p, n}, {b, h, a, 0}, {b, h, n, 0}, {b, h, p, 0}};
                 so.count = 4;
@@ -109,7 +113,7 @@ public:
             return xm_mamba3_siso_forward_states(in, n, a, out, states[0], states[1], states[2], states[3], stream,
                                                  alloc, err, errlen);
         };
-        ComputeDeviceOp(api_, ctx, 11, 15, attrs_, xm_mamba3_siso_validate, state, launch);
+        ComputeDeviceOp(api_, ctx, 11, 16, attrs_, xm_mamba3_siso_validate, state, launch);
     }
 
 private:
@@ -121,8 +125,10 @@ struct Mamba3SisoOp : Ort::CustomOpBase<Mamba3SisoOp, Mamba3SisoKernel> {
     void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new Mamba3SisoKernel(api, info); }
     const char *GetName() const { return "Mamba3SisoFn"; }
     const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
-    size_t GetInputTypeCount() const { return 15; }
-    ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    size_t GetInputTypeCount() const { return 16; }
+    ONNXTensorElementDataType GetInputType(size_t i) const {
+        return i == 15 ? ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64 : ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT;   // cu_seqlens
+    }
     OrtCustomOpInputOutputCharacteristic GetInputCharacteristic(size_t i) const {
         return i < 11 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
     }
@@ -148,14 +154,14 @@ public:
         Check(xm_gated_deltanet2_check_attrs(&attrs_, err, sizeof(err)), err);
     }
     void Compute(OrtKernelContext *ctx) {
-        const bool want = attrs_.output_final_state != 0;
-        auto state = [want](const xm_tensor_t *in) {
+        const bool want = attrs_.output_final_state != 0, packed = attrs_.has_cu_seqlens != 0;
+        auto state = [want, packed](const xm_tensor_t *in) {
             StateOutputs so;
             so.what = "output_final_state";
-            if (want) {   // [B, H, K, V]: q is [B, T, H, K] and v is [B, T, H, V] (validated)
+            if (want) {   // [B, H, K, V]: q is [B, T, H, K], v is [B, T, H, V], cu_seqlens [B+1] (validated)
                 so.count = 1;
                 so.rank[0] = 4;
-                so.shape[0][0] = in[0].shape[0];
+                so.shape[0][0] = packed ? in[7].shape[0] - 1 : in[0].shape[0];
                 so.shape[0][1] = in[0].shape[2];
                 so.shape[0][2] = in[0].shape[3];
                 so.shape[0][3] = in[2].shape[3];
@@ -166,7 +172,7 @@ public:
                          float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
             return xm_gated_deltanet2_forward_states(in, n, a, out, states[0], stream, alloc, err, errlen);
         };
-        ComputeDeviceOp(api_, ctx, 7, 7, attrs_, xm_gated_deltanet2_validate, state, launch);
+        ComputeDeviceOp(api_, ctx, 7, 8, attrs_, xm_gated_deltanet2_validate, state, launch);
     }
 
 private:
@@ -178,8 +184,13 @@ struct GatedDeltaNet2Op : Ort::CustomOpBase<GatedDeltaNet2Op, GatedDeltaNet2Kern
     void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new GatedDeltaNet2Kernel(api, info); }
     const char *GetName() const { return "GatedDeltaNet2Fn"; }
     const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
-    size_t GetInputTypeCount() const { return 7; }
-    ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    size_t GetInputTypeCount() const { return 8; }
+    ONNXTensorElementDataType GetInputType(size_t i) const {
+        return i == 7 ? ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64 : ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT;   // cu_seqlens
+    }
+    OrtCustomOpInputOutputCharacteristic GetInputCharacteristic(size_t i) const {
+        return i < 7 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
+    }
     size_t GetOutputTypeCount() const { return 2; }
     ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
     OrtCustomOpInputOutputCharacteristic GetOutputCharacteristic(size_t i) const {

@@ -56,13 +56,31 @@ inline View MakeView(const xm_tensor_t &t) {
     return v;
 }
 
-inline std::vector<View> MakeViews(const xm_tensor_t *inputs, size_t n_inputs, size_t expected, const char *op) {
+// Borrowed int64 vector (cu_seqlens): rank 1, at least two entries.
+struct IndexView {
+    const int64_t *data = nullptr;
+    int64_t count = 0;
+};
+
+inline IndexView MakeIndexView(const xm_tensor_t &t, const char *name) {
+    if (t.elem_type != XM_ELEM_INT64) Invalid(std::string(name) + " must be an int64 tensor");
+    if (t.rank != 1) Invalid(std::string(name) + " must have rank 1");
+    if (t.shape[0] < 2) Invalid(std::string(name) + " must hold at least two offsets");
+    if (t.data == nullptr) Invalid("non-empty tensor has a null data pointer");
+    return IndexView{static_cast<const int64_t *>(t.data), t.shape[0]};
+}
+
+// Float views of the first `nfloat` inputs (all of them by default); the
+// caller reads any others (cu_seqlens) with MakeIndexView.
+inline std::vector<View> MakeViews(const xm_tensor_t *inputs, size_t n_inputs, size_t expected, const char *op,
+                                   size_t nfloat = SIZE_MAX) {
     if (inputs == nullptr) Invalid(std::string(op) + " received a null input array");
     if (n_inputs != expected)
         Invalid(std::string(op) + " expects " + std::to_string(expected) + " inputs, got " + std::to_string(n_inputs));
     std::vector<View> v;
-    v.reserve(expected);
-    for (size_t i = 0; i < expected; ++i) v.push_back(MakeView(inputs[i]));
+    const size_t nf = nfloat < expected ? nfloat : expected;
+    v.reserve(nf);
+    for (size_t i = 0; i < nf; ++i) v.push_back(MakeView(inputs[i]));
     return v;
 }
 

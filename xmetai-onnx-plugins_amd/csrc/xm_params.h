@@ -45,6 +45,9 @@ struct GatedDeltaNet2Params {
     float scale;
     int pairwise_only;              // chunked path: take the pairwise decay products in every chunk (test switch)
     int vec4_keys;                  // chunked path: dk % 4 == 0 and q, k, g, beta 16-byte aligned
+    // Packed sequences: [batch + 1] token offsets along a single row of
+    // seqlen tokens (the tensors' batch dimension is 1), or nullptr.
+    const int64_t *cu_seqlens;
 };
 
 // Mamba3SisoFn (reference parameter block: mamba3_siso.h:10-36).
@@ -62,13 +65,16 @@ struct Mamba3SisoParams {
     // look-ahead); f_*: the state after the last token.
     const float *in_ssm, *in_angle, *in_k, *in_v;   // [batch, nheads, p, n], [.., a], [.., n], [.., p]
     float *f_ssm, *f_angle, *f_k, *f_v;
+    // Packed sequences: [batch + 1] token offsets along a single row of
+    // seqlen tokens (the tensors' batch dimension is 1), or nullptr.
+    const int64_t *cu_seqlens;
     int batch, seqlen, nheads, nheads_qk, n, p, a;
 };
 
 // Launchers (defined in the .hip translation units).  They enqueue on
 // `stream` and throw xm::Error on a launch failure.
 void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
-size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed);
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
 // Chunked fp32-MFMA path (dk <= 256).  Returns false, launching nothing, when
 // the shape is not one it takes (or XM_GDN2_PATH=seq).  `scratch` holds

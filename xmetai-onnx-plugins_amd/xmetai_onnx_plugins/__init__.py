@@ -94,7 +94,7 @@ def _desc_from_tensor(x) -> _capi.XmTensor:
         return _desc_from_shape((0,))
     if not isinstance(x, torch.Tensor):
         raise TypeError("inputs must be torch tensors or None")
-    elem = 1 if x.dtype == torch.float32 else 0
+    elem = {torch.float32: _capi.XM_ELEM_FLOAT, torch.int64: _capi.XM_ELEM_INT64}.get(x.dtype, 0)
     if x.numel() > 0:
         if not x.is_cuda:
             raise XmError(XM_ERR_INVALID_ARGUMENT, "inputs must be device tensors")
@@ -121,18 +121,27 @@ def _check(status: int, err: ctypes.Array) -> None:
         raise XmError(status, err.value.decode(errors="replace"))
 
 
-def validate(op: str, shapes: Sequence[Optional[Sequence[int]]], **attrs):
+def validate(op: str, shapes: Sequence[Optional[Sequence[int]]], elem_types: Optional[Sequence[int]] = None,
+             **attrs):
     """Runs the operator's host-side validation on shapes only (no device).
 
     ``op`` is ``"selective_scan"``, ``"mamba3_siso"`` or ``"gated_deltanet2"``;
-    ``shapes`` lists one shape per input (``None`` = absent).  Returns
-    ``(output_shape, scratch_bytes)`` or raises :class:`XmError`.
+    ``shapes`` lists one shape per input (``None`` = absent); ``elem_types``
+    one ONNX element type per input (default float; cu_seqlens is int64).
+    Returns ``(output_shape, scratch_bytes)`` or raises :class:`XmError`.
     """
     _, n = _capi.OPS[op]
-    if len(shapes) != n and not (op == "mamba3_siso" and len(shapes) == _capi.MAMBA3_INPUTS_WITH_STATES):
+    counts = {n}
+    if op == "mamba3_siso":
+        counts |= {_capi.MAMBA3_INPUTS_WITH_STATES, _capi.MAMBA3_INPUTS_PACKED}
+    if op == "gated_deltanet2":
+        counts |= {_capi.GDN2_INPUTS_PACKED}
+    if len(shapes) not in counts:
         raise TypeError(f"{op} takes {n} inputs")
     n = len(shapes)
-    arr = (_capi.XmTensor * n)(*[_desc_from_shape(s if s is not None else (0,)) for s in shapes])
+    types = list(elem_types) if elem_types is not None else [_capi.XM_ELEM_FLOAT] * n
+    arr = (_capi.XmTensor * n)(*[_desc_from_shape(s if s is not None else (0,), elem_type=e)
+                                 for s, e in zip(shapes, types)])
     a = _attrs(op, **attrs)
     out_shape = (ctypes.c_int64 * _capi.XM_MAX_RANK)()
     out_rank = ctypes.c_int32()
@@ -251,14 +260,18 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, del
 
 def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None, *, chunk_size=64,
                    has_d=None, has_z=None, input_states=None, return_final_states=False, has_input_states=None,
-                   has_cu_seqlens=False, allocator=None, stream=None):
+                   cu_seqlens=None, allocator=None, stream=None):
     """Mamba3SisoFn: returns [B,T,H,P].  ``has_d``/``has_z`` default to the
     presence of D/Z (an exported graph sets them explicitly; default 1).
 
     States (rejected by the reference, mamba3_siso_fn_ort.cpp:50-55; accepted
     here as a widening): ``input_states`` = (ssm [B,H,P,N], angle [B,H,A],
     k [B,H,N], v [B,H,P]) continues a previous call; ``return_final_states``
-    returns ``(y, (ssm, angle, k, v))`` after the last token."""
+    returns ``(y, (ssm, angle, k, v))`` after the last token.
+
+    Packed sequences (rejected by the reference, :56-58): ``cu_seqlens`` (int64
+    [N+1] device tensor) splits the single row of tokens (batch 1) into N
+    sequences; the states are then [N, ...], one per sequence."""
     def present(x):
         return x is not None and x.numel() > 0
     has_d = present(D) if has_d is None else has_d
@@ -267,34 +280,45 @@ def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=Non
     inputs = [Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D, Z]
     if has_input_states:
         inputs += list(input_states)
+    elif cu_seqlens is not None:
+        inputs += [None] * 4   # the state slots before cu_seqlens
+    if cu_seqlens is not None:
+        inputs.append(cu_seqlens)
     shapes = None   # shapes of other ranks fail validation before the launch
     if return_final_states and Q.dim() == 4 and V.dim() == 4 and Angles.dim() == 4:
-        b, h, pdim, n, a = Q.shape[0], V.shape[2], V.shape[3], Q.shape[3], Angles.shape[3]
+        b = cu_seqlens.shape[0] - 1 if cu_seqlens is not None else Q.shape[0]
+        h, pdim, n, a = V.shape[2], V.shape[3], Q.shape[3], Angles.shape[3]
         shapes = [(b, h, pdim, n), (b, h, a), (b, h, n), (b, h, pdim)]
     r = _run("mamba3_siso", inputs, 2, allocator, stream, state_shapes=shapes,
              chunk_size=chunk_size, has_d=int(bool(has_d)), has_z=int(bool(has_z)),
              return_final_states=int(bool(return_final_states)), has_input_states=int(bool(has_input_states)),
-             has_cu_seqlens=int(bool(has_cu_seqlens)))
+             has_cu_seqlens=int(cu_seqlens is not None))
     return (r[0], tuple(r[1])) if shapes is not None else r
 
 
 def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, use_qk_l2norm_in_kernel=True,
-                       output_final_state=False, use_gate_in_kernel=False, has_cu_seqlens=False,
+                       output_final_state=False, use_gate_in_kernel=False, cu_seqlens=None,
                        state_v_first=False, allocator=None, stream=None):
     """GatedDeltaNet2Fn: returns [B,T,H,V].
 
     With ``output_final_state=True`` (rejected by the reference,
     gated_deltanet2_fn_ort.cpp:49-51; accepted here as a widening) it returns
     ``(o, final_state)``, final_state [B,H,K,V] being the state after the last
-    token in initial_state's layout."""
+    token in initial_state's layout.
+
+    Packed sequences (rejected by the reference, gated_deltanet2_fn_ort.cpp:55-57):
+    ``cu_seqlens`` (int64 [N+1] device tensor) splits the single row of tokens
+    (batch 1) into N sequences; initial_state and final_state are then [N,H,K,V]."""
     shapes = None   # shapes of other ranks fail validation before the launch
     if output_final_state and q.dim() == 4 and v.dim() == 4:
-        shapes = [(q.shape[0], q.shape[2], q.shape[3], v.shape[3])]
-    r = _run("gated_deltanet2", [q, k, v, g, beta, w, initial_state], 2, allocator, stream,
+        n = cu_seqlens.shape[0] - 1 if cu_seqlens is not None else q.shape[0]
+        shapes = [(n, q.shape[2], q.shape[3], v.shape[3])]
+    inputs = [q, k, v, g, beta, w, initial_state] + ([cu_seqlens] if cu_seqlens is not None else [])
+    r = _run("gated_deltanet2", inputs, 2, allocator, stream,
              state_shapes=shapes,
              scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
              output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
-             has_cu_seqlens=int(bool(has_cu_seqlens)), state_v_first=int(bool(state_v_first)))
+             has_cu_seqlens=int(cu_seqlens is not None), state_v_first=int(bool(state_v_first)))
     return (r[0], r[1][0]) if shapes is not None else r
 
 

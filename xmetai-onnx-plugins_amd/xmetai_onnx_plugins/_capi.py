@@ -7,6 +7,7 @@ import os
 
 XM_MAX_RANK = 8
 XM_ELEM_FLOAT = 1
+XM_ELEM_INT64 = 7   # cu_seqlens
 
 XM_OK = 0
 XM_ERR_INVALID_ARGUMENT = 1
@@ -81,6 +82,8 @@ OPS = {
 STATE_OUTPUTS = {"selective_scan": ("return_last_state", 1), "gated_deltanet2": ("output_final_state", 1),
                  "mamba3_siso": ("return_final_states", 4)}
 MAMBA3_INPUTS_WITH_STATES = 15
+MAMBA3_INPUTS_PACKED = 16        # cu_seqlens at input 15
+GDN2_INPUTS_PACKED = 8           # cu_seqlens at input 7
 
 # Every symbol include/xmetai_recurrent.h declares.
 EXPORTED_SYMBOLS = [
