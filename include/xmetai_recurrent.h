@@ -19,7 +19,9 @@
  *  - Every input is REQUIRED; an "optional" input is a tensor with zero
  *    elements (reference: ort_common.h:93-95).  Its data pointer may be NULL.
  *  - Tensors are dense, row-major, fp32 (elem_type == XM_ELEM_FLOAT), on the
- *    device that is current when the entry point is called.
+ *    device that is current when the entry point is called.  The exceptions:
+ *    cu_seqlens offsets are int64, and SelectiveScanFn's data tensors may be
+ *    float16 or bfloat16 (its section says which).
  *  - Entry points return XM_OK or an xm_status_t error and, on error, write a
  *    NUL-terminated message into errbuf (when errbuf != NULL, errlen > 0).
  *    Messages match the reference's exception text where the reference has one.
@@ -44,6 +46,8 @@ extern "C" {
 #define XM_MAX_RANK 8
 #define XM_ELEM_FLOAT 1 /* ONNX TensorProto FLOAT */
 #define XM_ELEM_INT64 7 /* ONNX TensorProto INT64 (cu_seqlens) */
+#define XM_ELEM_FLOAT16 10  /* ONNX TensorProto FLOAT16 (SelectiveScanFn data) */
+#define XM_ELEM_BFLOAT16 16 /* ONNX TensorProto BFLOAT16 (SelectiveScanFn data) */
 
 typedef enum xm_status {
     XM_OK = 0,
@@ -58,7 +62,7 @@ typedef struct xm_tensor {
     const void *data;              /* device pointer, may be NULL when a dim is 0 */
     int64_t shape[XM_MAX_RANK];
     int32_t rank;
-    int32_t elem_type;             /* XM_ELEM_FLOAT */
+    int32_t elem_type;             /* XM_ELEM_* (ONNX TensorProto values) */
 } xm_tensor_t;
 
 /* Stream-ordered scratch allocator.  alloc() must return memory that is
@@ -77,6 +81,13 @@ typedef struct xm_allocator {
  * 7 delta_bias [D] or empty.  Output 0: y [B,D,L], the un-gated scan output
  * (reference: selective_scan_fwd_kernel.cuh:272-281; z only feeds a discarded
  * buffer there, :283-301, so y never depends on z).
+ * Element types: fp32 everywhere, or (a widening: the reference has half and
+ * bfloat16 kernels, selective_scan_fwd_fp16.cu:9-10 and _bf16.cu, that its
+ * fp32-only host, ort_common.h:90-92, cannot reach) u, delta, z and variable
+ * B/C in XM_ELEM_FLOAT16 or XM_ELEM_BFLOAT16, one type for all of them, with
+ * A, D, delta_bias and constant B/C in fp32: the reference's input_t /
+ * weight_t split.  The arithmetic is fp32; y has u's element type and
+ * last_state stays fp32.
  * Attributes (reference: selective_scan_fn_ort.cpp:50-56): delta_softplus
  * (int, default 0), return_last_state (int, default 0; the reference rejects
  * non-zero, here it selects the last-state output of
@@ -95,10 +106,11 @@ int xm_selective_scan_check_attrs(const xm_selective_scan_attrs_t *attrs, char *
 int xm_selective_scan_validate(const xm_tensor_t *inputs, size_t n_inputs,
                                const xm_selective_scan_attrs_t *attrs, int64_t *out_shape,
                                int32_t *out_rank, size_t *scratch_bytes, char *errbuf, size_t errlen);
-/* Validate and enqueue.  `out` is a device buffer of prod(out_shape) floats.
- * With return_last_state != 0 this entry point fails (use the one below). */
+/* Validate and enqueue.  `out` is a device buffer of prod(out_shape) elements
+ * of u's type.  With return_last_state != 0 this entry point fails (use the
+ * one below). */
 int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs,
-                              const xm_selective_scan_attrs_t *attrs, float *out, void *stream,
+                              const xm_selective_scan_attrs_t *attrs, void *out, void *stream,
                               const xm_allocator_t *alloc, char *errbuf, size_t errlen);
 /* As above; with return_last_state != 0 it also writes the scan state after
  * the last token to `last_state`, a device buffer [B, D, N] (zeros when L = 0).
@@ -107,7 +119,7 @@ int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs,
  * of the Mamba selective_scan_fn interface.  `last_state` is ignored (may be
  * NULL) when return_last_state == 0. */
 int xm_selective_scan_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
-                                     const xm_selective_scan_attrs_t *attrs, float *out, float *last_state,
+                                     const xm_selective_scan_attrs_t *attrs, void *out, float *last_state,
                                      void *stream, const xm_allocator_t *alloc, char *errbuf,
                                      size_t errlen);
 

@@ -206,15 +206,29 @@ def test_ss_empty_sequence_is_a_no_op():
     assert out == (2, 8, 0)
 
 
-def test_ss_non_float_input_rejected():
-    descs = [xp._desc_from_shape(s if s is not None else (0,)) for s in ss_shapes()]
-    descs[1].elem_type = 10  # FLOAT16
-    arr = (xp._capi.XmTensor * 8)(*descs)
-    a = _attrs("selective_scan")
-    err = ctypes.create_string_buffer(256)
-    st = xp.lib().xm_selective_scan_validate(arr, 8, ctypes.byref(a), None, None, None, err, 256)
-    assert st == xp.XM_ERR_INVALID_ARGUMENT
-    assert err.value.decode() == "TensorView expects float32 tensors"
+SS_TYPES_MSG = ("SelectiveScanFn: u, delta, z and variable B/C must share one element type; "
+                "constant B/C are float32")
+
+
+@pytest.mark.parametrize("half", [10, 16])   # FLOAT16, BFLOAT16
+def test_ss_16bit_data_types(half):
+    # Widening: u, delta, z and variable B/C in one 16-bit type (the reference's
+    # half / bfloat16 kernels); A, D, delta_bias and constant B/C stay float32.
+    data = [half, half, 1, half, half, 1, half, 1]
+    assert validate("selective_scan", ss_shapes(), data)[0] == (2, 8, 16)
+    const_b = [half, half, 1, 1, half, 1, half, 1]
+    assert validate("selective_scan", ss_shapes(bvar=False), const_b)[0] == (2, 8, 16)
+    for types, shapes, msg in (
+            ([1, half, 1, 1, 1, 1, 1, 1], ss_shapes(), SS_TYPES_MSG),             # mixed data types
+            ([half, half, 1, half, 1, 1, half, 1], ss_shapes(), SS_TYPES_MSG),    # variable C in fp32
+            ([half, half, 1, half, half, 1, 1, 1], ss_shapes(), SS_TYPES_MSG),    # z in fp32
+            ([half, half, 1, half, half, 1, half, 1], ss_shapes(bvar=False), SS_TYPES_MSG),   # 16-bit constant B
+            ([half, half, half, half, half, 1, half, 1], ss_shapes(), "TensorView expects float32 tensors"),   # A
+            ([half, half, 1, half, half, half, half, 1], ss_shapes(), "TensorView expects float32 tensors"),   # D
+            ([7, 7, 1, 7, 7, 1, 7, 1], ss_shapes(), "TensorView expects float32 tensors")):  # int64 data
+        with pytest.raises(XmError) as e:
+            validate("selective_scan", shapes, types)
+        assert e.value.message == msg
 
 
 def test_wrong_input_count():
@@ -484,6 +498,17 @@ def test_ort_descriptors_match_reference_contract():
                  "has_input_states", "has_cu_seqlens", "scale", "use_qk_l2norm_in_kernel", "output_final_state",
                  "use_gate_in_kernel", "state_v_first"):
         assert f'"{attr}"' in ops
+    # widening: float16 / bfloat16 SelectiveScanFn descriptors (data inputs 0, 1, 3, 4, 6 and y
+    # 16-bit; A, D, delta_bias and the state float), added right after the float one
+    assert "return (i <= 1 || i == 3 || i == 4 || i == 6) ? DT : ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT;" in ops
+    assert "return i == 0 ? DT : ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT;" in ops
+    add = ops[ops.index("OrtStatus *XmAddSelectiveScanFnOp"):]
+    add = add[:add.index("\n}\n")]
+    assert [add.index(g) for g in ("&g_selective_scan_op)", "&g_selective_scan_op_f16)",
+                                   "&g_selective_scan_op_bf16)")] == sorted(
+        add.index(g) for g in ("&g_selective_scan_op)", "&g_selective_scan_op_f16)", "&g_selective_scan_op_bf16)"))
+    assert "SelectiveScanOpT<ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16> g_selective_scan_op_f16;" in ops
+    assert "SelectiveScanOpT<ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16> g_selective_scan_op_bf16;" in ops
     sm = _src("softmax_cpu_ort.cpp")
     assert 'return "SoftmaxCPU";' in sm and '"CPUExecutionProvider"' in sm and '"axis", -1' in sm
     assert '#define XM_ORT_GPU_EP "ROCMExecutionProvider"' in _src("ort_glue.h")

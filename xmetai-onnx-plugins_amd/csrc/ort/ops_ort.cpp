@@ -13,6 +13,11 @@
 // Mamba3SisoFn with return_final_states=1 fills optional outputs 1-4 (ssm
 // [B,H,P,N], angle [B,H,A], k [B,H,N], v [B,H,P]) and with has_input_states=1
 // takes the same four as optional inputs 11-14.
+// Widening: SelectiveScanFn is also registered for float16 and bfloat16
+// data (u, delta, variable B/C, z and y; A, D, delta_bias and the state
+// stay float), the reference's half / bfloat16 kernel instantiations, which
+// its fp32-only host cannot reach.  ONNX Runtime picks the descriptor by the
+// node's input types; constant B/C with 16-bit data is a C ABI case only.
 // Widening: has_cu_seqlens=1 (GatedDeltaNet2Fn, Mamba3SisoFn) takes the
 // packed sequences' offsets as an optional int64 input (7 and 15); the
 // states then have one row per sequence.
@@ -51,7 +56,7 @@ public:
             }
             return so;
         };
-        auto launch = [](const xm_tensor_t *in, size_t n, const xm_selective_scan_attrs_t *a, float *out,
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_selective_scan_attrs_t *a, void *out,
                          float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
             return xm_selective_scan_forward_states(in, n, a, out, states[0], stream, alloc, err, errlen);
         };
@@ -63,18 +68,23 @@ private:
     xm_selective_scan_attrs_t attrs_{};
 };
 
-struct SelectiveScanOp : Ort::CustomOpBase<SelectiveScanOp, SelectiveScanKernel> {
+// DT: the element type of the data tensors (inputs 0, 1, 3, 4, 6 and output 0).
+template <ONNXTensorElementDataType DT>
+struct SelectiveScanOpT : Ort::CustomOpBase<SelectiveScanOpT<DT>, SelectiveScanKernel> {
     void *CreateKernel(const OrtApi &api, const OrtKernelInfo *info) const { return new SelectiveScanKernel(api, info); }
     const char *GetName() const { return "SelectiveScanFn"; }
     const char *GetExecutionProviderType() const { return XM_ORT_GPU_EP; }
     size_t GetInputTypeCount() const { return 8; }
-    ONNXTensorElementDataType GetInputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    ONNXTensorElementDataType GetInputType(size_t i) const {
+        return (i <= 1 || i == 3 || i == 4 || i == 6) ? DT : ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT;
+    }
     size_t GetOutputTypeCount() const { return 2; }
-    ONNXTensorElementDataType GetOutputType(size_t) const { return ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
+    ONNXTensorElementDataType GetOutputType(size_t i) const { return i == 0 ? DT : ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT; }
     OrtCustomOpInputOutputCharacteristic GetOutputCharacteristic(size_t i) const {
         return i == 0 ? INPUT_OUTPUT_REQUIRED : INPUT_OUTPUT_OPTIONAL;
     }
 };
+using SelectiveScanOp = SelectiveScanOpT<ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT>;
 
 // ---- Mamba3SisoFn ----------------------------------------------------------
 class Mamba3SisoKernel {
@@ -108,9 +118,9 @@ public:
             }
             return so;
         };
-        auto launch = [](const xm_tensor_t *in, size_t n, const xm_mamba3_siso_attrs_t *a, float *out,
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_mamba3_siso_attrs_t *a, void *out,
                          float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
-            return xm_mamba3_siso_forward_states(in, n, a, out, states[0], states[1], states[2], states[3], stream,
+            return xm_mamba3_siso_forward_states(in, n, a, static_cast<float *>(out), states[0], states[1], states[2], states[3], stream,
                                                  alloc, err, errlen);
         };
         ComputeDeviceOp(api_, ctx, 11, 16, attrs_, xm_mamba3_siso_validate, state, launch);
@@ -168,9 +178,9 @@ public:
             }
             return so;
         };
-        auto launch = [](const xm_tensor_t *in, size_t n, const xm_gated_deltanet2_attrs_t *a, float *out,
+        auto launch = [](const xm_tensor_t *in, size_t n, const xm_gated_deltanet2_attrs_t *a, void *out,
                          float *const *states, void *stream, const xm_allocator_t *alloc, char *err, size_t errlen) {
-            return xm_gated_deltanet2_forward_states(in, n, a, out, states[0], stream, alloc, err, errlen);
+            return xm_gated_deltanet2_forward_states(in, n, a, static_cast<float *>(out), states[0], stream, alloc, err, errlen);
         };
         ComputeDeviceOp(api_, ctx, 7, 8, attrs_, xm_gated_deltanet2_validate, state, launch);
     }
@@ -201,13 +211,18 @@ struct GatedDeltaNet2Op : Ort::CustomOpBase<GatedDeltaNet2Op, GatedDeltaNet2Kern
 // Descriptors live for the whole process: the domain that references them is
 // never released.
 SelectiveScanOp g_selective_scan_op;
+SelectiveScanOpT<ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16> g_selective_scan_op_f16;
+SelectiveScanOpT<ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16> g_selective_scan_op_bf16;
 Mamba3SisoOp g_mamba3_siso_op;
 GatedDeltaNet2Op g_gated_deltanet2_op;
 
 }  // namespace
 
 OrtStatus *XmAddSelectiveScanFnOp(const OrtApi &api, OrtCustomOpDomain *domain) {
-    return api.CustomOpDomain_Add(domain, &g_selective_scan_op);
+    OrtStatus *st = api.CustomOpDomain_Add(domain, &g_selective_scan_op);
+    if (st == nullptr) st = api.CustomOpDomain_Add(domain, &g_selective_scan_op_f16);
+    if (st == nullptr) st = api.CustomOpDomain_Add(domain, &g_selective_scan_op_bf16);
+    return st;
 }
 OrtStatus *XmAddMamba3SisoFnOp(const OrtApi &api, OrtCustomOpDomain *domain) {
     return api.CustomOpDomain_Add(domain, &g_mamba3_siso_op);

@@ -80,7 +80,8 @@ inline xm_tensor_t Describe(const OrtApi &api, const OrtValue *value) {
     api.ReleaseTensorTypeAndShapeInfo(info);
     ThrowIfFailed(api, st);
     d.rank = static_cast<int32_t>(rank);
-    d.elem_type = static_cast<int32_t>(type);   // ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT == XM_ELEM_FLOAT
+    // XM_ELEM_* take ONNX's values (FLOAT 1, INT64 7, FLOAT16 10, BFLOAT16 16)
+    d.elem_type = static_cast<int32_t>(type);
     void *data = nullptr;
     ThrowIfFailed(api, api.GetTensorMutableData(const_cast<OrtValue *>(value), &data));
     d.data = data;
@@ -129,7 +130,8 @@ struct StateOutputs {
 // execution provider's compute stream, enqueue.  Nothing synchronises the
 // host and nothing is cached on the kernel object.
 //   state(in) -> StateOutputs
-//   launch(in, n, &attrs, out, float *states[kMaxStateOutputs], stream, alloc, err, errlen) -> status
+//   launch(in, n, &attrs, void *out, float *states[kMaxStateOutputs], stream, alloc, err, errlen) -> status
+// (output 0 has the element type the op's descriptor declares for it)
 template <typename Attrs, typename Validate, typename State, typename Launch>
 void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t min_inputs, size_t max_inputs,
                      const Attrs &attrs, Validate validate, State state, Launch launch) {
@@ -192,7 +194,7 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t min_inputs
         ThrowIfFailed(api, api.KernelContext_GetAllocator(ctx, s.mem, &s.allocator));
         ap = &alloc;
     }
-    const int st = launch(in.data(), n_inputs, &attrs, static_cast<float *>(out_data), states, stream, ap, err,
+    const int st = launch(in.data(), n_inputs, &attrs, out_data, states, stream, ap, err,
                           sizeof(err));
     if (s.allocator != nullptr) api.ReleaseAllocator(s.allocator);
     Check(st, err);

@@ -20,9 +20,15 @@
 //    writes y with 16-byte stores.
 //  * z is never read: output 0 does not depend on it (reference
 //    selective_scan_fwd_kernel.cuh:280 vs :296-299).
+//  * The data tensors (u, delta, variable B/C, y) are fp32, or float16 /
+//    bfloat16 as in the reference's half and bfloat16 instantiations
+//    (input_t; A, D, bias, constant B/C are weight_t = fp32): loads convert
+//    to fp32, the arithmetic is fp32, y is rounded to nearest even.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "xm_hip.h"
 #include "xm_params.h"
@@ -95,32 +101,86 @@ struct F4 {
     float v[4];
 };
 
+// bfloat16 storage: the upper 16 bits of an fp32.
+struct Bf16 {
+    uint16_t bits;
+};
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float ToF(float x) { return x; }
+__device__ __forceinline__ float ToF(_Float16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ float ToF(Bf16 x) { return __uint_as_float(static_cast<uint32_t>(x.bits) << 16); }
+
+template <typename IT>
+__device__ __forceinline__ IT FromF(float x);
+template <>
+__device__ __forceinline__ float FromF<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ _Float16 FromF<_Float16>(float x) { return static_cast<_Float16>(x); }   // nearest even
+template <>
+__device__ __forceinline__ Bf16 FromF<Bf16>(float x) {   // nearest even; a NaN stays a (quiet) NaN
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return Bf16{static_cast<uint16_t>((u >> 16) | 0x40u)};
+    return Bf16{static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16)};
+}
+
 // Four consecutive tokens t..t+3 of a row.  The guarded form clamps every
 // address into the row and zeroes the lanes past the end with selects, so it
 // has no branches (branches around loads make the compiler wait on each one,
 // which would serialise the one-tile-ahead prefetch).
-__device__ __forceinline__ F4 LoadRow4Fast(const float *row, int t) {
-    const float4 x = *reinterpret_cast<const float4 *>(row + t);
-    return F4{{x.x, x.y, x.z, x.w}};
+// (16 bytes of fp32 or 8 bytes of 16-bit data per vector access)
+template <typename IT>
+__device__ __forceinline__ F4 LoadRow4Fast(const IT *row, int t) {
+    if constexpr (sizeof(IT) == 4) {
+        const float4 x = *reinterpret_cast<const float4 *>(row + t);
+        return F4{{x.x, x.y, x.z, x.w}};
+    } else if constexpr (std::is_same_v<IT, _Float16>) {
+        const h4 x = *reinterpret_cast<const h4 *>(row + t);
+        return F4{{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
+                   static_cast<float>(x[3])}};
+    } else {
+        const uint2 x = *reinterpret_cast<const uint2 *>(row + t);
+        return F4{{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u), __uint_as_float(x.y << 16),
+                   __uint_as_float(x.y & 0xffff0000u)}};
+    }
 }
 
-__device__ __forceinline__ F4 LoadRow4Guarded(const float *row, int t, int L, bool ok) {
+template <typename IT>
+__device__ __forceinline__ F4 LoadRow4Guarded(const IT *row, int t, int L, bool ok) {
     F4 r;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float v = row[min(t + e, L - 1)];
+        const float v = ToF(row[min(t + e, L - 1)]);
         r.v[e] = (ok && t + e < L) ? v : 0.0f;
     }
     return r;
 }
 
-__device__ __forceinline__ void StoreRow4(float *row, int t, int L, bool vec, const F4 &x) {
-    if (vec && t + 3 < L) {
+template <typename IT>
+__device__ __forceinline__ void StoreRow4Fast(IT *row, int t, const F4 &x) {
+    if constexpr (sizeof(IT) == 4) {
         *reinterpret_cast<float4 *>(row + t) = make_float4(x.v[0], x.v[1], x.v[2], x.v[3]);
+    } else if constexpr (std::is_same_v<IT, _Float16>) {
+        h4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = FromF<_Float16>(x.v[e]);
+        *reinterpret_cast<h4 *>(row + t) = y;
+    } else {
+        uint2 y;
+        y.x = static_cast<uint32_t>(FromF<Bf16>(x.v[0]).bits) | (static_cast<uint32_t>(FromF<Bf16>(x.v[1]).bits) << 16);
+        y.y = static_cast<uint32_t>(FromF<Bf16>(x.v[2]).bits) | (static_cast<uint32_t>(FromF<Bf16>(x.v[3]).bits) << 16);
+        *reinterpret_cast<uint2 *>(row + t) = y;
+    }
+}
+
+template <typename IT>
+__device__ __forceinline__ void StoreRow4(IT *row, int t, int L, bool vec, const F4 &x) {
+    if (vec && t + 3 < L) {
+        StoreRow4Fast(row, t, x);
     } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            if (t + e < L) row[t + e] = x.v[e];
+            if (t + e < L) row[t + e] = FromF<IT>(x.v[e]);
     }
 }
 
@@ -143,7 +203,7 @@ __device__ __forceinline__ float Softplus(float x) {
 // prefetch of u/delta/B/C stays in flight through the recurrence.  A ragged
 // last tile (seqlen % 32 != 0) is peeled off the loop and loaded with guards.
 // Without FAST every load is guarded (clamped address + select).
-template <int LPC, int SPL, bool BVAR, bool CVAR, bool FAST>
+template <typename IT, int LPC, int SPL, bool BVAR, bool CVAR, bool FAST>
 __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScanParams p) {
     constexpr int CPW = kThreads / LPC;      // channels per workgroup
     constexpr int NP = LPC * SPL;            // padded state count
@@ -175,13 +235,17 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
     const int nvalid = FAST ? CPW : min(CPW, dpg - cb * CPW);
 
     const size_t row0 = (static_cast<size_t>(b) * p.dim + cbase) * static_cast<size_t>(L);
-    const float *__restrict__ ub = p.u + row0;
-    const float *__restrict__ db = p.delta + row0;
-    float *__restrict__ ob = p.out + row0;
-    const float *__restrict__ Bb =
-        BVAR ? p.B + (static_cast<size_t>(b) * p.groups_b + g) * static_cast<size_t>(N) * L : nullptr;
-    const float *__restrict__ Cb =
-        CVAR ? p.C + (static_cast<size_t>(b) * p.groups_c + (BVAR ? g : 0)) * static_cast<size_t>(N) * L : nullptr;
+    const IT *__restrict__ ub = static_cast<const IT *>(p.u) + row0;
+    const IT *__restrict__ db = static_cast<const IT *>(p.delta) + row0;
+    IT *__restrict__ ob = static_cast<IT *>(p.out) + row0;
+    const IT *__restrict__ Bb =
+        BVAR ? static_cast<const IT *>(p.B) + (static_cast<size_t>(b) * p.groups_b + g) * static_cast<size_t>(N) * L
+             : nullptr;
+    const IT *__restrict__ Cb =
+        CVAR ? static_cast<const IT *>(p.C) + (static_cast<size_t>(b) * p.groups_c + (BVAR ? g : 0)) * static_cast<size_t>(N) * L
+             : nullptr;
+    const float *const Bw = static_cast<const float *>(p.B);   // constant B/C: fp32 weights
+    const float *const Cw = static_cast<const float *>(p.C);
 
     // ---- per-lane recurrence constants ------------------------------------
     // channel of this lane within the workgroup, and which block of SPL states
@@ -202,8 +266,8 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
         const bool ok = lane_ok && n < N;
         const size_t idx = static_cast<size_t>(dl) * N + n;
         A2[j] = ok ? p.A[idx] * kLog2eF : 0.0f;   // A_val *= kLog2e (kernel.cuh:170-178)
-        bco[j] = (!BVAR && ok) ? p.B[idx] : 0.0f;
-        cco[j] = (!CVAR && ok) ? p.C[idx] : 0.0f;
+        bco[j] = (!BVAR && ok) ? Bw[idx] : 0.0f;
+        cco[j] = (!CVAR && ok) ? Cw[idx] : 0.0f;
         if (!BVAR && !CVAR) bco[j] = bco[j] * cco[j];  // B*C folded (kernel.cuh:205-210)
         h[j] = 0.0f;
     }
@@ -240,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
             for (int k = 0; k < BCPT; ++k) {
                 const int it = min(tid + k * kThreads, NBC * per - 1);
                 const int r = it % per;
-                const float *row = ((BVAR && it < per) ? Bb : Cb) + static_cast<size_t>(r / kQ4) * L;
+                const IT *row = ((BVAR && it < per) ? Bb : Cb) + static_cast<size_t>(r / kQ4) * L;
                 bcreg[k] = LoadRow4Fast(row, t0 + (r % kQ4) * 4);
             }
         }
@@ -260,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
             for (int k = 0; k < BCPT; ++k) {
                 const int it = min(tid + k * kThreads, NBC * per - 1);
                 const int r = it % per;
-                const float *row = ((BVAR && it < per) ? Bb : Cb) + static_cast<size_t>(r / kQ4) * L;
+                const IT *row = ((BVAR && it < per) ? Bb : Cb) + static_cast<size_t>(r / kQ4) * L;
                 bcreg[k] = LoadRow4Guarded(row, t0 + (r % kQ4) * 4, L, true);
             }
         }
@@ -377,9 +441,9 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
                 F4 acc = skip[k];
                 const float4 x = *reinterpret_cast<const float4 *>(sY + c * kRow + q4 * 4);
                 acc.v[0] += x.x; acc.v[1] += x.y; acc.v[2] += x.z; acc.v[3] += x.w;
-                float *row = ob + static_cast<size_t>(c) * L;
+                IT *row = ob + static_cast<size_t>(c) * L;
                 if (FAST && full)
-                    *reinterpret_cast<float4 *>(row + t0 + q4 * 4) = make_float4(acc.v[0], acc.v[1], acc.v[2], acc.v[3]);
+                    StoreRow4Fast(row, t0 + q4 * 4, acc);
                 else
                     StoreRow4(row, t0 + q4 * 4, L, FAST, acc);
             }
@@ -446,26 +510,47 @@ Config ChooseConfig(int N) {
     return {16, 16};
 }
 
-template <int LPC, int SPL, bool VEC>
+template <typename IT, int LPC, int SPL, bool VEC>
 void LaunchLSV(const SelectiveScanParams &p, dim3 grid, hipStream_t stream) {
     if (p.b_var && p.c_var)
-        hipLaunchKernelGGL((SelectiveScanFwdKernel<LPC, SPL, true, true, VEC>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((SelectiveScanFwdKernel<IT, LPC, SPL, true, true, VEC>), grid, dim3(kThreads), 0, stream, p);
     else if (p.b_var)
-        hipLaunchKernelGGL((SelectiveScanFwdKernel<LPC, SPL, true, false, VEC>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((SelectiveScanFwdKernel<IT, LPC, SPL, true, false, VEC>), grid, dim3(kThreads), 0, stream, p);
     else if (p.c_var)
-        hipLaunchKernelGGL((SelectiveScanFwdKernel<LPC, SPL, false, true, VEC>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((SelectiveScanFwdKernel<IT, LPC, SPL, false, true, VEC>), grid, dim3(kThreads), 0, stream, p);
     else
-        hipLaunchKernelGGL((SelectiveScanFwdKernel<LPC, SPL, false, false, VEC>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((SelectiveScanFwdKernel<IT, LPC, SPL, false, false, VEC>), grid, dim3(kThreads), 0, stream, p);
 }
 
-template <int LPC, int SPL>
+template <typename IT, int LPC, int SPL>
 void LaunchLS(const SelectiveScanParams &p, int vec, dim3 grid, hipStream_t stream) {
     constexpr int CPW = kThreads / LPC;
-    if (vec && p.dim_per_group % CPW == 0) LaunchLSV<LPC, SPL, true>(p, grid, stream);
-    else LaunchLSV<LPC, SPL, false>(p, grid, stream);
+    if (vec && p.dim_per_group % CPW == 0) LaunchLSV<IT, LPC, SPL, true>(p, grid, stream);
+    else LaunchLSV<IT, LPC, SPL, false>(p, grid, stream);
 }
 
-bool Aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+// vector accesses are 4 elements: 16 bytes of fp32, 8 of 16-bit data
+bool AlignedVec(const void *ptr, int elem_bytes) {
+    return (reinterpret_cast<uintptr_t>(ptr) & static_cast<uintptr_t>(4 * elem_bytes - 1)) == 0;
+}
+
+template <typename IT>
+void LaunchTyped(const SelectiveScanParams &p, const Config &cfg, dim3 grid, hipStream_t stream) {
+    const int eb = static_cast<int>(sizeof(IT));
+    const int vec = (p.seqlen % 4 == 0) && AlignedVec(p.u, eb) && AlignedVec(p.delta, eb) && AlignedVec(p.out, eb) &&
+                    (!p.b_var || AlignedVec(p.B, eb)) && (!p.c_var || AlignedVec(p.C, eb));
+    switch (cfg.lpc * 100 + cfg.spl) {
+        case 104: LaunchLS<IT, 1, 4>(p, vec, grid, stream); break;
+        case 204: LaunchLS<IT, 2, 4>(p, vec, grid, stream); break;
+        case 404: LaunchLS<IT, 4, 4>(p, vec, grid, stream); break;
+        case 802: LaunchLS<IT, 8, 2>(p, vec, grid, stream); break;
+        case 1601: LaunchLS<IT, 16, 1>(p, vec, grid, stream); break;
+        case 804: LaunchLS<IT, 8, 4>(p, vec, grid, stream); break;
+        case 1604: LaunchLS<IT, 16, 4>(p, vec, grid, stream); break;
+        case 1608: LaunchLS<IT, 16, 8>(p, vec, grid, stream); break;
+        default: LaunchLS<IT, 16, 16>(p, vec, grid, stream); break;
+    }
+}
 
 }  // namespace
 
@@ -476,20 +561,10 @@ void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream_v) {
     const long long ncb = (p.dim_per_group + cpw - 1) / cpw;
     const long long blocks = ncb * p.groups_b * static_cast<long long>(p.batch);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "SelectiveScanFn launch exceeds the grid limit");
-    const int vec = (p.seqlen % 4 == 0) && Aligned16(p.u) && Aligned16(p.delta) && Aligned16(p.out) &&
-                    (!p.b_var || Aligned16(p.B)) && (!p.c_var || Aligned16(p.C));
     const dim3 grid(static_cast<unsigned>(blocks));
-    switch (cfg.lpc * 100 + cfg.spl) {
-        case 104: LaunchLS<1, 4>(p, vec, grid, stream); break;
-        case 204: LaunchLS<2, 4>(p, vec, grid, stream); break;
-        case 404: LaunchLS<4, 4>(p, vec, grid, stream); break;
-        case 802: LaunchLS<8, 2>(p, vec, grid, stream); break;
-        case 1601: LaunchLS<16, 1>(p, vec, grid, stream); break;
-        case 804: LaunchLS<8, 4>(p, vec, grid, stream); break;
-        case 1604: LaunchLS<16, 4>(p, vec, grid, stream); break;
-        case 1608: LaunchLS<16, 8>(p, vec, grid, stream); break;
-        default: LaunchLS<16, 16>(p, vec, grid, stream); break;
-    }
+    if (p.in_type == XM_ELEM_FLOAT16) LaunchTyped<_Float16>(p, cfg, grid, stream);
+    else if (p.in_type == XM_ELEM_BFLOAT16) LaunchTyped<Bf16>(p, cfg, grid, stream);
+    else LaunchTyped<float>(p, cfg, grid, stream);
     XM_LAUNCH_CHECK("SelectiveScanFn");
 }
 

@@ -16,6 +16,10 @@
 // accepted through xm_selective_scan_forward_states, which also writes the
 // scan state after the last token, [batch, dim, dstate] (the `last_state` of
 // the Mamba selective_scan_fn interface).
+// Widening: u, delta, z and variable B/C may be float16 or bfloat16 (one type
+// for all), as in the reference's half / bfloat16 kernel instantiations that
+// its fp32-only host cannot reach (ort_common.h:90-92); weights stay fp32 and
+// y takes u's type.
 #include "xm_common.h"
 #include "xm_params.h"
 
@@ -88,6 +92,14 @@ Plan Validate(const std::vector<View> &in, const xm_selective_scan_attrs_t &attr
     if (D.present() && !(D.rank() == 1 && D.shape[0] == dim)) Invalid("D must have shape (dim,)");
     if (z.present() && z.shape != u.shape) Invalid("z must have same shape as u");
     if (bias.present() && !(bias.rank() == 1 && bias.shape[0] == dim)) Invalid("delta_bias must have shape (dim,)");
+    // element types: the data tensors share u's; the weights are fp32
+    const int32_t et = u.elem;
+    const bool types_ok = delta.elem == et && (!z.present() || z.elem == et) &&
+                          (b_var ? B.elem == et : B.elem == XM_ELEM_FLOAT) &&
+                          (c_var ? C.elem == et : C.elem == XM_ELEM_FLOAT);
+    if (!types_ok)
+        Invalid("SelectiveScanFn: u, delta, z and variable B/C must share one element type; "
+                "constant B/C are float32");
 
     Plan plan;
     plan.out_shape = u.shape;
@@ -111,13 +123,24 @@ Plan Validate(const std::vector<View> &in, const xm_selective_scan_attrs_t &attr
     p.groups_c = static_cast<int>(groups_c);
     p.dim_per_group = static_cast<int>(dim / n_groups);
     p.delta_softplus = attrs.delta_softplus != 0;
+    p.in_type = et;
     return plan;
 }
 
-void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_selective_scan_attrs_t &attrs, float *out,
+// Views of the eight inputs: u, delta, B, C and z may be 16-bit.
+std::vector<View> SsViews(const xm_tensor_t *inputs, size_t n_inputs) {
+    if (inputs == nullptr) Invalid("SelectiveScanFn received a null input array");
+    if (n_inputs != kNumInputs)
+        Invalid("SelectiveScanFn expects " + std::to_string(kNumInputs) + " inputs, got " + std::to_string(n_inputs));
+    std::vector<View> v;
+    for (size_t i = 0; i < kNumInputs; ++i) v.push_back(MakeView(inputs[i], i <= 1 || i == 3 || i == 4 || i == 6));
+    return v;
+}
+
+void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_selective_scan_attrs_t &attrs, void *out,
              float *last_state, void *stream) {
     CheckAttrs(attrs);
-    auto views = MakeViews(inputs, n_inputs, kNumInputs, "SelectiveScanFn");
+    auto views = SsViews(inputs, n_inputs);
     Plan plan = Validate(views, attrs);
     const bool want_state = attrs.return_last_state != 0;
     if (want_state && last_state == nullptr) Invalid("return_last_state=1 needs a last_state buffer");
@@ -157,7 +180,7 @@ int xm_selective_scan_validate(const xm_tensor_t *inputs, size_t n_inputs, const
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
         xm::CheckAttrs(*attrs);
-        auto views = xm::MakeViews(inputs, n_inputs, xm::kNumInputs, "SelectiveScanFn");
+        auto views = xm::SsViews(inputs, n_inputs);
         xm::Plan plan = xm::Validate(views, *attrs);
         xm::WriteShape(plan.out_shape, out_shape, out_rank);
         if (scratch_bytes) *scratch_bytes = 0;
@@ -165,7 +188,7 @@ int xm_selective_scan_validate(const xm_tensor_t *inputs, size_t n_inputs, const
 }
 
 int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_selective_scan_attrs_t *attrs,
-                              float *out, void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
+                              void *out, void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
     (void)alloc;
     return xm::Guard(errbuf, errlen, [&] {
         if (attrs == nullptr) xm::Invalid("attrs is null");
@@ -175,7 +198,7 @@ int xm_selective_scan_forward(const xm_tensor_t *inputs, size_t n_inputs, const 
 }
 
 int xm_selective_scan_forward_states(const xm_tensor_t *inputs, size_t n_inputs,
-                                     const xm_selective_scan_attrs_t *attrs, float *out, float *last_state,
+                                     const xm_selective_scan_attrs_t *attrs, void *out, float *last_state,
                                      void *stream, const xm_allocator_t *alloc, char *errbuf, size_t errlen) {
     (void)alloc;
     return xm::Guard(errbuf, errlen, [&] {

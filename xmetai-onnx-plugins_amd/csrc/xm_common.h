@@ -31,17 +31,22 @@ private:
 
 // Row-major fp32 view of one input (reference: TensorView, ort_common.h:57-62).
 struct View {
-    const float *data = nullptr;
+    const float *data = nullptr;   // the address; 16-bit data where elem says so
     std::vector<int64_t> shape;
     size_t elements = 0;
+    int32_t elem = XM_ELEM_FLOAT;
     bool present() const { return elements > 0; }
     size_t rank() const { return shape.size(); }
 };
 
-inline View MakeView(const xm_tensor_t &t) {
+// allow_16bit: the SelectiveScanFn data tensors may also be float16 / bfloat16.
+inline View MakeView(const xm_tensor_t &t, bool allow_16bit = false) {
     if (t.rank < 0 || t.rank > XM_MAX_RANK) Invalid("tensor rank out of range");
-    if (t.elem_type != XM_ELEM_FLOAT) Invalid("TensorView expects float32 tensors");  // ort_common.h:90-92
+    const bool half = t.elem_type == XM_ELEM_FLOAT16 || t.elem_type == XM_ELEM_BFLOAT16;
+    if (t.elem_type != XM_ELEM_FLOAT && !(allow_16bit && half))
+        Invalid("TensorView expects float32 tensors");  // ort_common.h:90-92
     View v;
+    v.elem = t.elem_type;
     v.shape.assign(t.shape, t.shape + t.rank);
     size_t n = 1;
     for (int64_t d : v.shape) {

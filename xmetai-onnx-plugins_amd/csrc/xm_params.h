@@ -11,14 +11,17 @@ namespace xm {
 
 // SelectiveScanFn (reference parameter block: selective_scan.h:26-69).
 struct SelectiveScanParams {
-    const float *u;          // [batch, dim, seqlen]
-    const float *delta;      // [batch, dim, seqlen]
+    // Data tensors (u, delta, variable B/C, out) hold elements of in_type;
+    // weights (A, D, delta_bias, constant B/C) and last_state are fp32.
+    const void *u;           // [batch, dim, seqlen]
+    const void *delta;       // [batch, dim, seqlen]
     const float *A;          // [dim, dstate]
-    const float *B;          // b_var ? [batch, groups_b, dstate, seqlen] : [dim, dstate]
-    const float *C;          // c_var ? [batch, groups_c, dstate, seqlen] : [dim, dstate]
+    const void *B;           // b_var ? [batch, groups_b, dstate, seqlen] : [dim, dstate] (fp32)
+    const void *C;           // c_var ? [batch, groups_c, dstate, seqlen] : [dim, dstate] (fp32)
     const float *D;          // [dim] or nullptr
     const float *delta_bias; // [dim] or nullptr
-    float *out;              // [batch, dim, seqlen]
+    void *out;               // [batch, dim, seqlen]
+    int in_type;             // XM_ELEM_FLOAT, XM_ELEM_FLOAT16 or XM_ELEM_BFLOAT16
     float *last_state;       // [batch, dim, dstate]: h after the last token, or nullptr
     int batch, dim, seqlen, dstate;
     int b_var, c_var;

@@ -94,7 +94,8 @@ def _desc_from_tensor(x) -> _capi.XmTensor:
         return _desc_from_shape((0,))
     if not isinstance(x, torch.Tensor):
         raise TypeError("inputs must be torch tensors or None")
-    elem = {torch.float32: _capi.XM_ELEM_FLOAT, torch.int64: _capi.XM_ELEM_INT64}.get(x.dtype, 0)
+    elem = {torch.float32: _capi.XM_ELEM_FLOAT, torch.int64: _capi.XM_ELEM_INT64,
+            torch.float16: _capi.XM_ELEM_FLOAT16, torch.bfloat16: _capi.XM_ELEM_BFLOAT16}.get(x.dtype, 0)
     if x.numel() > 0:
         if not x.is_cuda:
             raise XmError(XM_ERR_INVALID_ARGUMENT, "inputs must be device tensors")
@@ -219,7 +220,9 @@ def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocato
     _check(getattr(lib(), f"xm_{op}_validate")(arr, n, ctypes.byref(a), out_shape, ctypes.byref(out_rank),
                                                ctypes.byref(scratch), err, len(err)), err)
     ref = inputs[out_like_index]
-    out = torch.empty(tuple(out_shape[i] for i in range(out_rank.value)), dtype=torch.float32, device=ref.device)
+    # SelectiveScanFn's y takes u's element type (fp32, or the 16-bit data types)
+    out_dtype = ref.dtype if op == "selective_scan" else torch.float32
+    out = torch.empty(tuple(out_shape[i] for i in range(out_rank.value)), dtype=out_dtype, device=ref.device)
     if stream is None:
         stream = torch.cuda.current_stream(ref.device)
     alloc_ptr = ctypes.byref(allocator.struct) if allocator is not None else None
@@ -248,7 +251,12 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, del
     With ``return_last_state=True`` (rejected by the reference's ORT kernel,
     selective_scan_fn_ort.cpp:52-55; accepted here as a widening) it returns
     ``(y, last_state)``, last_state [B,D,N] being the scan state after the
-    last token (zeros when L = 0)."""
+    last token (zeros when L = 0).
+
+    u, delta, z and variable B/C may be float16 or bfloat16 (all the same;
+    the reference's half / bfloat16 kernels, unreachable from its fp32 host):
+    A, D, delta_bias and constant B/C stay float32, y takes u's type and the
+    state stays float32."""
     shapes = None   # shapes of other ranks fail validation before the launch
     if return_last_state and u.dim() == 3 and A.dim() == 2:
         shapes = [(u.shape[0], u.shape[1], A.shape[1])]

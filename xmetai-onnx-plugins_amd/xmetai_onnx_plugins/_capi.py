@@ -8,6 +8,8 @@ import os
 XM_MAX_RANK = 8
 XM_ELEM_FLOAT = 1
 XM_ELEM_INT64 = 7   # cu_seqlens
+XM_ELEM_FLOAT16 = 10
+XM_ELEM_BFLOAT16 = 16
 
 XM_OK = 0
 XM_ERR_INVALID_ARGUMENT = 1
