@@ -405,7 +405,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic_from_profiles(op["workload"]),
-            "kernel": "SelectiveScanFwdKernel<8,2,true,true,true>",
+            "kernel": "SelectiveScanFwdKernel<float,8,2,true,true,true>",
             "algorithmic_bytes_per_launch": op["nbytes"],
             "kernel_ms_avg": round(ev_avg_ms, 4),
             "frac_of_achievable": round(achieved / ach, 4),
