@@ -47,6 +47,34 @@ for _p in (ROOT, PKG_DIR):
 
 METRIC = "tokens/s per op (GDN-2, sel-scan, Mamba-3) + % HBM roofline, 1 MI355X"
 HBM_PEAK_GBPS = 8000.0
+# Compute ceilings of one MI355X at 2.4 GHz: 256 CUs x 4 SIMDs x 16 lanes of
+# non-packed fp32 VALU (lane-instructions/s), and dense fp32 MFMA.
+VALU_LANE_OPS = 256 * 4 * 16 * 2.4e9
+MFMA_F32_FLOPS = 157.3e12
+
+
+def floors_us(name, s, nbytes):
+    """Lower bounds on one call's time, in microseconds.
+
+    hbm: algorithmic bytes at 8 TB/s.  valu: the essential per-element
+    instruction slots of the sequential recurrence (SS: delta*A, B*delta_u,
+    the state and output FMAs and exp2 at two slots = 6 per state-token;
+    GDN-2: 4 per state element per token; Mamba-3: decay, readout, update =
+    3), at one slot per lane per cycle.  mfma (GDN-2, head_k <= 256): the fp32
+    MFMA flops of the 16-token chunked form, 96*K*V + 2560*V per chunk-head
+    (K, V padded to 16)."""
+    f = {"hbm": nbytes / (HBM_PEAK_GBPS * 1e9) * 1e6}
+    if name == "selective_scan":
+        f["valu"] = s.batch * s.dim * s.seqlen * s.dstate * 6 / VALU_LANE_OPS * 1e6
+    elif name == "gated_deltanet2":
+        f["valu_sequential_form"] = s.batch * s.seqlen * s.nheads * s.dk * s.dv * 4 / VALU_LANE_OPS * 1e6
+        if s.dk <= 256:
+            kp, vp = -(-s.dk // 16) * 16, -(-s.dv // 16) * 16
+            chunks = s.batch * s.nheads * -(-s.seqlen // 16)
+            f["mfma"] = chunks * (96 * kp * vp + 2560 * vp) / MFMA_F32_FLOPS * 1e6
+    elif name == "mamba3_siso":
+        f["valu"] = s.batch * s.seqlen * s.nheads * s.headdim * s.dstate * 3 / VALU_LANE_OPS * 1e6
+    return {k: round(v, 1) for k, v in f.items()}
 
 
 def log(msg: str) -> None:
@@ -358,6 +386,10 @@ def main():
                  ms_per_call_median=round(med_ms, 4), ms_per_call_mean=round(ev_ms, 4),
                  tokens_per_s=op["tokens"] / (med_ms / 1e3), algorithmic_bytes=op["nbytes"],
                  achieved_GBps=round(gbps, 1), frac_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
+        # the form that runs: GDN-2 at head_k <= 256 is the chunked MFMA form
+        fl = floors_us(name, op["shape"], op["nbytes"])
+        binding = max((k for k in fl if k != "valu_sequential_form"), key=lambda k: fl[k])
+        r.update(floors_us=fl, binding_floor=binding, frac_of_binding_floor=round(fl[binding] / (med_ms * 1e3), 4))
         log(f"{name}: {med_ms:.3f} ms/call, {r['tokens_per_s']:.4g} tokens/s, {gbps:.0f} GB/s")
         if not args.no_cpu_baseline:
             budget = args.cpu_seconds
@@ -409,6 +441,8 @@ def main():
             "algorithmic_bytes_per_launch": op["nbytes"],
             "kernel_ms_avg": round(ev_avg_ms, 4),
             "frac_of_achievable": round(achieved / ach, 4),
+            "floors_us": ss["floors_us"],
+            "frac_of_valu_floor": round(ss["floors_us"]["valu"] / (ev_avg_ms * 1e3), 4),
         },
         "cpu_baseline": ss.get("cpu_baseline"),
         "achievable_hbm_GBps": round(ach, 1),
