@@ -22,6 +22,17 @@ def pytest_collection_modifyitems(config, items):
             item.add_marker(pytest.mark.usefixtures("_announce_gpu_case"))
 
 
+@pytest.fixture(params=["chunk", "seq"])
+def m3_path(request, monkeypatch):
+    """Mamba3SisoFn kernel under test: the chunked fp32-MFMA kernel (default)
+    or the token-by-token kernel (XM_M3_PATH=seq)."""
+    if request.param == "seq":
+        monkeypatch.setenv("XM_M3_PATH", "seq")
+    else:
+        monkeypatch.delenv("XM_M3_PATH", raising=False)
+    return request.param
+
+
 @pytest.fixture
 def _announce_gpu_case(request):
     sys.stdout.write(f"\n[gpu case] {request.node.nodeid}\n")

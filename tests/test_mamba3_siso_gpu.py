@@ -1,8 +1,10 @@
 """Mamba3SisoFn on the GPU vs the fp64 oracle (C restatement), through the
-C ABI.  Covers headdim_qk padding (N not a multiple of the key tiling),
-partial angle sets (A < N/2), grouped Q/K heads, the optional D and Z inputs,
-sequence lengths around the 16-token block, the row-block variants, and the
-benchmark shape on a subset of heads."""
+C ABI, for both kernels (the chunked fp32-MFMA kernel and, with
+XM_M3_PATH=seq, the token-by-token one).  Covers headdim_qk padding (N not a
+multiple of the key tiling), partial angle sets (A < N/2), grouped Q/K heads,
+the optional D and Z inputs, sequence lengths around the 16-token chunk and
+block, the 32-row workgroups, decay patterns, and the benchmark shape on a
+subset of heads."""
 
 import numpy as np
 import pytest
@@ -46,7 +48,7 @@ CASES = {
 
 
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_mamba3_parity(name):
+def test_mamba3_parity(name, m3_path):
     s = CASES[name]
     inp = W.mamba3_siso_inputs(s, seed=0)
     check(f"mamba3_siso/{name}", run_gpu(inp), run_ref(inp), TOL_M3)
@@ -54,19 +56,20 @@ def test_mamba3_parity(name):
 
 @pytest.mark.parametrize("shape", [(2, 33, 2, 65, 64), (1, 17, 2, 100, 256), (1, 64, 2, 32, 128),
                                    (1, 47, 3, 97, 192), (2, 31, 2, 3, 32)])
-def test_mamba3_row_blocks_and_ragged_token_blocks(shape):
+def test_mamba3_row_blocks_and_ragged_token_blocks(shape, m3_path):
     """Several 32-row workgroups per head with a partial last one, token counts
-    that end inside a block (32-token blocks for N <= 128, 16 above), Z present."""
+    that end inside a 16-token chunk or a 32-token block, Z present."""
     s = M(*shape, has_z=True)
     inp = W.mamba3_siso_inputs(s, seed=4)
     check("mamba3_siso/rows_" + "_".join(map(str, shape)), run_gpu(inp), run_ref(inp), TOL_M3)
 
 
 @pytest.mark.parametrize("pattern", ["mild", "mixed", "steep", "growth"])
-def test_mamba3_scaled_and_unscaled_blocks(pattern):
-    """Token blocks whose accumulated decay stays within e^+-40 run on the scaled
-    state; steeper ones (|sum ADT| > 40 within a block) take the per-token decay
-    loop.  Both, and blocks switching between them, must match the oracle."""
+def test_mamba3_decay_patterns(pattern, m3_path):
+    """Decay patterns: mild, alternating mild / steep 32-token stretches,
+    underflowing decays (-100 per token every 7th), and growth (+0.9 / -0.5).
+    The chunked kernel forms e^{cum_t - cum_s} per pair, so a steep stretch
+    underflows to zero exactly where the token-by-token product does."""
     s = M(2, 150, 2, 24, 64, has_z=pattern == "mixed")
     inp = W.mamba3_siso_inputs(s, seed=11)
     t = np.arange(s.seqlen)
@@ -82,7 +85,7 @@ def test_mamba3_scaled_and_unscaled_blocks(pattern):
     check(f"mamba3_siso/decay_{pattern}", run_gpu(inp), run_ref(inp), TOL_M3)
 
 
-def test_mamba3_long_angle_accumulation():
+def test_mamba3_long_angle_accumulation(m3_path):
     """4096 steps with large angle increments: the wrapped angle state must not
     drift from the fp64 oracle (the device accumulates it in fp64)."""
     s = M(1, 4096, 1, 8, 16)
@@ -92,7 +95,7 @@ def test_mamba3_long_angle_accumulation():
     check("mamba3_siso/long_angles", run_gpu(inp), run_ref(inp), TOL_M3)
 
 
-def test_mamba3_benchmark_shape_heads():
+def test_mamba3_benchmark_shape_heads(m3_path):
     """Benchmark shape 4 x 4096 x 32 heads, P=64, N=128: (b,h) pairs are
     independent; a subset is checked against the oracle over all 4096 tokens."""
     s = W.M3_MAIN

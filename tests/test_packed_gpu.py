@@ -87,7 +87,7 @@ def test_gdn2_packed_one_sequence_equals_unpacked():
 
 @pytest.mark.parametrize("n_qk,p_dim,hq", [(16, 8, 1), (64, 33, 2), (128, 64, 2), (256, 24, 2)])
 @pytest.mark.parametrize("with_states", [False, True])
-def test_m3_packed_matches_per_sequence(n_qk, p_dim, hq, with_states):
+def test_m3_packed_matches_per_sequence(n_qk, p_dim, hq, with_states, m3_path):
     import torch
     lengths = [45, 1, 0, 33, 70]
     T, H, N = sum(lengths), 2, len(lengths)

@@ -228,7 +228,7 @@ M3_CASES = {
 
 @pytest.mark.parametrize("with_inputs", [False, True])
 @pytest.mark.parametrize("name", sorted(M3_CASES))
-def test_m3_states_parity(name, with_inputs):
+def test_m3_states_parity(name, with_inputs, m3_path):
     s = M3_CASES[name]
     inp = W.mamba3_siso_inputs(s, seed=9)
     ins = m3_states_for(s, 10) if with_inputs else None
@@ -242,7 +242,7 @@ def test_m3_states_parity(name, with_inputs):
 
 @pytest.mark.parametrize("shape,split", [((2, 100, 4, 16, 32), 37), ((1, 70, 2, 65, 128), 32),
                                          ((1, 45, 2, 20, 256), 1)])
-def test_m3_states_chain(shape, split):
+def test_m3_states_chain(shape, split, m3_path):
     """Tokens [0, split) then [split, T) continued from the first call's states
     give the outputs and states of one call over [0, T)."""
     import torch

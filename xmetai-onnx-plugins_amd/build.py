@@ -49,6 +49,7 @@ SOURCES = [
     "gated_deltanet2.hip",
     "gated_deltanet2_chunk.hip",
     "mamba3_siso.hip",
+    "mamba3_siso_chunk.hip",
     "selective_scan_host.cpp",
     "gated_deltanet2_host.cpp",
     "mamba3_siso_host.cpp",

@@ -49,19 +49,18 @@
 
 #include <cstdlib>
 
+#include "mamba3_math.h"
 #include "xm_hip.h"
 #include "xm_params.h"
 
 namespace xm {
 namespace {
 
+using namespace m3;
+
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kRows = kThreads / 16;     // state rows per workgroup (one per 16-lane row group)
-constexpr float kPiF = 3.14159265358979323846f;                     // reference kPi (mamba3_siso_fwd.cu:15)
-constexpr double kTwoPiF = 2.0 * static_cast<double>(kPiF);         // reference kTwoPi = 2 * kPi: the wrap period
-constexpr double kRevPerRad = 0.15915494309189533577;               // 1 / (2 pi): radians -> revolutions
-constexpr double kInvTwoPiF = 1.0 / kTwoPiF;
 
 template <int KPT>
 struct M3Layout {
@@ -88,22 +87,6 @@ struct M3Layout {
     static_assert(kQ % 16 == 0 && kK % 16 == 0 && kV % 16 == 0, "LDS regions must stay 16-byte aligned");
     static_assert(kBytes <= 160 * 1024, "LDS budget");
 };
-
-__device__ __forceinline__ float FastSigmoid(float x) { return __fdividef(1.0f, 1.0f + __expf(-x)); }
-
-// tanh without branches: the odd Taylor series to x^9 below |x| = 0.25
-// (truncation < 1e-8 relative), above it 1 - 2 / (e^{2|x|} + 1) with the
-// hardware exp2 and reciprocal (about 5e-7 relative near 0.25, less above).
-__device__ __forceinline__ float TanhF(float x) {
-    const float ax = fabsf(x), x2 = ax * ax;
-    float p = fmaf(x2, 62.0f / 2835.0f, -17.0f / 315.0f);
-    p = fmaf(x2, p, 2.0f / 15.0f);
-    p = fmaf(x2, p, -1.0f / 3.0f);
-    const float small = fmaf(ax, x2 * p, ax);
-    const float e = __builtin_amdgcn_exp2f(fminf(ax * (2.0f * kLog2eF), 126.0f));
-    const float big = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
-    return copysignf(ax < 0.25f ? small : big, x);
-}
 
 template <int KPT>
 __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) {
@@ -437,6 +420,7 @@ void LaunchKPT(const Mamba3SisoParams &p, hipStream_t stream) {
 }  // namespace
 
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream_v) {
+    if (LaunchMamba3SisoChunked(p, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     const int kpt = (p.n + 15) / 16;
     if (kpt <= 4) LaunchKPT<4>(p, stream);

@@ -1,0 +1,613 @@
+// Mamba3SisoFn forward, chunked form on fp32 MFMA (gfx950, wave64).
+//
+// The recurrence (reference mamba3_siso_fwd.cu:79-171), per (b,h) with state
+// S [P,N]: S *= e^{ADT_t}; y_t = q^_t . S + (D + qk_t gamma_t) v_t;
+// S += v_t (x) k^_t w_t, with q^/k^ the rotated q/k, qk_t the unrotated dot
+// product and w_t = gamma_t + look_t (gamma_t = DT_t sigmoid(Trap_t), look_t =
+// DT_{t+1} (1 - sigmoid(Trap_{t+1})), 0 for the last token).  The decay is a
+// scalar per token, so over a chunk of kC = 16 tokens with cum_t the
+// inclusive sum of ADT from the chunk start the recurrence unrolls into
+// matrix products:
+//   y_t    = e^{cum_t} q^_t . S_prev + sum_{s<t} e^{cum_t - cum_s} w_s (q^_t . k^_s) v_s
+//            + (D + qk_t gamma_t) v_t
+//   S_next = e^{cum_15} S_prev + sum_s e^{cum_15 - cum_s} w_s v_s (x) k^_s
+// (equal to the token-by-token recurrence in exact arithmetic).
+//
+// A workgroup of 8 waves owns one (b,h) and 32 state rows (two 16-row
+// tiles) and walks the chunks in order.  Waves 0-3 (product waves) form the
+// matrix products and keep S^T in MFMA accumulator layout: product wave w
+// holds the key blocks [KBW w, KBW (w+1)) of 16 keys.  Waves 4-7 (preparation
+// waves) prepare the next chunk and finish the previous one.  Each SIMD runs
+// one wave of each kind, so the preparation's VALU work and the products'
+// MFMA work overlap.  Per chunk, with
+// v_mfma_f32_16x16x4_f32 (A[m][k] in lane m+16k, B[k][n] in lane n+16k,
+// D[m][n] in lane n+16(m/4), register m%4):
+//   G^T = K^ Q^T   over the wave's keys    (partial, summed across the waves)
+//   Y   = Q^ S^T   over the wave's keys    (partial, summed across the waves)
+//   S^T = e^{cum_15} S^T + K^T V'           (V'_s = e^{cum_15 - cum_s} w_s v_s)
+// and, after the barrier, preparation waves 0 and 1 each finish one 16-row
+// tile of the output: Y e^{cum_t} + (G o L) V + diag v, with L_ts = e^{cum_t - cum_s} w_s
+// for s < t, then the SiLU(Z) gate and the store.  An S^T tile register is
+// exactly the B operand of the Y product (keys 4(lane/16) + register), so the
+// state never moves.
+//
+// Preparation of chunk j+1 (rotated q^ and k^, V, per-token scalars) runs
+// while chunk j's products are formed, into one of three LDS buffers (chunk j
+// is read by the products, chunk j-1 by the finishing waves); one barrier per
+// chunk.  Lane (pair lane pq, token group tg) of preparation wave w rotates the pairs
+// w PPW + PL x + pq for tokens TPL tg .. TPL tg + TPL - 1.  The angle of a
+// pair is a prefix sum over the chunk (fp64: the token groups' sums are
+// scanned across lanes) on top of the carried wrapped angle, wrapped once per token
+// with the reference's period 2 (float)pi (equal to its wrap after every step
+// in exact arithmetic; mamba3_siso.hip does the same).  Tokens past the end
+// of the sequence are identity tokens: zero q, k and v, zero ADT and w.
+//
+// States, packed sequences and the look-ahead hand-over are those of the
+// token-by-token kernel (mamba3_siso.hip), which remains the path for
+// XM_M3_PATH=seq.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "mamba3_math.h"
+#include "xm_hip.h"
+#include "xm_matrix.h"
+#include "xm_params.h"
+
+namespace xm {
+namespace {
+
+using namespace m3;
+
+constexpr int kC = 16;          // tokens per chunk
+constexpr int kRows = 32;       // state rows per workgroup (two 16-row tiles)
+constexpr int kBufs = 3;        // chunk buffers: preparing j+1, products of j, finishing j-1
+constexpr int kTS = kC + 4;     // row stride (floats) of the [key][token] and [row][token] tiles
+
+constexpr int NW = 4;           // waves per role (4 product waves, 4 preparation waves)
+constexpr int NT = 2 * 64 * NW; // threads
+
+template <int KBW>   // 16-key blocks per product wave
+struct M3CLayout {
+    static constexpr int NP = 16 * NW * KBW;     // padded headdim_qk
+    static constexpr int PPW = NP / (2 * NW);    // pairs per wave in the preparation (8 KBW)
+    static constexpr int PL = KBW % 2 == 0 ? 16 : 8;   // pair lanes per token group
+    static constexpr int PB = PPW / PL;          // pairs per lane
+    static constexpr int TG = 64 / PL;           // token groups
+    static constexpr int TPL = kC / TG;          // tokens per lane
+    static constexpr int VPT = kRows * kC / (64 * NW);   // V values per preparation thread
+    // Row stride of the [token][key] q^ tile: 4 floats of padding put the 16
+    // rows a 16-lane ds_read_b128 phase touches on distinct banks.
+    static constexpr int QS = NP + 4;
+    // one chunk buffer (floats)
+    static constexpr int oQ = 0;                      // q^   [kC][QS]
+    static constexpr int oKT = oQ + kC * QS;          // k^T  [NP][kTS]
+    static constexpr int oVT = oKT + NP * kTS;        // V^T  [kRows][kTS]
+    static constexpr int oCum = oVT + kRows * kTS;    // cum_t
+    static constexpr int oEcum = oCum + kC;           // e^{cum_t}
+    static constexpr int oW = oEcum + kC;             // w_t = gamma_t + look_t
+    static constexpr int oGam = oW + kC;              // gamma_t
+    static constexpr int oQK = oGam + kC;             // partial q.k per wave [NW][kC]
+    static constexpr int kBuf = oQK + NW * kC;
+    // partial products per parity: [NW][3 tiles: G^T, Y rows 0-15, Y rows 16-31][64 lanes][4]
+    static constexpr int oPart = kBufs * kBuf;
+    static constexpr int kPart = NW * 3 * 64 * 4;
+    static constexpr size_t kBytes = sizeof(float) * (oPart + 2 * kPart);
+    static_assert(kBuf % 4 == 0 && QS % 4 == 0 && kTS % 4 == 0, "16-byte aligned tiles");
+    static_assert(kBytes <= 160 * 1024, "LDS budget");
+    static_assert(PB * PL == PPW && TPL * TG == kC && VPT * 64 * NW == kRows * kC, "lane mapping");
+};
+
+// Cross-row moves of one fp64 value per lane with the gfx950 lane-swap
+// instructions (rows are 16-lane groups r0..r3):
+// permlane16_swap(x, x) -> {[x0, x0, x2, x2], [x1, x1, x3, x3]},
+// permlane32_swap(x, x) -> {[x0, x1, x0, x1], [x2, x3, x2, x3]}.
+struct D2 {
+    double a, b;
+};
+__device__ __forceinline__ D2 Swap16(double x) {
+    const unsigned lo = static_cast<unsigned>(__double_as_longlong(x));
+    const unsigned hi = static_cast<unsigned>(static_cast<unsigned long long>(__double_as_longlong(x)) >> 32);
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return {__longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(h[0]) << 32) | l[0])),
+            __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(h[1]) << 32) | l[1]))};
+}
+__device__ __forceinline__ D2 Swap32(double x) {
+    const unsigned lo = static_cast<unsigned>(__double_as_longlong(x));
+    const unsigned hi = static_cast<unsigned>(static_cast<unsigned long long>(__double_as_longlong(x)) >> 32);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return {__longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(h[0]) << 32) | l[0])),
+            __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(h[1]) << 32) | l[1]))};
+}
+// Exclusive prefix over the rows: [0, a0, a0 + a1, (a0 + a1) + a2] for row values a_r.
+__device__ __forceinline__ double RowExclusiveScan(double a, int row) {
+    const D2 p = Swap16(a);                 // [a0, a0, a2, a2], [a1, a1, a3, a3]
+    const double pair = p.a + p.b;          // [a0+a1, a0+a1, a2+a3, a2+a3]
+    const double e1 = (row & 1) ? p.a : 0.0;
+    const double lo = Swap32(pair).a;       // a0 + a1 in every row
+    return row >= 2 ? lo + e1 : e1;
+}
+// Row 3's value in every row.
+__device__ __forceinline__ double RowBroadcast3(double x) {
+    return Swap16(Swap32(x).b).b;           // [x2, x3, x2, x3] -> [x3, x3, x3, x3]
+}
+// Inclusive prefix sum over the 16 lanes of each row (DPP row shifts; a lane
+// whose source is outside the row adds 0).
+__device__ __forceinline__ float RowInclusiveScan16(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, false));   // row_shr:1
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, false));   // row_shr:2
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, false));   // row_shr:4
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, false));   // row_shr:8
+    return x;
+}
+
+template <int KBW>
+__global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
+    using L = M3CLayout<KBW>;
+    constexpr int PPW = L::PPW, PL = L::PL, PB = L::PB, TPL = L::TPL, VPT = L::VPT, QS = L::QS;
+
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float *part = smem + L::oPart;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool product_wave = wave < NW;
+    const int w = wave % NW;              // index within the role
+    const int rtid = tid % (64 * NW);     // thread index within the role
+    const int i16 = lane & 15, g4 = lane >> 4;
+    const int N = p.n, P = p.p, A = p.a, H = p.nheads;
+    const int half_n = N / 2;
+    const int nrb = (P + kRows - 1) / kRows;
+    // the nrb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
+    const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int rb = wg % nrb;
+    const int bh = wg / nrb;
+    const int b = bh / H, h = bh % H;
+    const int gq = h / (H / p.nheads_qk);
+    const int r0 = rb * kRows;
+    const float dval = p.D ? p.D[h] : 0.0f;
+    int T = p.seqlen;
+    size_t tok0 = static_cast<size_t>(b) * T;    // in [B*T] for Q/K/V/Angles/Z
+    size_t sbase = static_cast<size_t>(bh) * T;  // in [B*H*T] for ADT/DT/Trap
+    if (p.cu_seqlens != nullptr) {
+        const long long lo = min(max(p.cu_seqlens[b], 0LL), static_cast<long long>(p.seqlen));
+        const long long hi = min(max(p.cu_seqlens[b + 1], lo), static_cast<long long>(p.seqlen));
+        tok0 = static_cast<size_t>(lo);
+        sbase = static_cast<size_t>(h) * p.seqlen + static_cast<size_t>(lo);
+        T = static_cast<int>(hi - lo);
+    }
+    // The offsets come from a vector load: make the sequence's range
+    // wave-uniform so the buffer descriptors built from it stay in SGPRs.
+    T = __builtin_amdgcn_readfirstlane(T);
+    tok0 = Uniform64(tok0);
+    sbase = Uniform64(sbase);
+    const float *dtr = p.DT + sbase;
+    const float *trr = p.Trap + sbase;
+    const float *adr = p.ADT + sbase;
+    const size_t q_stride = static_cast<size_t>(p.nheads_qk) * N;
+    const float *qbase = p.Q + (tok0 * p.nheads_qk + gq) * N;
+    const float *kbase = p.K + (tok0 * p.nheads_qk + gq) * N;
+    const size_t a_stride = static_cast<size_t>(H) * A;
+    const float *abase = p.Angles + (tok0 * H + h) * A;
+    const size_t v_stride = static_cast<size_t>(H) * P;
+    const size_t vbase = (tok0 * H + h) * P;   // also the output / Z base
+
+    // ---- preparation lanes: pairs w PPW + PL x + pq, tokens TPL tg + s.  Inputs
+    // are read with raw buffer loads through per-chunk descriptors that end at
+    // the sequence's last token, so tokens past the end, padded pairs (keys
+    // >= N) and pairs without an angle (>= A) read zeros with no branch:
+    // zero angle increments, zero q/k (padded pairs) and zero DT/ADT/V (a
+    // zero w and v make a token past the end an identity token).
+    const int pq = lane % PL, tg = lane / PL;
+    int pr[PB], qoff[PB][TPL], aoff[PB][TPL];
+    float2 qbias[PB], kbias[PB];
+    double carry[PB];   // wrapped angle after the last prepared token
+#pragma unroll
+    for (int x = 0; x < PB; ++x) {
+        pr[x] = w * PPW + PL * x + pq;
+        const bool real = pr[x] < half_n, rot = pr[x] < A;
+        const int pc = min(pr[x], half_n - 1);
+        const float2 qb = *reinterpret_cast<const float2 *>(p.Q_bias + static_cast<size_t>(h) * N + 2 * pc);
+        const float2 kb = *reinterpret_cast<const float2 *>(p.K_bias + static_cast<size_t>(h) * N + 2 * pc);
+        qbias[x] = real ? qb : make_float2(0.0f, 0.0f);
+        kbias[x] = real ? kb : make_float2(0.0f, 0.0f);
+        carry[x] = (p.in_angle != nullptr && rot) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + pr[x]]) : 0.0;
+#pragma unroll
+        for (int s = 0; s < TPL; ++s) {
+            qoff[x][s] = real ? ((TPL * tg + s) * static_cast<int>(q_stride) + 2 * pr[x]) * 4 : kOutOfRange;
+            aoff[x][s] = rot ? ((TPL * tg + s) * static_cast<int>(a_stride) + pr[x]) * 4 : kOutOfRange;
+        }
+    }
+    const int vrow = rtid & 31;
+    int voff[VPT];
+#pragma unroll
+    for (int u = 0; u < VPT; ++u)
+        voff[u] = r0 + vrow < P ? (((rtid >> 5) + 2 * NW * u) * static_cast<int>(v_stride) + r0 + vrow) * 4 : kOutOfRange;
+    // bytes of a [token][stride] tensor from the chunk at c0 to the end of the
+    // sequence's last row of `width` elements
+    auto rows_bytes = [&](int c0, size_t stride, int width) {
+        return static_cast<int>((static_cast<size_t>(T - c0 - 1) * stride + width) * 4);
+    };
+
+    // Raw inputs of one chunk, prefetched two chunks ahead into one of two
+    // register sets (chunk parity), or, where registers are short (more than
+    // 128 keys), one chunk ahead into one set.
+    constexpr bool DB = KBW <= 2;
+    struct Raw {
+        float2 qv[PB][TPL], kv[PB][TPL];
+        float ang[PB][TPL], dts[TPL], vreg[VPT];
+        float sdt, strap, sadt, sdt1, strap1;   // preparation wave 3, lane t < kC
+    };
+    Raw raw0, raw1;
+    auto load_prep = [&](int c0, Raw &r) __attribute__((always_inline)) {
+        float2 (&qv)[PB][TPL] = r.qv;
+        float2 (&kv)[PB][TPL] = r.kv;
+        float (&ang)[PB][TPL] = r.ang;
+        float (&dts)[TPL] = r.dts;
+        float (&vreg)[VPT] = r.vreg;
+        const Rsrc rq = MakeRsrc(qbase + c0 * q_stride, rows_bytes(c0, q_stride, N));
+        const Rsrc rk = MakeRsrc(kbase + c0 * q_stride, rows_bytes(c0, q_stride, N));
+        const Rsrc ra = MakeRsrc(abase + c0 * a_stride, rows_bytes(c0, a_stride, A));
+        const Rsrc rd = MakeRsrc(dtr + c0, (T - c0) * 4);
+#pragma unroll
+        for (int s = 0; s < TPL; ++s) {
+            dts[s] = BufF(rd, (TPL * tg + s) * 4);
+#pragma unroll
+            for (int x = 0; x < PB; ++x) {
+                qv[x][s] = BufF2(rq, qoff[x][s]);
+                kv[x][s] = BufF2(rk, qoff[x][s]);
+                ang[x][s] = BufF(ra, aoff[x][s]);
+            }
+        }
+        const Rsrc rv = MakeRsrc(p.V + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
+#pragma unroll
+        for (int u = 0; u < VPT; ++u) vreg[u] = BufF(rv, voff[u]);
+        {   // every preparation wave loads them (same load count on every path); wave NW-1 uses them
+            const Rsrc rt = MakeRsrc(trr + c0, (T - c0) * 4);
+            const Rsrc rad = MakeRsrc(adr + c0, (T - c0) * 4);
+            r.sdt = BufF(rd, i16 * 4);
+            r.strap = BufF(rt, i16 * 4);
+            r.sadt = BufF(rad, i16 * 4);
+            r.sdt1 = BufF(rd, (i16 + 1) * 4);
+            r.strap1 = BufF(rt, (i16 + 1) * 4);
+        }
+    };
+
+    // rotated q^ / k^ (and the unrotated q.k), V^T and the per-token scalars of
+    // the chunk into buffer bf
+    auto prep = [&](float *bf, const Raw &r) __attribute__((always_inline)) {
+        const float2 (&qv)[PB][TPL] = r.qv;
+        const float2 (&kv)[PB][TPL] = r.kv;
+        const float (&ang)[PB][TPL] = r.ang;
+        const float (&dts)[TPL] = r.dts;
+        const float (&vreg)[VPT] = r.vreg;
+        float qk[TPL];
+#pragma unroll
+        for (int s = 0; s < TPL; ++s) qk[s] = 0.0f;
+#pragma unroll
+        for (int x = 0; x < PB; ++x) {
+            double pre[TPL], acc = 0.0;
+#pragma unroll
+            for (int s = 0; s < TPL; ++s) {
+                acc += static_cast<double>(TanhF(ang[x][s])) * static_cast<double>(dts[s]) * static_cast<double>(kPiF);
+                pre[s] = acc;
+            }
+            // exclusive prefix of the token groups' sums (lanes pq + PL tg)
+            double excl;
+            if constexpr (PL == 16) {
+                excl = RowExclusiveScan(acc, tg);   // token groups are rows
+            } else {
+                double incl = acc;
+#pragma unroll
+                for (int d = PL; d < 64; d <<= 1) {
+                    const double y = __shfl_up(incl, d);
+                    incl = lane >= d ? incl + y : incl;
+                }
+                excl = incl - acc;
+            }
+            const double base = carry[x] + excl;
+            double th = 0.0;
+            float kc0[TPL], kc1[TPL];
+#pragma unroll
+            for (int s = 0; s < TPL; ++s) {
+                th = base + pre[s];
+                th -= kTwoPiF * floor(th * kInvTwoPiF);   // wrap_two_pi (reference :26-28)
+                // a pair without an angle keeps theta = 0: sin 0 = 0, cos 0 = 1
+                const float rev = static_cast<float>(th * kRevPerRad);
+                const float sn = __builtin_amdgcn_sinf(rev), c = __builtin_amdgcn_cosf(rev);
+                const float2 q = make_float2(qv[x][s].x + qbias[x].x, qv[x][s].y + qbias[x].y);
+                const float2 k = make_float2(kv[x][s].x + kbias[x].x, kv[x][s].y + kbias[x].y);
+                qk[s] = fmaf(q.x, k.x, fmaf(q.y, k.y, qk[s]));   // unrotated q.k (reference :89-106)
+                *reinterpret_cast<float2 *>(bf + L::oQ + (TPL * tg + s) * QS + 2 * pr[x]) =
+                    make_float2(q.x * c - q.y * sn, q.x * sn + q.y * c);
+                kc0[s] = k.x * c - k.y * sn;
+                kc1[s] = k.x * sn + k.y * c;
+            }
+            if constexpr (TPL == 4) {
+                StF4(bf + L::oKT + (2 * pr[x]) * kTS + 4 * tg, v4f{kc0[0], kc0[1], kc0[2], kc0[3]});
+                StF4(bf + L::oKT + (2 * pr[x] + 1) * kTS + 4 * tg, v4f{kc1[0], kc1[1], kc1[2], kc1[3]});
+            } else {
+                *reinterpret_cast<float2 *>(bf + L::oKT + (2 * pr[x]) * kTS + TPL * tg) = make_float2(kc0[0], kc0[1]);
+                *reinterpret_cast<float2 *>(bf + L::oKT + (2 * pr[x] + 1) * kTS + TPL * tg) = make_float2(kc1[0], kc1[1]);
+            }
+            // the chunk's last token
+            if constexpr (PL == 16) carry[x] = RowBroadcast3(th);
+            else carry[x] = __shfl(th, pq + 64 - PL);
+        }
+        // q.k partial over this wave's pairs, per token
+#pragma unroll
+        for (int s = 0; s < TPL; ++s) {
+            float v = qk[s];
+            v += DppF<0xB1>(v);    // quad_perm [1,0,3,2]
+            v += DppF<0x4E>(v);    // quad_perm [2,3,0,1]
+            v += DppF<0x141>(v);   // row_half_mirror: the 8 lanes of a half row
+            if constexpr (PL == 16) v += DppF<0x128>(v);   // row_ror:8
+            if (pq == 0) bf[L::oQK + w * kC + TPL * tg + s] = v;
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow * kTS + (rtid >> 5) + 2 * NW * u] = vreg[u];
+        if (w == NW - 1) {
+            const float gam = r.sdt * FastSigmoid(r.strap);
+            const float look = r.sdt1 * (1.0f - FastSigmoid(r.strap1));   // zero DT past the end
+            const float cum = RowInclusiveScan16(r.sadt);   // over the chunk's 16 tokens (lanes 0-15)
+            if (lane < kC) {
+                bf[L::oCum + lane] = cum;
+                bf[L::oEcum + lane] = __expf(cum);
+                bf[L::oW + lane] = gam + look;
+                bf[L::oGam + lane] = gam;
+            }
+        }
+    };
+
+    // ---- state: S^T tile (key block kb, row tile pt), lane i16 + 16 g4,
+    // register r = S[row r0 + 16 pt + i16][key 16 (KBW w + kb) + 4 g4 + r]
+    v4f S[KBW][2];
+    {
+        const float look0 = (p.in_ssm != nullptr && T > 0) ? dtr[0] * (1.0f - FastSigmoid(trr[0])) : 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < KBW; ++kb)
+#pragma unroll
+            for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = r0 + 16 * pt + i16, key = 16 * (KBW * w + kb) + 4 * g4 + r;
+                    float v = 0.0f;
+                    if (product_wave && p.in_ssm != nullptr && row < P && key < N) {
+                        const float vl = p.in_v[static_cast<size_t>(bh) * P + row];
+                        const float kl = p.in_k[static_cast<size_t>(bh) * N + key];
+                        v = fmaf(vl, kl * look0, p.in_ssm[(static_cast<size_t>(bh) * P + row) * N + key]);
+                    }
+                    S[kb][pt][r] = v;
+                }
+    }
+
+    // ---- products of one chunk: partial G^T and Y to LDS, then the state update
+    auto products = [&](const float *bf, float *pp) __attribute__((always_inline)) {
+        float qa[KBW][4], ka[KBW][4], kt[KBW][4];
+#pragma unroll
+        for (int kb = 0; kb < KBW; ++kb) {
+            const int nb0 = 16 * (KBW * w + kb);
+            const v4f q4 = LdsF4(bf + L::oQ + i16 * QS + nb0 + 4 * g4);
+            const v4f t4 = LdsF4(bf + L::oKT + (nb0 + i16) * kTS + 4 * g4);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                qa[kb][ks] = q4[ks];                                       // q^[t = i16][key nb0 + 4 g4 + ks]
+                ka[kb][ks] = bf[L::oKT + (nb0 + 4 * g4 + ks) * kTS + i16];  // k^[s = i16][same key]
+                kt[kb][ks] = t4[ks];                                       // k^[s = 4 g4 + ks][key nb0 + i16]
+            }
+        }
+        const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4);
+        const v4f w4 = LdsF4(bf + L::oW + 4 * g4);
+        const float cum15 = bf[L::oCum + kC - 1], ecum15 = bf[L::oEcum + kC - 1];
+        v4f vt[2];
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) vt[pt] = LdsF4(bf + L::oVT + (16 * pt + i16) * kTS + 4 * g4);
+
+        v4f gp = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < KBW; ++kb)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) gp = Mfma(ka[kb][ks], qa[kb][ks], gp);   // G^T[s][t]
+        v4f yp[2];
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) {
+            yp[pt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < KBW; ++kb)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) yp[pt] = Mfma(qa[kb][ks], S[kb][pt][ks], yp[pt]);   // Y[t][row]
+        }
+        StF4(pp + ((w * 3 + 0) * 64 + lane) * 4, gp);
+        StF4(pp + ((w * 3 + 1) * 64 + lane) * 4, yp[0]);
+        StF4(pp + ((w * 3 + 2) * 64 + lane) * 4, yp[1]);
+
+        // S^T = e^{cum_15} S^T + K^T V',  V'[s][row] = e^{cum_15 - cum_s} w_s v_s[row]
+        float cs[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cs[r] = __expf(cum15 - cum4[r]) * w4[r];
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) {
+            float vs[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vs[r] = vt[pt][r] * cs[r];
+#pragma unroll
+            for (int kb = 0; kb < KBW; ++kb) {
+                S[kb][pt] *= ecum15;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) S[kb][pt] = Mfma(kt[kb][ks], vs[ks], S[kb][pt]);
+            }
+        }
+    };
+
+    // ---- output rows 16 pt .. 16 pt + 15 of the chunk at c0 (preparation waves 0 and 1)
+    const int orow = r0 + 16 * w + i16;
+    int ooff[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        ooff[r] = (w < 2 && orow < P) ? ((4 * g4 + r) * static_cast<int>(v_stride) + orow) * 4 : kOutOfRange;
+    // Z of the rows a finishing wave stores.  Issued before the next chunk's
+    // prefetch, so waiting for Z never waits for the prefetch.
+    auto load_z = [&](int c0, float (&zr)[4]) __attribute__((always_inline)) {
+        const Rsrc rz = MakeRsrc(p.Z + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) zr[r] = BufF(rz, ooff[r]);
+    };
+    auto finish = [&](int c0, const float *bf, const float *pp, const float (&zr)[4]) __attribute__((always_inline)) {
+        const int pt = w;
+        const Rsrc ro = MakeRsrc(p.out + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
+        v4f g = LdsF4(pp + lane * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
+        v4f qk4 = LdsF4(bf + L::oQK + 4 * g4);
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) {
+            g += LdsF4(pp + ((w2 * 3 + 0) * 64 + lane) * 4);
+            ys += LdsF4(pp + ((w2 * 3 + 1 + pt) * 64 + lane) * 4);
+            qk4 += LdsF4(bf + L::oQK + w2 * kC + 4 * g4);
+        }
+        const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4);
+        const v4f ecum4 = LdsF4(bf + L::oEcum + 4 * g4);
+        const v4f w4 = LdsF4(bf + L::oW + 4 * g4);
+        const v4f gam4 = LdsF4(bf + L::oGam + 4 * g4);
+        const float cumt = bf[L::oCum + i16];
+        const v4f vt = LdsF4(bf + L::oVT + (16 * pt + i16) * kTS + 4 * g4);
+        // M[t = i16][s = 4 g4 + ks] = G[t][s] e^{cum_t - cum_s} w_s for s < t (A operand)
+        float m[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int s = 4 * g4 + ks;
+            m[ks] = s < i16 ? g[ks] * (__expf(cumt - cum4[ks]) * w4[ks]) : 0.0f;
+        }
+        // acc[r] (t = 4 g4 + r, this lane's row): e^{cum_t} Y + (D + qk_t gamma_t) v_t
+        v4f acc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(ecum4[r], ys[r], fmaf(qk4[r], gam4[r], dval) * vt[r]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = Mfma(m[ks], vt[ks], acc);   // + sum_{s<t} M[t][s] v_s
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float y = acc[r];
+            if (p.Z != nullptr) y *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
+            BufStF(ro, ooff[r], y);   // tokens past the end and rows >= P are dropped
+        }
+    };
+
+    const int nch = (T + kC - 1) / kC;
+    auto buf = [&](int j) { return smem + (j % kBufs) * L::kBuf; };
+    auto par = [&](int j) { return part + (j & 1) * L::kPart; };
+    if (nch > 0) {   // workgroup-uniform: an empty sequence passes its states through
+        if (!product_wave) {
+            load_prep(0, raw0);
+            if constexpr (DB) load_prep(min(1, nch - 1) * kC, raw1);
+            prep(buf(0), raw0);
+            if constexpr (!DB) load_prep(min(1, nch - 1) * kC, raw0);
+        }
+        __syncthreads();
+        // iteration j: products of chunk j | prefetch of chunk j+2 (into the
+        // set chunk j used), finishing of chunk j-1, preparation of chunk j+1;
+        // unrolled by two for the register sets; the last chunk is peeled
+        auto iter = [&](int j, Raw &ld, const Raw &pr_) __attribute__((always_inline)) {
+            if (product_wave) {
+                products(buf(j), par(j));
+            } else {
+                const int jf = max(j - 1, 0);   // the chunk to finish (from j = 1 on)
+                float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (p.Z != nullptr) load_z(jf * kC, zr);
+                if constexpr (DB) load_prep(min(j + 2, nch - 1) * kC, ld);
+                if (j > 0 && w < 2) finish(jf * kC, buf(jf), par(jf), zr);
+                prep(buf(j + 1), pr_);
+                if constexpr (!DB) load_prep(min(j + 2, nch - 1) * kC, ld);
+            }
+            __syncthreads();
+        };
+        if (nch > 1) {
+            for (int j = 0;; j += 2) {
+                iter(j, DB ? raw0 : raw0, DB ? raw1 : raw0);
+                if (j + 2 >= nch) break;
+                iter(j + 1, DB ? raw1 : raw0, raw0);
+                if (j + 3 >= nch) break;
+            }
+        }
+        float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (product_wave) {
+            products(buf(nch - 1), par(nch - 1));
+        } else if (nch > 1 && w < 2) {
+            if (p.Z != nullptr) load_z((nch - 2) * kC, zr);
+            finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
+        }
+        __syncthreads();
+        if (!product_wave && w < 2) {
+            if (p.Z != nullptr) load_z((nch - 1) * kC, zr);
+            finish((nch - 1) * kC, buf(nch - 1), par(nch - 1), zr);
+        }
+    }
+
+    if (p.f_ssm != nullptr) {
+        if (product_wave) {
+#pragma unroll
+            for (int kb = 0; kb < KBW; ++kb)
+#pragma unroll
+                for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = r0 + 16 * pt + i16, key = 16 * (KBW * w + kb) + 4 * g4 + r;
+                        if (row < P && key < N) p.f_ssm[(static_cast<size_t>(bh) * P + row) * N + key] = S[kb][pt][r];
+                    }
+        } else if (rb == 0) {
+#pragma unroll
+            for (int x = 0; x < PB; ++x)
+                if (tg == 0 && pr[x] < A)
+                    p.f_angle[static_cast<size_t>(bh) * A + pr[x]] = static_cast<float>(carry[x]);
+        }
+        if (tid < kRows && r0 + tid < P) {
+            const size_t o = static_cast<size_t>(bh) * P + r0 + tid;
+            p.f_v[o] = T > 0 ? p.V[vbase + static_cast<size_t>(T - 1) * v_stride + r0 + tid]
+                             : (p.in_v != nullptr ? p.in_v[o] : 0.0f);
+        }
+        if (rb == 0) {
+            // the last chunk's buffer is intact: its k^T column of the last token
+            const int tl = T > 0 ? (T - 1) - (nch - 1) * kC : 0;
+            const float *kt = smem + ((nch > 0 ? nch - 1 : 0) % kBufs) * L::kBuf + L::oKT;
+            for (int i = tid; i < N; i += NT) {
+                const size_t o = static_cast<size_t>(bh) * N + i;
+                p.f_k[o] = T > 0 ? kt[i * kTS + tl] : (p.in_k != nullptr ? p.in_k[o] : 0.0f);
+            }
+        }
+    }
+}
+
+template <int KBW>
+void LaunchChunk(const Mamba3SisoParams &p, hipStream_t stream) {
+    using L = M3CLayout<KBW>;
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
+    if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
+    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW>), dim3(static_cast<unsigned>(blocks)), dim3(NT), L::kBytes, stream, p);
+}
+
+}  // namespace
+
+bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream_v) {
+    const char *path = std::getenv("XM_M3_PATH");
+    if (path != nullptr && std::strcmp(path, "seq") == 0) return false;
+    // Per-chunk buffer descriptors hold 32-bit byte sizes: the token rows of
+    // Q/K, Angles and V/Z/out of one sequence must each span less than 2 GiB.
+    const size_t widest = std::max({static_cast<size_t>(p.nheads_qk) * p.n, static_cast<size_t>(p.nheads) * p.a,
+                                    static_cast<size_t>(p.nheads) * p.p});
+    if (static_cast<size_t>(p.seqlen) * widest * sizeof(float) >= (size_t{1} << 31)) return false;
+    hipStream_t stream = static_cast<hipStream_t>(stream_v);
+    // headdim_qk padded to 64, 128, 192 or 256 keys
+    if (p.n <= 64) LaunchChunk<1>(p, stream);
+    else if (p.n <= 128) LaunchChunk<2>(p, stream);
+    else if (p.n <= 192) LaunchChunk<3>(p, stream);
+    else if (p.n <= 256) LaunchChunk<4>(p, stream);
+    else return false;
+    XM_LAUNCH_CHECK("Mamba3SisoFn (chunked)");
+    return true;
+}
+
+}  // namespace xm

@@ -86,6 +86,9 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
+// Chunked fp32-MFMA path (headdim_qk <= 256).  Returns false, launching
+// nothing, when XM_M3_PATH=seq asks for the token-by-token kernel.
+bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream);
 // Enqueues a kernel that writes `count` zeros (no memset node in a captured graph).
 void LaunchFillZeros(float *dst, size_t count, void *stream);
 
