@@ -60,9 +60,11 @@ def floors_us(name, s, nbytes):
     instruction slots of the sequential recurrence (SS: delta*A, B*delta_u,
     the state and output FMAs and exp2 at two slots = 6 per state-token;
     GDN-2: 4 per state element per token; Mamba-3: decay, readout, update =
-    3), at one slot per lane per cycle.  mfma (GDN-2, head_k <= 256): the fp32
-    MFMA flops of the 16-token chunked form, 96*K*V + 2560*V per chunk-head
-    (K, V padded to 16)."""
+    3), at one slot per lane per cycle; where a chunked form runs it is
+    reported as valu_sequential_form.  mfma: the fp32 MFMA flops of the
+    16-token chunked forms: GDN-2 (head_k <= 256) 96*K*V + 2560*V per
+    chunk-head (K, V padded to 16); Mamba-3 (N <= 256) 32*(80*N + 512) per
+    chunk and 32-row block (N padded to 64)."""
     f = {"hbm": nbytes / (HBM_PEAK_GBPS * 1e9) * 1e6}
     if name == "selective_scan":
         f["valu"] = s.batch * s.dim * s.seqlen * s.dstate * 6 / VALU_LANE_OPS * 1e6
@@ -73,7 +75,11 @@ def floors_us(name, s, nbytes):
             chunks = s.batch * s.nheads * -(-s.seqlen // 16)
             f["mfma"] = chunks * (96 * kp * vp + 2560 * vp) / MFMA_F32_FLOPS * 1e6
     elif name == "mamba3_siso":
-        f["valu"] = s.batch * s.seqlen * s.nheads * s.headdim * s.dstate * 3 / VALU_LANE_OPS * 1e6
+        f["valu_sequential_form"] = s.batch * s.seqlen * s.nheads * s.headdim * s.dstate * 3 / VALU_LANE_OPS * 1e6
+        if s.dstate <= 256:
+            np_ = -(-s.dstate // 64) * 64
+            chunks = s.batch * s.nheads * -(-s.headdim // 32) * -(-s.seqlen // 16)
+            f["mfma"] = chunks * 32 * (80 * np_ + 512) / MFMA_F32_FLOPS * 1e6
     return {k: round(v, 1) for k, v in f.items()}
 
 
