@@ -58,12 +58,6 @@ constexpr float kDecayHi = 0x1p60f;
 constexpr int kSP = 20;                  // pitch of the 16-wide LDS matrices (odd multiple of 4)
 constexpr int kTile = 16 * kSP;          // one 16 x 16 matrix in LDS
 
-// Orders this wave's LDS accesses before and after (the LDS unit serves one
-// wave's operations in order; this stops the compiler from moving them).
-__device__ __forceinline__ void WaveSync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
 
 // DPP move within a row of 16 lanes; lanes whose source is outside the row keep `old`.
 template <int CTRL>

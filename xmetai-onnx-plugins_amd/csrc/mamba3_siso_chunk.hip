@@ -16,8 +16,9 @@
 // A workgroup of 8 waves owns one (b,h) and 32 state rows (two 16-row
 // tiles) and walks the chunks in order.  Waves 0-3 (product waves) form the
 // matrix products and keep S^T in MFMA accumulator layout: product wave w
-// holds the key blocks [KBW w, KBW (w+1)) of 16 keys.  Waves 4-7 (preparation
-// waves) prepare the next chunk and finish the previous one.  Each SIMD runs
+// holds the key blocks [KBW w, KBW (w+1)) of 16 keys; product waves 0 and 1
+// also finish the previous chunk.  Waves 4-7 (preparation waves) prepare the
+// next chunk.  Each SIMD runs
 // one wave of each kind, so the preparation's VALU work and the products'
 // MFMA work overlap.  Per chunk, with
 // v_mfma_f32_16x16x4_f32 (A[m][k] in lane m+16k, B[k][n] in lane n+16k,
@@ -25,8 +26,8 @@
 //   G^T = K^ Q^T   over the wave's keys    (partial, summed across the waves)
 //   Y   = Q^ S^T   over the wave's keys    (partial, summed across the waves)
 //   S^T = e^{cum_15} S^T + K^T V'           (V'_s = e^{cum_15 - cum_s} w_s v_s)
-// and, after the barrier, preparation waves 0 and 1 each finish one 16-row
-// tile of the output: Y e^{cum_t} + (G o L) V + diag v, with L_ts = e^{cum_t - cum_s} w_s
+// and, after the barrier, product waves 0 and 1 each finish one 16-row tile
+// of the output: Y e^{cum_t} + (G o L) V + diag v, with L_ts = e^{cum_t - cum_s} w_s
 // for s < t, then the SiLU(Z) gate and the store.  An S^T tile register is
 // exactly the B operand of the Y product (keys 4(lane/16) + register), so the
 // state never moves.
@@ -444,14 +445,14 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         }
     };
 
-    // ---- output rows 16 pt .. 16 pt + 15 of the chunk at c0 (preparation waves 0 and 1)
+    // ---- output rows 16 pt .. 16 pt + 15 of the chunk at c0 (product waves 0 and 1)
     const int orow = r0 + 16 * w + i16;
     int ooff[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         ooff[r] = (w < 2 && orow < P) ? ((4 * g4 + r) * static_cast<int>(v_stride) + orow) * 4 : kOutOfRange;
-    // Z of the rows a finishing wave stores.  Issued before the next chunk's
-    // prefetch, so waiting for Z never waits for the prefetch.
+    // Z of the rows a finishing wave stores, loaded before the products so the
+    // MFMA work covers the latency.
     auto load_z = [&](int c0, float (&zr)[4]) __attribute__((always_inline)) {
         const Rsrc rz = MakeRsrc(p.Z + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
 #pragma unroll
@@ -511,13 +512,13 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         // unrolled by two for the register sets; the last chunk is peeled
         auto iter = [&](int j, Raw &ld, const Raw &pr_) __attribute__((always_inline)) {
             if (product_wave) {
-                products(buf(j), par(j));
-            } else {
                 const int jf = max(j - 1, 0);   // the chunk to finish (from j = 1 on)
                 float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (p.Z != nullptr) load_z(jf * kC, zr);
-                if constexpr (DB) load_prep(min(j + 2, nch - 1) * kC, ld);
+                products(buf(j), par(j));
                 if (j > 0 && w < 2) finish(jf * kC, buf(jf), par(jf), zr);
+            } else {
+                if constexpr (DB) load_prep(min(j + 2, nch - 1) * kC, ld);
                 prep(buf(j + 1), pr_);
                 if constexpr (!DB) load_prep(min(j + 2, nch - 1) * kC, ld);
             }
@@ -533,13 +534,12 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         }
         float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (product_wave) {
+            if (p.Z != nullptr && nch > 1) load_z((nch - 2) * kC, zr);
             products(buf(nch - 1), par(nch - 1));
-        } else if (nch > 1 && w < 2) {
-            if (p.Z != nullptr) load_z((nch - 2) * kC, zr);
-            finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
+            if (nch > 1 && w < 2) finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
         }
         __syncthreads();
-        if (!product_wave && w < 2) {
+        if (product_wave && w < 2) {
             if (p.Z != nullptr) load_z((nch - 1) * kC, zr);
             finish((nch - 1) * kC, buf(nch - 1), par(nch - 1), zr);
         }

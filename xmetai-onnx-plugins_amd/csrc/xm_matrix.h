@@ -36,6 +36,14 @@ __device__ __forceinline__ float BufF(Rsrc r, int voff) {
 __device__ __forceinline__ void BufStF(Rsrc r, int voff, float x) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, voff, 0, 0);
 }
+// Orders this wave's LDS accesses before and after (the LDS unit serves one
+// wave's operations in order; this stops the compiler from moving them), so
+// a wave can read back what its other lanes just wrote.
+__device__ __forceinline__ void WaveSync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 // A 64-bit value known to be equal in every lane, in SGPRs.
 __device__ __forceinline__ size_t Uniform64(size_t x) {
     const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(x));
