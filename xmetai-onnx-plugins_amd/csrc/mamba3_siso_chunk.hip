@@ -229,11 +229,22 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
 #pragma unroll
     for (int u = 0; u < VPT; ++u)
         voff[u] = r0 + vrow < P ? (((rtid >> 5) + 2 * NW * u) * static_cast<int>(v_stride) + r0 + vrow) * 4 : kOutOfRange;
-    // bytes of a [token][stride] tensor from the chunk at c0 to the end of the
-    // sequence's last row of `width` elements
-    auto rows_bytes = [&](int c0, size_t stride, int width) {
-        return static_cast<int>((static_cast<size_t>(T - c0 - 1) * stride + width) * 4);
-    };
+    // One descriptor per tensor, fixed for the whole sequence: it ends at the
+    // sequence's last token, so a token past the end is out of range.  A
+    // chunk's token offset goes into the per-lane offset (the range check
+    // covers only that operand); kOutOfRange plus any in-range offset stays
+    // out of range (no wrap below 2^32).  The host keeps T * stride * 4 < 2^31.
+    auto seq_bytes = [&](size_t stride) { return static_cast<int>(static_cast<size_t>(T) * stride * 4); };
+    const Rsrc rq = MakeRsrc(qbase, seq_bytes(q_stride));
+    const Rsrc rk = MakeRsrc(kbase, seq_bytes(q_stride));
+    const Rsrc ra = MakeRsrc(abase, seq_bytes(a_stride));
+    const Rsrc rd = MakeRsrc(dtr, T * 4);
+    const Rsrc rt = MakeRsrc(trr, T * 4);
+    const Rsrc rad = MakeRsrc(adr, T * 4);
+    const Rsrc rv = MakeRsrc(p.V + vbase, seq_bytes(v_stride));
+    const int qs4 = static_cast<int>(q_stride) * 4, as4 = static_cast<int>(a_stride) * 4, vs4 = static_cast<int>(v_stride) * 4;
+    // per-lane offset + chunk offset, added as unsigned (no signed overflow near 2^31)
+    auto off = [](int a, int b) { return static_cast<int>(static_cast<unsigned>(a) + static_cast<unsigned>(b)); };
 
     // Raw inputs of one chunk, prefetched two chunks ahead into one of two
     // register sets (chunk parity), or, where registers are short (more than
@@ -251,32 +262,25 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         float (&ang)[PB][TPL] = r.ang;
         float (&dts)[TPL] = r.dts;
         float (&vreg)[VPT] = r.vreg;
-        const Rsrc rq = MakeRsrc(qbase + c0 * q_stride, rows_bytes(c0, q_stride, N));
-        const Rsrc rk = MakeRsrc(kbase + c0 * q_stride, rows_bytes(c0, q_stride, N));
-        const Rsrc ra = MakeRsrc(abase + c0 * a_stride, rows_bytes(c0, a_stride, A));
-        const Rsrc rd = MakeRsrc(dtr + c0, (T - c0) * 4);
+        const int cq = c0 * qs4, ca = c0 * as4, cv = c0 * vs4, cd = c0 * 4;
 #pragma unroll
         for (int s = 0; s < TPL; ++s) {
-            dts[s] = BufF(rd, (TPL * tg + s) * 4);
+            dts[s] = BufF(rd, off(cd, (TPL * tg + s) * 4));
 #pragma unroll
             for (int x = 0; x < PB; ++x) {
-                qv[x][s] = BufF2(rq, qoff[x][s]);
-                kv[x][s] = BufF2(rk, qoff[x][s]);
-                ang[x][s] = BufF(ra, aoff[x][s]);
+                qv[x][s] = BufF2(rq, off(qoff[x][s], cq));
+                kv[x][s] = BufF2(rk, off(qoff[x][s], cq));
+                ang[x][s] = BufF(ra, off(aoff[x][s], ca));
             }
         }
-        const Rsrc rv = MakeRsrc(p.V + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
 #pragma unroll
-        for (int u = 0; u < VPT; ++u) vreg[u] = BufF(rv, voff[u]);
-        {   // every preparation wave loads them (same load count on every path); wave NW-1 uses them
-            const Rsrc rt = MakeRsrc(trr + c0, (T - c0) * 4);
-            const Rsrc rad = MakeRsrc(adr + c0, (T - c0) * 4);
-            r.sdt = BufF(rd, i16 * 4);
-            r.strap = BufF(rt, i16 * 4);
-            r.sadt = BufF(rad, i16 * 4);
-            r.sdt1 = BufF(rd, (i16 + 1) * 4);
-            r.strap1 = BufF(rt, (i16 + 1) * 4);
-        }
+        for (int u = 0; u < VPT; ++u) vreg[u] = BufF(rv, off(voff[u], cv));
+        // every preparation wave loads them (same load count on every path); wave NW-1 uses them
+        r.sdt = BufF(rd, off(cd, i16 * 4));
+        r.strap = BufF(rt, off(cd, i16 * 4));
+        r.sadt = BufF(rad, off(cd, i16 * 4));
+        r.sdt1 = BufF(rd, off(cd, (i16 + 1) * 4));
+        r.strap1 = BufF(rt, off(cd, (i16 + 1) * 4));
     };
 
     // rotated q^ / k^ (and the unrotated q.k), V^T and the per-token scalars of
@@ -453,14 +457,14 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         ooff[r] = (w < 2 && orow < P) ? ((4 * g4 + r) * static_cast<int>(v_stride) + orow) * 4 : kOutOfRange;
     // Z of the rows a finishing wave stores, loaded before the products so the
     // MFMA work covers the latency.
+    const Rsrc rz = MakeRsrc(p.Z != nullptr ? p.Z + vbase : p.out, p.Z != nullptr ? seq_bytes(v_stride) : 0);
+    const Rsrc ro = MakeRsrc(p.out + vbase, seq_bytes(v_stride));
     auto load_z = [&](int c0, float (&zr)[4]) __attribute__((always_inline)) {
-        const Rsrc rz = MakeRsrc(p.Z + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) zr[r] = BufF(rz, ooff[r]);
+        for (int r = 0; r < 4; ++r) zr[r] = BufF(rz, off(ooff[r], c0 * vs4));
     };
     auto finish = [&](int c0, const float *bf, const float *pp, const float (&zr)[4]) __attribute__((always_inline)) {
         const int pt = w;
-        const Rsrc ro = MakeRsrc(p.out + vbase + c0 * v_stride, rows_bytes(c0, v_stride, P));
         v4f g = LdsF4(pp + lane * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
         v4f qk4 = LdsF4(bf + L::oQK + 4 * g4);
 #pragma unroll
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         for (int r = 0; r < 4; ++r) {
             float y = acc[r];
             if (p.Z != nullptr) y *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
-            BufStF(ro, ooff[r], y);   // tokens past the end and rows >= P are dropped
+            BufStF(ro, off(ooff[r], c0 * vs4), y);   // tokens past the end and rows >= P are dropped
         }
     };
 
