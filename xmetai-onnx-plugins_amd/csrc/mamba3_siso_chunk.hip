@@ -67,18 +67,18 @@ constexpr int kRows = 32;       // state rows per workgroup (two 16-row tiles)
 constexpr int kBufs = 3;        // chunk buffers: preparing j+1, products of j, finishing j-1
 constexpr int kTS = kC + 4;     // row stride (floats) of the [key][token] and [row][token] tiles
 
-constexpr int NW = 4;           // waves per role (4 product waves, 4 preparation waves)
-constexpr int NT = 2 * 64 * NW; // threads
+constexpr int NW = 4;           // product waves
 
-template <int KBW>   // 16-key blocks per product wave
+template <int KBW, int NPW>   // 16-key blocks per product wave, preparation waves
 struct M3CLayout {
+    static constexpr int NT = 64 * (NW + NPW);   // threads
     static constexpr int NP = 16 * NW * KBW;     // padded headdim_qk
-    static constexpr int PPW = NP / (2 * NW);    // pairs per wave in the preparation (8 KBW)
-    static constexpr int PL = KBW % 2 == 0 ? 16 : 8;   // pair lanes per token group
+    static constexpr int PPW = NP / (2 * NPW);   // pairs per preparation wave
+    static constexpr int PL = PPW % 16 == 0 ? 16 : 8;   // pair lanes per token group
     static constexpr int PB = PPW / PL;          // pairs per lane
-    static constexpr int TG = 64 / PL;           // token groups
+    static constexpr int TG = 64 / PL;           // token groups (4 rows, or 8 half rows)
     static constexpr int TPL = kC / TG;          // tokens per lane
-    static constexpr int VPT = kRows * kC / (64 * NW);   // V values per preparation thread
+    static constexpr int VPT = kRows * kC / (64 * NPW);   // V values per preparation thread
     // Row stride of the [token][key] q^ tile: 4 floats of padding put the 16
     // rows a 16-lane ds_read_b128 phase touches on distinct banks.
     static constexpr int QS = NP + 4;
@@ -90,15 +90,15 @@ struct M3CLayout {
     static constexpr int oEcum = oCum + kC;           // e^{cum_t}
     static constexpr int oW = oEcum + kC;             // w_t = gamma_t + look_t
     static constexpr int oGam = oW + kC;              // gamma_t
-    static constexpr int oQK = oGam + kC;             // partial q.k per wave [NW][kC]
-    static constexpr int kBuf = oQK + NW * kC;
+    static constexpr int oQK = oGam + kC;             // partial q.k per preparation wave [NPW][kC]
+    static constexpr int kBuf = oQK + NPW * kC;
     // partial products per parity: [NW][3 tiles: G^T, Y rows 0-15, Y rows 16-31][64 lanes][4]
     static constexpr int oPart = kBufs * kBuf;
     static constexpr int kPart = NW * 3 * 64 * 4;
     static constexpr size_t kBytes = sizeof(float) * (oPart + 2 * kPart);
     static_assert(kBuf % 4 == 0 && QS % 4 == 0 && kTS % 4 == 0, "16-byte aligned tiles");
     static_assert(kBytes <= 160 * 1024, "LDS budget");
-    static_assert(PB * PL == PPW && TPL * TG == kC && VPT * 64 * NW == kRows * kC, "lane mapping");
+    static_assert(PPW % 8 == 0 && PB * PL == PPW && TPL * TG == kC && VPT * 64 * NPW == kRows * kC, "lane mapping");
 };
 
 // Cross-row moves of one fp64 value per lane with the gfx950 lane-swap
@@ -132,10 +132,26 @@ __device__ __forceinline__ double RowExclusiveScan(double a, int row) {
     const double lo = Swap32(pair).a;       // a0 + a1 in every row
     return row >= 2 ? lo + e1 : e1;
 }
+// Exclusive prefix over 8 token groups laid out as half rows (lane l holds
+// group 2 (l / 16) + (l / 8) % 2): the partner half row by DPP row_ror:8,
+// then the row sums across rows.
+__device__ __forceinline__ double DppRor8(double x) {
+    const long long v = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x128, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_mov_dpp(static_cast<int>(v >> 32), 0x128, 0xf, 0xf, true);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
+}
+__device__ __forceinline__ double HalfRowExclusiveScan(double a, int lane);
 // Row 3's value in every row.
 __device__ __forceinline__ double RowBroadcast3(double x) {
     return Swap16(Swap32(x).b).b;           // [x2, x3, x2, x3] -> [x3, x3, x3, x3]
 }
+__device__ __forceinline__ double HalfRowExclusiveScan(double a, int lane) {
+    const double partner = DppRor8(a);
+    const bool upper = (lane & 8) != 0;
+    return RowExclusiveScan(a + partner, lane >> 4) + (upper ? partner : 0.0);
+}
+
 // Inclusive prefix sum over the 16 lanes of each row (DPP row shifts; a lane
 // whose source is outside the row adds 0).
 __device__ __forceinline__ float RowInclusiveScan16(float x) {
@@ -146,9 +162,10 @@ __device__ __forceinline__ float RowInclusiveScan16(float x) {
     return x;
 }
 
-template <int KBW>
-__global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
-    using L = M3CLayout<KBW>;
+template <int KBW, int NPW>
+__global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoParams p) {
+    using L = M3CLayout<KBW, NPW>;
+    constexpr int NT = L::NT;
     constexpr int PPW = L::PPW, PL = L::PL, PB = L::PB, TPL = L::TPL, VPT = L::VPT, QS = L::QS;
 
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -158,8 +175,8 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool product_wave = wave < NW;
-    const int w = wave % NW;              // index within the role
-    const int rtid = tid % (64 * NW);     // thread index within the role
+    const int w = product_wave ? wave : wave - NW;   // index within the role
+    const int rtid = product_wave ? tid : tid - 64 * NW;   // thread index within the role
     const int i16 = lane & 15, g4 = lane >> 4;
     const int N = p.n, P = p.p, A = p.a, H = p.nheads;
     const int half_n = N / 2;
@@ -228,7 +245,7 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     int voff[VPT];
 #pragma unroll
     for (int u = 0; u < VPT; ++u)
-        voff[u] = r0 + vrow < P ? (((rtid >> 5) + 2 * NW * u) * static_cast<int>(v_stride) + r0 + vrow) * 4 : kOutOfRange;
+        voff[u] = r0 + vrow < P ? (((rtid >> 5) + 2 * NPW * u) * static_cast<int>(v_stride) + r0 + vrow) * 4 : kOutOfRange;
     // One descriptor per tensor, fixed for the whole sequence: it ends at the
     // sequence's last token, so a token past the end is out of range.  A
     // chunk's token offset goes into the per-lane offset (the range check
@@ -304,17 +321,8 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
             }
             // exclusive prefix of the token groups' sums (lanes pq + PL tg)
             double excl;
-            if constexpr (PL == 16) {
-                excl = RowExclusiveScan(acc, tg);   // token groups are rows
-            } else {
-                double incl = acc;
-#pragma unroll
-                for (int d = PL; d < 64; d <<= 1) {
-                    const double y = __shfl_up(incl, d);
-                    incl = lane >= d ? incl + y : incl;
-                }
-                excl = incl - acc;
-            }
+            if constexpr (PL == 16) excl = RowExclusiveScan(acc, tg);   // token groups are rows
+            else excl = HalfRowExclusiveScan(acc, lane);                 // token groups are half rows
             const double base = carry[x] + excl;
             double th = 0.0;
             float kc0[TPL], kc1[TPL];
@@ -341,8 +349,16 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
                 *reinterpret_cast<float2 *>(bf + L::oKT + (2 * pr[x] + 1) * kTS + TPL * tg) = make_float2(kc1[0], kc1[1]);
             }
             // the chunk's last token
-            if constexpr (PL == 16) carry[x] = RowBroadcast3(th);
-            else carry[x] = __shfl(th, pq + 64 - PL);
+            if constexpr (PL == 16) {
+                carry[x] = RowBroadcast3(th);
+            } else {
+                // row 3 holds groups 6 (lower half) and 7; the DPP move runs in
+                // every lane before the select (a move inside a branch would
+                // read inactive lanes)
+                const double v = RowBroadcast3(th);
+                const double vr = DppRor8(v);
+                carry[x] = (lane & 8) ? v : vr;
+            }
         }
         // q.k partial over this wave's pairs, per token
 #pragma unroll
@@ -355,8 +371,8 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
             if (pq == 0) bf[L::oQK + w * kC + TPL * tg + s] = v;
         }
 #pragma unroll
-        for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow * kTS + (rtid >> 5) + 2 * NW * u] = vreg[u];
-        if (w == NW - 1) {
+        for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow * kTS + (rtid >> 5) + 2 * NPW * u] = vreg[u];
+        if (w == NPW - 1) {
             const float gam = r.sdt * FastSigmoid(r.strap);
             const float look = r.sdt1 * (1.0f - FastSigmoid(r.strap1));   // zero DT past the end
             const float cum = RowInclusiveScan16(r.sadt);   // over the chunk's 16 tokens (lanes 0-15)
@@ -468,11 +484,12 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
         v4f g = LdsF4(pp + lane * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
         v4f qk4 = LdsF4(bf + L::oQK + 4 * g4);
 #pragma unroll
-        for (int w2 = 1; w2 < NW; ++w2) {
+        for (int w2 = 1; w2 < NW; ++w2) {   // product waves' partials
             g += LdsF4(pp + ((w2 * 3 + 0) * 64 + lane) * 4);
             ys += LdsF4(pp + ((w2 * 3 + 1 + pt) * 64 + lane) * 4);
-            qk4 += LdsF4(bf + L::oQK + w2 * kC + 4 * g4);
         }
+#pragma unroll
+        for (int w2 = 1; w2 < NPW; ++w2) qk4 += LdsF4(bf + L::oQK + w2 * kC + 4 * g4);   // preparation waves' q.k
         const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4);
         const v4f ecum4 = LdsF4(bf + L::oEcum + 4 * g4);
         const v4f w4 = LdsF4(bf + L::oW + 4 * g4);
@@ -503,50 +520,52 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     const int nch = (T + kC - 1) / kC;
     auto buf = [&](int j) { return smem + (j % kBufs) * L::kBuf; };
     auto par = [&](int j) { return part + (j & 1) * L::kPart; };
-    if (nch > 0) {   // workgroup-uniform: an empty sequence passes its states through
-        if (!product_wave) {
-            load_prep(0, raw0);
-            if constexpr (DB) load_prep(min(1, nch - 1) * kC, raw1);
-            prep(buf(0), raw0);
-            if constexpr (!DB) load_prep(min(1, nch - 1) * kC, raw0);
-        }
+    // Each role runs its own loop (the same barriers, in the same order), so
+    // the registers one role carries across chunks (the state S; the
+    // prefetched inputs and angle carries) never have to coexist.
+    // Iteration j: products of chunk j and finishing of chunk j-1 | prefetch of
+    // chunk j+2, preparation of chunk j+1.  The last chunk is peeled.
+    if (nch > 0 && product_wave) {   // workgroup-uniform: an empty sequence passes its states through
         __syncthreads();
-        // iteration j: products of chunk j | prefetch of chunk j+2 (into the
-        // set chunk j used), finishing of chunk j-1, preparation of chunk j+1;
-        // unrolled by two for the register sets; the last chunk is peeled
+        for (int j = 0; j + 1 < nch; ++j) {
+            const int jf = max(j - 1, 0);   // the chunk to finish (from j = 1 on)
+            float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (p.Z != nullptr) load_z(jf * kC, zr);
+            products(buf(j), par(j));
+            if (j > 0 && w < 2) finish(jf * kC, buf(jf), par(jf), zr);
+            __syncthreads();
+        }
+        float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p.Z != nullptr && nch > 1) load_z((nch - 2) * kC, zr);
+        products(buf(nch - 1), par(nch - 1));
+        if (nch > 1 && w < 2) finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
+        __syncthreads();
+        if (w < 2) {
+            if (p.Z != nullptr) load_z((nch - 1) * kC, zr);
+            finish((nch - 1) * kC, buf(nch - 1), par(nch - 1), zr);
+        }
+    } else if (nch > 0) {
+        load_prep(0, raw0);
+        if constexpr (DB) load_prep(min(1, nch - 1) * kC, raw1);
+        prep(buf(0), raw0);
+        if constexpr (!DB) load_prep(min(1, nch - 1) * kC, raw0);
+        __syncthreads();
+        // unrolled by two for the register sets (chunk parity)
         auto iter = [&](int j, Raw &ld, const Raw &pr_) __attribute__((always_inline)) {
-            if (product_wave) {
-                const int jf = max(j - 1, 0);   // the chunk to finish (from j = 1 on)
-                float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (p.Z != nullptr) load_z(jf * kC, zr);
-                products(buf(j), par(j));
-                if (j > 0 && w < 2) finish(jf * kC, buf(jf), par(jf), zr);
-            } else {
-                if constexpr (DB) load_prep(min(j + 2, nch - 1) * kC, ld);
-                prep(buf(j + 1), pr_);
-                if constexpr (!DB) load_prep(min(j + 2, nch - 1) * kC, ld);
-            }
+            if constexpr (DB) load_prep(min(j + 2, nch - 1) * kC, ld);
+            prep(buf(j + 1), pr_);
+            if constexpr (!DB) load_prep(min(j + 2, nch - 1) * kC, ld);
             __syncthreads();
         };
         if (nch > 1) {
             for (int j = 0;; j += 2) {
-                iter(j, DB ? raw0 : raw0, DB ? raw1 : raw0);
+                iter(j, raw0, DB ? raw1 : raw0);
                 if (j + 2 >= nch) break;
                 iter(j + 1, DB ? raw1 : raw0, raw0);
                 if (j + 3 >= nch) break;
             }
         }
-        float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (product_wave) {
-            if (p.Z != nullptr && nch > 1) load_z((nch - 2) * kC, zr);
-            products(buf(nch - 1), par(nch - 1));
-            if (nch > 1 && w < 2) finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
-        }
-        __syncthreads();
-        if (product_wave && w < 2) {
-            if (p.Z != nullptr) load_z((nch - 1) * kC, zr);
-            finish((nch - 1) * kC, buf(nch - 1), par(nch - 1), zr);
-        }
+        __syncthreads();   // the products of the last chunk
     }
 
     if (p.f_ssm != nullptr) {
@@ -583,14 +602,15 @@ __global__ __launch_bounds__(NT) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     }
 }
 
-template <int KBW>
+template <int KBW, int NPW>
 void LaunchChunk(const Mamba3SisoParams &p, hipStream_t stream) {
-    using L = M3CLayout<KBW>;
+    using L = M3CLayout<KBW, NPW>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW>),
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NPW>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
-    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW>), dim3(static_cast<unsigned>(blocks)), dim3(NT), L::kBytes, stream, p);
+    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NPW>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
+                       stream, p);
 }
 
 }  // namespace
@@ -605,10 +625,10 @@ bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream_v) {
     if (static_cast<size_t>(p.seqlen) * widest * sizeof(float) >= (size_t{1} << 31)) return false;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     // headdim_qk padded to 64, 128, 192 or 256 keys
-    if (p.n <= 64) LaunchChunk<1>(p, stream);
-    else if (p.n <= 128) LaunchChunk<2>(p, stream);
-    else if (p.n <= 192) LaunchChunk<3>(p, stream);
-    else if (p.n <= 256) LaunchChunk<4>(p, stream);
+    if (p.n <= 64) LaunchChunk<1, 4>(p, stream);
+    else if (p.n <= 128) LaunchChunk<2, 8>(p, stream);
+    else if (p.n <= 192) LaunchChunk<3, 4>(p, stream);
+    else if (p.n <= 256) LaunchChunk<4, 4>(p, stream);
     else return false;
     XM_LAUNCH_CHECK("Mamba3SisoFn (chunked)");
     return true;
