@@ -67,9 +67,7 @@ constexpr int kRows = 32;       // state rows per workgroup (two 16-row tiles)
 constexpr int kBufs = 3;        // chunk buffers: preparing j+1, products of j, finishing j-1
 constexpr int kTS = kC + 4;     // row stride (floats) of the [key][token] and [row][token] tiles
 
-constexpr int NW = 4;           // product waves
-
-template <int KBW, int NPW>   // 16-key blocks per product wave, preparation waves
+template <int KBW, int NW, int NPW>   // 16-key blocks per product wave, product waves, preparation waves
 struct M3CLayout {
     static constexpr int NT = 64 * (NW + NPW);   // threads
     static constexpr int NP = 16 * NW * KBW;     // padded headdim_qk
@@ -162,9 +160,9 @@ __device__ __forceinline__ float RowInclusiveScan16(float x) {
     return x;
 }
 
-template <int KBW, int NPW>
+template <int KBW, int NW, int NPW>
 __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoParams p) {
-    using L = M3CLayout<KBW, NPW>;
+    using L = M3CLayout<KBW, NW, NPW>;
     constexpr int NT = L::NT;
     constexpr int PPW = L::PPW, PL = L::PL, PB = L::PB, TPL = L::TPL, VPT = L::VPT, QS = L::QS;
 
@@ -292,7 +290,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         }
 #pragma unroll
         for (int u = 0; u < VPT; ++u) vreg[u] = BufF(rv, off(voff[u], cv));
-        // every preparation wave loads them (same load count on every path); wave NW-1 uses them
+        // every preparation wave loads them (same load count on every path); wave NPW-1 uses them
         r.sdt = BufF(rd, off(cd, i16 * 4));
         r.strap = BufF(rt, off(cd, i16 * 4));
         r.sadt = BufF(rad, off(cd, i16 * 4));
@@ -602,14 +600,14 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     }
 }
 
-template <int KBW, int NPW>
+template <int KBW, int NW, int NPW>
 void LaunchChunk(const Mamba3SisoParams &p, hipStream_t stream) {
-    using L = M3CLayout<KBW, NPW>;
+    using L = M3CLayout<KBW, NW, NPW>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NPW>),
+    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
-    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NPW>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
+    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NW, NPW>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
                        stream, p);
 }
 
@@ -625,10 +623,10 @@ bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream_v) {
     if (static_cast<size_t>(p.seqlen) * widest * sizeof(float) >= (size_t{1} << 31)) return false;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     // headdim_qk padded to 64, 128, 192 or 256 keys
-    if (p.n <= 64) LaunchChunk<1, 4>(p, stream);
-    else if (p.n <= 128) LaunchChunk<2, 8>(p, stream);
-    else if (p.n <= 192) LaunchChunk<3, 4>(p, stream);
-    else if (p.n <= 256) LaunchChunk<4, 4>(p, stream);
+    if (p.n <= 64) LaunchChunk<1, 4, 4>(p, stream);
+    else if (p.n <= 128) LaunchChunk<2, 4, 8>(p, stream);   // 8 product waves: slower (more partials)
+    else if (p.n <= 192) LaunchChunk<3, 4, 4>(p, stream);
+    else if (p.n <= 256) LaunchChunk<4, 4, 4>(p, stream);
     else return false;
     XM_LAUNCH_CHECK("Mamba3SisoFn (chunked)");
     return true;
