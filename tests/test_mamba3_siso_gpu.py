@@ -113,3 +113,25 @@ def test_mamba3_benchmark_shape_heads(m3_path):
     sub["Z"] = None
     check("mamba3_siso/b4_t4096_h32_p64_n128_heads", y[b:b + 1, :, hs], run_ref(sub), TOL_M3)
     assert np.isfinite(y).all()
+
+
+def test_mamba3_long_sequence(m3_path):
+    """65536 tokens (4096 chunks): chunk offsets far into the buffers and the
+    angle carry over many chunks, against the oracle."""
+    s = M(1, 65536, 1, 16, 16, angles=8)
+    inp = W.mamba3_siso_inputs(s, seed=21)
+    check("mamba3_siso/t65536", run_gpu(inp), run_ref(inp), TOL_M3)
+
+
+def test_mamba3_path_switch_selects_the_other_kernel(monkeypatch):
+    """XM_M3_PATH=seq runs the token-by-token kernel: its summation order
+    differs from the chunked kernel's, so the two outputs are close but not
+    bit-identical (both kernels are then exercised by the tests above)."""
+    s = M(1, 64, 2, 32, 64)
+    inp = W.mamba3_siso_inputs(s, seed=22)
+    monkeypatch.delenv("XM_M3_PATH", raising=False)
+    chunked = run_gpu(inp)
+    monkeypatch.setenv("XM_M3_PATH", "seq")
+    sequential = run_gpu(inp)
+    assert not np.array_equal(chunked, sequential)
+    check("mamba3_siso/chunked_vs_seq", chunked, sequential, TOL_M3)
