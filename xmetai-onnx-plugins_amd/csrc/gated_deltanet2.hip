@@ -555,7 +555,7 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
 }  // namespace
 
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed) {
-    if (dk <= 256 && !packed) return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv);   // chunked path
+    if (dk <= kGdn2ChunkKeyLimit && !packed) return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv);   // chunked path
     if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch (packed sequences always take it)
     const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
     const size_t rows = static_cast<size_t>(batch) * nheads * cap;
@@ -566,7 +566,7 @@ size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
-    // dk <= 256: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
+    // dk <= 384: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
     if (p.cu_seqlens == nullptr && LaunchGatedDeltaNet2Chunked(p, scratch, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.dk > kMaxLdsKeys)

@@ -1,4 +1,4 @@
-// GatedDeltaNet2Fn forward for gfx950: chunked form on fp32 MFMA (dk <= 256).
+// GatedDeltaNet2Fn forward for gfx950: chunked form on fp32 MFMA (dk <= 384).
 //
 // The reference recurrence (gated_deltanet2_fwd.cu:82-140), per (b,h), with
 // qhat, khat the normalised q, k, d = exp(g), bk = beta*khat, wv = w*v:
@@ -51,7 +51,6 @@ namespace xm {
 namespace {
 
 constexpr int kC = 16;                   // tokens per chunk
-constexpr int kChunkKeyLimit = 256;     // dk handled by the chunked path
 constexpr float kL2EpsC = 1.0e-6f;       // reference kL2NormEps (gated_deltanet2_fwd.cu:14)
 constexpr float kDecayLo = 0x1p-60f;     // fast-path range of the cumulative decays
 constexpr float kDecayHi = 0x1p60f;
@@ -542,11 +541,13 @@ struct ChunkConfig {
 };
 
 // Two key tiles (32 keys) per wave, ks = a power of two waves per column
-// tile (keys padded to 32 ks).  Fewer splits leave too few waves for the
-// chip (one wave per SIMD at best, and half the SIMDs idle for 4 x 16 heads
-// of 128 x 128); more add cross-wave exchanges.
+// tile (keys padded to 32 ks) up to 256 keys; 10 or 12 waves for 257-320 and
+// 321-384 keys.  Fewer splits leave too few waves for the chip (one wave per
+// SIMD at best, and half the SIMDs idle for 4 x 16 heads of 128 x 128); more
+// add cross-wave exchanges.
 ChunkConfig ChooseChunk(int dk) {
     const int kq = (dk + 15) / 16;
+    if (kq > 16) return ChunkConfig{2, kq <= 20 ? 10 : 12};
     ChunkConfig c{kq >= 2 ? 2 : 1, 1};
     const int need = (kq + c.kpw - 1) / c.kpw;
     while (c.ks < need) c.ks *= 2;
@@ -569,6 +570,7 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
 #define XM_GDN2_RECUR(KPW_, KS_) \
     if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecur<KPW_, KS_>(p, c0, wn, kq, s_in, s_out, stream);
     XM_GDN2_RECUR(1, 1) XM_GDN2_RECUR(2, 1) XM_GDN2_RECUR(2, 2) XM_GDN2_RECUR(2, 4) XM_GDN2_RECUR(2, 8)
+    XM_GDN2_RECUR(2, 10) XM_GDN2_RECUR(2, 12)
 #undef XM_GDN2_RECUR
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }
@@ -576,7 +578,7 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
 }  // namespace
 
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
-    if (dk > kChunkKeyLimit) return 0;
+    if (dk > kGdn2ChunkKeyLimit) return 0;
     const ChunkConfig c = ChooseChunk(dk);
     const int kq = c.kpw * c.ks;
     const int nchunks = (seqlen + kC - 1) / kC;
@@ -591,7 +593,7 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, v
     const char *path = std::getenv("XM_GDN2_PATH");
     if (path != nullptr && std::strcmp(path, "seq") == 0) return false;
     if (p.cu_seqlens != nullptr) return false;   // packed sequences: the fused kernel
-    if (p.dk > kChunkKeyLimit) return false;
+    if (p.dk > kGdn2ChunkKeyLimit) return false;
     // the recurrence's 32-bit buffer offsets span 16 tokens of [B,T,H,V]
     if (static_cast<long long>(p.nheads) * p.dv >= (1LL << 25)) return false;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
