@@ -62,7 +62,7 @@ def floors_us(name, s, nbytes):
     GDN-2: 4 per state element per token; Mamba-3: decay, readout, update =
     3), at one slot per lane per cycle; where a chunked form runs it is
     reported as valu_sequential_form.  mfma: the fp32 MFMA flops of the
-    16-token chunked forms: GDN-2 (head_k <= 384) 96*K*V + 2560*V per
+    16-token chunked forms: GDN-2 (head_k <= 512) 96*K*V + 2560*V per
     chunk-head (K, V padded to 16); Mamba-3 (N <= 256) 32*(80*N + 512) per
     chunk and 32-row block (N padded to 64)."""
     f = {"hbm": nbytes / (HBM_PEAK_GBPS * 1e9) * 1e6}
@@ -70,7 +70,7 @@ def floors_us(name, s, nbytes):
         f["valu"] = s.batch * s.dim * s.seqlen * s.dstate * 6 / VALU_LANE_OPS * 1e6
     elif name == "gated_deltanet2":
         f["valu_sequential_form"] = s.batch * s.seqlen * s.nheads * s.dk * s.dv * 4 / VALU_LANE_OPS * 1e6
-        if s.dk <= 384:
+        if s.dk <= 512:
             kp, vp = -(-s.dk // 16) * 16, -(-s.dv // 16) * 16
             chunks = s.batch * s.nheads * -(-s.seqlen // 16)
             f["mfma"] = chunks * (96 * kp * vp + 2560 * vp) / MFMA_F32_FLOPS * 1e6

@@ -5,9 +5,10 @@ dims that are not multiples of the column tiling), initial states, Q/K
 normalisation on and off, several batches, token counts around the
 1024-token preparation chunk, and overlapping calls on one device.
 
-Three device paths: the chunked fp32-MFMA kernel (dk <= 384, the default
-there), the token-sequential register kernel (dk <= 512; forced for
-dk <= 384 with XM_GDN2_PATH=seq) and the LDS-state kernel (dk > 512).  The
+Three device paths: the chunked fp32-MFMA kernel (dk <= 512, the default
+there), the token-sequential register kernel (dk <= 512; forced with
+XM_GDN2_PATH=seq, and taken by packed sequences) and the LDS-state kernel
+(dk > 512).  The
 parity cases run on both paths where both apply; the chunked path's
 pairwise fallback (forced with XM_GDN2_PAIRWISE=1, or taken by chunks with
 extreme decays) has its own cases."""
@@ -54,7 +55,8 @@ CASES = {
     "k320_v64": S(2, 40, 2, 320, 64),
     "k352_v20_chunk12": S(1, 37, 2, 352, 20),
     "k384_v16": S(1, 33, 1, 384, 16, per_key_gates=True),
-    "k385_v16_seq": S(1, 19, 1, 385, 16),
+    "k385_v16": S(1, 19, 1, 385, 16),
+    "k448_v40": S(2, 35, 1, 448, 40),
     "k512_v7_perkey": S(1, 12, 1, 512, 7, per_key_gates=True),
     "k513_lds_path": S(1, 21, 2, 513, 20),
     "k600_v33_lds_path": S(2, 40, 2, 600, 33),
@@ -72,8 +74,8 @@ CASES = {
 def test_gdn2_parity(name, path, monkeypatch):
     s = CASES[name]
     if path == "seq":
-        if s.dk > 384:
-            pytest.skip("dk > 384 has one path")
+        if s.dk > 512:
+            pytest.skip("dk > 512 has one path")
         monkeypatch.setenv("XM_GDN2_PATH", "seq")
     inp = W.gated_deltanet2_inputs(s, seed=0)
     check(f"gated_deltanet2/{name}/{path}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2)

@@ -566,7 +566,7 @@ size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
-    // dk <= 384: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
+    // dk <= 512: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
     if (p.cu_seqlens == nullptr && LaunchGatedDeltaNet2Chunked(p, scratch, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.dk > kMaxLdsKeys)

@@ -84,7 +84,7 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
 // GatedDeltaNet2ChunkScratchBytes bytes: the prepared chunk vectors of one
 // window of up to 2048 tokens, and the state carried between windows.
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
-constexpr int kGdn2ChunkKeyLimit = 384;   // head_k handled by the chunked path
+constexpr int kGdn2ChunkKeyLimit = 512;   // head_k handled by the chunked path (packed sequences excepted)
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
 // Chunked fp32-MFMA path (headdim_qk <= 256).  Returns false, launching
