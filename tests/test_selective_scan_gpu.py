@@ -120,3 +120,37 @@ def test_selective_scan_mamba_2p8b_layer():
     assert torch.equal(selective_scan_fn(*args_u, delta_softplus=True), y * 2)
     # deterministic
     assert torch.equal(selective_scan_fn(*args, delta_softplus=True), y)
+
+
+@pytest.mark.parametrize("L", [4, 5])
+def test_selective_scan_softplus_range(L):
+    """delta' = softplus(delta + bias) over [-80, 80] and at the branch point 20,
+    read out exactly: A = 0 (no decay), u one-hot at token 0, B = 1 and C one-hot
+    on state 0, D = 0, so y[:, :, 0] = delta'.  The reference returns x for
+    x > 20 (selective_scan_fwd_kernel.cuh:157-159): required bit for bit; below,
+    within a few ulp plus the rounding of x * log2(e) carried through exp2.
+    L = 4 takes the 16-byte path, L = 5 the guarded one."""
+    import torch
+    D, N = 4096, 16
+    special = np.array([20.0, np.nextafter(np.float32(20), np.float32(21)), np.nextafter(np.float32(20), np.float32(0)),
+                        0.0, -0.0, 1e-30, -1e-30, 1e-7, -1e-7, 0.5, -0.5, 20.5, 80.0, -80.0], np.float32)
+    x = np.concatenate([special, np.linspace(-80, 80, D - special.size, dtype=np.float32)])
+    dev = torch.device("cuda")
+    delta = torch.zeros(1, D, L, device=dev)
+    delta[0, :, 0] = torch.from_numpy(x).to(dev)
+    u = torch.zeros(1, D, L, device=dev)
+    u[0, :, 0] = 1.0
+    A = torch.zeros(D, N, device=dev)
+    Bm = torch.ones(1, 1, N, L, device=dev)
+    Cm = torch.zeros(1, 1, N, L, device=dev)
+    Cm[:, :, 0] = 1.0
+    y = selective_scan_fn(u, delta, A, Bm, Cm, torch.zeros(D, device=dev), None, torch.zeros(D, device=dev),
+                          delta_softplus=True)
+    got = y[0, :, 0].cpu().numpy().astype(np.float64)
+    xd = x.astype(np.float64)
+    big = x > 20
+    assert np.array_equal(got[big], xd[big])
+    ref = np.log1p(np.exp(xd[~big]))
+    bound = (8 + 2 * np.abs(xd[~big])) * 2.0 ** -24 * ref
+    err = np.abs(got[~big] - ref)
+    assert np.all(err <= bound), (xd[~big][np.argmax(err / bound)], float((err / bound).max()))
