@@ -65,6 +65,8 @@ CASES = {
     "t1024": S(1, 1024, 2, 32, 16),
     "t1025_chunk_carry": S(1, 1025, 2, 32, 16),
     "t2100_two_carries": S(2, 2100, 1, 64, 32, per_key_gates=True),
+    "t2100_k320_window_carry": S(1, 2100, 1, 320, 16),
+    "t2060_k512_window_carry_perkey": S(1, 2060, 1, 512, 8, per_key_gates=True),
     "t1500_lds_carry": S(1, 1500, 1, 600, 16),
 }
 

@@ -127,6 +127,7 @@ GDN_CASES = {
     "t1500_lds_carry": S(1, 1500, 1, 600, 16),
     "k1024_lds_path_perkey": S(1, 12, 1, 1024, 7, per_key_gates=True),
     "t4100_three_windows": S(1, 4100, 2, 64, 24),
+    "k448_t2100_window_carry": S(1, 2100, 1, 448, 12, per_key_gates=True),
 }
 
 
@@ -153,7 +154,8 @@ def test_gdn2_final_state_rows_per_column(rows, monkeypatch):
     check(f"gated_deltanet2_state/rows{rows}/S", st, ref_st, TOL_GDN2)
 
 
-@pytest.mark.parametrize("shape,split", [((2, 300, 4, 128, 128), 123), ((1, 1100, 2, 600, 24), 1030)])
+@pytest.mark.parametrize("shape,split", [((2, 300, 4, 128, 128), 123), ((1, 700, 2, 384, 16), 333),
+                                         ((1, 1100, 2, 600, 24), 1030)])
 def test_gdn2_final_state_chains(shape, split):
     """Tokens [0, split) then [split, T) started from the first call's final
     state give the outputs and final state of one call over [0, T)."""
