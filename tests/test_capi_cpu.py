@@ -254,7 +254,7 @@ def test_gdn2_valid_and_scratch():
     # headdim_k <= 512 (chunked path): per (b,h) and 16-token chunk of a window
     # of up to 128 chunks, E, R, Ut tiles (256 floats per 16 keys each), G_15
     # (16 per 16 keys), T and M T (256 each), q and k multipliers (16 each);
-    # keys padded to 16 * kpw * ks (kpw = 2 and ks a power of two up to 128
+    # keys padded to 16 * kpw * ks (kpw = 2 and ks = ceil(tiles / 2) up to 128
     # keys, kpw = 4 and ks = ceil(tiles / 4) above);
     # plus the state carried between windows when there is more than one
     def chunk_scratch(B, T, H, K, V):
@@ -263,9 +263,7 @@ def test_gdn2_valid_and_scratch():
             kpw, ks = 4, -(-kq // 4)
         else:
             kpw = 2 if kq >= 2 else 1
-            ks = 1
-            while ks * kpw < kq:
-                ks *= 2
+            ks = -(-kq // kpw)
         kq = kpw * ks
         block = 3 * kq * 256 + 16 * kq + 512 + 32
         nch = -(-T // 16)
@@ -273,7 +271,7 @@ def test_gdn2_valid_and_scratch():
         return a256(B * H * win * block * 4) + (a256(B * H * K * V * 4) if nch > 128 else 0)
     assert scratch == chunk_scratch(2, 5, 3, 16, 8)
     for T, K, V in ((100, 128, 64), (3000, 128, 128), (17, 100, 7), (2049, 256, 16), (2048, 33, 40),
-                    (3000, 512, 64), (40, 300, 16), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8)):
+                    (3000, 512, 64), (40, 300, 16), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8)):
         assert validate("gated_deltanet2", gdn_shapes(T=T, K=K, V=V))[1] == chunk_scratch(2, T, 3, K, V), (T, K, V)
     # packed sequences (headdim_k <= 512) take the fused kernel: no scratch
     # headdim_k > 512: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded

@@ -46,6 +46,8 @@ CASES = {
     "k17_v15_partial": S(2, 20, 2, 17, 15),
     "k32_v33_nos0": S(1, 40, 2, 32, 33, initial_state=False),
     "k64_v64_perkey": S(2, 50, 2, 64, 64, per_key_gates=True),
+    "k80_v24_three_waves": S(2, 45, 2, 80, 24),
+    "k96_t2100_three_waves_window_carry": S(1, 2100, 1, 96, 16, per_key_gates=True),
     "k100_v48": S(1, 31, 3, 100, 48),
     "k128_v128_nol2": S(1, 24, 2, 128, 128, l2norm=False),
     "k128_v65_partial_wave": S(2, 64, 4, 128, 65),
