@@ -236,9 +236,36 @@ int xm_gated_deltanet2_forward_states(const xm_tensor_t *inputs, size_t n_inputs
 int xm_softmax_cpu(const float *in, const int64_t *shape, int32_t rank, int64_t axis, float *out,
                    char *errbuf, size_t errlen);
 
+/* ---- Kernel-selection overrides (tests and tuning) ---------------------------
+ * Process-wide switches that force a kernel variant the dispatchers would not
+ * pick by themselves, so that parity tests can run every variant; value 0
+ * restores the dispatcher's own choice.  Production callers never need them.
+ *   "gdn2_path"      1: GatedDeltaNet2Fn sequential fused kernel (headdim_k <= 512)
+ *   "gdn2_pairwise"  1: every chunk of the chunked GDN-2 path forms A and M pairwise
+ *   "gdn2_rows"      1, 2, 4: rows of 16 lanes per value column of the fused kernel
+ *   "m3_path"        1: Mamba3SisoFn token-by-token kernel
+ *   "ss_lpc"         1, 2, 4, 8, 16: SelectiveScanFn lanes per channel (d_state <= 16)
+ *   "ss_split"       1: SelectiveScanFn channel-block kernel only; 2: the
+ *                    sequence-split kernel wherever it applies
+ * The values are read with one atomic load per launch; a change affects calls
+ * made after it.  No counterpart in the reference (its variants are fixed at
+ * compile time).  xm_set_kernel_override returns XM_ERR_INVALID_ARGUMENT for
+ * an unknown name or value; xm_get_kernel_override returns -1 for an unknown
+ * name. */
+int xm_set_kernel_override(const char *name, int64_t value, char *errbuf, size_t errlen);
+int64_t xm_get_kernel_override(const char *name);
+
 /* ---- Library ---------------------------------------------------------------
  * Version string and a description of the build (target, kernel variants). */
 const char *xm_version(void);
+/* The kernels the calling host thread's last *_forward / *_forward_states
+ * call enqueued, in launch order, ';'-separated, each with its template
+ * arguments and " xN" when launched N > 1 times, e.g.
+ * "Gdn2ChunkPrepKernel x2;Gdn2ChunkRecurKernel<2,4> x2" (booleans as 0/1;
+ * rocprofv3 prints the same kernels as demangled signatures).  Diagnostics
+ * for benchmarks and tests; the string is valid until the thread's next call.
+ * No counterpart in the reference. */
+const char *xm_last_launches(void);
 
 #ifdef __cplusplus
 } /* extern "C" */

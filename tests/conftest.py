@@ -22,14 +22,28 @@ def pytest_collection_modifyitems(config, items):
             item.add_marker(pytest.mark.usefixtures("_announce_gpu_case"))
 
 
+@pytest.fixture
+def override():
+    """Sets kernel-selection overrides (xm_set_kernel_override) for one test
+    and restores the previous values afterwards."""
+    import xmetai_onnx_plugins as xp
+    touched = {}
+
+    def set_(name, value):
+        if name not in touched:
+            touched[name] = xp.get_kernel_override(name)
+        xp.set_kernel_override(name, int(value))
+
+    yield set_
+    for name, prev in touched.items():
+        xp.set_kernel_override(name, prev)
+
+
 @pytest.fixture(params=["chunk", "seq"])
-def m3_path(request, monkeypatch):
+def m3_path(request, override):
     """Mamba3SisoFn kernel under test: the chunked fp32-MFMA kernel (default)
-    or the token-by-token kernel (XM_M3_PATH=seq)."""
-    if request.param == "seq":
-        monkeypatch.setenv("XM_M3_PATH", "seq")
-    else:
-        monkeypatch.delenv("XM_M3_PATH", raising=False)
+    or the token-by-token kernel (m3_path override 1)."""
+    override("m3_path", 1 if request.param == "seq" else 0)
     return request.param
 
 

@@ -1,22 +1,57 @@
 """Helpers shared by the GPU parity tests.
 
-Error measure (reported per case, gated by the tolerance written in each test):
+Error measures (reported per case, gated by the tolerances below), with
+``ref`` the fp64 oracle evaluated on the same fp32 inputs:
+
     max_abs  = max |gpu - ref|
-    norm_err = max |gpu - ref| / max(1, max |ref|)
-with ``ref`` the fp64 oracle evaluated on the same fp32 inputs.  When the
-environment variable XM_PARITY_REPORT names a file, every check appends one
-JSON line with these figures.
+    norm_err = max |gpu - ref| / max(1, max |ref|)                  (whole tensor)
+    row_err  = max over rows r of max_r |gpu - ref| / max(1, max_r |ref|)
+
+A row is a line along the last axis (the value columns of one token and head,
+or the tokens of one selective-scan channel).  ``row_err`` is the per-element
+gate |gpu - ref| <= tol_row * max(1, max |ref| of that row): an output whose
+magnitude grows along the sequence (GatedDeltaNet2Fn without the L2 norm)
+cannot hide an error in its small early rows behind the large late ones.
+When the environment variable XM_PARITY_REPORT names a file, every check
+appends one JSON line with these figures and the kernel overrides in force.
+
+Gates (measured worst on MI355X over the whole GPU suite, per operator and
+kernel path, times about 10):
+
+    op        worst norm_err   worst row_err   gate norm / row
+    SS        2.5e-7           5.7e-7          3e-6 / 6e-6
+    Mamba-3   3.0e-7           5.0e-7          3e-6 / 5e-6
+    GDN-2     3.7e-7           3.7e-7          4e-6 / 4e-6
+    GPU vs GPU (chained calls, packed vs plain, chunked vs token-by-token):
+              2.0e-7           2.6e-7          2e-6 / 2e-6
+
+Ill-conditioned cases (an exploding GDN-2 state without the L2 norm, growing
+decays, thousands of large angle steps) lose accuracy in any fp32 evaluation
+order.  For them the test also runs the oracle in fp32 with the reference's
+operation order and the gate becomes max(gate, 8 x that fp32 error): the
+device must be as accurate as the reference's own fp32 recurrence.  Measured:
+GDN-2 without L2 norm row_err 7.0e-5 against 9.0e-5 for the fp32 order;
+Mamba-3 growth 6.5e-6 against 5.9e-6; long angle runs 3.7e-6 against 6.3e-6.
 """
 
 import json
 import os
+from typing import NamedTuple
 
 import numpy as np
 
-# Tolerances on norm_err (fp32 device path vs fp64 oracle).
-TOL_SS = 1e-4
-TOL_M3 = 1e-4
-TOL_GDN2 = 2e-4
+
+class Gate(NamedTuple):
+    norm: float   # bound on norm_err
+    row: float    # bound on row_err
+
+
+# fp32 device path vs the fp64 oracle, per operator
+TOL_SS = Gate(3e-6, 6e-6)
+TOL_M3 = Gate(3e-6, 5e-6)
+TOL_GDN2 = Gate(4e-6, 4e-6)
+TOL_GPU = Gate(2e-6, 2e-6)   # one device path against another
+FP32_FACTOR = 8.0            # ill-conditioned cases: multiple of the fp32-order oracle's error
 
 
 def to_dev(x, device="cuda"):
@@ -27,23 +62,54 @@ def to_dev(x, device="cuda"):
 
 
 def errors(got, ref):
+    """(max_abs, norm_err, ref_inf, row_err) of `got` against `ref`."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     if got.size == 0:
-        return 0.0, 0.0, 0.0
-    d = np.abs(got - ref)
+        return 0.0, 0.0, 0.0, 0.0
     assert np.all(np.isfinite(got)), "non-finite output"
+    d = np.abs(got - ref)
     max_abs = float(d.max())
     ref_inf = float(np.abs(ref).max())
-    return max_abs, max_abs / max(1.0, ref_inf), ref_inf
+    rows = max(1, ref.shape[-1]) if ref.ndim else 1
+    d2 = d.reshape(-1, rows)
+    r2 = np.abs(ref).reshape(-1, rows)
+    row_err = float((d2.max(axis=1) / np.maximum(1.0, r2.max(axis=1))).max())
+    return max_abs, max_abs / max(1.0, ref_inf), ref_inf, row_err
 
 
-def check(name, got, ref, tol):
-    max_abs, norm_err, ref_inf = errors(got, ref)
+def _overrides():
+    try:
+        import xmetai_onnx_plugins as xp
+        from xmetai_onnx_plugins import _capi
+    except ImportError:
+        return {}
+    if xp._lib is None:
+        return {}
+    return {k: v for k in _capi.KERNEL_OVERRIDES if (v := xp.get_kernel_override(k)) != 0}
+
+
+def check(name, got, ref, gate, ref32=None):
+    """Gates norm_err <= gate.norm and row_err <= gate.row (a plain number
+    bounds both).  With ``ref32`` (the oracle in fp32, reference operation
+    order) each bound is raised to FP32_FACTOR times that evaluation's own
+    error against ``ref``."""
+    if not isinstance(gate, Gate):
+        gate = Gate(float(gate), float(gate))
+    tol, tol_row = gate
+    extra = {}
+    if ref32 is not None:
+        _, n32, _, r32 = errors(ref32, ref)
+        tol = max(tol, FP32_FACTOR * n32)
+        tol_row = max(tol_row, FP32_FACTOR * r32)
+        extra = dict(fp32_norm_err=n32, fp32_row_err=r32)
+    max_abs, norm_err, ref_inf, row_err = errors(got, ref)
     path = os.environ.get("XM_PARITY_REPORT")
     if path:
         with open(path, "a") as f:
-            f.write(json.dumps(dict(case=name, max_abs=max_abs, norm_err=norm_err, ref_inf=ref_inf, tol=tol)) + "\n")
+            f.write(json.dumps(dict(case=name, max_abs=max_abs, norm_err=norm_err, row_err=row_err, ref_inf=ref_inf,
+                                    tol=tol, tol_row=tol_row, overrides=_overrides(), **extra)) + "\n")
     assert norm_err <= tol, f"{name}: max_abs={max_abs:.3e} norm_err={norm_err:.3e} > tol={tol:.1e}"
+    assert row_err <= tol_row, f"{name}: row_err={row_err:.3e} > tol_row={tol_row:.1e} (max_abs={max_abs:.3e})"
     return max_abs, norm_err

@@ -201,6 +201,31 @@ def test_ss_extent_checks_beyond_reference(idx, shape, msg):
     assert e.value.message == msg
 
 
+@pytest.mark.parametrize("kw", [dict(), dict(bvar=False, cvar=False), dict(has_d=False)])
+def test_ss_dstate_zero_is_accepted_like_reference(kw):
+    # The reference only caps d_state at 256 (selective_scan_fn_ort.cpp:99-105);
+    # with d_state = 0 its state loop is empty and y = D * u.
+    out, scratch = validate("selective_scan", ss_shapes(N=0, **kw))
+    assert out == (2, 8, 16) and scratch == 0
+
+
+def test_kernel_overrides_roundtrip():
+    from xmetai_onnx_plugins import _capi
+    for name, values in _capi.KERNEL_OVERRIDES.items():
+        assert xp.get_kernel_override(name) == 0
+        for v in values:
+            with xp.kernel_override(name, v):
+                assert xp.get_kernel_override(name) == v
+        assert xp.get_kernel_override(name) == 0
+    assert xp.get_kernel_override("no_such_switch") == -1
+    with pytest.raises(XmError) as e:
+        xp.set_kernel_override("no_such_switch", 1)
+    assert e.value.status == xp.XM_ERR_INVALID_ARGUMENT
+    with pytest.raises(XmError):
+        xp.set_kernel_override("ss_lpc", 3)
+    assert xp.get_kernel_override("ss_lpc") == 0
+
+
 def test_ss_empty_sequence_is_a_no_op():
     out, _ = validate("selective_scan", ss_shapes(L=0))
     assert out == (2, 8, 0)

@@ -1,6 +1,6 @@
 """Mamba3SisoFn on the GPU vs the fp64 oracle (C restatement), through the
 C ABI, for both kernels (the chunked fp32-MFMA kernel and, with
-XM_M3_PATH=seq, the token-by-token one).  Covers headdim_qk padding (N not a
+the m3_path override, the token-by-token one).  Covers headdim_qk padding (N not a
 multiple of the key tiling), partial angle sets (A < N/2), grouped Q/K heads,
 the optional D and Z inputs, sequence lengths around the 16-token chunk and
 block, the 32-row workgroups, decay patterns, and the benchmark shape on a
@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from oracle import cref
-from parity import TOL_M3, check, to_dev
+from parity import TOL_GPU, TOL_M3, check, to_dev
 from xmetai_onnx_plugins import mamba3_siso_fn, workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -25,8 +25,8 @@ def run_gpu(inp):
     return y.cpu().numpy()
 
 
-def run_ref(inp):
-    return cref.mamba3_siso(*(inp[k] for k in KEYS), dtype=np.float64)
+def run_ref(inp, dtype=np.float64):
+    return cref.mamba3_siso(*(inp[k] for k in KEYS), dtype=dtype)
 
 
 M = W.Mamba3SisoShape
@@ -82,7 +82,7 @@ def test_mamba3_decay_patterns(pattern, m3_path):
     else:
         adt = np.where(t % 2 == 0, 0.9, -0.5)                   # growth within the bound
     inp["ADT"] = np.broadcast_to(adt.astype(np.float32), inp["ADT"].shape).copy()
-    check(f"mamba3_siso/decay_{pattern}", run_gpu(inp), run_ref(inp), TOL_M3)
+    check(f"mamba3_siso/decay_{pattern}", run_gpu(inp), run_ref(inp), TOL_M3, ref32=run_ref(inp, np.float32))
 
 
 def test_mamba3_long_angle_accumulation(m3_path):
@@ -92,7 +92,7 @@ def test_mamba3_long_angle_accumulation(m3_path):
     inp = W.mamba3_siso_inputs(s, seed=5)
     inp["DT"] = np.full_like(inp["DT"], 2.0)
     inp["ADT"] = np.full_like(inp["ADT"], -0.05)
-    check("mamba3_siso/long_angles", run_gpu(inp), run_ref(inp), TOL_M3)
+    check("mamba3_siso/long_angles", run_gpu(inp), run_ref(inp), TOL_M3, ref32=run_ref(inp, np.float32))
 
 
 def test_mamba3_benchmark_shape_heads(m3_path):
@@ -123,15 +123,18 @@ def test_mamba3_long_sequence(m3_path):
     check("mamba3_siso/t65536", run_gpu(inp), run_ref(inp), TOL_M3)
 
 
-def test_mamba3_path_switch_selects_the_other_kernel(monkeypatch):
-    """XM_M3_PATH=seq runs the token-by-token kernel: its summation order
+def test_mamba3_path_switch_selects_the_other_kernel(override):
+    """The m3_path override runs the token-by-token kernel: its summation order
     differs from the chunked kernel's, so the two outputs are close but not
     bit-identical (both kernels are then exercised by the tests above)."""
     s = M(1, 64, 2, 32, 64)
     inp = W.mamba3_siso_inputs(s, seed=22)
-    monkeypatch.delenv("XM_M3_PATH", raising=False)
+    import xmetai_onnx_plugins as xp
+    override("m3_path", 0)
     chunked = run_gpu(inp)
-    monkeypatch.setenv("XM_M3_PATH", "seq")
+    assert xp.last_launches() == ["Mamba3ChunkKernel<1,4,4>"]
+    override("m3_path", 1)
     sequential = run_gpu(inp)
+    assert xp.last_launches() == ["Mamba3FwdKernel<4>"]
     assert not np.array_equal(chunked, sequential)
-    check("mamba3_siso/chunked_vs_seq", chunked, sequential, TOL_M3)
+    check("mamba3_siso/chunked_vs_seq", chunked, sequential, TOL_GPU)

@@ -57,11 +57,33 @@ def test_selective_scan_parity(name):
     check(f"selective_scan/{name}", run_gpu(inp, s.delta_softplus), run_ref(inp, s.delta_softplus), TOL_SS)
 
 
-@pytest.mark.parametrize("lpc", ["4", "8", "16"])
-def test_selective_scan_lane_layouts_agree(lpc, monkeypatch):
+@pytest.mark.parametrize("has_d", [True, False])
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_selective_scan_dstate_zero(has_d, dtype):
+    """d_state = 0: the reference's state loop is empty and y = D * u
+    (selective_scan_fwd_kernel.cuh:161,166), zeros without D; bit-exact
+    (one fp32 product, rounded once to the data type)."""
+    import torch
+    tdt = getattr(torch, dtype)
+    Bn, Dn, L = 2, 37, 131
+    rng = np.random.default_rng(3)
+    u = torch.from_numpy(rng.standard_normal((Bn, Dn, L)).astype(np.float32)).to("cuda", tdt)
+    delta = torch.from_numpy(rng.standard_normal((Bn, Dn, L)).astype(np.float32)).to("cuda", tdt)
+    A = torch.empty((Dn, 0), device="cuda")
+    Bm = torch.empty((Bn, 0, L), device="cuda", dtype=tdt)
+    D = torch.from_numpy(rng.standard_normal(Dn).astype(np.float32)).cuda() if has_d else None
+    y = selective_scan_fn(u, delta, A, Bm, Bm, D, None, None, delta_softplus=True)
+    torch.cuda.synchronize()
+    want = (D[None, :, None] * u.float()).to(tdt) if has_d else torch.zeros_like(u)
+    assert y.dtype == tdt
+    assert torch.equal(y, want)
+
+
+@pytest.mark.parametrize("lpc", [4, 8, 16])
+def test_selective_scan_lane_layouts_agree(lpc, override):
     s = W.SelectiveScanShape(2, 200, 96, 16)
     inp = W.selective_scan_inputs(s, seed=1)
-    monkeypatch.setenv("XM_SS_LPC", lpc)
+    override("ss_lpc", lpc)
     check(f"selective_scan/lpc{lpc}", run_gpu(inp), run_ref(inp), TOL_SS)
 
 

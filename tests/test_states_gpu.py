@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from oracle import cref
-from parity import TOL_GDN2, TOL_M3, TOL_SS, check, to_dev
+from parity import TOL_GPU, TOL_GDN2, TOL_M3, TOL_SS, check, to_dev
 from xmetai_onnx_plugins import gated_deltanet2_fn, mamba3_siso_fn, selective_scan_fn, workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -69,11 +69,11 @@ def test_ss_last_state_parity(name):
     np.testing.assert_array_equal(y, ss_gpu(inp, state=False))   # the state write leaves y alone
 
 
-@pytest.mark.parametrize("lpc", ["4", "8", "16"])
-def test_ss_last_state_lane_layouts(lpc, monkeypatch):
+@pytest.mark.parametrize("lpc", [4, 8, 16])
+def test_ss_last_state_lane_layouts(lpc, override):
     s = W.SelectiveScanShape(2, 70, 45, 16)
     inp = W.selective_scan_inputs(s, seed=5)
-    monkeypatch.setenv("XM_SS_LPC", lpc)
+    override("ss_lpc", lpc)
     y, h = ss_gpu(inp)
     ref_y, ref_h = ss_ref(inp)
     check(f"selective_scan_state/lpc{lpc}/y", y, ref_y, TOL_SS)
@@ -143,11 +143,12 @@ def test_gdn2_final_state_parity(name):
     np.testing.assert_array_equal(o, gdn_gpu(inp, s, state=False))   # the state write leaves o alone
 
 
-@pytest.mark.parametrize("rows", ["1", "2", "4"])
-def test_gdn2_final_state_rows_per_column(rows, monkeypatch):
+@pytest.mark.parametrize("rows", [1, 2, 4])
+def test_gdn2_final_state_rows_per_column(rows, override):
     s = S(2, 37, 3, 64, 40)
     inp = W.gated_deltanet2_inputs(s, seed=7)
-    monkeypatch.setenv("XM_GDN2_ROWS", rows)
+    override("gdn2_path", 1)   # the sequential kernel's column layouts
+    override("gdn2_rows", rows)
     o, st = gdn_gpu(inp, s)
     ref_o, ref_st = gdn_ref(inp, s)
     check(f"gated_deltanet2_state/rows{rows}/o", o, ref_o, TOL_GDN2)
@@ -172,8 +173,8 @@ def test_gdn2_final_state_chains(shape, split):
     whole = o.cpu().numpy()
     chained = torch.cat([o1, o2], dim=1).cpu().numpy()
     # the same arithmetic in the same order, with the state passing through fp32 memory
-    check(f"gated_deltanet2_state/chain_{split}/o", chained, whole, 1e-5)
-    check(f"gated_deltanet2_state/chain_{split}/S", st2.cpu().numpy(), st.cpu().numpy(), 1e-5)
+    check(f"gated_deltanet2_state/chain_{split}/o", chained, whole, TOL_GPU)
+    check(f"gated_deltanet2_state/chain_{split}/S", st2.cpu().numpy(), st.cpu().numpy(), TOL_GPU)
 
 
 # ---------------------------------------------------------------------------
@@ -269,5 +270,5 @@ def test_m3_states_chain(shape, split, m3_path):
     y1, st1 = mamba3_siso_fn(*part(0, split), return_final_states=True)
     y2, st2 = mamba3_siso_fn(*part(split, T), input_states=st1, return_final_states=True)
     torch.cuda.synchronize()
-    check(f"mamba3_state/chain_{split}/y", torch.cat([y1, y2], dim=1).cpu().numpy(), y.cpu().numpy(), 1e-5)
-    check_m3_states(f"mamba3_state/chain_{split}", [x.cpu().numpy() for x in st2], [x.cpu().numpy() for x in st], 1e-5)
+    check(f"mamba3_state/chain_{split}/y", torch.cat([y1, y2], dim=1).cpu().numpy(), y.cpu().numpy(), TOL_GPU)
+    check_m3_states(f"mamba3_state/chain_{split}", [x.cpu().numpy() for x in st2], [x.cpu().numpy() for x in st], TOL_GPU)

@@ -5,7 +5,9 @@
 Every HIP and C++ source under ``csrc/`` is compiled with hipcc for gfx950
 (objects under ``_build/``) and linked into
 ``xmetai_onnx_plugins/libxmetai_recurrent.so``, which exports the C ABI of
-``include/xmetai_recurrent.h``.  When ONNX Runtime headers are available
+``include/xmetai_recurrent.h``.  ``csrc/probe/hbm_stream.hip`` becomes
+``libxm_hbm_probe.so``, the streaming kernels bench.py times for the
+achievable HBM bandwidth (not part of the operator library).  When ONNX Runtime headers are available
 (``--ort-include`` or ``ORT_INCLUDE_DIR``), the custom-op layer under
 ``csrc/ort/`` is built as ``libxmetai_onnx_plugins_ort.so`` (exports
 ``RegisterCustomOps``, ``include/xmetai_onnx_plugins_ort.h``) on top of it.
@@ -28,6 +30,7 @@ BUILD = os.path.join(HERE, "_build")
 PKG = os.path.join(HERE, "xmetai_onnx_plugins")
 LIB = os.path.join(PKG, "libxmetai_recurrent.so")
 ORT_LIB = os.path.join(PKG, "libxmetai_onnx_plugins_ort.so")
+PROBE_LIB = os.path.join(PKG, "libxm_hbm_probe.so")   # benchmark-only HBM streaming probe
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -89,6 +92,12 @@ def build(jobs: int | None = None, ort_include: str | None = None, ort_lib: str 
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     subprocess.run(cmd, check=True, capture_output=not verbose)
     os.replace(tmp, LIB)
+
+    probe_obj = _compile("probe/hbm_stream.hip", [])
+    tmp = PROBE_LIB + ".tmp"
+    subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, probe_obj], check=True,
+                   capture_output=not verbose)
+    os.replace(tmp, PROBE_LIB)
 
     ort_include = ort_include or os.environ.get("ORT_INCLUDE_DIR")
     ort_lib = ort_lib or os.environ.get("ORT_LIB_DIR")

@@ -482,12 +482,11 @@ struct FusedConfig {
 // one row wins from one wave per SIMD (1024 waves) up, two rows only from two
 // waves per SIMD (2048), else four (at most 8 keys per lane).  8-wave
 // workgroups when they still give one workgroup per CU, else 4-wave ones.
-// XM_GDN2_ROWS (1, 2 or 4) forces the rows per column where the keys fit, for
+// The gdn2_rows override (1, 2 or 4) forces the rows per column where the keys fit, for
 // tuning and tests.
 FusedConfig ChooseFused(const GatedDeltaNet2Params &p) {
     const long long cols = static_cast<long long>(p.batch) * p.nheads * p.dv;
-    const char *env = std::getenv("XM_GDN2_ROWS");
-    const int forced = env ? std::atoi(env) : 0;
+    const int forced = static_cast<int>(GetOverride(kOverrideGdn2Rows));
     FusedConfig best{0, 0, 8};
     for (int r : {1, 2, 4}) {
         const int kt = KeyTile(p.dk, r);
@@ -507,8 +506,8 @@ void LaunchFused(const GatedDeltaNet2Params &p, hipStream_t stream) {
     using L = FusedLayout<KT, NW, R>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.dv + L::COLS - 1) / L::COLS);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2FusedKernel<KT, NW, R>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2FusedKernel<KT, NW, R>), static_cast<int>(L::kBytes));
+    XM_NOTE_LAUNCH("Gdn2FusedKernel", {}, KT, NW, R);
     hipLaunchKernelGGL((Gdn2FusedKernel<KT, NW, R>), dim3(static_cast<unsigned>(blocks)), dim3(L::THREADS), L::kBytes,
                        stream, p);
 }
@@ -541,6 +540,7 @@ template <int KPL>
 void LaunchPrep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
     const long long rows = static_cast<long long>(p.batch) * p.nheads * tc;
     const long long blocks = (rows + 3) / 4;
+    XM_NOTE_LAUNCH("Gdn2PrepKernel", {}, KPL);
     hipLaunchKernelGGL((Gdn2PrepKernel<KPL>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, p, t0, tc);
 }
 
@@ -594,13 +594,13 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v)
     if (bh * ((p.dv + 15) / 16) > 2147483647LL || bh * kChunkTokens / 4 > 2147483647LL)
         throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel), static_cast<int>(lds));
     for (int t0 = 0; t0 < p.seqlen; t0 += p.chunk_cap) {
         const int tc = std::min(p.chunk_cap, p.seqlen - t0);
         Prep(p, t0, tc, stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn preparation");
         const long long blocks = bh * ((p.dv + 15) / 16);
+        XM_NOTE_LAUNCH("Gdn2RecurLdsKernel", {}, );
         hipLaunchKernelGGL(Gdn2RecurLdsKernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, p, t0, tc);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn recurrence");
     }

@@ -565,6 +565,7 @@ void LaunchRecur(const GatedDeltaNet2Params &p, int c0, int wn, int kq, const fl
     const int vt = (p.dv + 15) / 16;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * vt;
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS);
     hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, stream,
                        p, c0, wn, s_in, s_out);
 }
@@ -595,16 +596,14 @@ size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk
 }
 
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream_v) {
-    const char *path = std::getenv("XM_GDN2_PATH");
-    if (path != nullptr && std::strcmp(path, "seq") == 0) return false;
+    if (GetOverride(kOverrideGdn2Path) == 1) return false;
     if (p.cu_seqlens != nullptr) return false;   // packed sequences: the fused kernel
     if (p.dk > kGdn2ChunkKeyLimit) return false;
     // the recurrence's 32-bit buffer offsets span 16 tokens of [B,T,H,V]
     if (static_cast<long long>(p.nheads) * p.dv >= (1LL << 25)) return false;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     GatedDeltaNet2Params q = p;
-    const char *pw = std::getenv("XM_GDN2_PAIRWISE");
-    q.pairwise_only = pw != nullptr && std::atoi(pw) != 0;
+    q.pairwise_only = GetOverride(kOverrideGdn2Pairwise) != 0;
     auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
     q.vec4_keys = p.dk % 4 == 0 && a16(p.q) && a16(p.k) && a16(p.g) && a16(p.beta);
     const ChunkConfig c = ChooseChunk(p.dk);
@@ -622,6 +621,7 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, v
         const long long items = static_cast<long long>(heads) * wn;
         const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
         if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+        XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
         hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(static_cast<unsigned>(pblocks)), dim3(64 * kPrepWaves), 0, stream,
                            q, c0, wn, kq);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");

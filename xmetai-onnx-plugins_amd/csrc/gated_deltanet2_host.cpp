@@ -101,6 +101,7 @@ Plan Prepare(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet
 
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t &attrs, float *out,
              float *final_state, void *stream, const xm_allocator_t *alloc) {
+    ResetLaunches();
     CheckAttrs(attrs);
     Plan plan = Prepare(inputs, n_inputs, attrs);
     if (out == nullptr) Invalid("output pointer is null");

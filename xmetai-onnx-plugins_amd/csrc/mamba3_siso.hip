@@ -412,8 +412,8 @@ void LaunchKPT(const Mamba3SisoParams &p, hipStream_t stream) {
     using L = M3Layout<KPT>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3FwdKernel<KPT>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3FwdKernel<KPT>), static_cast<int>(L::kBytes));
+    XM_NOTE_LAUNCH("Mamba3FwdKernel", {}, KPT);
     hipLaunchKernelGGL((Mamba3FwdKernel<KPT>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), L::kBytes, stream, p);
 }
 

@@ -44,8 +44,8 @@
 // of the sequence are identity tokens: zero q, k and v, zero ADT and w.
 //
 // States, packed sequences and the look-ahead hand-over are those of the
-// token-by-token kernel (mamba3_siso.hip), which remains the path for
-// XM_M3_PATH=seq.
+// token-by-token kernel (mamba3_siso.hip), which remains the path under the
+// m3_path override.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -605,8 +605,8 @@ void LaunchChunk(const Mamba3SisoParams &p, hipStream_t stream) {
     using L = M3CLayout<KBW, NW, NPW>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    XM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L::kBytes)));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW>), static_cast<int>(L::kBytes));
+    XM_NOTE_LAUNCH("Mamba3ChunkKernel", {}, KBW, NW, NPW);
     hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NW, NPW>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
                        stream, p);
 }
@@ -614,8 +614,7 @@ void LaunchChunk(const Mamba3SisoParams &p, hipStream_t stream) {
 }  // namespace
 
 bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream_v) {
-    const char *path = std::getenv("XM_M3_PATH");
-    if (path != nullptr && std::strcmp(path, "seq") == 0) return false;
+    if (GetOverride(kOverrideM3Path) == 1) return false;
     // Per-chunk buffer descriptors hold 32-bit byte sizes: the token rows of
     // Q/K, Angles and V/Z/out of one sequence must each span less than 2 GiB.
     const size_t widest = std::max({static_cast<size_t>(p.nheads_qk) * p.n, static_cast<size_t>(p.nheads) * p.a,

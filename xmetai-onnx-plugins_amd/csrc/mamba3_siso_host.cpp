@@ -150,6 +150,7 @@ Plan Prepare(const xm_tensor_t *inputs, size_t n_inputs, const xm_mamba3_siso_at
 
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_mamba3_siso_attrs_t &attrs, float *out,
              float *const *states, void *stream) {
+    ResetLaunches();
     CheckAttrs(attrs);
     Plan plan = Prepare(inputs, n_inputs, attrs);
     if (out == nullptr) Invalid("output pointer is null");

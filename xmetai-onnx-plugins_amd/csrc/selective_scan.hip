@@ -26,6 +26,7 @@
 //    to fp32, the arithmetic is fp32, y is rounded to nearest even.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <type_traits>
@@ -490,12 +491,11 @@ struct Config {
     int lpc, spl;
 };
 
-// States per lane and lanes per channel by dstate.  XM_SS_LPC overrides the
-// lanes per channel for dstate <= 16 (1, 2, 4, 8 or 16), for tuning.
+// States per lane and lanes per channel by dstate.  The ss_lpc override sets
+// the lanes per channel for dstate <= 16 (1, 2, 4, 8 or 16), for tests and tuning.
 Config ChooseConfig(int N) {
     if (N <= 16) {
-        const char *env = std::getenv("XM_SS_LPC");
-        const int forced = env ? std::atoi(env) : 0;
+        const int forced = static_cast<int>(GetOverride(kOverrideSsLpc));
         switch (forced) {
             case 4: if (N > 8) return {4, 4}; break;
             case 8: return {8, 2};
@@ -514,8 +514,22 @@ Config ChooseConfig(int N) {
     return {16, 16};
 }
 
+template <typename IT>
+constexpr const char *TypeTag() {
+    return sizeof(IT) == 4 ? "float" : (std::is_same_v<IT, _Float16> ? "half" : "bfloat16");
+}
+
+template <typename IT, int LPC, int SPL, bool BVAR, bool CVAR, bool VEC>
+void NoteSs() {
+    XM_NOTE_LAUNCH("SelectiveScanFwdKernel", {TypeTag<IT>()}, LPC, SPL, BVAR, CVAR, VEC);
+}
+
 template <typename IT, int LPC, int SPL, bool VEC>
 void LaunchLSV(const SelectiveScanParams &p, dim3 grid, hipStream_t stream) {
+    if (p.b_var && p.c_var) NoteSs<IT, LPC, SPL, true, true, VEC>();
+    else if (p.b_var) NoteSs<IT, LPC, SPL, true, false, VEC>();
+    else if (p.c_var) NoteSs<IT, LPC, SPL, false, true, VEC>();
+    else NoteSs<IT, LPC, SPL, false, false, VEC>();
     if (p.b_var && p.c_var)
         hipLaunchKernelGGL((SelectiveScanFwdKernel<IT, LPC, SPL, true, true, VEC>), grid, dim3(kThreads), 0, stream, p);
     else if (p.b_var)
@@ -556,10 +570,40 @@ void LaunchTyped(const SelectiveScanParams &p, const Config &cfg, dim3 grid, hip
     }
 }
 
+// d_state = 0: no state, y = D * u (zeros without D); reference
+// selective_scan_fwd_kernel.cuh:161 (out = D * u) with an empty state loop (:166).
+template <typename IT>
+__global__ __launch_bounds__(256) void SelectiveScanSkipKernel(SelectiveScanParams p) {
+    const size_t total = static_cast<size_t>(p.batch) * p.dim * p.seqlen;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    const IT *u = static_cast<const IT *>(p.u);
+    IT *out = static_cast<IT *>(p.out);
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int d = static_cast<int>((i / static_cast<size_t>(p.seqlen)) % static_cast<size_t>(p.dim));
+        const float dv = p.D != nullptr ? p.D[d] : 0.0f;
+        out[i] = FromF<IT>(dv * ToF(u[i]));
+    }
+}
+
+template <typename IT>
+void LaunchSkip(const SelectiveScanParams &p, hipStream_t stream) {
+    const size_t total = static_cast<size_t>(p.batch) * p.dim * p.seqlen;
+    const size_t blocks = std::min<size_t>((total + 255) / 256, 8192);
+    XM_NOTE_LAUNCH("SelectiveScanSkipKernel", {TypeTag<IT>()}, );
+    hipLaunchKernelGGL(SelectiveScanSkipKernel<IT>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
+}
+
 }  // namespace
 
 void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream_v) {
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
+    if (p.dstate == 0) {
+        if (p.in_type == XM_ELEM_FLOAT16) LaunchSkip<_Float16>(p, stream);
+        else if (p.in_type == XM_ELEM_BFLOAT16) LaunchSkip<Bf16>(p, stream);
+        else LaunchSkip<float>(p, stream);
+        XM_LAUNCH_CHECK("SelectiveScanFn (d_state 0)");
+        return;
+    }
     const Config cfg = ChooseConfig(p.dstate);
     const int cpw = kThreads / cfg.lpc;
     const long long ncb = (p.dim_per_group + cpw - 1) / cpw;

@@ -2,10 +2,12 @@
 //
 // Mirrors the reference adapter selective_scan_fn_ort.cpp:50-197 (constructor
 // checks, MaybeInsertGroupDim, the Compute validation and its messages).
+// d_state = 0 is accepted as in the reference (its state loop is empty,
+// selective_scan_fwd_kernel.cuh:161,166): y = D * u, or zeros without D.
 // Differences, all on inputs the reference leaves unchecked and would read out
 // of bounds or with mismatched strides:
 //   - B/C/D/z/delta_bias extents must equal the extents the kernel reads;
-//   - rank > 4 for B/C, dstate < 1 and n_groups < 1 are rejected;
+//   - rank > 4 for B/C and n_groups < 1 are rejected;
 //   - an empty u (any dimension 0) yields an empty output with no launch;
 //   - no uint32 stride limit (the kernels index with 64-bit bases).
 // No scratch is needed: the reference's per-chunk state buffer `x` is written
@@ -63,7 +65,6 @@ Plan Validate(const std::vector<View> &in, const xm_selective_scan_attrs_t &attr
     const int64_t dstate = A.shape[1];
     if (A.shape[0] != dim) Invalid("A dimension mismatch with u");
     if (dstate > 256) Invalid("selective_scan supports d_state up to 256");
-    if (dstate < 1) Invalid("selective_scan requires d_state >= 1");
     if (batch > INT32_MAX || dim > INT32_MAX || seqlen > INT32_MAX) Invalid("u dimension is out of range");
 
     const bool b_var = B.rank() >= 3;
@@ -139,6 +140,7 @@ std::vector<View> SsViews(const xm_tensor_t *inputs, size_t n_inputs) {
 
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_selective_scan_attrs_t &attrs, void *out,
              float *last_state, void *stream) {
+    ResetLaunches();
     CheckAttrs(attrs);
     auto views = SsViews(inputs, n_inputs);
     Plan plan = Validate(views, attrs);

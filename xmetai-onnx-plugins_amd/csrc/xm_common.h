@@ -8,6 +8,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <initializer_list>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -133,6 +134,34 @@ int Guard(char *errbuf, size_t errlen, Fn &&fn) {
         return XM_ERR_DEVICE;
     }
 }
+
+// Kernel-selection overrides, set through xm_set_kernel_override (tests and
+// tuning); 0 everywhere means the dispatchers' own choice.  Read with one
+// relaxed atomic load per launch.
+enum Override {
+    kOverrideGdn2Path,       // 1: GatedDeltaNet2Fn sequential fused kernel
+    kOverrideGdn2Pairwise,   // 1: pairwise A and M in every chunk
+    kOverrideGdn2Rows,       // rows of 16 lanes per value column of the fused kernel
+    kOverrideM3Path,         // 1: Mamba3SisoFn token-by-token kernel
+    kOverrideSsLpc,          // lanes per channel of the selective scan (dstate <= 16)
+    kOverrideSsSplit,        // selective scan: 1 channel blocks only, 2 sequence-split
+    kOverrideCount
+};
+int64_t GetOverride(Override which);
+
+// Per host thread, the kernels the current entry-point call has enqueued
+// (reported by xm_last_launches): reset at the start of each forward call.
+void ResetLaunches();
+void NoteLaunch(const char *name);
+// "Base<a,b,...>" with the template arguments of one instantiation.
+std::string KernelName(const char *base, std::initializer_list<const char *> types, std::initializer_list<int> args);
+// Records one launch of an instantiation; the name is built once per call site
+// and instantiation (a function-local static inside the launching template).
+#define XM_NOTE_LAUNCH(base, types, ...)                                                    \
+    do {                                                                                    \
+        static const std::string xm_name_ = ::xm::KernelName(base, types, {__VA_ARGS__});   \
+        ::xm::NoteLaunch(xm_name_.c_str());                                                 \
+    } while (0)
 
 // Stream-ordered scratch: forwards to the caller's allocator or to the
 // library's default pool (defined in xm_runtime.hip).  Freed on scope exit;

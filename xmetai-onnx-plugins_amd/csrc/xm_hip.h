@@ -24,6 +24,10 @@
 
 namespace xm {
 
+// Raises `kernel`'s dynamic-LDS limit to `bytes` on the current device the
+// first time a launch needs it; later launches skip the runtime call.
+void EnsureDynamicLds(const void *kernel, int bytes);
+
 constexpr float kLog2eF = 1.4426950408889634f;  // M_LOG2E as float
 
 // Moves `x` across lanes with a DPP control (row-local patterns only).

@@ -80,7 +80,7 @@ void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed);
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
 // Chunked fp32-MFMA path (dk <= kGdn2ChunkKeyLimit).  Returns false, launching nothing, when
-// the shape is not one it takes (or XM_GDN2_PATH=seq).  `scratch` holds
+// the shape is not one it takes (or the gdn2_path override asks for the sequential kernel).  `scratch` holds
 // GatedDeltaNet2ChunkScratchBytes bytes: the prepared chunk vectors of one
 // window of up to 2048 tokens, and the state carried between windows.
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
@@ -88,7 +88,7 @@ constexpr int kGdn2ChunkKeyLimit = 512;   // head_k handled by the chunked path 
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
 // Chunked fp32-MFMA path (headdim_qk <= 256).  Returns false, launching
-// nothing, when XM_M3_PATH=seq asks for the token-by-token kernel.
+// nothing, when the m3_path override asks for the token-by-token kernel.
 bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream);
 // Enqueues a kernel that writes `count` zeros (no memset node in a captured graph).
 void LaunchFillZeros(float *dst, size_t count, void *stream);

@@ -1,10 +1,15 @@
-// Library-wide runtime pieces: the default stream-ordered scratch pool and
-// the version string.
+// Library-wide runtime pieces: the default stream-ordered scratch pool, the
+// once-per-device kernel attributes, the kernel-selection overrides and the
+// version string.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <cstring>
+#include <map>
 #include <mutex>
 #include <unordered_map>
+#include <utility>
 
 #include "xm_common.h"
 #include "xm_hip.h"
@@ -59,12 +64,124 @@ __global__ __launch_bounds__(256) void FillZerosKernel(float *dst, size_t count)
 void LaunchFillZeros(float *dst, size_t count, void *stream) {
     if (count == 0) return;
     const size_t blocks = std::min<size_t>((count + 255) / 256, 4096);
+    XM_NOTE_LAUNCH("FillZerosKernel", {}, );
     hipLaunchKernelGGL(FillZerosKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), dst, count);
     XM_LAUNCH_CHECK("zero fill");
 }
 
+namespace {
+std::mutex g_attr_mu;
+std::map<std::pair<const void *, int>, int> g_dyn_lds;   // (kernel, device) -> dynamic LDS limit set
+}  // namespace
+
+void EnsureDynamicLds(const void *kernel, int bytes) {
+    int dev = 0;
+    XM_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_attr_mu);
+    int &set = g_dyn_lds[{kernel, dev}];
+    if (bytes <= set) return;
+    XM_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    set = bytes;
+}
+
+namespace {
+struct OverrideSpec {
+    const char *name;
+    int64_t allowed[6];   // accepted non-default values, 0-terminated
+};
+// Index order of the Override enum.
+constexpr OverrideSpec kOverrides[kOverrideCount] = {
+    {"gdn2_path", {1, 0}},               // 1: the sequential fused kernel
+    {"gdn2_pairwise", {1, 0}},           // 1: pairwise A and M in every chunk
+    {"gdn2_rows", {1, 2, 4, 0}},         // rows of 16 lanes per value column (sequential kernel)
+    {"m3_path", {1, 0}},                 // 1: the token-by-token kernel
+    {"ss_lpc", {1, 2, 4, 8, 16, 0}},     // lanes per channel (dstate <= 16)
+    {"ss_split", {1, 2, 0}},             // 1: one workgroup per channel block; 2: sequence-split
+};
+std::atomic<int64_t> g_override[kOverrideCount];
+
+int FindOverride(const char *name) {
+    if (name == nullptr) return -1;
+    for (int i = 0; i < kOverrideCount; ++i)
+        if (std::strcmp(name, kOverrides[i].name) == 0) return i;
+    return -1;
+}
+}  // namespace
+
+int64_t GetOverride(Override which) { return g_override[which].load(std::memory_order_relaxed); }
+
+namespace {
+struct LaunchLog {
+    const char *names[16];
+    int counts[16];
+    int n = 0;
+    std::string text;
+};
+thread_local LaunchLog t_launches;
+}  // namespace
+
+void ResetLaunches() { t_launches.n = 0; }
+
+void NoteLaunch(const char *name) {
+    LaunchLog &l = t_launches;
+    for (int i = 0; i < l.n; ++i)
+        if (l.names[i] == name) {
+            ++l.counts[i];
+            return;
+        }
+    if (l.n < 16) {
+        l.names[l.n] = name;
+        l.counts[l.n++] = 1;
+    }
+}
+
+std::string KernelName(const char *base, std::initializer_list<const char *> types, std::initializer_list<int> args) {
+    std::string s = base;
+    if (types.size() + args.size() == 0) return s;
+    s += '<';
+    bool first = true;
+    for (const char *t : types) {
+        s += first ? "" : ",";
+        s += t;
+        first = false;
+    }
+    for (int a : args) {
+        s += first ? "" : ",";
+        s += std::to_string(a);
+        first = false;
+    }
+    return s + '>';
+}
+
 }  // namespace xm
+
+extern "C" int xm_set_kernel_override(const char *name, int64_t value, char *errbuf, size_t errlen) {
+    return xm::Guard(errbuf, errlen, [&] {
+        const int i = xm::FindOverride(name);
+        if (i < 0) xm::Invalid(std::string("unknown kernel override ") + (name ? name : "(null)"));
+        bool ok = value == 0;
+        for (int64_t v : xm::kOverrides[i].allowed) ok = ok || (v != 0 && v == value);
+        if (!ok) xm::Invalid(std::string("value out of range for kernel override ") + name);
+        xm::g_override[i].store(value, std::memory_order_relaxed);
+    });
+}
+
+extern "C" int64_t xm_get_kernel_override(const char *name) {
+    const int i = xm::FindOverride(name);
+    return i < 0 ? -1 : xm::g_override[i].load(std::memory_order_relaxed);
+}
+
+extern "C" const char *xm_last_launches(void) {
+    xm::LaunchLog &l = xm::t_launches;
+    l.text.clear();
+    for (int i = 0; i < l.n; ++i) {
+        if (i) l.text += ';';
+        l.text += l.names[i];
+        if (l.counts[i] > 1) l.text += " x" + std::to_string(l.counts[i]);
+    }
+    return l.text.c_str();
+}
 
 extern "C" const char *xm_version(void) {
     return "xmetai-recurrent 0.1.0 (gfx950; SelectiveScanFn, Mamba3SisoFn, GatedDeltaNet2Fn)";

@@ -28,7 +28,7 @@ from ._capi import (XM_ERR_ALLOC, XM_ERR_DEVICE, XM_ERR_INVALID_ARGUMENT, XM_ERR
                     EXPORTED_SYMBOLS, LIB_PATH)
 
 __all__ = [
-    "XmError", "lib", "version", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn", "softmax_cpu",
+    "XmError", "lib", "version", "last_launches", "set_kernel_override", "get_kernel_override", "kernel_override", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn", "softmax_cpu",
     "validate", "TorchAllocator", "EXPORTED_SYMBOLS", "LIB_PATH",
     "XM_OK", "XM_ERR_INVALID_ARGUMENT", "XM_ERR_UNSUPPORTED", "XM_ERR_DEVICE", "XM_ERR_ALLOC",
 ]
@@ -63,6 +63,41 @@ def lib() -> ctypes.CDLL:
 
 def version() -> str:
     return lib().xm_version().decode()
+
+
+def last_launches() -> list:
+    """Kernels this thread's last operator call enqueued (names as rocprofv3
+    prints them, with " xN" for repeated launches)."""
+    s = lib().xm_last_launches().decode()
+    return s.split(";") if s else []
+
+
+def set_kernel_override(name: str, value: int) -> None:
+    """Forces a kernel variant process-wide (tests and tuning); 0 restores the
+    dispatcher's choice.  Names and values: ``_capi.KERNEL_OVERRIDES``."""
+    err = ctypes.create_string_buffer(256)
+    _check(lib().xm_set_kernel_override(name.encode(), int(value), err, len(err)), err)
+
+
+def get_kernel_override(name: str) -> int:
+    return int(lib().xm_get_kernel_override(name.encode()))
+
+
+class kernel_override:
+    """Context manager: ``with kernel_override("m3_path", 1): ...`` restores the
+    previous value on exit."""
+
+    def __init__(self, name: str, value: int):
+        self.name, self.value, self.prev = name, value, None
+
+    def __enter__(self):
+        self.prev = get_kernel_override(self.name)
+        set_kernel_override(self.name, self.value)
+        return self
+
+    def __exit__(self, *exc):
+        set_kernel_override(self.name, self.prev)
+        return False
 
 
 # ---------------------------------------------------------------------------

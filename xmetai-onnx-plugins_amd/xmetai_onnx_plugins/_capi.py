@@ -90,7 +90,13 @@ GDN2_INPUTS_PACKED = 8           # cu_seqlens at input 7
 # Every symbol include/xmetai_recurrent.h declares.
 EXPORTED_SYMBOLS = [
     f"xm_{op}_{fn}" for op in OPS for fn in ("attrs_default", "check_attrs", "validate", "forward")
-] + [f"xm_{op}_forward_states" for op in STATE_OUTPUTS] + ["xm_softmax_cpu", "xm_version"]
+] + [f"xm_{op}_forward_states" for op in STATE_OUTPUTS] + ["xm_softmax_cpu", "xm_set_kernel_override",
+                                                              "xm_get_kernel_override", "xm_last_launches",
+                                                              "xm_version"]
+
+# Kernel-selection overrides (xm_set_kernel_override) and the values each accepts besides 0.
+KERNEL_OVERRIDES = {"gdn2_path": (1,), "gdn2_pairwise": (1,), "gdn2_rows": (1, 2, 4), "m3_path": (1,),
+                    "ss_lpc": (1, 2, 4, 8, 16), "ss_split": (1, 2)}
 
 
 def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
@@ -120,6 +126,12 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.xm_softmax_cpu.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
     lib.xm_softmax_cpu.restype = ctypes.c_int
+    lib.xm_set_kernel_override.argtypes = [ctypes.c_char_p, ctypes.c_int64, ctypes.c_char_p, ctypes.c_size_t]
+    lib.xm_set_kernel_override.restype = ctypes.c_int
+    lib.xm_get_kernel_override.argtypes = [ctypes.c_char_p]
+    lib.xm_get_kernel_override.restype = ctypes.c_int64
+    lib.xm_last_launches.argtypes = []
+    lib.xm_last_launches.restype = ctypes.c_char_p
     lib.xm_version.argtypes = []
     lib.xm_version.restype = ctypes.c_char_p
     return lib
