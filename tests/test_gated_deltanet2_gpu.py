@@ -70,6 +70,12 @@ CASES = {
     "t2100_k320_window_carry": S(1, 2100, 1, 320, 16),
     "t2060_k512_window_carry_perkey": S(1, 2060, 1, 512, 8, per_key_gates=True),
     "t1500_lds_carry": S(1, 1500, 1, 600, 16),
+    # above 2048 keys the state tile lives in scratch (any head_k, as the
+    # reference's generic kernel): 1100 tokens cross one preparation-chunk carry
+    "k2049_v20_tile_store": S(1, 40, 2, 2049, 20),
+    "k4096_v64_t1100_carry": S(1, 1100, 1, 4096, 64),
+    "k4096_v64_t1100_carry_nos0": S(1, 1100, 1, 4096, 64, initial_state=False),
+    "k3000_v33_perkey": S(2, 30, 1, 3000, 33, per_key_gates=True),
 }
 
 

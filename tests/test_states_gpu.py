@@ -128,6 +128,8 @@ GDN_CASES = {
     "k1024_lds_path_perkey": S(1, 12, 1, 1024, 7, per_key_gates=True),
     "t4100_three_windows": S(1, 4100, 2, 64, 24),
     "k448_t2100_window_carry": S(1, 2100, 1, 448, 12, per_key_gates=True),
+    "k2100_tile_store": S(1, 30, 2, 2100, 20),
+    "k4096_t1100_tile_store_carry": S(1, 1100, 1, 4096, 16),
 }
 
 

@@ -29,7 +29,16 @@
 //    khat, beta*khat*d, qhat*d, d and qhat.khat for a chunk of <= 1024 tokens
 //    to scratch; the recurrence keeps the [dk_pad x 16 columns] state tile in
 //    LDS and carries the fp32 state across chunks through scratch
-//    (reference :101-102, :133-139).
+//    (reference :101-102, :133-139).  Above 2048 keys the tile (128 KiB at
+//    2048) no longer fits in LDS: the same recurrence then keeps it in a
+//    scratch region of its own (Gdn2RecurLdsKernel<true>), in the tile's
+//    lane order, so a wave's state accesses stay 256-byte contiguous; the
+//    region also carries the state across chunks.  Its preparation loops over
+//    the keys (Gdn2PrepLoopKernel).  This is the reference's generic kernel's
+//    arrangement (state in global memory, gated_deltanet2_fwd.cu:142-233),
+//    with no key limit.
+//  * The tokens per preparation chunk (<= 1024) follow from the scratch bytes
+//    available: a caller with a fixed scratch budget gets shorter chunks.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -45,7 +54,7 @@ constexpr int kThreads = 256;
 constexpr int kChunkTokens = 1024;   // reference kGatedDeltaNet2PrepareTokens (gated_deltanet2.h:11)
 constexpr int kFusedKeyLimit = 512;  // register-state kernel: up to 4 rows x 16 lanes x 8 keys per column
                                      // (the reference's register path stops at 256, gated_deltanet2.h:10)
-constexpr int kMaxLdsKeys = 2048;    // LDS-state path: dk_pad * 16 columns * 4 B <= 128 KiB
+constexpr int kMaxLdsKeys = 2048;    // LDS-state tile: dk_pad * 16 columns * 4 B <= 128 KiB; above, scratch
 constexpr float kL2Eps = 1.0e-6f;    // reference kL2NormEps (gated_deltanet2_fwd.cu:14)
 
 // Prepared row of one (b,h,t): [khat | beta*khat*d | qhat*d | d], kp floats
@@ -100,6 +109,50 @@ __global__ __launch_bounds__(kThreads) void Gdn2PrepKernel(GatedDeltaNet2Params 
             dst[3 * kp + kd] = d;
             qk = fmaf(qn, kn, qk);
         }
+    }
+    qk = WaveSum64(qk);
+    if (lane == 0) p.prep_qk[static_cast<size_t>(bh) * p.chunk_cap + tl] = qk;
+}
+
+// The same preparation for any dk (dk_pad > 2048): one wave per row, the sums
+// of squares in a first pass over the keys and the four vectors in a second
+// (the row is re-read from cache).
+__global__ __launch_bounds__(kThreads) void Gdn2PrepLoopKernel(GatedDeltaNet2Params p, int t0, int tc) {
+    const int lane = threadIdx.x & 63;
+    const long long row = static_cast<long long>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    const long long rows = static_cast<long long>(p.batch) * p.nheads * tc;
+    if (row >= rows) return;  // uniform per wave
+    const int tl = static_cast<int>(row % tc);
+    const int bh = static_cast<int>(row / tc);
+    const int b = bh / p.nheads, h = bh % p.nheads;
+    const int t = t0 + tl;
+    const int dk = p.dk, kp = p.dk_pad;
+    const size_t src = ((static_cast<size_t>(b) * p.seqlen + t) * p.nheads + h) * static_cast<size_t>(dk);
+    float qs = 0.0f, ks = 0.0f;
+    for (int kd = lane; kd < dk; kd += 64) {
+        const float q = p.q[src + kd], k = p.k[src + kd];
+        qs = fmaf(q, q, qs);
+        ks = fmaf(k, k, ks);
+    }
+    float q_mul = p.scale, k_mul = 1.0f;
+    if (p.l2norm) {
+        // reference :58-62: q_mul = scale * rsqrt(sum + eps); k_mul = rsqrt(sum + eps)
+        q_mul *= rsqrtf(WaveSum64(qs) + kL2Eps);
+        k_mul = rsqrtf(WaveSum64(ks) + kL2Eps);
+    }
+    float *dst = p.prepared + (static_cast<size_t>(bh) * p.chunk_cap + tl) * static_cast<size_t>(PrepRow(kp));
+    float qk = 0.0f;
+    for (int kd = lane; kd < kp; kd += 64) {
+        const bool ok = kd < dk;
+        const float kn = ok ? p.k[src + kd] * k_mul : 0.0f;           // khat
+        const float qn = ok ? p.q[src + kd] * q_mul : 0.0f;           // qhat
+        const float d = ok ? expf(p.g[src + kd]) : 0.0f;              // exp(g)
+        const float bk = ok ? p.beta[src + kd] * kn : 0.0f;           // beta * khat
+        dst[kd] = kn;
+        dst[kp + kd] = bk * d;
+        dst[2 * kp + kd] = qn * d;
+        dst[3 * kp + kd] = d;
+        qk = fmaf(qn, kn, qk);
     }
     qk = WaveSum64(qk);
     if (lane == 0) p.prep_qk[static_cast<size_t>(bh) * p.chunk_cap + tl] = qk;
@@ -385,10 +438,14 @@ __global__ __launch_bounds__(64 * NW) void Gdn2FusedKernel(GatedDeltaNet2Params 
 // ---------------------------------------------------------------------------
 // LDS-state recurrence (dk > 512)
 // ---------------------------------------------------------------------------
+// GLOBAL: the tile lives in a scratch region of its own (p.state, one
+// [dk_pad x 16] tile per (b,h, column block) in the same lane order), which
+// also carries it from one token chunk to the next.
+template <bool GLOBAL>
 __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Params p, int t0, int tc) {
     // State tile: key kd = kg*kt + j of column cl lives at (j*16 + cl)*16 + kg, so
     // the 16 lanes of a row touch 16 consecutive floats (no bank conflicts).
-    extern __shared__ __attribute__((aligned(16))) float sS[];
+    extern __shared__ __attribute__((aligned(16))) float sLds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int kg = lane & 15, cg = lane >> 4;
@@ -403,14 +460,18 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
     const int col = vb * 16 + cl;
     const bool col_ok = col < dv;
     const int row = PrepRow(kp);
+    float *const sS = GLOBAL ? p.state + static_cast<size_t>(bh * nvb + vb) * kp * 16 : sLds;
 
     const float *sinit = nullptr;
-    if (t0 > 0) sinit = p.state;
+    if (t0 > 0) sinit = GLOBAL ? nullptr : p.state;   // GLOBAL: the tile already holds the carry
     else if (p.initial_state) sinit = p.initial_state;
     const size_t sbase = static_cast<size_t>(bh) * dk * dv;
-    for (int j = 0; j < kt; ++j) {
-        const int kd = kg * kt + j;
-        sS[(j * 16 + cl) * 16 + kg] = (sinit && kd < dk && col_ok) ? sinit[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
+    if (!GLOBAL || t0 == 0) {
+        for (int j = 0; j < kt; ++j) {
+            const int kd = kg * kt + j;
+            sS[(j * 16 + cl) * 16 + kg] =
+                (sinit && kd < dk && col_ok) ? sinit[sbase + static_cast<size_t>(kd) * dv + col] : 0.0f;
+        }
     }
     // Each lane touches only its own (key, column) cells: no barrier needed.
 
@@ -449,7 +510,8 @@ __global__ __launch_bounds__(kThreads) void Gdn2RecurLdsKernel(GatedDeltaNet2Par
         if (kg == 0 && col_ok) p.out[vidx] = o;
     }
     // carry to the next chunk, or the final state after the last one
-    float *dst = t0 + tc < p.seqlen ? p.state : p.final_state;
+    // (GLOBAL: the tile is the carry; only the final state is copied out)
+    float *dst = t0 + tc < p.seqlen ? (GLOBAL ? nullptr : p.state) : p.final_state;
     if (dst != nullptr) {
         for (int j = 0; j < kt; ++j) {
             const int kd = kg * kt + j;
@@ -549,28 +611,70 @@ void Prep(const GatedDeltaNet2Params &p, int t0, int tc, hipStream_t stream) {
     if (kpl <= 4) LaunchPrep<4>(p, t0, tc, stream);
     else if (kpl <= 8) LaunchPrep<8>(p, t0, tc, stream);
     else if (kpl <= 16) LaunchPrep<16>(p, t0, tc, stream);
-    else LaunchPrep<32>(p, t0, tc, stream);
+    else if (kpl <= 32) LaunchPrep<32>(p, t0, tc, stream);
+    else {
+        const long long blocks = (static_cast<long long>(p.batch) * p.nheads * tc + 3) / 4;
+        XM_NOTE_LAUNCH("Gdn2PrepLoopKernel", {}, );
+        hipLaunchKernelGGL(Gdn2PrepLoopKernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, p, t0,
+                           tc);
+    }
+}
+
+// Scratch of the dk > 512 path for a budget of `cap` bytes: tokens per
+// preparation chunk (at most 1024, fewer when the budget is smaller) and the
+// regions, each 256-byte aligned: prepared vectors | qhat.khat per row | state.
+// The state region is the carry between chunks ([B,H,dk,dv], only when the
+// sequence spans several chunks), or above 2048 keys the recurrence's own tile
+// store ([B*H*column blocks][dk_pad x 16]).
+struct LdsPlan {
+    int chunk_cap = 0;     // 0: the budget cannot hold one token
+    bool global_state = false;
+    size_t prep = 0, qk = 0, state = 0;
+    size_t total() const { return prep + qk + state; }
+};
+
+LdsPlan PlanLds(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
+    LdsPlan l;
+    const size_t bh = static_cast<size_t>(batch) * nheads;
+    const size_t kp = static_cast<size_t>(PadKeysLds(dk));
+    l.global_state = kp > static_cast<size_t>(kMaxLdsKeys);
+    const size_t tile_store = Align256(bh * ((dv + 15) / 16) * kp * 16 * sizeof(float));
+    const size_t carry = Align256(bh * dk * dv * sizeof(float));
+    const size_t per_token = bh * (PrepRow(static_cast<int>(kp)) + 1) * sizeof(float);
+    auto fill = [&](int c) {
+        l.chunk_cap = c;
+        l.prep = Align256(bh * c * PrepRow(static_cast<int>(kp)) * sizeof(float));
+        l.qk = Align256(bh * c * sizeof(float));
+        l.state = l.global_state ? tile_store : (c < seqlen ? carry : 0);
+    };
+    fill(std::min(seqlen, kChunkTokens));
+    if (l.total() <= cap) return l;
+    // a shorter chunk: the state region is then always needed
+    const size_t state = l.global_state ? tile_store : carry;
+    const size_t room = cap > state + 512 ? cap - state - 512 : 0;   // 512: the two alignment pads
+    const int c = static_cast<int>(std::min<size_t>(room / per_token, static_cast<size_t>(kChunkTokens)));
+    if (c < 1) {
+        l.chunk_cap = 0;
+        return l;
+    }
+    fill(c);
+    return l;
 }
 
 }  // namespace
 
-size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed) {
-    if (dk <= kGdn2ChunkKeyLimit && !packed) return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv);   // chunked path
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
+    if (dk <= kGdn2ChunkKeyLimit && !packed)   // chunked path
+        return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv, cap);
     if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch (packed sequences always take it)
-    const size_t cap = static_cast<size_t>(std::min(seqlen, kChunkTokens));
-    const size_t rows = static_cast<size_t>(batch) * nheads * cap;
-    const size_t state = seqlen > kChunkTokens ? static_cast<size_t>(batch) * nheads * dk * dv : 0;
-    // regions: prepared vectors | qhat.khat per row | carried state, each 256-byte aligned
-    return Align256(rows * PrepRow(PadKeysLds(dk)) * sizeof(float)) + Align256(rows * sizeof(float)) +
-           state * sizeof(float);
+    const LdsPlan l = PlanLds(batch, seqlen, nheads, dk, dv, cap);
+    return l.chunk_cap == 0 ? SIZE_MAX : l.total();
 }
 
-void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v) {
+void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_bytes, void *stream_v) {
     // dk <= 512: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
-    if (p.cu_seqlens == nullptr && LaunchGatedDeltaNet2Chunked(p, scratch, stream_v)) return;
+    if (p.cu_seqlens == nullptr && LaunchGatedDeltaNet2Chunked(p, scratch, scratch_bytes, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
-    if (p.dk > kMaxLdsKeys)
-        throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn supports headdim_k up to 2048");
     if (p.cu_seqlens != nullptr && p.dk > kFusedKeyLimit)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn with cu_seqlens supports headdim_k up to 512");
     if (p.dk <= kFusedKeyLimit) {
@@ -580,28 +684,36 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream_v)
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn");
         return;
     }
-    // dk > 512: preparation in token chunks, state in LDS, carried through scratch
+    // dk > 512: preparation in token chunks, state in LDS (or above 2048 keys in
+    // a scratch region of its own), carried through scratch
+    const LdsPlan l = PlanLds(p.batch, p.seqlen, p.nheads, p.dk, p.dv, scratch_bytes);
+    if (l.chunk_cap == 0 || l.total() > scratch_bytes || (l.total() > 0 && scratch == nullptr))
+        throw Error(XM_ERR_ALLOC, "GatedDeltaNet2Fn: the scratch buffer is smaller than the call needs");
     p.dk_pad = PadKeysLds(p.dk);
-    p.chunk_cap = std::min(p.seqlen, kChunkTokens);
-    const size_t rows = static_cast<size_t>(p.batch) * p.nheads * p.chunk_cap;
+    p.chunk_cap = l.chunk_cap;
     char *base = static_cast<char *>(scratch);
     p.prepared = reinterpret_cast<float *>(base);
-    base += Align256(rows * PrepRow(p.dk_pad) * sizeof(float));
-    p.prep_qk = reinterpret_cast<float *>(base);
-    base += Align256(rows * sizeof(float));
-    p.state = p.seqlen > kChunkTokens ? reinterpret_cast<float *>(base) : nullptr;
+    p.prep_qk = reinterpret_cast<float *>(base + l.prep);
+    p.state = l.state > 0 ? reinterpret_cast<float *>(base + l.prep + l.qk) : nullptr;
     const long long bh = static_cast<long long>(p.batch) * p.nheads;
-    if (bh * ((p.dv + 15) / 16) > 2147483647LL || bh * kChunkTokens / 4 > 2147483647LL)
+    if (bh * ((p.dv + 15) / 16) > 2147483647LL || (bh * p.chunk_cap + 3) / 4 > 2147483647LL)
         throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-    const size_t lds = static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
-    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel), static_cast<int>(lds));
+    const size_t lds = l.global_state ? 0 : static_cast<size_t>(p.dk_pad) * 16 * sizeof(float);
+    if (!l.global_state) EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2RecurLdsKernel<false>), static_cast<int>(lds));
     for (int t0 = 0; t0 < p.seqlen; t0 += p.chunk_cap) {
         const int tc = std::min(p.chunk_cap, p.seqlen - t0);
         Prep(p, t0, tc, stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn preparation");
         const long long blocks = bh * ((p.dv + 15) / 16);
-        XM_NOTE_LAUNCH("Gdn2RecurLdsKernel", {}, );
-        hipLaunchKernelGGL(Gdn2RecurLdsKernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, p, t0, tc);
+        if (l.global_state) {
+            XM_NOTE_LAUNCH("Gdn2RecurLdsKernel", {}, 1);
+            hipLaunchKernelGGL(Gdn2RecurLdsKernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream,
+                               p, t0, tc);
+        } else {
+            XM_NOTE_LAUNCH("Gdn2RecurLdsKernel", {}, 0);
+            hipLaunchKernelGGL(Gdn2RecurLdsKernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds,
+                               stream, p, t0, tc);
+        }
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn recurrence");
     }
 }

@@ -581,21 +581,43 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }
 
-}  // namespace
+// Scratch of one call for a budget of `cap` bytes: the chunks per window (at
+// most 128, fewer when the budget is smaller; 0 when one chunk does not fit)
+// and the bytes of the prepared blocks and of the state carried between
+// windows (only when the sequence spans several windows).
+struct WindowPlan {
+    int win = 0;
+    size_t blocks = 0, carry = 0;
+    size_t total() const { return blocks + carry; }
+};
 
-size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv) {
-    if (dk > kGdn2ChunkKeyLimit) return 0;
+WindowPlan PlanWindows(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
     const ChunkConfig c = ChooseChunk(dk);
-    const int kq = c.kpw * c.ks;
+    const size_t per_chunk = static_cast<size_t>(batch) * nheads * BlockFloats(c.kpw * c.ks) * sizeof(float);
     const int nchunks = (seqlen + kC - 1) / kC;
-    const int win = std::min(nchunks, kWindowChunks);
-    const size_t heads = static_cast<size_t>(batch) * nheads;
-    size_t bytes = Align256(heads * win * BlockFloats(kq) * sizeof(float));
-    if (nchunks > kWindowChunks) bytes += Align256(heads * dk * dv * sizeof(float));
-    return bytes;
+    WindowPlan w;
+    w.win = std::min(nchunks, kWindowChunks);
+    w.blocks = Align256(per_chunk * w.win);
+    w.carry = w.win < nchunks ? Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float)) : 0;
+    if (w.total() <= cap) return w;
+    // shorter windows: the carry is then always needed
+    w.carry = Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float));
+    const size_t room = cap > w.carry + 256 ? cap - w.carry - 256 : 0;   // 256: the alignment pad
+    w.win = static_cast<int>(std::min<size_t>(room / per_chunk, static_cast<size_t>(w.win)));
+    w.blocks = Align256(per_chunk * w.win);
+    if (w.win < 1) w = WindowPlan{};
+    return w;
 }
 
-bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream_v) {
+}  // namespace
+
+size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
+    if (dk > kGdn2ChunkKeyLimit) return 0;
+    const WindowPlan w = PlanWindows(batch, seqlen, nheads, dk, dv, cap);
+    return w.win == 0 ? SIZE_MAX : w.total();
+}
+
+bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, size_t scratch_bytes, void *stream_v) {
     if (GetOverride(kOverrideGdn2Path) == 1) return false;
     if (p.cu_seqlens != nullptr) return false;   // packed sequences: the fused kernel
     if (p.dk > kGdn2ChunkKeyLimit) return false;
@@ -609,12 +631,14 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, v
     const ChunkConfig c = ChooseChunk(p.dk);
     const int kq = c.kpw * c.ks;
     const int nchunks = (p.seqlen + kC - 1) / kC;
-    const int win = std::min(nchunks, kWindowChunks);
+    const WindowPlan plan = PlanWindows(p.batch, p.seqlen, p.nheads, p.dk, p.dv, scratch_bytes);
+    if (plan.win == 0 || plan.total() > scratch_bytes || scratch == nullptr)
+        throw Error(XM_ERR_ALLOC, "GatedDeltaNet2Fn: the scratch buffer is smaller than the call needs");
+    const int win = plan.win;
     const size_t heads = static_cast<size_t>(p.batch) * p.nheads;
     char *base = static_cast<char *>(scratch);
     q.prepared = reinterpret_cast<float *>(base);
-    base += Align256(heads * win * BlockFloats(kq) * sizeof(float));
-    float *const carry = nchunks > kWindowChunks ? reinterpret_cast<float *>(base) : nullptr;
+    float *const carry = plan.carry > 0 ? reinterpret_cast<float *>(base + plan.blocks) : nullptr;
     for (int c0 = 0; c0 < nchunks; c0 += win) {
         const int wn = std::min(win, nchunks - c0);
         const bool first = c0 == 0, last = c0 + wn >= nchunks;

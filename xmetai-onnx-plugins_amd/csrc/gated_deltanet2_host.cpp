@@ -3,10 +3,13 @@
 // (constructor checks in the same order, ValidateInputs and its messages,
 // ToIntDim, output shape = v.shape).
 //
-// Scratch (requested from the caller's allocator, reference :86-111): none for
-// headdim_k <= 512 (one fused kernel); above that, the prepared per-token
-// vectors of one <=1024-token chunk and the fp32 state carried between chunks
-// when seqlen > 1024.
+// Scratch (requested from the caller's allocator, reference :86-111): for
+// headdim_k <= 512 the chunked path's prepared blocks of one window of up to
+// 128 16-token chunks plus the state carried between windows (packed
+// sequences and the sequential kernel take none); above 512 keys the prepared
+// per-token vectors of one <=1024-token chunk, the state carried between
+// chunks, and above 2048 keys the recurrence's state tiles.  Any headdim_k is
+// accepted, as in the reference's generic kernel (gated_deltanet2_fwd.cu:142-233).
 //
 // Widening: output_final_state = 1, which the reference rejects (:49-51), is
 // accepted through xm_gated_deltanet2_forward_states, which also writes the
@@ -74,7 +77,6 @@ Plan Validate(const std::vector<View> &in, const IndexView *cu, const xm_gated_d
     p.nheads = ToIntDim(q.shape[2], "nheads");
     p.dk = ToIntDim(q.shape[3], "headdim_k");
     p.dv = ToIntDim(v.shape[3], "headdim_v");
-    if (p.dk > 2048) Unsupported("GatedDeltaNet2Fn supports headdim_k up to 2048");
     if (cu != nullptr && p.dk > 512) Unsupported("GatedDeltaNet2Fn with cu_seqlens supports headdim_k up to 512");
     p.cu_seqlens = cu != nullptr ? cu->data : nullptr;
     p.q = q.data;
@@ -101,6 +103,17 @@ Plan Prepare(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet
 
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t &attrs, float *out,
              float *final_state, void *stream, const xm_allocator_t *alloc) {
+    const GatedDeltaNet2Params p = GatedDeltaNet2Plan(inputs, n_inputs, attrs, out, final_state);
+    const size_t bytes = GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv, p.cu_seqlens != nullptr);
+    Scratch scratch(alloc, stream);
+    void *buf = scratch.Get(bytes);
+    LaunchGatedDeltaNet2(p, buf, bytes, stream);
+}
+
+}  // namespace
+
+GatedDeltaNet2Params GatedDeltaNet2Plan(const xm_tensor_t *inputs, size_t n_inputs,
+                                        const xm_gated_deltanet2_attrs_t &attrs, float *out, float *final_state) {
     ResetLaunches();
     CheckAttrs(attrs);
     Plan plan = Prepare(inputs, n_inputs, attrs);
@@ -109,12 +122,9 @@ void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet
     if (want_state && final_state == nullptr) Invalid("output_final_state=1 needs a final_state buffer");
     plan.params.out = out;
     plan.params.final_state = want_state ? final_state : nullptr;
-    Scratch scratch(alloc, stream);
-    void *buf = scratch.Get(plan.scratch);
-    LaunchGatedDeltaNet2(plan.params, buf, stream);
+    return plan.params;
 }
 
-}  // namespace
 }  // namespace xm
 
 extern "C" {

@@ -7,6 +7,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "xmetai_recurrent.h"
+
 namespace xm {
 
 // SelectiveScanFn (reference parameter block: selective_scan.h:26-69).
@@ -77,15 +79,26 @@ struct Mamba3SisoParams {
 // Launchers (defined in the .hip translation units).  They enqueue on
 // `stream` and throw xm::Error on a launch failure.
 void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
-size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed);
-void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, void *stream);
+// GatedDeltaNet2Fn host validation (gated_deltanet2_host.cpp): the attribute
+// and shape checks of the reference, and the launch parameters of the call.
+GatedDeltaNet2Params GatedDeltaNet2Plan(const xm_tensor_t *inputs, size_t n_inputs,
+                                        const xm_gated_deltanet2_attrs_t &attrs, float *out, float *final_state);
+// Scratch bytes of one call when at most `cap` bytes are available: the
+// chunked windows and the token chunks of the dk > 512 path shrink to fit.
+// 0 when the call needs none; SIZE_MAX when not even the smallest layout fits.
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed,
+                                  size_t cap = SIZE_MAX);
+// `scratch` holds `scratch_bytes` bytes; the layout is the one
+// GatedDeltaNet2ScratchBytes chose for cap = scratch_bytes.
+void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_bytes, void *stream);
 // Chunked fp32-MFMA path (dk <= kGdn2ChunkKeyLimit).  Returns false, launching nothing, when
 // the shape is not one it takes (or the gdn2_path override asks for the sequential kernel).  `scratch` holds
-// GatedDeltaNet2ChunkScratchBytes bytes: the prepared chunk vectors of one
-// window of up to 2048 tokens, and the state carried between windows.
-size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv);
+// scratch_bytes >= GatedDeltaNet2ChunkScratchBytes(..., scratch_bytes) bytes: the
+// prepared chunk vectors of one window of up to 2048 tokens (shorter windows
+// when the bytes are fewer), and the state carried between windows.
+size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, size_t cap = SIZE_MAX);
 constexpr int kGdn2ChunkKeyLimit = 512;   // head_k handled by the chunked path (packed sequences excepted)
-bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, void *stream);
+bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, size_t scratch_bytes, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
 // Chunked fp32-MFMA path (headdim_qk <= 256).  Returns false, launching
 // nothing, when the m3_path override asks for the token-by-token kernel.
