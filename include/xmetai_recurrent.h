@@ -224,6 +224,21 @@ int xm_gated_deltanet2_forward_states(const xm_tensor_t *inputs, size_t n_inputs
                                       float *final_state, void *stream, const xm_allocator_t *alloc,
                                       char *errbuf, size_t errlen);
 
+/* xm_gated_deltanet2_forward with no allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * scratch comes from a fixed 64 MiB array in device memory that each GPU the
+ * library runs on holds until the process ends; the chunked path's windows
+ * and the preparation chunks of head_k > 512 shrink to fit it, and a call that
+ * cannot fit (e.g. a carried state of 64 MiB or more) fails with
+ * XM_ERR_UNSUPPORTED before anything is enqueued.  It calls no hipMalloc or
+ * hipFree.  Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU (concurrent streams) race and must be serialised by the caller.
+ * Results equal xm_gated_deltanet2_forward's.  output_final_state must be 0. */
+int xm_gated_deltanet2_forward_noalloc(const xm_tensor_t *inputs, size_t n_inputs,
+                                       const xm_gated_deltanet2_attrs_t *attrs, float *out, void *stream,
+                                       char *errbuf, size_t errlen);
+
 /* ---- SoftmaxCPU (CPU execution provider) ------------------------------------
  * Softmax of a HOST fp32 tensor of any rank along `axis` (ONNX attribute
  * "axis", int, default -1; negative values count from the last dimension).

@@ -51,6 +51,7 @@ SOURCES = [
     "selective_scan.hip",
     "gated_deltanet2.hip",
     "gated_deltanet2_chunk.hip",
+    "gated_deltanet2_noalloc.hip",
     "mamba3_siso.hip",
     "mamba3_siso_chunk.hip",
     "selective_scan_host.cpp",

@@ -90,7 +90,7 @@ GDN2_INPUTS_PACKED = 8           # cu_seqlens at input 7
 # Every symbol include/xmetai_recurrent.h declares.
 EXPORTED_SYMBOLS = [
     f"xm_{op}_{fn}" for op in OPS for fn in ("attrs_default", "check_attrs", "validate", "forward")
-] + [f"xm_{op}_forward_states" for op in STATE_OUTPUTS] + ["xm_softmax_cpu", "xm_set_kernel_override",
+] + [f"xm_{op}_forward_states" for op in STATE_OUTPUTS] + ["xm_gated_deltanet2_forward_noalloc", "xm_softmax_cpu", "xm_set_kernel_override",
                                                               "xm_get_kernel_override", "xm_last_launches",
                                                               "xm_version"]
 
@@ -123,6 +123,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
             f.argtypes = [T, ctypes.c_size_t, A, ctypes.c_void_p] + [ctypes.c_void_p] * nstate + [
                 ctypes.c_void_p, ctypes.POINTER(XmAllocator), ctypes.c_char_p, ctypes.c_size_t]
             f.restype = ctypes.c_int
+    f = lib.xm_gated_deltanet2_forward_noalloc
+    f.argtypes = [T, ctypes.c_size_t, ctypes.POINTER(GatedDeltaNet2Attrs), ctypes.c_void_p, ctypes.c_void_p,
+                  ctypes.c_char_p, ctypes.c_size_t]
+    f.restype = ctypes.c_int
     lib.xm_softmax_cpu.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
     lib.xm_softmax_cpu.restype = ctypes.c_int
