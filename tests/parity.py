@@ -4,34 +4,37 @@ Error measures (reported per case, gated by the tolerances below), with
 ``ref`` the fp64 oracle evaluated on the same fp32 inputs:
 
     max_abs  = max |gpu - ref|
-    norm_err = max |gpu - ref| / max(1, max |ref|)                  (whole tensor)
-    row_err  = max over rows r of max_r |gpu - ref| / max(1, max_r |ref|)
+    norm_err = max |gpu - ref| / max |ref|                              (whole tensor)
+    row_err  = max over rows r of max_r |gpu - ref| / max(max_r |ref|, 1e-3 max |ref|)
 
-A row is a line along the last axis (the value columns of one token and head,
-or the tokens of one selective-scan channel).  ``row_err`` is the per-element
-gate |gpu - ref| <= tol_row * max(1, max |ref| of that row): an output whose
-magnitude grows along the sequence (GatedDeltaNet2Fn without the L2 norm)
-cannot hide an error in its small early rows behind the large late ones.
+Both are relative to the output's own scale (GDN-2 outputs are ~1e-3, so an
+absolute bound would be loose).  A row is a line along the last axis (the
+value columns of one token and head, or the tokens of one selective-scan
+channel).  ``row_err`` is the per-element gate
+|gpu - ref| <= tol_row * max(max |ref| of the row, 1e-3 max |ref|): an output
+whose magnitude grows along the sequence (GatedDeltaNet2Fn without the L2
+norm) cannot hide an error in its small early rows behind the large late ones.
 When the environment variable XM_PARITY_REPORT names a file, every check
 appends one JSON line with these figures and the kernel overrides in force.
 
-Gates (measured worst on MI355X over the whole GPU suite, per operator and
-kernel path, times about 10):
+Gates (measured worst on MI355X over the whole GPU suite, every kernel path,
+times about 10):
 
     op        worst norm_err   worst row_err   gate norm / row
-    SS        2.5e-7           5.7e-7          3e-6 / 6e-6
-    Mamba-3   3.0e-7           5.0e-7          3e-6 / 5e-6
-    GDN-2     3.7e-7           3.7e-7          4e-6 / 4e-6
+    SS        2.5e-7           1.3e-6          3e-6 / 2e-5
+    Mamba-3   5.8e-7           4.2e-6          6e-6 / 4e-5
+    GDN-2     7.8e-7           1.1e-5          8e-6 / 1.2e-4
     GPU vs GPU (chained calls, packed vs plain, chunked vs token-by-token):
-              2.0e-7           2.6e-7          2e-6 / 2e-6
+              5.0e-7           5.5e-6          5e-6 / 6e-5
 
 Ill-conditioned cases (an exploding GDN-2 state without the L2 norm, growing
-decays, thousands of large angle steps) lose accuracy in any fp32 evaluation
-order.  For them the test also runs the oracle in fp32 with the reference's
-operation order and the gate becomes max(gate, 8 x that fp32 error): the
-device must be as accurate as the reference's own fp32 recurrence.  Measured:
-GDN-2 without L2 norm row_err 7.0e-5 against 9.0e-5 for the fp32 order;
-Mamba-3 growth 6.5e-6 against 5.9e-6; long angle runs 3.7e-6 against 6.3e-6.
+or hard-reset decays, thousands of large angle steps) lose accuracy in any
+fp32 evaluation order.  For them the test also runs the oracle in fp32 with
+the reference's operation order and each bound becomes max(gate, 8 x that
+fp32 error): the device must be about as accurate as the reference's own
+fp32 recurrence.  Measured (device / fp32 order, row_err): GDN-2 without L2
+norm 3.4e-6 / 1.7e-6; Mamba-3 growth 6.5e-6 / 4.4e-6; long angle runs
+3.7e-6 / 6.3e-6; GDN-2 hard reset (-200) 3.0e-5 / 1.3e-6, within the base gate.
 """
 
 import json
@@ -47,10 +50,10 @@ class Gate(NamedTuple):
 
 
 # fp32 device path vs the fp64 oracle, per operator
-TOL_SS = Gate(3e-6, 6e-6)
-TOL_M3 = Gate(3e-6, 5e-6)
-TOL_GDN2 = Gate(4e-6, 4e-6)
-TOL_GPU = Gate(2e-6, 2e-6)   # one device path against another
+TOL_SS = Gate(3e-6, 2e-5)
+TOL_M3 = Gate(6e-6, 4e-5)
+TOL_GDN2 = Gate(8e-6, 1.2e-4)
+TOL_GPU = Gate(5e-6, 6e-5)   # one device path against another
 FP32_FACTOR = 8.0            # ill-conditioned cases: multiple of the fp32-order oracle's error
 
 
@@ -72,11 +75,14 @@ def errors(got, ref):
     d = np.abs(got - ref)
     max_abs = float(d.max())
     ref_inf = float(np.abs(ref).max())
-    rows = max(1, ref.shape[-1]) if ref.ndim else 1
+    scale = ref_inf if ref_inf > 0 else 1.0
+    # a last axis of length 1 (a one-state SS state, a one-token output) makes
+    # every element its own row: the tensor is then one row
+    rows = ref.shape[-1] if ref.ndim and ref.shape[-1] > 1 else ref.size
     d2 = d.reshape(-1, rows)
     r2 = np.abs(ref).reshape(-1, rows)
-    row_err = float((d2.max(axis=1) / np.maximum(1.0, r2.max(axis=1))).max())
-    return max_abs, max_abs / max(1.0, ref_inf), ref_inf, row_err
+    row_err = float((d2.max(axis=1) / np.maximum(1e-3 * scale, r2.max(axis=1))).max())
+    return max_abs, max_abs / scale, ref_inf, row_err
 
 
 def _overrides():
