@@ -42,6 +42,11 @@ CASES = {
     "n130_padded": M(1, 25, 2, 20, 130),
     "n192": M(1, 19, 2, 16, 192),
     "n256": M(1, 21, 2, 24, 256),
+    # above 256 keys the token-by-token kernel runs on either setting (24 and
+    # 32 keys per lane, each token's q / k read from LDS)
+    "n384_p64_z": M(1, 40, 2, 64, 384, has_z=True),
+    "n512_p64_z": M(2, 37, 2, 64, 512, has_z=True),
+    "n512_a50_t70": M(1, 70, 1, 40, 512, angles=50),
     "p65_rowblocks": M(2, 35, 2, 65, 32),
     "t100_hq2": M(2, 100, 4, 16, 32, nheads_qk=2),
 }

@@ -73,7 +73,7 @@ struct M3Layout {
     // gfx950 serves ds_read_b128 16 lanes at a time from 64 banks: for 8 and
     // 16 keys per lane, 16 bytes of padding per 256 bytes keep the 16 key
     // groups of a row on distinct banks.
-    static constexpr bool PAD = KPT == 8 || KPT == 16;
+    static constexpr bool PAD = KPT == 8 || KPT == 16 || KPT == 32;
     static constexpr int NPS = PAD ? NP + 4 * ((NP - 1) / 64) : NP;   // floats per token row of sQ / sK
     __host__ __device__ static constexpr int Pos(int i) { return PAD ? i + 4 * (i / 64) : i; }
     // dynamic LDS (bytes), doubles first
@@ -311,16 +311,25 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         float oreg[TB / 16];
 #pragma unroll
         for (int u = 0; u < TB / 16; ++u) oreg[u] = 0.0f;
-        float cq[KPT], ck[KPT], nq[KPT], nk[KPT];
+        // up to 16 keys per lane, token tt+1's q and k are read while token tt
+        // computes; above that the second register set would spill, and each
+        // token reads its own
+        constexpr bool PREF = KPT <= 16;
+        float cq[KPT], ck[KPT], nq[PREF ? KPT : 1], nk[PREF ? KPT : 1];
         float cdec, cks, cdiag, cv, ndec = 1.0f, nks = 0.0f, ndiag = 0.0f, nv = 0.0f;
-        LoadKeys<KPT>(qb, cq);
-        LoadKeys<KPT>(kb, ck);
+        if constexpr (PREF) {
+            LoadKeys<KPT>(qb, cq);
+            LoadKeys<KPT>(kb, ck);
+        }
         cdec = sc[0]; cks = sc[TB]; cdiag = sc[2 * TB]; cv = vr[0];
 #pragma unroll
         for (int tt = 0; tt < TB; ++tt) {
+            if constexpr (!PREF) LoadKeys<KPT>(qb + tt * NPS, cq);
             if (tt + 1 < TB) {
-                LoadKeys<KPT>(qb + (tt + 1) * NPS, nq);
-                LoadKeys<KPT>(kb + (tt + 1) * NPS, nk);
+                if constexpr (PREF) {
+                    LoadKeys<KPT>(qb + (tt + 1) * NPS, nq);
+                    LoadKeys<KPT>(kb + (tt + 1) * NPS, nk);
+                }
                 ndec = sc[tt + 1]; nks = sc[TB + tt + 1]; ndiag = sc[2 * TB + tt + 1]; nv = vr[(tt + 1) * kRows];
             }
             float a0 = 0.0f, a1 = 0.0f;
@@ -335,12 +344,15 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
             }
             const float y = fmaf(cdiag, cv, RowSum16(a0 + a1));
             const float vk = cv * cks;
+            if constexpr (!PREF) LoadKeys<KPT>(kb + tt * NPS, ck);   // after the readout: q and k not live together
 #pragma unroll
             for (int j = 0; j < KPT; ++j) S[j] = fmaf(vk, ck[j], S[j]);   // S += V (x) k_rot (gamma + look)
             oreg[tt / 16] = kg == (tt & 15) ? y : oreg[tt / 16];
             if (tt + 1 < TB) {
+                if constexpr (PREF) {
 #pragma unroll
-                for (int j = 0; j < KPT; ++j) { cq[j] = nq[j]; ck[j] = nk[j]; }
+                    for (int j = 0; j < KPT; ++j) { cq[j] = nq[j]; ck[j] = nk[j]; }
+                }
                 cdec = ndec; cks = nks; cdiag = ndiag; cv = nv;
             }
         }
@@ -426,7 +438,9 @@ void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream_v) {
     if (kpt <= 4) LaunchKPT<4>(p, stream);
     else if (kpt <= 8) LaunchKPT<8>(p, stream);
     else if (kpt <= 12) LaunchKPT<12>(p, stream);
-    else LaunchKPT<16>(p, stream);
+    else if (kpt <= 16) LaunchKPT<16>(p, stream);
+    else if (kpt <= 24) LaunchKPT<24>(p, stream);
+    else LaunchKPT<32>(p, stream);
     XM_LAUNCH_CHECK("Mamba3SisoFn");
 }
 

@@ -2,9 +2,12 @@
 // Mirrors mamba3_siso_fn_ort.cpp:43-227 of the reference (constructor checks
 // in the same order, ValidateInputs and its messages, ToIntDim, output shape
 // = V.shape) and the launcher's re-checks (mamba3_siso_fwd.cu:177-188).
-// The fused kernel keeps the state in VGPRs, so headdim_qk is limited to 256
-// (the reference's limit is its shared-memory budget, P*N + A + 4N + 128
-// floats).  No scratch.
+// The kernels keep the state in VGPRs and a block of rotated q/k rows in LDS,
+// which bounds headdim_qk at 512 (32 keys per lane of a 16-lane row, 16-token
+// blocks: 155 KiB of LDS).  The reference's limit is its shared-memory budget
+// of P*N + A + 4N + 128 floats (mamba3_siso_fwd.cu:190-207), N = 576 at P = 64
+// on a 160 KiB device; N up to 256 takes the chunked fp32-MFMA kernel, above
+// that the token-by-token kernel.  No scratch.
 //
 // Widening: has_input_states = 1 and return_final_states = 1, which the
 // reference rejects (:50-55), are accepted.  The states are (ssm [B,H,P,N],
@@ -101,7 +104,7 @@ Plan Validate(const std::vector<View> &in, const IndexView *cu, const xm_mamba3_
     p.nheads = ToIntDim(V.shape[2], "nheads");
     p.p = ToIntDim(V.shape[3], "headdim_v");
     p.a = ToIntDim(Ang.shape[3], "headdim_angles");
-    if (p.n > 256) Unsupported("Mamba3SisoFn supports headdim_qk up to 256");
+    if (p.n > 512) Unsupported("Mamba3SisoFn supports headdim_qk up to 512");
     p.Q = Q.data;
     p.K = K.data;
     p.V = V.data;
