@@ -49,6 +49,7 @@ COMMON = [
 SOURCES = [
     "xm_runtime.hip",
     "selective_scan.hip",
+    "selective_scan_seg.hip",
     "gated_deltanet2.hip",
     "gated_deltanet2_chunk.hip",
     "gated_deltanet2_noalloc.hip",

@@ -56,6 +56,7 @@ extern "C" int xm_gated_deltanet2_forward_noalloc(const xm_tensor_t *inputs, siz
                                                   const xm_gated_deltanet2_attrs_t *attrs, float *out, void *stream,
                                                   char *errbuf, size_t errlen) {
     return xm::Guard(errbuf, errlen, [&] {
+        xm::ResetLaunches();
         if (attrs == nullptr) xm::Invalid("attrs is null");
         if (attrs->output_final_state != 0)
             xm::Invalid("GatedDeltaNet2Fn with output_final_state=1 needs a final_state output "

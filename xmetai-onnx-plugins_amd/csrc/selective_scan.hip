@@ -33,11 +33,18 @@
 
 #include "xm_hip.h"
 #include "xm_params.h"
+#include "selective_scan_dev.h"
 
 namespace xm {
 namespace {
 
+using namespace ssdev;
+
 constexpr int kThreads = 256;
+// Sequence-split selection: single-pass workgroups below this count (one per
+// CU), sequences at least this long.
+constexpr long long kSegMaxChannelBlocks = 256;
+constexpr int kSegMinSeqlen = 256;
 
 // Tokens per tile: 32 fp32 = one 128-byte line per (channel, tile), so every
 // line of u and delta is consumed by the load that fetched it (rows are
@@ -62,145 +69,6 @@ __device__ __forceinline__ float LaneGroupSum(float x) {
     if constexpr (LPC >= 8) x += DppF<0x141>(x);
     if constexpr (LPC >= 16) x += DppF<0x128>(x);
     return x;
-}
-
-// Sums of four values (tokens 0..3) over the 8 lanes {c, c+8, ..., c+56} of
-// one channel c = lane % 8, with the gfx950 lane-swap instructions:
-// permlane32_swap(a, b) yields [a.lo32, b.lo32] and [a.hi32, b.hi32], and
-// permlane16_swap(a, b) yields [a.r0, b.r0, a.r2, b.r2] and [a.r1, b.r1, a.r3,
-// b.r3] (r = 16-lane row), so adding the two halves of each swap halves the
-// number of lanes and of values at once.  Seven instructions instead of the
-// twelve of four separate 3-step reductions.  On return every lane of row r
-// holds the channel sum of token {0, 2, 1, 3}[r] (see SwapReducedToken).
-__device__ __forceinline__ float SwapReduce8x4(const float (&y)[4]) {
-    const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[0]), __float_as_uint(y[1]), false, false);
-    const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[2]), __float_as_uint(y[3]), false, false);
-    const float y01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);   // lanes 0-31: y0, 32-63: y1
-    const float y23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);   // lanes 0-31: y2, 32-63: y3
-    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(y01), __float_as_uint(y23), false, false);
-    const float z = __uint_as_float(q[0]) + __uint_as_float(q[1]);         // rows: y0, y2, y1, y3
-    return z + DppF<0x128>(z);                                             // lanes c and c+8 of a row
-}
-
-// The same for 4 lanes per channel, {c, c+16, c+32, c+48} with c = lane % 16:
-// the two swap stages alone reduce over the 4 lanes (six instructions).
-__device__ __forceinline__ float SwapReduce4x4(const float (&y)[4]) {
-    const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[0]), __float_as_uint(y[1]), false, false);
-    const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[2]), __float_as_uint(y[3]), false, false);
-    const float y01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);
-    const float y23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);
-    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(y01), __float_as_uint(y23), false, false);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
-__device__ __forceinline__ int SwapReducedToken(int lane) {
-    const int r = lane >> 4;
-    return ((r & 1) << 1) | (r >> 1);
-}
-
-struct F4 {
-    float v[4];
-};
-
-// bfloat16 storage: the upper 16 bits of an fp32.
-struct Bf16 {
-    uint16_t bits;
-};
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float ToF(float x) { return x; }
-__device__ __forceinline__ float ToF(_Float16 x) { return static_cast<float>(x); }
-__device__ __forceinline__ float ToF(Bf16 x) { return __uint_as_float(static_cast<uint32_t>(x.bits) << 16); }
-
-template <typename IT>
-__device__ __forceinline__ IT FromF(float x);
-template <>
-__device__ __forceinline__ float FromF<float>(float x) { return x; }
-template <>
-__device__ __forceinline__ _Float16 FromF<_Float16>(float x) { return static_cast<_Float16>(x); }   // nearest even
-template <>
-__device__ __forceinline__ Bf16 FromF<Bf16>(float x) {   // nearest even; a NaN stays a (quiet) NaN
-    const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return Bf16{static_cast<uint16_t>((u >> 16) | 0x40u)};
-    return Bf16{static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16)};
-}
-
-// Four consecutive tokens t..t+3 of a row.  The guarded form clamps every
-// address into the row and zeroes the lanes past the end with selects, so it
-// has no branches (branches around loads make the compiler wait on each one,
-// which would serialise the one-tile-ahead prefetch).
-// (16 bytes of fp32 or 8 bytes of 16-bit data per vector access)
-template <typename IT>
-__device__ __forceinline__ F4 LoadRow4Fast(const IT *row, int t) {
-    if constexpr (sizeof(IT) == 4) {
-        const float4 x = *reinterpret_cast<const float4 *>(row + t);
-        return F4{{x.x, x.y, x.z, x.w}};
-    } else if constexpr (std::is_same_v<IT, _Float16>) {
-        const h4 x = *reinterpret_cast<const h4 *>(row + t);
-        return F4{{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
-                   static_cast<float>(x[3])}};
-    } else {
-        const uint2 x = *reinterpret_cast<const uint2 *>(row + t);
-        return F4{{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u), __uint_as_float(x.y << 16),
-                   __uint_as_float(x.y & 0xffff0000u)}};
-    }
-}
-
-template <typename IT>
-__device__ __forceinline__ F4 LoadRow4Guarded(const IT *row, int t, int L, bool ok) {
-    F4 r;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float v = ToF(row[min(t + e, L - 1)]);
-        r.v[e] = (ok && t + e < L) ? v : 0.0f;
-    }
-    return r;
-}
-
-template <typename IT>
-__device__ __forceinline__ void StoreRow4Fast(IT *row, int t, const F4 &x) {
-    if constexpr (sizeof(IT) == 4) {
-        *reinterpret_cast<float4 *>(row + t) = make_float4(x.v[0], x.v[1], x.v[2], x.v[3]);
-    } else if constexpr (std::is_same_v<IT, _Float16>) {
-        h4 y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = FromF<_Float16>(x.v[e]);
-        *reinterpret_cast<h4 *>(row + t) = y;
-    } else {
-        uint2 y;
-        y.x = static_cast<uint32_t>(FromF<Bf16>(x.v[0]).bits) | (static_cast<uint32_t>(FromF<Bf16>(x.v[1]).bits) << 16);
-        y.y = static_cast<uint32_t>(FromF<Bf16>(x.v[2]).bits) | (static_cast<uint32_t>(FromF<Bf16>(x.v[3]).bits) << 16);
-        *reinterpret_cast<uint2 *>(row + t) = y;
-    }
-}
-
-template <typename IT>
-__device__ __forceinline__ void StoreRow4(IT *row, int t, int L, bool vec, const F4 &x) {
-    if (vec && t + 3 < L) {
-        StoreRow4Fast(row, t, x);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (t + e < L) row[t + e] = FromF<IT>(x.v[e]);
-    }
-}
-
-// softplus of the reference (selective_scan_fwd_kernel.cuh:157-159):
-// x <= 20 ? log1p(exp(x)) : x, evaluated as max(x, 0) + log1p(t) with
-// t = exp(-|x|) <= 1 on the hardware exp2/log2 (v_exp_f32, v_log_f32).
-// u = 1 + t rounds with error c = (u - 1) - t, exact by Fast2Sum (Dekker,
-// 1971) since t <= 1; log1p(t) = log(u) + log(1 - c/u) ~= log(u) - c, where
-// dropping 1/u in [1/2, 1] changes the result by |c| t/u, under 2^-24
-// relative.  For x > 20 the log term is below exp(-20) < ulp(x)/2, so the sum
-// rounds to x exactly, the reference's other branch; +-inf and NaN pass
-// through as in the reference.  Twelve issue slots against seventeen for
-// log(1+e) * e / ((1+e) - 1) with its branches.
-__device__ __forceinline__ float Softplus(float x) {
-    constexpr float kLn2 = 0.69314718055994531f;
-    const float t = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2eF);
-    const float u = 1.0f + t;
-    const float c = (u - 1.0f) - t;
-    return fmaxf(x, 0.0f) + fmaf(__builtin_amdgcn_logf(u), kLn2, -c);
 }
 
 // FAST: seqlen % 4 == 0, 16-byte aligned rows and dim_per_group % CPW == 0.
@@ -514,11 +382,6 @@ Config ChooseConfig(int N) {
     return {16, 16};
 }
 
-template <typename IT>
-constexpr const char *TypeTag() {
-    return sizeof(IT) == 4 ? "float" : (std::is_same_v<IT, _Float16> ? "half" : "bfloat16");
-}
-
 template <typename IT, int LPC, int SPL, bool BVAR, bool CVAR, bool VEC>
 void NoteSs() {
     XM_NOTE_LAUNCH("SelectiveScanFwdKernel", {TypeTag<IT>()}, LPC, SPL, BVAR, CVAR, VEC);
@@ -608,6 +471,15 @@ void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream_v) {
     const int cpw = kThreads / cfg.lpc;
     const long long ncb = (p.dim_per_group + cpw - 1) / cpw;
     const long long blocks = ncb * p.groups_b * static_cast<long long>(p.batch);
+    // Fewer channel blocks than CUs and a sequence long enough to split: scan
+    // segments of the sequence in parallel, one workgroup per channel
+    // (ss_split override: 1 keeps the channel blocks, 2 always splits).
+    const int64_t split = GetOverride(kOverrideSsSplit);
+    if (SelectiveScanSegFits(p) &&
+        (split == 2 || (split == 0 && blocks < kSegMaxChannelBlocks && p.seqlen >= kSegMinSeqlen))) {
+        LaunchSelectiveScanSeg(p, stream);
+        return;
+    }
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "SelectiveScanFn launch exceeds the grid limit");
     const dim3 grid(static_cast<unsigned>(blocks));
     if (p.in_type == XM_ELEM_FLOAT16) LaunchTyped<_Float16>(p, cfg, grid, stream);

@@ -150,7 +150,8 @@ enum Override {
 int64_t GetOverride(Override which);
 
 // Per host thread, the kernels the current entry-point call has enqueued
-// (reported by xm_last_launches): reset at the start of each forward call.
+// (reported by xm_last_launches): reset at the start of each forward call,
+// which also clears a HIP error left on the thread by earlier calls.
 void ResetLaunches();
 void NoteLaunch(const char *name);
 // "Base<a,b,...>" with the template arguments of one instantiation.

@@ -79,6 +79,11 @@ struct Mamba3SisoParams {
 // Launchers (defined in the .hip translation units).  They enqueue on
 // `stream` and throw xm::Error on a launch failure.
 void LaunchSelectiveScan(const SelectiveScanParams &p, void *stream);
+// Sequence-parallel form (selective_scan_seg.hip): one workgroup per channel,
+// segments of the sequence scanned at once.  Fits: 1 <= dstate <= 256 and one
+// batch row of B/C below 2 GiB.
+bool SelectiveScanSegFits(const SelectiveScanParams &p);
+void LaunchSelectiveScanSeg(const SelectiveScanParams &p, void *stream);
 // GatedDeltaNet2Fn host validation (gated_deltanet2_host.cpp): the attribute
 // and shape checks of the reference, and the launch parameters of the call.
 GatedDeltaNet2Params GatedDeltaNet2Plan(const xm_tensor_t *inputs, size_t n_inputs,

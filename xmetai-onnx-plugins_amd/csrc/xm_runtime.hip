@@ -121,7 +121,14 @@ struct LaunchLog {
 thread_local LaunchLog t_launches;
 }  // namespace
 
-void ResetLaunches() { t_launches.n = 0; }
+void ResetLaunches() {
+    t_launches.n = 0;
+    // hipGetLastError reports the last error of any runtime call on this
+    // thread, including the caller's own (a framework probing devices leaves
+    // one behind).  Clear it so the launch checks of this call see only the
+    // launches it makes.
+    (void)hipGetLastError();
+}
 
 void NoteLaunch(const char *name) {
     LaunchLog &l = t_launches;

@@ -57,6 +57,15 @@ def lib() -> ctypes.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `python xmetai-onnx-plugins_amd/build.py` "
                 "(there is no fallback implementation)")
+        # torch wheels carry their own HIP runtime (torch/lib/libamdhip64.so).
+        # Import torch first so the library binds to that runtime; loaded
+        # before it, the library would pull in /opt/rocm's libamdhip64 and the
+        # process would hold two runtimes whose streams and device pointers do
+        # not mix (every launch then fails with hipErrorNoDevice).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         _lib = _capi.declare(ctypes.CDLL(LIB_PATH))
     return _lib
 
