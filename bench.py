@@ -105,6 +105,7 @@ def make_ops():
                     gen=lambda: W.selective_scan_inputs(host_shape, seed=0), keys=keys,
                     device_extra=lambda dev: dict(z=_device_normal((s.batch, s.dim, s.seqlen), dev, seed=0)),
                     call=lambda d: xp.selective_scan_fn(*(d[k] for k in keys), delta_softplus=True),
+                    prepare=lambda d: xp.selective_scan_fn(*(d[k] for k in keys), delta_softplus=True, prepare=True),
                     tokens=s.batch * s.seqlen, nbytes=W.selective_scan_bytes(s),
                     config=dict(batch=s.batch, dim=s.dim, seqlen=s.seqlen, dstate=s.dstate, variable_B_C=True,
                                 delta_softplus=True, has_D=True, has_z=True, has_delta_bias=True))
@@ -115,6 +116,7 @@ def make_ops():
         return dict(name="gated_deltanet2", workload="gated_deltanet2_b4_t4096_h16_k128_v128", shape=s,
                     gen=lambda: W.gated_deltanet2_inputs(s, seed=0), keys=keys,
                     call=lambda d: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale),
+                    prepare=lambda d: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale, prepare=True),
                     tokens=s.batch * s.seqlen, nbytes=W.gated_deltanet2_bytes(s),
                     config=dict(batch=s.batch, seqlen=s.seqlen, nheads=s.nheads, dk=s.dk, dv=s.dv,
                                 initial_state=True, l2norm=True))
@@ -125,6 +127,7 @@ def make_ops():
         return dict(name="mamba3_siso", workload="mamba3_siso_b4_t4096_h32_p64_n128", shape=s,
                     gen=lambda: W.mamba3_siso_inputs(s, seed=0), keys=keys,
                     call=lambda d: xp.mamba3_siso_fn(*(d[k] for k in keys)),
+                    prepare=lambda d: xp.mamba3_siso_fn(*(d[k] for k in keys), prepare=True),
                     tokens=s.batch * s.seqlen, nbytes=W.mamba3_siso_bytes(s),
                     config=dict(batch=s.batch, seqlen=s.seqlen, nheads=s.nheads, headdim=s.headdim,
                                 dstate=s.dstate, angles=s.a, has_d=True, has_z=False))
@@ -146,20 +149,30 @@ def to_device(inputs, dev):
 
 
 def time_op(op, dev_inputs, steps, warmup, settle_ms=0.0):
+    """Per-call HIP-event times (ms) on the current stream and the wall time of
+    the `steps` timed calls.  Ops with a "prepare" entry are timed through a
+    PreparedCall (argument blocks built once, the same C entry point and
+    kernels per call), so a call of a few microseconds is not timed behind the
+    Python front end's per-call descriptor work."""
     import torch
+    if "prepare" in op:
+        prepared = op["prepare"](dev_inputs)
+        call = lambda: prepared()
+    else:
+        call = lambda: op["call"](dev_inputs)
     end = time.perf_counter() + settle_ms / 1e3
     while time.perf_counter() < end:   # untimed: the clock settles under this load
         for _ in range(8):
-            op["call"](dev_inputs)
+            call()
         torch.cuda.synchronize()
     for _ in range(warmup):
-        op["call"](dev_inputs)
+        call()
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
     for a, b in ev:
         a.record()
-        op["call"](dev_inputs)
+        call()
         b.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -345,19 +358,23 @@ def time_extra_configs(dev, steps, settle_ms):
         if name.startswith("selective_scan"):
             keys = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
             inp = W.selective_scan_inputs(s, seed=0)
-            call = lambda d, s=s, keys=keys: xp.selective_scan_fn(*(d[k] for k in keys), delta_softplus=s.delta_softplus)
+            prep = lambda d, s=s, keys=keys: xp.selective_scan_fn(*(d[k] for k in keys),
+                                                                  delta_softplus=s.delta_softplus, prepare=True)
             nbytes = W.selective_scan_bytes(s)
         else:
             keys = ("q", "k", "v", "g", "beta", "w", "initial_state")
             inp = W.gated_deltanet2_inputs(s, seed=0)
-            call = lambda d, s=s, keys=keys: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale)
+            prep = lambda d, s=s, keys=keys: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale,
+                                                                   prepare=True)
             nbytes = W.gated_deltanet2_bytes(s)
         d = to_device(inp, dev)
-        _, per = time_op(dict(call=call), d, steps, 2, settle_ms)
+        _, per = time_op(dict(prepare=prep), d, steps, 2, settle_ms)
+        kernels = xp.last_launches()
         ms = statistics.median(per)
         tokens = s.batch * s.seqlen
         out[name] = dict(ms_per_call_median=round(ms, 4), tokens_per_s=tokens / (ms / 1e3),
-                         achieved_GBps=round(nbytes / (ms / 1e3) / 1e9, 1), algorithmic_bytes=nbytes)
+                         achieved_GBps=round(nbytes / (ms / 1e3) / 1e9, 1), algorithmic_bytes=nbytes,
+                         kernels=kernels)
         log(f"{name}: {ms:.3f} ms/call")
         del d, inp
         torch.cuda.empty_cache()

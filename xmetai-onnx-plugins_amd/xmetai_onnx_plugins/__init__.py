@@ -28,7 +28,7 @@ from ._capi import (XM_ERR_ALLOC, XM_ERR_DEVICE, XM_ERR_INVALID_ARGUMENT, XM_ERR
                     EXPORTED_SYMBOLS, LIB_PATH)
 
 __all__ = [
-    "XmError", "lib", "version", "last_launches", "set_kernel_override", "get_kernel_override", "kernel_override", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn", "softmax_cpu",
+    "XmError", "PreparedCall", "lib", "version", "last_launches", "set_kernel_override", "get_kernel_override", "kernel_override", "selective_scan_fn", "mamba3_siso_fn", "gated_deltanet2_fn", "softmax_cpu",
     "validate", "TorchAllocator", "EXPORTED_SYMBOLS", "LIB_PATH",
     "XM_OK", "XM_ERR_INVALID_ARGUMENT", "XM_ERR_UNSUPPORTED", "XM_ERR_DEVICE", "XM_ERR_ALLOC",
 ]
@@ -247,11 +247,43 @@ class TorchAllocator:
 # operators
 # ---------------------------------------------------------------------------
 
+class PreparedCall:
+    """One operator call whose argument blocks are built once (``prepare=True``
+    on the operator functions).  Calling it enqueues the same forward again:
+    the same input, output and state buffers, on the stream it was prepared
+    for, through the same C entry point.  It skips the per-call work of the
+    plain functions (tensor descriptors, attribute blocks, output allocation),
+    which is most of the host time of a small call.  The caller keeps the
+    inputs alive; ``out`` and ``states`` are overwritten by every call, and a
+    call returns what the operator function would have."""
+
+    def __init__(self, fn, args, err, keep, device_index, out, states, result):
+        self._fn = fn
+        self._args = args
+        self._err = err
+        self._keep = keep
+        self._device_index = device_index
+        self.out = out
+        self.states = states
+        self._result = result
+
+    def __call__(self):
+        import torch
+        if torch.cuda.current_device() != self._device_index:
+            with torch.cuda.device(self._device_index):
+                st = self._fn(*self._args)
+        else:
+            st = self._fn(*self._args)
+        _check(st, self._err)
+        return self._result
+
+
 def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocator], stream,
-         state_shapes=None, **attrs):
+         state_shapes=None, prepare=False, **attrs):
     """Validates and enqueues one operator call.  With ``state_shapes`` (one
     shape per state buffer) set it calls the op's ``_forward_states`` entry
-    point and returns ``(out, [state, ...])``."""
+    point and returns ``(out, [state, ...])``.  With ``prepare`` it enqueues
+    nothing and returns a :class:`PreparedCall` instead."""
     import torch
     n = len(inputs)
     descs = [_desc_from_tensor(x) for x in inputs]
@@ -271,24 +303,30 @@ def _run(op: str, inputs, out_like_index: int, allocator: Optional[TorchAllocato
         stream = torch.cuda.current_stream(ref.device)
     alloc_ptr = ctypes.byref(allocator.struct) if allocator is not None else None
     out_ptr = ctypes.c_void_p(out.data_ptr() if out.numel() else None)
-    with torch.cuda.device(ref.device):
-        if state_shapes is None:
-            st = getattr(lib(), f"xm_{op}_forward")(arr, n, ctypes.byref(a), out_ptr,
-                                                    ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
-            _check(st, err)
-            return out
+    stream_ptr = ctypes.c_void_p(stream.cuda_stream)
+    if state_shapes is None:
+        fn = getattr(lib(), f"xm_{op}_forward")
+        args = (arr, n, ctypes.byref(a), out_ptr, stream_ptr, alloc_ptr, err, len(err))
+        states, result = None, out
+    else:
         states = [torch.empty(tuple(int(d) for d in sh), dtype=torch.float32, device=ref.device)
                   for sh in state_shapes]
-        st = getattr(lib(), f"xm_{op}_forward_states")(
-            arr, n, ctypes.byref(a), out_ptr,
-            *(ctypes.c_void_p(x.data_ptr() if x.numel() else None) for x in states),
-            ctypes.c_void_p(stream.cuda_stream), alloc_ptr, err, len(err))
+        fn = getattr(lib(), f"xm_{op}_forward_states")
+        args = (arr, n, ctypes.byref(a), out_ptr,
+                *(ctypes.c_void_p(x.data_ptr() if x.numel() else None) for x in states),
+                stream_ptr, alloc_ptr, err, len(err))
+        result = (out, states)
+    if prepare:
+        keep = (inputs, arr, a, allocator, stream)
+        return PreparedCall(fn, args, err, keep, ref.device.index, out, states, result)
+    with torch.cuda.device(ref.device):
+        st = fn(*args)
     _check(st, err)
-    return out, states
+    return result
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, delta_softplus=False,
-                      return_last_state=False, allocator=None, stream=None):
+                      return_last_state=False, allocator=None, stream=None, prepare=False):
     """SelectiveScanFn: returns y [B,D,L] (the un-gated scan output; z is
     validated and otherwise unused, as in selective_scan_fwd_kernel.cuh:272-301).
 
@@ -300,19 +338,24 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, *, del
     u, delta, z and variable B/C may be float16 or bfloat16 (all the same;
     the reference's half / bfloat16 kernels, unreachable from its fp32 host):
     A, D, delta_bias and constant B/C stay float32, y takes u's type and the
-    state stays float32."""
+    state stays float32.  ``prepare=True`` returns a :class:`PreparedCall`
+    (same for the other operators)."""
     shapes = None   # shapes of other ranks fail validation before the launch
     if return_last_state and u.dim() == 3 and A.dim() == 2:
         shapes = [(u.shape[0], u.shape[1], A.shape[1])]
     r = _run("selective_scan", [u, delta, A, B, C, D, z, delta_bias], 0, allocator, stream,
-             state_shapes=shapes,
+             state_shapes=shapes, prepare=prepare,
              delta_softplus=int(bool(delta_softplus)), return_last_state=int(bool(return_last_state)))
+    if prepare:
+        if shapes is not None:
+            r._result = (r.out, r.states[0])
+        return r
     return (r[0], r[1][0]) if shapes is not None else r
 
 
 def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=None, *, chunk_size=64,
                    has_d=None, has_z=None, input_states=None, return_final_states=False, has_input_states=None,
-                   cu_seqlens=None, allocator=None, stream=None):
+                   cu_seqlens=None, allocator=None, stream=None, prepare=False):
     """Mamba3SisoFn: returns [B,T,H,P].  ``has_d``/``has_z`` default to the
     presence of D/Z (an exported graph sets them explicitly; default 1).
 
@@ -341,16 +384,20 @@ def mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Q_bias, K_bias, Angles, D=None, Z=Non
         b = cu_seqlens.shape[0] - 1 if cu_seqlens is not None else Q.shape[0]
         h, pdim, n, a = V.shape[2], V.shape[3], Q.shape[3], Angles.shape[3]
         shapes = [(b, h, pdim, n), (b, h, a), (b, h, n), (b, h, pdim)]
-    r = _run("mamba3_siso", inputs, 2, allocator, stream, state_shapes=shapes,
+    r = _run("mamba3_siso", inputs, 2, allocator, stream, state_shapes=shapes, prepare=prepare,
              chunk_size=chunk_size, has_d=int(bool(has_d)), has_z=int(bool(has_z)),
              return_final_states=int(bool(return_final_states)), has_input_states=int(bool(has_input_states)),
              has_cu_seqlens=int(cu_seqlens is not None))
+    if prepare:
+        if shapes is not None:
+            r._result = (r.out, tuple(r.states))
+        return r
     return (r[0], tuple(r[1])) if shapes is not None else r
 
 
 def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, use_qk_l2norm_in_kernel=True,
                        output_final_state=False, use_gate_in_kernel=False, cu_seqlens=None,
-                       state_v_first=False, allocator=None, stream=None):
+                       state_v_first=False, allocator=None, stream=None, prepare=False):
     """GatedDeltaNet2Fn: returns [B,T,H,V].
 
     With ``output_final_state=True`` (rejected by the reference,
@@ -367,10 +414,14 @@ def gated_deltanet2_fn(q, k, v, g, beta, w, initial_state=None, *, scale=1.0, us
         shapes = [(n, q.shape[2], q.shape[3], v.shape[3])]
     inputs = [q, k, v, g, beta, w, initial_state] + ([cu_seqlens] if cu_seqlens is not None else [])
     r = _run("gated_deltanet2", inputs, 2, allocator, stream,
-             state_shapes=shapes,
+             state_shapes=shapes, prepare=prepare,
              scale=scale, use_qk_l2norm_in_kernel=int(bool(use_qk_l2norm_in_kernel)),
              output_final_state=int(bool(output_final_state)), use_gate_in_kernel=int(bool(use_gate_in_kernel)),
              has_cu_seqlens=int(cu_seqlens is not None), state_v_first=int(bool(state_v_first)))
+    if prepare:
+        if shapes is not None:
+            r._result = (r.out, r.states[0])
+        return r
     return (r[0], r[1][0]) if shapes is not None else r
 
 
