@@ -58,7 +58,9 @@ def floors_us(name, s, nbytes):
 
     hbm: algorithmic bytes at 8 TB/s.  valu: the essential per-element
     instruction slots of the sequential recurrence (SS: delta*A, B*delta_u,
-    the state and output FMAs and exp2 at two slots = 6 per state-token;
+    the state and output FMAs, and exp2, which issues at 26.5 lane-ops per CU
+    per cycle against 63 for v_fma_f32 on MI355X (independent chains, all
+    CUs), i.e. 2.4 slots: 6.4 per state-token;
     GDN-2: 4 per state element per token; Mamba-3: decay, readout, update =
     3), at one slot per lane per cycle; where a chunked form runs it is
     reported as valu_sequential_form.  mfma: the fp32 MFMA flops of the
@@ -67,7 +69,7 @@ def floors_us(name, s, nbytes):
     chunk and 32-row block (N padded to 64)."""
     f = {"hbm": nbytes / (HBM_PEAK_GBPS * 1e9) * 1e6}
     if name == "selective_scan":
-        f["valu"] = s.batch * s.dim * s.seqlen * s.dstate * 6 / VALU_LANE_OPS * 1e6
+        f["valu"] = s.batch * s.dim * s.seqlen * s.dstate * 6.4 / VALU_LANE_OPS * 1e6
     elif name == "gated_deltanet2":
         f["valu_sequential_form"] = s.batch * s.seqlen * s.nheads * s.dk * s.dv * 4 / VALU_LANE_OPS * 1e6
         if s.dk <= 512:

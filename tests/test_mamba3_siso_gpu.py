@@ -137,9 +137,46 @@ def test_mamba3_path_switch_selects_the_other_kernel(override):
     import xmetai_onnx_plugins as xp
     override("m3_path", 0)
     chunked = run_gpu(inp)
-    assert xp.last_launches() == ["Mamba3ChunkKernel<1,4,4>"]
+    assert xp.last_launches() == ["Mamba3ChunkKernel<1,4,4,0>"]
     override("m3_path", 1)
     sequential = run_gpu(inp)
     assert xp.last_launches() == ["Mamba3FwdKernel<4>"]
     assert not np.array_equal(chunked, sequential)
     check("mamba3_siso/chunked_vs_seq", chunked, sequential, TOL_GPU)
+
+
+def test_mamba3_token_rows_past_2gib(m3_path):
+    """1 x 65536 tokens x 64 heads, P = 128, N = 16 with Z: the V, Z and output
+    token rows of the sequence span 2 GiB each, past a buffer descriptor's
+    32-bit range, so the chunked kernel reads and writes through per-chunk
+    descriptors (LONG).  Inputs are drawn on the device with the benchmark's
+    distributions; heads 0 and 41 over all 65536 tokens against the oracle."""
+    import math
+    import torch
+    import xmetai_onnx_plugins as xp
+    from xmetai_onnx_plugins import mamba3_siso_fn
+    B, T, H, P, N, A = 1, 65536, 64, 128, 16, 8
+    g = torch.Generator(device="cuda")
+    g.manual_seed(31)
+    rn = lambda *shape: torch.randn(shape, generator=g, device="cuda")
+    ru = lambda *shape: torch.rand(shape, generator=g, device="cuda")
+    V = rn(B, T, H, P)
+    DT = torch.nn.functional.softplus(rn(B, H, T) + (-4.0 + 2.0 * ru(H))[None, :, None])
+    ADT = -torch.exp(ru(H) * math.log(16.0))[None, :, None] * DT
+    Q, K = rn(B, T, H, N) / math.sqrt(N), rn(B, T, H, N) / math.sqrt(N)
+    Trap, Angles, D = ru(B, H, T), ru(B, T, H, A), rn(H)
+    Qb, Kb = rn(H, N) / math.sqrt(N), rn(H, N) / math.sqrt(N)
+    Z = rn(B, T, H, P)
+    y = mamba3_siso_fn(Q, K, V, ADT, DT, Trap, Qb, Kb, Angles, D, Z)
+    torch.cuda.synchronize()
+    if m3_path == "chunk":
+        assert xp.last_launches() == ["Mamba3ChunkKernel<1,4,4,1>"], xp.last_launches()
+    hs = [0, 41]
+    host = lambda x: np.ascontiguousarray(x.cpu().numpy())
+    sub = dict(Q=host(Q[:, :, hs]), K=host(K[:, :, hs]), V=host(V[:, :, hs]), ADT=host(ADT[:, hs]),
+               DT=host(DT[:, hs]), Trap=host(Trap[:, hs]), Q_bias=host(Qb[hs]), K_bias=host(Kb[hs]),
+               Angles=host(Angles[:, :, hs]), D=host(D[hs]), Z=host(Z[:, :, hs]))
+    got = host(y[:, :, hs])
+    del V, Z, y
+    torch.cuda.empty_cache()
+    check(f"mamba3_siso/t65536_h64_p128_rows_past_2gib/{m3_path}", got, run_ref(sub), TOL_M3)

@@ -160,7 +160,10 @@ __device__ __forceinline__ float RowInclusiveScan16(float x) {
     return x;
 }
 
-template <int KBW, int NW, int NPW>
+// LONG: some tensor's token rows of one sequence span 2 GiB or more, beyond a
+// buffer descriptor's 32-bit range; every chunk then reads and writes through
+// descriptors that start at its own first token.
+template <int KBW, int NW, int NPW, bool LONG>
 __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     using L = M3CLayout<KBW, NW, NPW>;
     constexpr int NT = L::NT;
@@ -248,8 +251,15 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // sequence's last token, so a token past the end is out of range.  A
     // chunk's token offset goes into the per-lane offset (the range check
     // covers only that operand); kOutOfRange plus any in-range offset stays
-    // out of range (no wrap below 2^32).  The host keeps T * stride * 4 < 2^31.
+    // out of range (no wrap below 2^32).  Without LONG the host keeps
+    // T * stride * 4 < 2^31; with LONG (below) each chunk has its own
+    // descriptors, from its first token to its last valid one.
     auto seq_bytes = [&](size_t stride) { return static_cast<int>(static_cast<size_t>(T) * stride * 4); };
+    // (`rows` tokens from c0: DT and Trap reach one token into the next chunk,
+    // the look-ahead of the chunk's last token)
+    auto chunk_rsrc = [&](const float *base, size_t stride, int c0, int rows = kC) __attribute__((always_inline)) {
+        return MakeRsrc(base + static_cast<size_t>(c0) * stride, static_cast<int>(static_cast<size_t>(min(T - c0, rows)) * stride * 4));
+    };
     const Rsrc rq = MakeRsrc(qbase, seq_bytes(q_stride));
     const Rsrc rk = MakeRsrc(kbase, seq_bytes(q_stride));
     const Rsrc ra = MakeRsrc(abase, seq_bytes(a_stride));
@@ -277,25 +287,32 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         float (&ang)[PB][TPL] = r.ang;
         float (&dts)[TPL] = r.dts;
         float (&vreg)[VPT] = r.vreg;
-        const int cq = c0 * qs4, ca = c0 * as4, cv = c0 * vs4, cd = c0 * 4;
+        const int cq = LONG ? 0 : c0 * qs4, ca = LONG ? 0 : c0 * as4, cv = LONG ? 0 : c0 * vs4, cd = LONG ? 0 : c0 * 4;
+        const Rsrc q_ = LONG ? chunk_rsrc(qbase, q_stride, c0) : rq;
+        const Rsrc k_ = LONG ? chunk_rsrc(kbase, q_stride, c0) : rk;
+        const Rsrc a_ = LONG ? chunk_rsrc(abase, a_stride, c0) : ra;
+        const Rsrc d_ = LONG ? chunk_rsrc(dtr, 1, c0, kC + 1) : rd;
+        const Rsrc t_ = LONG ? chunk_rsrc(trr, 1, c0, kC + 1) : rt;
+        const Rsrc ad_ = LONG ? chunk_rsrc(adr, 1, c0) : rad;
+        const Rsrc v_ = LONG ? chunk_rsrc(p.V + vbase, v_stride, c0) : rv;
 #pragma unroll
         for (int s = 0; s < TPL; ++s) {
-            dts[s] = BufF(rd, off(cd, (TPL * tg + s) * 4));
+            dts[s] = BufF(d_, off(cd, (TPL * tg + s) * 4));
 #pragma unroll
             for (int x = 0; x < PB; ++x) {
-                qv[x][s] = BufF2(rq, off(qoff[x][s], cq));
-                kv[x][s] = BufF2(rk, off(qoff[x][s], cq));
-                ang[x][s] = BufF(ra, off(aoff[x][s], ca));
+                qv[x][s] = BufF2(q_, off(qoff[x][s], cq));
+                kv[x][s] = BufF2(k_, off(qoff[x][s], cq));
+                ang[x][s] = BufF(a_, off(aoff[x][s], ca));
             }
         }
 #pragma unroll
-        for (int u = 0; u < VPT; ++u) vreg[u] = BufF(rv, off(voff[u], cv));
+        for (int u = 0; u < VPT; ++u) vreg[u] = BufF(v_, off(voff[u], cv));
         // every preparation wave loads them (same load count on every path); wave NPW-1 uses them
-        r.sdt = BufF(rd, off(cd, i16 * 4));
-        r.strap = BufF(rt, off(cd, i16 * 4));
-        r.sadt = BufF(rad, off(cd, i16 * 4));
-        r.sdt1 = BufF(rd, off(cd, (i16 + 1) * 4));
-        r.strap1 = BufF(rt, off(cd, (i16 + 1) * 4));
+        r.sdt = BufF(d_, off(cd, i16 * 4));
+        r.strap = BufF(t_, off(cd, i16 * 4));
+        r.sadt = BufF(ad_, off(cd, i16 * 4));
+        r.sdt1 = BufF(d_, off(cd, (i16 + 1) * 4));
+        r.strap1 = BufF(t_, off(cd, (i16 + 1) * 4));
     };
 
     // rotated q^ / k^ (and the unrotated q.k), V^T and the per-token scalars of
@@ -475,7 +492,10 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     const Rsrc ro = MakeRsrc(p.out + vbase, seq_bytes(v_stride));
     auto load_z = [&](int c0, float (&zr)[4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) zr[r] = BufF(rz, off(ooff[r], c0 * vs4));
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (LONG) zr[r] = BufF(chunk_rsrc(p.Z + vbase, v_stride, c0), ooff[r]);
+            else zr[r] = BufF(rz, off(ooff[r], c0 * vs4));
+        }
     };
     auto finish = [&](int c0, const float *bf, const float *pp, const float (&zr)[4]) __attribute__((always_inline)) {
         const int pt = w;
@@ -511,7 +531,9 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         for (int r = 0; r < 4; ++r) {
             float y = acc[r];
             if (p.Z != nullptr) y *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
-            BufStF(ro, off(ooff[r], c0 * vs4), y);   // tokens past the end and rows >= P are dropped
+            // tokens past the end and rows >= P are dropped
+            if constexpr (LONG) BufStF(chunk_rsrc(p.out + vbase, v_stride, c0), ooff[r], y);
+            else BufStF(ro, off(ooff[r], c0 * vs4), y);
         }
     };
 
@@ -600,32 +622,42 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     }
 }
 
-template <int KBW, int NW, int NPW>
-void LaunchChunk(const Mamba3SisoParams &p, hipStream_t stream) {
+template <int KBW, int NW, int NPW, bool LONG>
+void LaunchChunkL(const Mamba3SisoParams &p, hipStream_t stream) {
     using L = M3CLayout<KBW, NW, NPW>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW>), static_cast<int>(L::kBytes));
-    XM_NOTE_LAUNCH("Mamba3ChunkKernel", {}, KBW, NW, NPW);
-    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NW, NPW>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW, LONG>), static_cast<int>(L::kBytes));
+    XM_NOTE_LAUNCH("Mamba3ChunkKernel", {}, KBW, NW, NPW, LONG);
+    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NW, NPW, LONG>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
                        stream, p);
+}
+
+template <int KBW, int NW, int NPW>
+void LaunchChunk(const Mamba3SisoParams &p, bool long_rows, hipStream_t stream) {
+    if (long_rows) LaunchChunkL<KBW, NW, NPW, true>(p, stream);
+    else LaunchChunkL<KBW, NW, NPW, false>(p, stream);
 }
 
 }  // namespace
 
 bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream_v) {
     if (GetOverride(kOverrideM3Path) == 1) return false;
-    // Per-chunk buffer descriptors hold 32-bit byte sizes: the token rows of
-    // Q/K, Angles and V/Z/out of one sequence must each span less than 2 GiB.
+    // Buffer descriptors hold 32-bit byte sizes.  The token rows of Q/K,
+    // Angles and V/Z/out of one sequence below 2 GiB each: one descriptor per
+    // tensor for the whole sequence.  From 2 GiB on: per-chunk descriptors
+    // (16 token rows each must stay below 2 GiB).
     const size_t widest = std::max({static_cast<size_t>(p.nheads_qk) * p.n, static_cast<size_t>(p.nheads) * p.a,
                                     static_cast<size_t>(p.nheads) * p.p});
-    if (static_cast<size_t>(p.seqlen) * widest * sizeof(float) >= (size_t{1} << 31)) return false;
+    const size_t row_bytes = widest * sizeof(float);
+    if (row_bytes * kC >= (size_t{1} << 31)) return false;
+    const bool long_rows = static_cast<size_t>(p.seqlen) * row_bytes >= (size_t{1} << 31);
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     // headdim_qk padded to 64, 128, 192 or 256 keys
-    if (p.n <= 64) LaunchChunk<1, 4, 4>(p, stream);
-    else if (p.n <= 128) LaunchChunk<2, 4, 8>(p, stream);   // 8 product waves: slower (more partials)
-    else if (p.n <= 192) LaunchChunk<3, 4, 4>(p, stream);
-    else if (p.n <= 256) LaunchChunk<4, 4, 4>(p, stream);
+    if (p.n <= 64) LaunchChunk<1, 4, 4>(p, long_rows, stream);
+    else if (p.n <= 128) LaunchChunk<2, 4, 8>(p, long_rows, stream);   // 8 product waves: slower (more partials)
+    else if (p.n <= 192) LaunchChunk<3, 4, 4>(p, long_rows, stream);
+    else if (p.n <= 256) LaunchChunk<4, 4, 4>(p, long_rows, stream);
     else return false;
     XM_LAUNCH_CHECK("Mamba3SisoFn (chunked)");
     return true;
