@@ -340,12 +340,44 @@ def packed_gdn(N=3, T=20, H=3, K=16, V=8, s0=True, cu=None):
     return shapes + [cu or (N + 1,)], [1] * 7 + [I64]
 
 
-def test_gdn2_packed_sequences_valid_no_scratch():
+def packed_chunk_scratch(N, T, H, K, V):
+    """Scratch of the chunked path for N packed sequences along T tokens.  A
+    window holds chunks [c0, c0 + win) of every sequence (win = min(ceil(T/16),
+    128), or every chunk when that costs at most twice the blocks or 512 MiB);
+    per head its blocks are at most min(win * N, ceil(T/16) + N), of
+    3*kq*256 + 16*kq + 544 floats each (kq = key tiles, padded to the
+    recurrence's key split).  Plus the carried state [N,H,K,V] when a sequence
+    can span windows, and the per-window block offsets [windows][N+1] ints;
+    each region 256-byte aligned."""
+    a256 = lambda x: -(-x // 256) * 256
+    kq = -(-K // 16)
+    kq = 4 * -(-kq // 4) if kq > 8 else (kq if kq < 2 else 2 * -(-kq // 2))
+    nch = -(-T // 16)
+    per = H * (3 * kq * 256 + 16 * kq + 544) * 4
+    win = min(nch, 128)
+    blocks = a256(per * min(win * N, nch + N))
+    if win < nch and a256(per * (nch + N)) <= max(2 * blocks, 512 << 20):
+        win = nch   # one window over every chunk: no empty windows to step through
+        blocks = a256(per * (nch + N))
+    carry = a256(N * H * K * V * 4) if win < nch else 0
+    return blocks + carry + a256(-(-nch // win) * (N + 1) * 4)
+
+
+def test_gdn2_packed_sequences_valid_scratch():
     # Widening: cu_seqlens (input 7, int64 [N+1]) packs N sequences; the
-    # fused kernel takes them (no scratch at any headdim_k up to 512).
+    # chunked path takes them at any headdim_k up to 512, with global-chunk
+    # windows and the chunk offsets in scratch.
     for K in (16, 128, 256, 512):
         shapes, types = packed_gdn(K=K)
-        assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1) == ((1, 20, 3, 8), 0)
+        assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1) == \
+            ((1, 20, 3, 8), packed_chunk_scratch(3, 20, 3, K, 8))
+    # 4000 tokens in 5 sequences: one window over every chunk
+    shapes, types = packed_gdn(N=5, T=4000, K=64)
+    assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1)[1] == packed_chunk_scratch(5, 4000, 3, 64, 8)
+    # one 2^20-token sequence at 16 x 256 x 256: windows of 128 chunks, the state carried
+    shapes, types = packed_gdn(N=1, T=1 << 20, H=16, K=256, V=256)
+    assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1)[1] == \
+        packed_chunk_scratch(1, 1 << 20, 16, 256, 256)
     shapes, types = packed_gdn(s0=False)
     assert validate("gated_deltanet2", shapes, types, has_cu_seqlens=1)[0] == (1, 20, 3, 8)
 

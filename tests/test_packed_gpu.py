@@ -6,8 +6,10 @@ reference rejects it, gated_deltanet2_fn_ort.cpp:55-57, mamba3_siso_fn_ort.cpp:
 sequence.  Each packed call is checked against the fp64 oracle run on every
 sequence by itself, with that sequence's initial state: outputs and final
 states.  Covered: empty and one-token sequences, lengths that end inside a
-token block, every GDN-2 key layout up to headdim_k 512, Mamba-3 with and
-without input states.
+token block, every GDN-2 key layout up to headdim_k 512 on the chunked path
+(global-chunk windows, a sequence's state carried between windows) and on the
+sequential kernel, sequences spanning several windows, runs of empty
+sequences, Mamba-3 with and without input states.
 """
 
 import numpy as np
@@ -32,24 +34,33 @@ def cu_dev(lengths):
     return torch.from_numpy(offsets(lengths)).to("cuda")
 
 
-# ---------------------------------------------------------------------------
-# GatedDeltaNet2Fn
-# ---------------------------------------------------------------------------
+@pytest.fixture(params=["chunk", "seq"])
+def gdn2_path(request, override):
+    """GatedDeltaNet2Fn kernel under test: the chunked MFMA path (default) or
+    the sequential fused kernel (gdn2_path override 1)."""
+    override("gdn2_path", 1 if request.param == "seq" else 0)
+    return request.param
 
-@pytest.mark.parametrize("dk,dv", [(16, 8), (64, 40), (128, 65), (320, 24), (512, 16)])
-@pytest.mark.parametrize("with_state", [False, True])
-def test_gdn2_packed_matches_per_sequence(dk, dv, with_state):
+
+def gdn2_packed_check(lengths, H, dk, dv, with_state, path, seed, tag):
+    """Runs one packed call and checks every sequence against the oracle run
+    on it alone."""
     import torch
-    lengths = [37, 0, 1, 16, 50]
-    T, H, N = sum(lengths), 2, len(lengths)
+    import xmetai_onnx_plugins as xp
+    T, N = sum(lengths), len(lengths)
     s = W.GatedDeltaNet2Shape(1, T, H, dk, dv, initial_state=False)
-    inp = W.gated_deltanet2_inputs(s, seed=12)
-    rng = np.random.default_rng(13)
+    inp = W.gated_deltanet2_inputs(s, seed=seed)
+    rng = np.random.default_rng(seed + 1)
     s0 = (0.05 * rng.standard_normal((N, H, dk, dv))).astype(np.float32) if with_state else None
     o, st = gated_deltanet2_fn(*(to_dev(inp[k]) for k in GDN_KEYS), None if s0 is None else to_dev(s0),
                                scale=s.scale, use_qk_l2norm_in_kernel=s.l2norm, output_final_state=True,
                                cu_seqlens=cu_dev(lengths))
     torch.cuda.synchronize()
+    launched = xp.last_launches()
+    if path == "chunk":
+        assert any(k.startswith("Gdn2ChunkRecurKernel") and ",1>" in k for k in launched), launched
+    else:
+        assert any(k.startswith("Gdn2FusedKernel") for k in launched), launched
     o, st = o.cpu().numpy(), st.cpu().numpy()
     assert o.shape == (1, T, H, dv) and st.shape == (N, H, dk, dv)
     cu = offsets(lengths)
@@ -62,8 +73,45 @@ def test_gdn2_packed_matches_per_sequence(dk, dv, with_state):
         part = [np.ascontiguousarray(inp[k][:, lo:hi]) for k in GDN_KEYS]
         ro, rs = cref.gated_deltanet2(*part, init, scale=s.scale, use_qk_l2norm=s.l2norm, dtype=np.float64,
                                       return_state=True)
-        check(f"gdn2_packed/{dk}x{dv}/seq{n}/o", o[:, lo:hi], ro, TOL_GDN2)
-        check(f"gdn2_packed/{dk}x{dv}/seq{n}/S", st[n:n + 1], rs, TOL_GDN2)
+        check(f"{tag}/{path}/seq{n}/o", o[:, lo:hi], ro, TOL_GDN2)
+        check(f"{tag}/{path}/seq{n}/S", st[n:n + 1], rs, TOL_GDN2)
+
+
+# ---------------------------------------------------------------------------
+# GatedDeltaNet2Fn
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dk,dv", [(16, 8), (64, 40), (128, 65), (320, 24), (512, 16)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_gdn2_packed_matches_per_sequence(dk, dv, with_state, gdn2_path):
+    gdn2_packed_check([37, 0, 1, 16, 50], 2, dk, dv, with_state, gdn2_path, 12, f"gdn2_packed/{dk}x{dv}")
+
+
+@pytest.mark.parametrize("dk,dv", [(64, 32), (128, 128), (256, 20)])
+def test_gdn2_packed_long_sequences(dk, dv):
+    """Sequences of 1500-3000 tokens with empty and short ones between them
+    (one window over every chunk)."""
+    gdn2_packed_check([3000, 0, 1500, 17, 2100, 5], 2, dk, dv, True, "chunk", 31, f"gdn2_packed_long/{dk}x{dv}")
+
+
+def test_gdn2_packed_across_windows():
+    """50007 tokens at headdim_k 512: one window over every chunk would take
+    641 MB of prepared blocks, so the row is stepped in windows of 128 chunks
+    per sequence; the 30000- and 20000-token sequences carry their states
+    through 15 and 10 windows."""
+    gdn2_packed_check([30000, 7, 20000], 2, 512, 16, True, "chunk", 33, "gdn2_packed_windows")
+
+
+def test_gdn2_packed_many_sequences_with_empties():
+    """300 sequences of 0 to 40 tokens, a third of them empty, runs of empties
+    included: more sequences than a window has slots, found through the chunk
+    offsets; every empty sequence passes its initial state through."""
+    rng = np.random.default_rng(41)
+    lengths = [int(x) for x in rng.integers(1, 41, 300)]
+    for i in rng.choice(300, 100, replace=False):
+        lengths[i] = 0
+    lengths[10:30] = [0] * 20
+    gdn2_packed_check(lengths, 2, 64, 24, True, "chunk", 42, "gdn2_packed_many")
 
 
 def test_gdn2_packed_one_sequence_equals_unpacked():

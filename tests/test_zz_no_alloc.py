@@ -22,9 +22,9 @@ def _entry():
     return xp.lib().xm_gated_deltanet2_forward_noalloc   # argument types declared in _capi
 
 
-def _call_noalloc(descs, s, out_ptr, stream_ptr):
+def _call_noalloc(descs, s, out_ptr, stream_ptr, **extra):
     arr = (_capi.XmTensor * len(descs))(*descs)
-    attrs = xp._attrs("gated_deltanet2", scale=s.scale, use_qk_l2norm_in_kernel=int(s.l2norm))
+    attrs = xp._attrs("gated_deltanet2", scale=s.scale, use_qk_l2norm_in_kernel=int(s.l2norm), **extra)
     err = ctypes.create_string_buffer(512)
     st = _entry()(arr, len(descs), ctypes.byref(attrs), out_ptr, stream_ptr, err, len(err))
     return st, err.value.decode()
@@ -67,8 +67,32 @@ def test_noalloc_wide_keys(shape):
 
 
 @pytest.mark.gpu
+def test_noalloc_packed_sequences():
+    # packed sequences on the chunked path: 32 heads x 128 x 64 need 112 MB of
+    # prepared blocks per 128-chunk window; in 64 MiB the windows shrink, and
+    # the 3000- and 2100-token sequences carry their states across them
+    import torch
+    lengths = [3000, 0, 1500, 17, 2100]
+    s = S(1, sum(lengths), 32, 128, 64, initial_state=False)
+    inp = W.gated_deltanet2_inputs(s, seed=5)
+    keys = KEYS[:-1]
+    d = {k: to_dev(inp[k]) for k in keys}
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)).to("cuda")
+    ref = xp.gated_deltanet2_fn(*(d[k] for k in keys), None, scale=s.scale, use_qk_l2norm_in_kernel=int(s.l2norm),
+                                cu_seqlens=cu)
+    out = torch.full_like(ref, float("nan"))
+    descs = [xp._desc_from_tensor(d[k]) for k in keys] + [xp._desc_from_tensor(None), xp._desc_from_tensor(cu)]
+    st, msg = _call_noalloc(descs, s, out.data_ptr(), torch.cuda.current_stream().cuda_stream, has_cu_seqlens=1)
+    assert st == xp.XM_OK, msg
+    launched = xp.last_launches()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
+    assert any(k.startswith("Gdn2ChunkRecurKernel") for k in launched), launched
+
+
+@pytest.mark.gpu
 def test_noalloc_without_scratch_needs():
-    # packed sequences and the sequential kernel take no scratch: nothing is looked up
+    # the sequential kernel takes no scratch: nothing is looked up
     import torch
     s = S(1, 40, 2, 64, 16, initial_state=False)
     with xp.kernel_override("gdn2_path", 1):

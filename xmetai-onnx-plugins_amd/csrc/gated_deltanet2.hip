@@ -664,16 +664,16 @@ LdsPlan PlanLds(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
 }  // namespace
 
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
-    if (dk <= kGdn2ChunkKeyLimit && !packed)   // chunked path
-        return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv, cap);
-    if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch (packed sequences always take it)
+    if (dk <= kGdn2ChunkKeyLimit)   // chunked path (packed sequences included)
+        return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv, packed, cap);
+    if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch
     const LdsPlan l = PlanLds(batch, seqlen, nheads, dk, dv, cap);
     return l.chunk_cap == 0 ? SIZE_MAX : l.total();
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_bytes, void *stream_v) {
-    // dk <= 512: gated_deltanet2_chunk.hip; packed sequences take the fused kernel
-    if (p.cu_seqlens == nullptr && LaunchGatedDeltaNet2Chunked(p, scratch, scratch_bytes, stream_v)) return;
+    // dk <= 512: gated_deltanet2_chunk.hip (the fused kernel under the gdn2_path override)
+    if (LaunchGatedDeltaNet2Chunked(p, scratch, scratch_bytes, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     if (p.cu_seqlens != nullptr && p.dk > kFusedKeyLimit)
         throw Error(XM_ERR_UNSUPPORTED, "GatedDeltaNet2Fn with cu_seqlens supports headdim_k up to 512");

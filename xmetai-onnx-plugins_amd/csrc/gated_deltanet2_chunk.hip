@@ -194,6 +194,26 @@ __device__ __forceinline__ void PairwiseAM(const GatedDeltaNet2Params &p, size_t
     PairSteps(std::make_integer_sequence<int, kC>{}, p, rowbase, live, kq, lane & 15, lane >> 4, qm, km, dst);
 }
 
+// Largest b with off[b] <= g (off non-decreasing over [0, n], off[0] = 0 <= g
+// < off[n]): the packed sequence that holds global chunk g.
+__device__ __forceinline__ int SequenceOfChunk(const int *off, int n, int g) {
+    int lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= g) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Token range [lo, hi) of packed sequence b, clamped to the row.
+__device__ __forceinline__ void PackedRange(const GatedDeltaNet2Params &p, int b, size_t &tok0, int &T) {
+    const long long lo = min(max(p.cu_seqlens[b], 0LL), static_cast<long long>(p.seqlen));
+    const long long hi = min(max(p.cu_seqlens[b + 1], lo), static_cast<long long>(p.seqlen));
+    tok0 = static_cast<size_t>(lo);
+    T = static_cast<int>(hi - lo);
+}
+
 // ---------------------------------------------------------------------------
 // Preparation: one wave per (b,h,chunk) of the window
 // ---------------------------------------------------------------------------
@@ -201,14 +221,32 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     __shared__ float sw[kPrepWaves][4][kTile];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int m16 = lane & 15, g4 = lane >> 4;
-    const int T = p.seqlen, H = p.nheads;
+    const int H = p.nheads;
+    // rows of the window's blocks: (b, h), or h alone for packed sequences,
+    // whose window holds chunks [c0, c0 + W) of every sequence, sequence b's at
+    // blocks [chunk_off[b], chunk_off[b + 1]) of the row
+    const bool packed = p.chunk_off != nullptr;
+    const long long rows = packed ? H : static_cast<long long>(p.batch) * H;
     const long long item = static_cast<long long>(blockIdx.x) * kPrepWaves + w;
-    if (item >= static_cast<long long>(p.batch) * H * wn) return;   // whole wave; no workgroup barrier here
-    const int bh = static_cast<int>(item / wn), cw = static_cast<int>(item % wn);
-    const int b = bh / H, h = bh % H;
-    const int t0 = (c0 + cw) * kC;
+    if (item >= rows * wn) return;   // whole wave; no workgroup barrier here
+    const int row = static_cast<int>(item / wn), cw = static_cast<int>(item % wn);
+    int h, T, t0;
+    size_t tok0;
+    if (!packed) {
+        const int b = row / H;
+        h = row % H;
+        T = p.seqlen;
+        tok0 = static_cast<size_t>(b) * T;
+        t0 = (c0 + cw) * kC;
+    } else {
+        h = row;
+        if (cw >= p.chunk_off[p.batch]) return;   // past the window's blocks: never read
+        const int b = SequenceOfChunk(p.chunk_off, p.batch, cw);
+        PackedRange(p, b, tok0, T);
+        t0 = (c0 + cw - p.chunk_off[b]) * kC;
+    }
     const bool live = t0 + m16 < T;
-    const size_t rowbase = ((static_cast<size_t>(b) * T + min(t0 + m16, T - 1)) * H + h) * p.dk;
+    const size_t rowbase = ((tok0 + min(t0 + m16, T - 1)) * H + h) * p.dk;
     float *const blk = p.prepared + static_cast<size_t>(item) * BlockFloats(kq);
     float *const wTr = sw[w][0], *const wA = sw[w][1], *const wT = sw[w][2], *const wTT = sw[w][3];
 
@@ -363,27 +401,29 @@ struct RecurLayout {
     static constexpr int kFloats = KS > 1 ? 2 * KS * 512 : 1;
 };
 
+// One (b,h) row's chunks [cs, cs + nrun) of its sequence, whose prepared
+// blocks sit at window-local indices [cw0, cw0 + nrun) of `prep_row` (the row's
+// wn blocks of the window).  tok0: the sequence's first token in the [B*T]
+// token rows; T: its length; sbase: the row's offset in the [B,H,K,V] states.
+// The state comes from s_in (zeros when null) and goes to s_out (not written
+// when null).  Every wave of the workgroup calls it with the same arguments.
 template <int KPW, int KS>
-__global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Params p, int c0, int wn,
-                                                                const float *s_in, float *s_out) {
+__device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, float *sXp, int h, size_t tok0, int T,
+                                             int cs, int cw0, int nrun, int wn, const float *prep_row, size_t sbase,
+                                             const float *s_in, float *s_out) {
     using L = RecurLayout<KPW, KS>;
     constexpr int KQ = L::KQ, FB = L::FB;
     constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oG = 3 * KQ * 256;   // block offsets (floats)
     constexpr int oT = oG + 16 * KQ, oMT = oT + 256, oMul = oT + 512;
-    __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
 
-    const int T = p.seqlen, H = p.nheads, dk = p.dk, dv = p.dv;
+    const int H = p.nheads, dk = p.dk, dv = p.dv;
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4;
     const int VT = (dv + 15) / 16;
-    const int blk = XcdLocalBlock(blockIdx.x, gridDim.x);
-    const int bh = blk / VT, vt = blk % VT;
-    const int b = bh / H, h = bh % H;
+    const int vt = XcdLocalBlock(blockIdx.x, gridDim.x) % VT;
     const int col = vt * 16 + (lane & 15);
     const bool col_ok = col < dv;
-    const size_t sbase = static_cast<size_t>(bh) * dk * dv;
-    const float *const prep0 = p.prepared + static_cast<size_t>(bh) * wn * FB;
-    const Rsrc rblk = MakeRsrc(prep0, wn * FB * 4);   // this head's prepared blocks of the window
+    const Rsrc rblk = MakeRsrc(prep_row, wn * FB * 4);   // this head row's prepared blocks of the window
     // byte offsets, from a chunk's first token in [B,T,H,V], of this lane's
     // tokens 4(l/16)+i in its column (out of range for columns past dv); the
     // per-chunk descriptors of w, v and out end after the chunk's last valid
@@ -393,7 +433,7 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
 #pragma unroll
     for (int i = 0; i < 4; ++i) vo[i] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
     auto rows_bytes = [&](int t0) { return ((min(T - t0, kC) - 1) * HV + dv) * 4; };
-    auto token_base = [&](const float *x, int t0) { return x + ((static_cast<size_t>(b) * T + t0) * H + h) * dv; };
+    auto token_base = [&](const float *x, int t0) { return x + ((tok0 + t0) * H + h) * dv; };
 
     v4f S[KPW];
 #pragma unroll
@@ -406,124 +446,128 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
         }
     }
 
-    // Loads are issued on every path (chunk indices clamped to the window):
-    // with a load count that depends on the path, the compiler's wait counts
-    // turn conservative and a consumer waits for the newest prefetches too.
-    const int lo = lane * 16, go = g4 * 16;   // a lane's 16 bytes of a tile; a lane group's of a row vector
-    auto load_ops = [&](int cw, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
-        const int sb = cw * (FB * 4);
+    if (nrun > 0) {   // workgroup-uniform
+        // Loads are issued on every path (chunk indices clamped to the range):
+        // with a load count that depends on the path, the compiler's wait
+        // counts turn conservative and a consumer waits for the newest
+        // prefetches too.
+        const int lo = lane * 16, go = g4 * 16;   // a lane's 16 bytes of a tile; a lane group's of a row vector
+        auto load_ops = [&](int j, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
+            const int sb = (cw0 + j) * (FB * 4);
 #pragma unroll
-        for (int kt = 0; kt < KPW; ++kt) {
-            const int kg = ks * KPW + kt;
-            o.e[kt] = BufF4(rblk, lo, sb + (oE + kg * 256) * 4);
-            o.r[kt] = BufF4(rblk, lo, sb + (oR + kg * 256) * 4);
-        }
-        const int t0 = (c0 + cw) * kC;
-        const Rsrc rw = MakeRsrc(token_base(p.w, t0), rows_bytes(t0));
-        const Rsrc rv = MakeRsrc(token_base(p.v, t0), rows_bytes(t0));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o.w[i] = BufF(rw, vo[i]);
-            o.v[i] = BufF(rv, vo[i]);
-        }
-        o.km = BufF4(rblk, go, sb + (oMul + 16) * 4);
-        o.t = BufF4(rblk, lo, sb + oT * 4);
-        o.qm = BufF4(rblk, go, sb + oMul * 4);
-        o.mt = BufF4(rblk, lo, sb + oMT * 4);
-#pragma unroll
-        for (int kt = 0; kt < KPW; ++kt) {
-            const int kg = ks * KPW + kt;
-            o.g[kt] = BufF4(rblk, go, sb + (oG + kg * 16) * 4);
-            o.ut[kt] = BufF4(rblk, lo, sb + (oU + kg * 256) * 4);
-        }
-    };
-
-    // One chunk: partial E' S0, R' S0 over this wave's keys, summed across the
-    // KS waves (one barrier; the partial buffers alternate by chunk parity, so
-    // a wave that runs ahead writes the other buffer, and cannot run two
-    // chunks ahead past the next barrier); y = WV - km o E' S0; U = T y;
-    // O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut'^T (km o U).  The
-    // operand set then receives chunk cw + 2.
-    // the output of a chunk, O = q_mul o R' S0 + (M T) Y, as this wave's
-    // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the 4
-    // with ii % KS == ks); published with the next chunk's E' S0 partials and summed
-    // by wave 0, so the output products are spread over the waves
-    v4f op = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto store_out = [&](int t0, const v4f &out) __attribute__((always_inline)) {
-        const Rsrc ro = MakeRsrc(token_base(p.out, t0), rows_bytes(t0));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
-    };
-    auto sum_out = [&](const float *xp) __attribute__((always_inline)) -> v4f {
-        v4f out = LdsF4(xp + 256 + lane * 4);
-#pragma unroll
-        for (int z = 1; z < KS; ++z) out += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
-        return out;
-    };
-    auto step = [&](int cw, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
-        const int t0 = (c0 + cw) * kC;
-        v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
-#pragma unroll
-        for (int kt = 0; kt < KPW; ++kt) {
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                xe = Mfma(o.e[kt][ii], S[kt][ii], xe);
-                xr = Mfma(o.r[kt][ii], S[kt][ii], xr);
+            for (int kt = 0; kt < KPW; ++kt) {
+                const int kg = ks * KPW + kt;
+                o.e[kt] = BufF4(rblk, lo, sb + (oE + kg * 256) * 4);
+                o.r[kt] = BufF4(rblk, lo, sb + (oR + kg * 256) * 4);
             }
-        }
-        if constexpr (KS > 1) {
-            float *const xp = sXp + (cw & 1) * (KS * 512);
-            StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
-            StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);   // output partial of chunk cw - 1
-            __syncthreads();
-            // the same summation order in every wave: identical U everywhere
-            xe = LdsF4(xp + lane * 4);
+            const int t0 = (cs + j) * kC;
+            const Rsrc rw = MakeRsrc(token_base(p.w, t0), rows_bytes(t0));
+            const Rsrc rv = MakeRsrc(token_base(p.v, t0), rows_bytes(t0));
 #pragma unroll
-            for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
-            if (ks == 0 && cw > 0) store_out(t0 - kC, sum_out(xp));
-        }
-        v4f y;   // w, v are zero past the sequence end and dv
+            for (int i = 0; i < 4; ++i) {
+                o.w[i] = BufF(rw, vo[i]);
+                o.v[i] = BufF(rv, vo[i]);
+            }
+            o.km = BufF4(rblk, go, sb + (oMul + 16) * 4);
+            o.t = BufF4(rblk, lo, sb + oT * 4);
+            o.qm = BufF4(rblk, go, sb + oMul * 4);
+            o.mt = BufF4(rblk, lo, sb + oMT * 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) y[i] = o.w[i] * o.v[i] - o.km[i] * xe[i];   // rows of E' S0 times k_mul
-        v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
-        op = o.qm * xr;   // rows of R' S0 times q_mul
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-            if (ii % KS == ks) op = Mfma(o.mt[ii], y[ii], op);   // wave-uniform
-        if constexpr (KS == 1) store_out(t0, op);
-        const v4f uk = o.km * u;   // the update's Ut' is unnormalised
-#pragma unroll
-        for (int kt = 0; kt < KPW; ++kt) {
-            S[kt] *= o.g[kt];
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], uk[ii], S[kt]);
-        }
-        load_ops(min(cw + 2, wn - 1), o);
-    };
+            for (int kt = 0; kt < KPW; ++kt) {
+                const int kg = ks * KPW + kt;
+                o.g[kt] = BufF4(rblk, go, sb + (oG + kg * 16) * 4);
+                o.ut[kt] = BufF4(rblk, lo, sb + (oU + kg * 256) * 4);
+            }
+        };
 
-    // two operand sets in turn, with compile-time roles
-    // (the sets' loads in the same order as in the loop: an interleaved
-    // prologue would set the loop's wait counts to its own, shorter distances)
-    ChunkOperands<KPW> opa, opb;
-    load_ops(0, opa);
-    __builtin_amdgcn_sched_barrier(0);
-    load_ops(min(1, wn - 1), opb);
-    // each step leaves the loop or goes on to the other set's step: a path
-    // from one set's step back to itself (no newer loads outstanding, to the
-    // compiler) would take its wait counts to zero
-    for (int cw = 0;; cw += 2) {
-        step(cw, opa);
-        if (cw + 1 >= wn) break;
-        step(cw + 1, opb);
-        if (cw + 2 >= wn) break;
-    }
-    if constexpr (KS > 1) {   // output of the last chunk
-        float *const xp = sXp + (wn & 1) * (KS * 512);
-        StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);
-        __syncthreads();
-        if (ks == 0) store_out((c0 + wn - 1) * kC, sum_out(xp));
+        // One chunk: partial E' S0, R' S0 over this wave's keys, summed across
+        // the KS waves (one barrier; the partial buffers alternate by chunk
+        // parity, so a wave that runs ahead writes the other buffer, and cannot
+        // run two chunks ahead past the next barrier); y = WV - km o E' S0;
+        // U = T y; O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut'^T
+        // (km o U).  The operand set then receives chunk j + 2.
+        // The output of a chunk, O = q_mul o R' S0 + (M T) Y, as this wave's
+        // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the
+        // 4 with ii % KS == ks); published with the next chunk's E' S0 partials
+        // and summed by wave 0, so the output products are spread over the waves.
+        v4f op = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto store_out = [&](int t0, const v4f &out) __attribute__((always_inline)) {
+            const Rsrc ro = MakeRsrc(token_base(p.out, t0), rows_bytes(t0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
+        };
+        auto sum_out = [&](const float *xp) __attribute__((always_inline)) -> v4f {
+            v4f out = LdsF4(xp + 256 + lane * 4);
+#pragma unroll
+            for (int z = 1; z < KS; ++z) out += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
+            return out;
+        };
+        auto step = [&](int j, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
+            const int t0 = (cs + j) * kC;
+            v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
+#pragma unroll
+            for (int kt = 0; kt < KPW; ++kt) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    xe = Mfma(o.e[kt][ii], S[kt][ii], xe);
+                    xr = Mfma(o.r[kt][ii], S[kt][ii], xr);
+                }
+            }
+            if constexpr (KS > 1) {
+                float *const xp = sXp + (j & 1) * (KS * 512);
+                StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
+                StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);   // output partial of chunk j - 1
+                __syncthreads();
+                // the same summation order in every wave: identical U everywhere
+                xe = LdsF4(xp + lane * 4);
+#pragma unroll
+                for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
+                if (ks == 0 && j > 0) store_out(t0 - kC, sum_out(xp));
+            }
+            v4f y;   // w, v are zero past the sequence end and dv
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[i] = o.w[i] * o.v[i] - o.km[i] * xe[i];   // rows of E' S0 times k_mul
+            v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
+            op = o.qm * xr;   // rows of R' S0 times q_mul
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+                if (ii % KS == ks) op = Mfma(o.mt[ii], y[ii], op);   // wave-uniform
+            if constexpr (KS == 1) store_out(t0, op);
+            const v4f uk = o.km * u;   // the update's Ut' is unnormalised
+#pragma unroll
+            for (int kt = 0; kt < KPW; ++kt) {
+                S[kt] *= o.g[kt];
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], uk[ii], S[kt]);
+            }
+            load_ops(min(j + 2, nrun - 1), o);
+        };
+
+        // two operand sets in turn, with compile-time roles
+        // (the sets' loads in the same order as in the loop: an interleaved
+        // prologue would set the loop's wait counts to its own, shorter distances)
+        ChunkOperands<KPW> opa, opb;
+        load_ops(0, opa);
+        __builtin_amdgcn_sched_barrier(0);
+        load_ops(min(1, nrun - 1), opb);
+        // each step leaves the loop or goes on to the other set's step: a path
+        // from one set's step back to itself (no newer loads outstanding, to the
+        // compiler) would take its wait counts to zero
+        for (int j = 0;; j += 2) {
+            step(j, opa);
+            if (j + 1 >= nrun) break;
+            step(j + 1, opb);
+            if (j + 2 >= nrun) break;
+        }
+        if constexpr (KS > 1) {   // output of the last chunk
+            float *const xp = sXp + (nrun & 1) * (KS * 512);
+            StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);
+            __syncthreads();
+            if (ks == 0) store_out((cs + nrun - 1) * kC, sum_out(xp));
+            __syncthreads();   // the partial buffers are reused by the workgroup's next run
+        }
     }
     if (s_out != nullptr && col_ok) {
 #pragma unroll
@@ -533,6 +577,51 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
             for (int i = 0; i < 4; ++i)
                 if (kb + i < dk) s_out[sbase + static_cast<size_t>(kb + i) * dv + col] = S[kt][i];
         }
+    }
+}
+
+// Unpacked: a workgroup owns (b, h, column tile) and the window's wn chunks
+// of its sequence, the state from s_in to s_out.
+// Packed (chunk_off set): the window holds chunks [c0, c0 + W) of every
+// sequence, sequence b's at blocks [chunk_off[b], chunk_off[b + 1]) of each
+// head's wn blocks.  Workgroup (slot, h, column tile) takes sequences slot,
+// slot + slots, ... that have chunks in the window.  A range that starts the
+// sequence reads initial_state (zeros when absent), any other the carry
+// (p.state); one that ends it writes final_state (if requested), any other
+// the carry, in place: a workgroup reads and writes only its own rows and
+// columns.
+template <int KPW, int KS, bool PACKED>
+__global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Params p, int c0, int wn,
+                                                                const float *s_in, float *s_out) {
+    using L = RecurLayout<KPW, KS>;
+    __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
+    const int H = p.nheads;
+    const int VT = (p.dv + 15) / 16;
+    const int row = XcdLocalBlock(blockIdx.x, gridDim.x) / VT;
+    const size_t kv = static_cast<size_t>(p.dk) * p.dv;
+    if constexpr (!PACKED) {
+        const int b = row / H, h = row % H;
+        Gdn2RecurRun<KPW, KS>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, c0, 0, wn, wn,
+                              p.prepared + static_cast<size_t>(row) * wn * L::FB, static_cast<size_t>(row) * kv,
+                              s_in, s_out);
+        return;
+    } else {
+    const int n = p.batch;
+    const int slots = static_cast<int>(gridDim.x) / (H * VT);
+    const int slot = row / H, h = row % H;
+    const float *const prep_row = p.prepared + static_cast<size_t>(h) * wn * L::FB;
+    for (int b = slot; b < n; b += slots) {   // workgroup-uniform
+        const int i0 = p.chunk_off[b], nrun = p.chunk_off[b + 1] - i0;
+        if (nrun <= 0) continue;   // no chunks in this window
+        size_t tok0;
+        int T;
+        PackedRange(p, b, tok0, T);
+        const int nch = (T + kC - 1) / kC;
+        const size_t sbase = (static_cast<size_t>(b) * H + h) * kv;
+        const float *in = c0 == 0 ? p.initial_state : p.state;
+        float *out = c0 + nrun == nch ? p.final_state : p.state;
+        Gdn2RecurRun<KPW, KS>(p, sXp, h, tok0, T, c0, i0, nrun, wn, prep_row, sbase, in, out);
+    }
     }
 }
 
@@ -563,11 +652,21 @@ void LaunchRecur(const GatedDeltaNet2Params &p, int c0, int wn, int kq, const fl
                  hipStream_t stream) {
     if (kq != RecurLayout<KPW, KS>::KQ) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
     const int vt = (p.dv + 15) / 16;
-    const long long blocks = static_cast<long long>(p.batch) * p.nheads * vt;
+    // packed: min(sequences, chunks) slots per (h, column tile); a slot's
+    // workgroup takes every slots-th sequence that meets the window
+    const long long rows = p.chunk_off != nullptr ? std::min(p.batch, wn) : p.batch;
+    const long long blocks = rows * p.nheads * vt;
+    if (blocks == 0) return;   // no packed sequences
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-    XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS);
-    hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, stream,
-                       p, c0, wn, s_in, s_out);
+    if (p.chunk_off != nullptr) {
+        XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS, 1);
+        hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, true>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0,
+                           stream, p, c0, wn, s_in, s_out);
+    } else {
+        XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS, 0);
+        hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, false>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0,
+                           stream, p, c0, wn, s_in, s_out);
+    }
 }
 
 void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0, int wn, int kq, const float *s_in,
@@ -581,45 +680,125 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }
 
-// Scratch of one call for a budget of `cap` bytes: the chunks per window (at
-// most 128, fewer when the budget is smaller; 0 when one chunk does not fit)
-// and the bytes of the prepared blocks and of the state carried between
-// windows (only when the sequence spans several windows).
+// Scratch of one call for a budget of `cap` bytes: the chunks per window and
+// sequence (at most 128, fewer when the budget is smaller; 0 when one chunk
+// does not fit) and the bytes of the prepared blocks, of the state carried
+// between windows (only when a sequence can span several windows) and, for
+// packed sequences, of the per-window block offsets.  A window holds chunks
+// [c0, c0 + win) of every sequence.  Unpacked, that is win blocks per (b, h).
+// Packed (batch sequences along one row of seqlen tokens; no sequence is
+// longer than the row), a window's blocks per head are the sequences' chunks
+// in it, stored one sequence after the other: at most min(win * batch,
+// ceil(seqlen / 16) + batch) of them (each sequence's last chunk may be
+// partial); sequence b's start at offs[w][b], [nwin][batch + 1] ints.
 struct WindowPlan {
     int win = 0;
-    size_t blocks = 0, carry = 0;
-    size_t total() const { return blocks + carry; }
+    int nchunks = 0;   // sequence-local chunks the windows step over
+    int slots = 0;     // blocks per head of one window
+    size_t blocks = 0, carry = 0, offsets = 0;
+    size_t total() const { return blocks + carry + offsets; }
 };
 
-WindowPlan PlanWindows(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
+WindowPlan PlanWindows(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
     const ChunkConfig c = ChooseChunk(dk);
-    const size_t per_chunk = static_cast<size_t>(batch) * nheads * BlockFloats(c.kpw * c.ks) * sizeof(float);
+    const size_t rows = static_cast<size_t>(packed ? 1 : batch) * nheads;
+    const size_t per_block = rows * BlockFloats(c.kpw * c.ks) * sizeof(float);
+    const size_t carry = Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float));
     const int nchunks = (seqlen + kC - 1) / kC;
-    WindowPlan w;
-    w.win = std::min(nchunks, kWindowChunks);
-    w.blocks = Align256(per_chunk * w.win);
-    w.carry = w.win < nchunks ? Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float)) : 0;
+    const long long all_blocks = static_cast<long long>(nchunks) + batch;   // packed: every sequence's chunks
+    auto make = [&](int win, bool with_carry) {
+        WindowPlan w;
+        w.win = win;
+        w.nchunks = nchunks;
+        w.slots = packed ? static_cast<int>(std::min<long long>(static_cast<long long>(win) * batch, all_blocks)) : win;
+        w.blocks = Align256(per_block * w.slots);
+        w.carry = with_carry ? carry : 0;
+        const size_t nwin = (nchunks + win - 1) / win;
+        w.offsets = packed ? Align256(nwin * (static_cast<size_t>(batch) + 1) * sizeof(int)) : 0;
+        return w;
+    };
+    const int win0 = std::min(nchunks, kWindowChunks);
+    WindowPlan w = make(win0, win0 < nchunks);
+    if (packed && win0 < nchunks) {
+        // The host does not know the sequences' lengths, so it steps through
+        // windows up to the row's length, the later ones empty when the
+        // sequences are shorter: each costs two launch gaps.  One window over
+        // every chunk avoids them; taken when its blocks stay within twice
+        // the windowed ones or 512 MiB (with sequences of at most 2048
+        // tokens on average the windowed plan already holds every chunk).
+        const WindowPlan one = make(nchunks, false);
+        if (one.blocks <= std::max<size_t>(2 * w.blocks, size_t{512} << 20) && one.total() <= cap) return one;
+    }
     if (w.total() <= cap) return w;
-    // shorter windows: the carry is then always needed
-    w.carry = Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float));
-    const size_t room = cap > w.carry + 256 ? cap - w.carry - 256 : 0;   // 256: the alignment pad
-    w.win = static_cast<int>(std::min<size_t>(room / per_chunk, static_cast<size_t>(w.win)));
-    w.blocks = Align256(per_chunk * w.win);
-    if (w.win < 1) w = WindowPlan{};
-    return w;
+    // shorter windows (the carry is then always needed): the largest that fits
+    for (int win = win0 - 1; win >= 1; --win) {
+        w = make(win, true);
+        if (w.total() <= cap) return w;
+    }
+    return WindowPlan{};
+}
+
+// Packed sequences: for every window w, offs[w][b] = the chunks in [w win,
+// (w + 1) win) of sequences 0..b-1 (b = 0..n): where sequence b's blocks of
+// window w start.  An empty sequence, which no recurrence workgroup visits,
+// passes its initial state (zeros without one) to final_state here.  One
+// workgroup.
+__global__ __launch_bounds__(256) void Gdn2PackedChunksKernel(GatedDeltaNet2Params p, int *offs, int win, int nwin) {
+    __shared__ int part[256];
+    const int n = p.batch, tid = threadIdx.x;
+    const int per = (n + 255) / 256;
+    const int b0 = min(n, tid * per), b1 = min(n, b0 + per);
+    auto chunks = [&](int b) {
+        size_t tok0;
+        int T;
+        PackedRange(p, b, tok0, T);
+        return (T + kC - 1) / kC;
+    };
+    for (int w = 0; w < nwin; ++w) {   // workgroup-uniform
+        int *const off = offs + static_cast<size_t>(w) * (n + 1);
+        auto in_window = [&](int b) { return min(max(chunks(b) - w * win, 0), win); };
+        int sum = 0;
+        for (int b = b0; b < b1; ++b) sum += in_window(b);
+        part[tid] = sum;
+        __syncthreads();
+        if (tid == 0) {   // exclusive prefix of the 256 partial sums
+            int acc = 0;
+            for (int i = 0; i < 256; ++i) {
+                const int v = part[i];
+                part[i] = acc;
+                acc += v;
+            }
+            off[n] = acc;
+        }
+        __syncthreads();
+        int acc = part[tid];
+        for (int b = b0; b < b1; ++b) {
+            off[b] = acc;
+            acc += in_window(b);
+        }
+        __syncthreads();   // part is rewritten by the next window
+    }
+    if (p.final_state != nullptr) {
+        const size_t hkv = static_cast<size_t>(p.nheads) * p.dk * p.dv;
+        for (int b = 0; b < n; ++b) {   // workgroup-uniform
+            if (chunks(b) > 0) continue;
+            float *dst = p.final_state + static_cast<size_t>(b) * hkv;
+            const float *src = p.initial_state != nullptr ? p.initial_state + static_cast<size_t>(b) * hkv : nullptr;
+            for (size_t i = tid; i < hkv; i += 256) dst[i] = src != nullptr ? src[i] : 0.0f;
+        }
+    }
 }
 
 }  // namespace
 
-size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
+size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
     if (dk > kGdn2ChunkKeyLimit) return 0;
-    const WindowPlan w = PlanWindows(batch, seqlen, nheads, dk, dv, cap);
+    const WindowPlan w = PlanWindows(batch, seqlen, nheads, dk, dv, packed, cap);
     return w.win == 0 ? SIZE_MAX : w.total();
 }
 
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, size_t scratch_bytes, void *stream_v) {
     if (GetOverride(kOverrideGdn2Path) == 1) return false;
-    if (p.cu_seqlens != nullptr) return false;   // packed sequences: the fused kernel
     if (p.dk > kGdn2ChunkKeyLimit) return false;
     // the recurrence's 32-bit buffer offsets span 16 tokens of [B,T,H,V]
     if (static_cast<long long>(p.nheads) * p.dv >= (1LL << 25)) return false;
@@ -630,17 +809,30 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
     q.vec4_keys = p.dk % 4 == 0 && a16(p.q) && a16(p.k) && a16(p.g) && a16(p.beta);
     const ChunkConfig c = ChooseChunk(p.dk);
     const int kq = c.kpw * c.ks;
-    const int nchunks = (p.seqlen + kC - 1) / kC;
-    const WindowPlan plan = PlanWindows(p.batch, p.seqlen, p.nheads, p.dk, p.dv, scratch_bytes);
+    const bool packed = p.cu_seqlens != nullptr;
+    const WindowPlan plan = PlanWindows(p.batch, p.seqlen, p.nheads, p.dk, p.dv, packed, scratch_bytes);
     if (plan.win == 0 || plan.total() > scratch_bytes || scratch == nullptr)
         throw Error(XM_ERR_ALLOC, "GatedDeltaNet2Fn: the scratch buffer is smaller than the call needs");
-    const int win = plan.win;
-    const size_t heads = static_cast<size_t>(p.batch) * p.nheads;
+    const int win = plan.win, nchunks = plan.nchunks;
+    // rows of a window's prepared blocks: (b, h), or h for packed sequences
+    const size_t heads = static_cast<size_t>(packed ? 1 : p.batch) * p.nheads;
     char *base = static_cast<char *>(scratch);
     q.prepared = reinterpret_cast<float *>(base);
     float *const carry = plan.carry > 0 ? reinterpret_cast<float *>(base + plan.blocks) : nullptr;
+    int *offs = nullptr;
+    if (packed) {
+        offs = reinterpret_cast<int *>(base + plan.blocks + plan.carry);
+        q.state = carry;
+        q.chunk_off = offs;
+        XM_NOTE_LAUNCH("Gdn2PackedChunksKernel", {}, );
+        hipLaunchKernelGGL(Gdn2PackedChunksKernel, dim3(1), dim3(256), 0, stream, q, offs, win,
+                           (nchunks + win - 1) / win);
+        XM_LAUNCH_CHECK("GatedDeltaNet2Fn packed chunk offsets");
+    }
     for (int c0 = 0; c0 < nchunks; c0 += win) {
-        const int wn = std::min(win, nchunks - c0);
+        // packed: this window's block offsets, and plan.slots blocks per head
+        if (packed) q.chunk_off = offs + static_cast<size_t>(c0 / win) * (p.batch + 1);
+        const int wn = packed ? plan.slots : std::min(win, nchunks - c0);
         const bool first = c0 == 0, last = c0 + wn >= nchunks;
         const long long items = static_cast<long long>(heads) * wn;
         const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
@@ -649,7 +841,10 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
         hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(static_cast<unsigned>(pblocks)), dim3(64 * kPrepWaves), 0, stream,
                            q, c0, wn, kq);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
-        LaunchRecurAny(q, c, c0, wn, kq, first ? p.initial_state : carry, last ? p.final_state : carry, stream);
+        if (packed)   // the kernel picks each sequence's state buffers itself
+            LaunchRecurAny(q, c, c0, wn, kq, nullptr, nullptr, stream);
+        else
+            LaunchRecurAny(q, c, c0, wn, kq, first ? p.initial_state : carry, last ? p.final_state : carry, stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk recurrence");
     }
     return true;

@@ -53,6 +53,9 @@ struct GatedDeltaNet2Params {
     // Packed sequences: [batch + 1] token offsets along a single row of
     // seqlen tokens (the tensors' batch dimension is 1), or nullptr.
     const int64_t *cu_seqlens;
+    // Chunked path with packed sequences: [batch + 1] prefix sums of the
+    // sequences' 16-token chunk counts (device scratch), or nullptr.
+    const int *chunk_off;
 };
 
 // Mamba3SisoFn (reference parameter block: mamba3_siso.h:10-36).
@@ -101,8 +104,11 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_
 // scratch_bytes >= GatedDeltaNet2ChunkScratchBytes(..., scratch_bytes) bytes: the
 // prepared chunk vectors of one window of up to 2048 tokens (shorter windows
 // when the bytes are fewer), and the state carried between windows.
-size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, size_t cap = SIZE_MAX);
-constexpr int kGdn2ChunkKeyLimit = 512;   // head_k handled by the chunked path (packed sequences excepted)
+// With `packed`, batch is the number of sequences packed along one row of
+// seqlen tokens.
+size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed = false,
+                                       size_t cap = SIZE_MAX);
+constexpr int kGdn2ChunkKeyLimit = 512;   // head_k handled by the chunked path
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, size_t scratch_bytes, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
 // Chunked fp32-MFMA path (headdim_qk <= 256).  Returns false, launching
