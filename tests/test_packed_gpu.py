@@ -182,3 +182,75 @@ def test_m3_packed_matches_per_sequence(n_qk, p_dim, hq, with_states, m3_path):
             if nm == "angle":
                 g = r + (np.mod(g - r + two_pi / 2, two_pi) - two_pi / 2)
             check(f"{tag}/{nm}", g, r, TOL_M3)
+
+
+# ---------------------------------------------------------------------------
+# Token rows that no sequence covers
+# ---------------------------------------------------------------------------
+
+def _covered(cu, T):
+    """Tokens covered by the sequences [lo_b, hi_b) (lo_b = clamp(cu[b]), hi_b =
+    clamp(max(cu[b + 1], lo_b)), the kernels' reading of the offsets)."""
+    cov = np.zeros(T, bool)
+    ranges = []
+    for b in range(len(cu) - 1):
+        lo = min(max(cu[b], 0), T)
+        hi = min(max(cu[b + 1], lo), T)
+        cov[lo:hi] = True
+        ranges.append((lo, hi))
+    return cov, ranges
+
+
+GAP_CASES = {"head_and_tail_gaps": ([3, 20, 20, 50], 64), "non_monotone": ([10, 12, 2, 4], 16)}
+
+
+@pytest.mark.parametrize("case", sorted(GAP_CASES))
+def test_gdn2_packed_uncovered_rows_are_zero(case, gdn2_path):
+    """Offsets that leave token rows outside every sequence (cu[0] > 0,
+    cu[N] < T, or non-monotone offsets): those rows of the output are zeros
+    (the buffer holds NaN before the call); the covered rows match the oracle
+    per sequence."""
+    import torch
+    cu, T = GAP_CASES[case]
+    H, dk, dv = 2, 32, 16
+    s = W.GatedDeltaNet2Shape(1, T, H, dk, dv, initial_state=False)
+    inp = W.gated_deltanet2_inputs(s, seed=51)
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda")
+    call = gated_deltanet2_fn(*(to_dev(inp[k]) for k in GDN_KEYS), None, scale=s.scale, cu_seqlens=cu_t,
+                              prepare=True)
+    call.out.fill_(float("nan"))
+    o = call().cpu().numpy()
+    cov, ranges = _covered(cu, T)
+    assert np.all(o[:, ~cov] == 0.0)
+    for n, (lo, hi) in enumerate(ranges):
+        if hi > lo:
+            part = [np.ascontiguousarray(inp[k][:, lo:hi]) for k in GDN_KEYS]
+            ro = cref.gated_deltanet2(*part, None, scale=s.scale, use_qk_l2norm=s.l2norm, dtype=np.float64)
+            check(f"gdn2_packed_gaps/{case}/{gdn2_path}/seq{n}", o[:, lo:hi], ro, TOL_GDN2)
+
+
+@pytest.mark.parametrize("case", sorted(GAP_CASES))
+def test_m3_packed_uncovered_rows_are_zero(case, m3_path):
+    import torch
+    cu, T = GAP_CASES[case]
+    s = W.Mamba3SisoShape(1, T, 2, 16, 32, has_z=True)
+    inp = W.mamba3_siso_inputs(s, seed=52)
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda")
+    call = mamba3_siso_fn(*(to_dev(inp[k]) for k in M3_KEYS), cu_seqlens=cu_t, prepare=True)
+    call.out.fill_(float("nan"))
+    y = call().cpu().numpy()
+    cov, ranges = _covered(cu, T)
+    assert np.all(y[:, ~cov] == 0.0)
+    for n, (lo, hi) in enumerate(ranges):
+        if hi > lo:
+            part = {}
+            for k in M3_KEYS:
+                x = inp[k]
+                if x is None or k in ("Q_bias", "K_bias", "D"):
+                    part[k] = x
+                elif k in ("ADT", "DT", "Trap"):
+                    part[k] = np.ascontiguousarray(x[:, :, lo:hi])
+                else:
+                    part[k] = np.ascontiguousarray(x[:, lo:hi])
+            ry = cref.mamba3_siso(*(part[k] for k in M3_KEYS), dtype=np.float64)
+            check(f"m3_packed_gaps/{case}/{m3_path}/seq{n}", y[:, lo:hi], ry, TOL_M3)

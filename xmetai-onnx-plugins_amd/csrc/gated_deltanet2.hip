@@ -672,6 +672,9 @@ size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int
 }
 
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_bytes, void *stream_v) {
+    // packed: token rows outside every sequence are zeros, not left unwritten
+    if (p.cu_seqlens != nullptr)
+        LaunchPackedGaps(p.out, static_cast<size_t>(p.nheads) * p.dv, p.cu_seqlens, p.batch, p.seqlen, stream_v);
     // dk <= 512: gated_deltanet2_chunk.hip (the fused kernel under the gdn2_path override)
     if (LaunchGatedDeltaNet2Chunked(p, scratch, scratch_bytes, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);

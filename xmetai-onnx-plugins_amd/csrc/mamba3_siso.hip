@@ -432,6 +432,9 @@ void LaunchKPT(const Mamba3SisoParams &p, hipStream_t stream) {
 }  // namespace
 
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream_v) {
+    // packed: token rows outside every sequence are zeros, not left unwritten
+    if (p.cu_seqlens != nullptr)
+        LaunchPackedGaps(p.out, static_cast<size_t>(p.nheads) * p.p, p.cu_seqlens, p.batch, p.seqlen, stream_v);
     if (LaunchMamba3SisoChunked(p, stream_v)) return;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     const int kpt = (p.n + 15) / 16;

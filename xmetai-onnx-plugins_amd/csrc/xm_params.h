@@ -116,5 +116,9 @@ void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);
 bool LaunchMamba3SisoChunked(const Mamba3SisoParams &p, void *stream);
 // Enqueues a kernel that writes `count` zeros (no memset node in a captured graph).
 void LaunchFillZeros(float *dst, size_t count, void *stream);
+// Packed sequences: enqueues a kernel that zeros the token rows of out
+// ([seqlen][row_floats]) outside every sequence [cu[b], cu[b + 1]) (clamped as
+// the operator kernels clamp them); run before the operator's kernels.
+void LaunchPackedGaps(float *out, size_t row_floats, const int64_t *cu, int n, int seqlen, void *stream);
 
 }  // namespace xm

@@ -71,6 +71,51 @@ void LaunchFillZeros(float *dst, size_t count, void *stream) {
 }
 
 namespace {
+// Packed sequences: zeros the token rows of `out` ([seqlen][row_floats]) that
+// no sequence covers.  Sequence b covers [lo_b, hi_b), lo_b = clamp(cu[b]),
+// hi_b = clamp(max(cu[b + 1], lo_b)), the ranges the operator kernels use;
+// non-decreasing offsets cover exactly [lo_0, hi_{n-1}), other offsets are
+// checked sequence by sequence (malformed input: time linear in n per row).
+// A workgroup takes rows blockIdx.x, blockIdx.x + gridDim.x, ...
+__global__ __launch_bounds__(256) void PackedGapsKernel(float *out, size_t row_floats, const int64_t *cu, int n,
+                                                        int seqlen) {
+    __shared__ int s_monotone;
+    if (threadIdx.x == 0) s_monotone = 1;
+    __syncthreads();
+    bool mono = true;
+    for (int b = threadIdx.x; b < n; b += blockDim.x) mono = mono && cu[b] <= cu[b + 1];
+    if (!mono) s_monotone = 0;
+    __syncthreads();
+    const bool monotone = s_monotone != 0;
+    const long long L = seqlen;
+    auto clampt = [&](long long x) { return min(max(x, 0LL), L); };
+    const long long first = clampt(cu[0]), last = clampt(max(cu[n], first));
+    for (long long t = blockIdx.x; t < L; t += gridDim.x) {   // workgroup-uniform
+        bool covered = false;
+        if (monotone) {
+            covered = t >= first && t < last;
+        } else {
+            for (int b = 0; b < n && !covered; ++b) {
+                const long long lo = clampt(cu[b]), hi = clampt(max(cu[b + 1], lo));
+                covered = t >= lo && t < hi;
+            }
+        }
+        if (!covered)
+            for (size_t i = threadIdx.x; i < row_floats; i += blockDim.x) out[static_cast<size_t>(t) * row_floats + i] = 0.0f;
+    }
+}
+}  // namespace
+
+void LaunchPackedGaps(float *out, size_t row_floats, const int64_t *cu, int n, int seqlen, void *stream) {
+    if (seqlen <= 0 || row_floats == 0) return;
+    const int blocks = std::min(seqlen, 1024);
+    XM_NOTE_LAUNCH("PackedGapsKernel", {}, );
+    hipLaunchKernelGGL(PackedGapsKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), out, row_floats, cu, n, seqlen);
+    XM_LAUNCH_CHECK("packed sequence gaps");
+}
+
+namespace {
 std::mutex g_attr_mu;
 std::map<std::pair<const void *, int>, int> g_dyn_lds;   // (kernel, device) -> dynamic LDS limit set
 }  // namespace
