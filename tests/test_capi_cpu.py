@@ -280,11 +280,18 @@ def test_gdn2_valid_and_scratch():
     # of up to 128 chunks, E, R, Ut tiles (256 floats per 16 keys each), G_15
     # (16 per 16 keys), T and M T (256 each), q and k multipliers (16 each);
     # keys padded to 16 * kpw * ks (kpw = 2 and ks = ceil(tiles / 2) up to 128
-    # keys, kpw = 4 and ks = ceil(tiles / 4) above);
+    # keys; 3 tiles x 4 waves for 129-192 keys; 3 tiles x 8 waves for 257-384
+    # keys when the launch has fewer than 128 column-tile workgroups; else
+    # kpw = 4 and ks = ceil(tiles / 4));
     # plus the state carried between windows when there is more than one
     def chunk_scratch(B, T, H, K, V):
         kq = -(-K // 16)
-        if kq > 8:
+        groups = B * H * -(-V // 16)
+        if 8 < kq <= 12:
+            kpw, ks = 3, 4
+        elif 16 < kq <= 24 and groups < 128:
+            kpw, ks = 3, 8
+        elif kq > 8:
             kpw, ks = 4, -(-kq // 4)
         else:
             kpw = 2 if kq >= 2 else 1

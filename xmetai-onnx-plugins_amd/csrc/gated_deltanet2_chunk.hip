@@ -634,13 +634,26 @@ struct ChunkConfig {
 // 65-96 keys measured 11-12% faster).  Fewer splits leave too few
 // waves for the chip (one wave per SIMD at best, and half the SIMDs idle for
 // 4 x 16 heads of 128 x 128): four tiles per wave measured 7-28% slower
-// there.  Above 128 keys, four key tiles per wave and 3-8 waves (keys padded
-// to 64 ks): the cross-wave exchange shrinks, and at most 512 threads keeps
-// the register cap at 256 (two tiles per wave with 10-16 waves spill).
-// Measured 11-22% faster than two tiles per wave for 160-256 keys.
-ChunkConfig ChooseChunk(int dk) {
+// there.  Above 128 keys, three or four key tiles per wave (at most 512
+// threads keep the register cap at 256; two tiles per wave with 10-16 waves
+// spill), measured 11-22% faster than two tiles per wave for 160-256 keys.
+// A CU has 4 SIMDs, so 5-7 waves put two on some SIMD, whose doubled MFMA
+// work every chunk's barrier waits for: 129-192 keys take 4 waves of 3
+// tiles (3 waves of 4 before: -2 to -9%); 257-384 keys take 8 waves of 3
+// tiles when the launch has fewer column-tile workgroups than half the CUs
+// (2 x 2048 x 4 heads at 320-384 x 64: -7 to -11%), and 4 tiles in
+// ceil(tiles / 4) waves otherwise (the padding to 24 tiles costs more than
+// the imbalance when every CU has work: 4 x 2048 x 32 heads at 320 x 64,
+// +7%).  The gdn2_kpw4 override keeps 4 tiles and ceil(tiles / 4) waves
+// above 128 keys.  `groups`: the launch's column-tile workgroups.
+ChunkConfig ChooseChunk(int dk, long long groups) {
     const int kq = (dk + 15) / 16;
-    if (kq > 8) return ChunkConfig{4, (kq + 3) / 4};
+    if (kq > 8) {
+        if (GetOverride(kOverrideGdn2Kpw4) == 1) return ChunkConfig{4, (kq + 3) / 4};
+        if (kq <= 12) return ChunkConfig{3, 4};
+        if (kq > 16 && kq <= 24 && groups < 128) return ChunkConfig{3, 8};
+        return ChunkConfig{4, (kq + 3) / 4};
+    }
     ChunkConfig c{kq >= 2 ? 2 : 1, 1};
     const int need = (kq + c.kpw - 1) / c.kpw;
     c.ks = need;
@@ -674,8 +687,8 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
 #define XM_GDN2_RECUR(KPW_, KS_) \
     if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecur<KPW_, KS_>(p, c0, wn, kq, s_in, s_out, stream);
     XM_GDN2_RECUR(1, 1) XM_GDN2_RECUR(2, 1) XM_GDN2_RECUR(2, 2) XM_GDN2_RECUR(2, 3) XM_GDN2_RECUR(2, 4)
-    XM_GDN2_RECUR(4, 3) XM_GDN2_RECUR(4, 4) XM_GDN2_RECUR(4, 5) XM_GDN2_RECUR(4, 6) XM_GDN2_RECUR(4, 7)
-    XM_GDN2_RECUR(4, 8)
+    XM_GDN2_RECUR(3, 4) XM_GDN2_RECUR(3, 8) XM_GDN2_RECUR(4, 3) XM_GDN2_RECUR(4, 4) XM_GDN2_RECUR(4, 5)
+    XM_GDN2_RECUR(4, 6) XM_GDN2_RECUR(4, 7) XM_GDN2_RECUR(4, 8)
 #undef XM_GDN2_RECUR
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }
@@ -700,7 +713,7 @@ struct WindowPlan {
 };
 
 WindowPlan PlanWindows(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
-    const ChunkConfig c = ChooseChunk(dk);
+    const ChunkConfig c = ChooseChunk(dk, static_cast<long long>(batch) * nheads * ((dv + 15) / 16));
     const size_t rows = static_cast<size_t>(packed ? 1 : batch) * nheads;
     const size_t per_block = rows * BlockFloats(c.kpw * c.ks) * sizeof(float);
     const size_t carry = Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float));
@@ -807,7 +820,7 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
     q.pairwise_only = GetOverride(kOverrideGdn2Pairwise) != 0;
     auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
     q.vec4_keys = p.dk % 4 == 0 && a16(p.q) && a16(p.k) && a16(p.g) && a16(p.beta);
-    const ChunkConfig c = ChooseChunk(p.dk);
+    const ChunkConfig c = ChooseChunk(p.dk, static_cast<long long>(p.batch) * p.nheads * ((p.dv + 15) / 16));
     const int kq = c.kpw * c.ks;
     const bool packed = p.cu_seqlens != nullptr;
     const WindowPlan plan = PlanWindows(p.batch, p.seqlen, p.nheads, p.dk, p.dv, packed, scratch_bytes);

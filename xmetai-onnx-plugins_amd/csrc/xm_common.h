@@ -145,6 +145,7 @@ enum Override {
     kOverrideM3Path,         // 1: Mamba3SisoFn token-by-token kernel
     kOverrideSsLpc,          // lanes per channel of the selective scan (dstate <= 16)
     kOverrideSsSplit,        // selective scan: 1 channel blocks only, 2 sequence-split
+    kOverrideGdn2Kpw4,       // 1: GDN-2 chunked recurrence above 128 keys with 4 key tiles per wave, ceil(tiles/4) waves
     kOverrideCount
 };
 int64_t GetOverride(Override which);
