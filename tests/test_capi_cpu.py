@@ -299,8 +299,13 @@ def test_gdn2_valid_and_scratch():
         kq = kpw * ks
         block = 3 * kq * 256 + 16 * kq + 512 + 32
         nch = -(-T // 16)
+        # windows of 128 chunks, or of up to 128 MiB of blocks, balanced in length
+        per_block = B * H * block * 4
         win = min(nch, 128)
-        return a256(B * H * win * block * 4) + (a256(B * H * K * V * 4) if nch > 128 else 0)
+        fit = min((128 << 20) // per_block, nch)
+        if fit > win:
+            win = -(-nch // -(-nch // fit))
+        return a256(per_block * win) + (a256(B * H * K * V * 4) if win < nch else 0)
     assert scratch == chunk_scratch(2, 5, 3, 16, 8)
     for T, K, V in ((100, 128, 64), (3000, 128, 128), (17, 100, 7), (2049, 256, 16), (2048, 33, 40),
                     (3000, 512, 64), (40, 300, 16), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8)):

@@ -93,6 +93,24 @@ def test_gdn2_parity(name, path, override):
     check(f"gated_deltanet2/{name}/{path}", run_gpu(inp, s), run_ref(inp, s), TOL_GDN2, ref32=ref32)
 
 
+WINDOW_CASES = ["k96_t2100_three_waves_window_carry", "t2100_two_carries", "t2100_k320_window_carry",
+                "t2060_k512_window_carry_perkey"]
+
+
+@pytest.mark.parametrize("name", WINDOW_CASES)
+def test_gdn2_windows_of_128_chunks(name, override):
+    """The chunked path stepped in 128-chunk windows (gdn2_windowed; the
+    default sizes windows to 128 MiB of blocks, one window at these shapes):
+    the state crosses windows through the carry."""
+    import xmetai_onnx_plugins as xp
+    s = CASES[name]
+    override("gdn2_windowed", 1)
+    inp = W.gated_deltanet2_inputs(s, seed=0)
+    got = run_gpu(inp, s)
+    assert any(k.startswith("Gdn2ChunkPrepKernel x") for k in xp.last_launches()), xp.last_launches()
+    check(f"gated_deltanet2/{name}/windows128", got, run_ref(inp, s), TOL_GDN2)
+
+
 @pytest.mark.parametrize("shape", [(1, 37, 2, 64, 40), (2, 50, 2, 128, 33), (1, 20, 1, 256, 16), (1, 9, 2, 5, 3)])
 def test_gdn2_chunk_pairwise_fallback(shape, override):
     """The chunked path with every chunk on the pairwise decay products."""

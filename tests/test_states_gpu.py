@@ -145,6 +145,19 @@ def test_gdn2_final_state_parity(name):
     np.testing.assert_array_equal(o, gdn_gpu(inp, s, state=False))   # the state write leaves o alone
 
 
+@pytest.mark.parametrize("name", ["t4100_three_windows", "k448_t2100_window_carry"])
+def test_gdn2_final_state_windows_of_128_chunks(name, override):
+    """The final state after 128-chunk windows (gdn2_windowed), the state
+    carried between them."""
+    s = GDN_CASES[name]
+    inp = W.gated_deltanet2_inputs(s, seed=6)
+    override("gdn2_windowed", 1)
+    o, st = gdn_gpu(inp, s)
+    ref_o, ref_st = gdn_ref(inp, s)
+    check(f"gated_deltanet2_state/{name}/windows128/o", o, ref_o, TOL_GDN2)
+    check(f"gated_deltanet2_state/{name}/windows128/S", st, ref_st, TOL_GDN2)
+
+
 @pytest.mark.parametrize("rows", [1, 2, 4])
 def test_gdn2_final_state_rows_per_column(rows, override):
     s = S(2, 37, 3, 64, 40)

@@ -730,9 +730,25 @@ WindowPlan PlanWindows(int batch, int seqlen, int nheads, int dk, int dv, bool p
         w.offsets = packed ? Align256(nwin * (static_cast<size_t>(batch) + 1) * sizeof(int)) : 0;
         return w;
     };
-    const int win0 = std::min(nchunks, kWindowChunks);
+    int win0 = std::min(nchunks, kWindowChunks);
+    if (!packed && GetOverride(kOverrideGdn2Windowed) != 1) {
+        // Windows of up to 128 MiB of blocks, balanced in length: fewer
+        // launches, and preparation launches with enough waves to fill the
+        // chip (a 128-chunk window of a few heads is about one wave per SIMD,
+        // latency-bound).  Measured against 128-chunk windows (interleaved):
+        // 1 x 8192 x 4 heads at 128 x 128 0.503 -> 0.452 ms; 1 x 16384 x 16
+        // at 64 x 64 0.953 -> 0.897; 2 x 8192 x 8 at 128 x 128 0.584 ->
+        // 0.564; 1 x 16384 x 8 at 256 x 256 1.615 -> 1.545 (four windows of
+        // 107 MB; two of 214 MB took 1.745, their blocks falling out of the
+        // 256 MB last-level cache before the recurrence reads them).
+        const size_t fit = std::min<size_t>((size_t{128} << 20) / per_block, static_cast<size_t>(nchunks));
+        if (fit > static_cast<size_t>(win0)) {
+            const int nwin = (nchunks + static_cast<int>(fit) - 1) / static_cast<int>(fit);
+            win0 = (nchunks + nwin - 1) / nwin;
+        }
+    }
     WindowPlan w = make(win0, win0 < nchunks);
-    if (packed && win0 < nchunks) {
+    if (packed && win0 < nchunks && GetOverride(kOverrideGdn2Windowed) == 0) {
         // The host does not know the sequences' lengths, so it steps through
         // windows up to the row's length, the later ones empty when the
         // sequences are shorter: each costs two launch gaps.  One window over

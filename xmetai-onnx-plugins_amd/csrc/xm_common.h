@@ -146,6 +146,7 @@ enum Override {
     kOverrideSsLpc,          // lanes per channel of the selective scan (dstate <= 16)
     kOverrideSsSplit,        // selective scan: 1 channel blocks only, 2 sequence-split
     kOverrideGdn2Kpw4,       // 1: GDN-2 chunked recurrence above 128 keys with 4 key tiles per wave, ceil(tiles/4) waves
+    kOverrideGdn2Windowed,   // 1: GDN-2 chunked path in windows of 128 chunks (not sized to 128 MiB / one packed window)
     kOverrideCount
 };
 int64_t GetOverride(Override which);

@@ -144,6 +144,7 @@ constexpr OverrideSpec kOverrides[kOverrideCount] = {
     {"ss_lpc", {1, 2, 4, 8, 16, 0}},     // lanes per channel (dstate <= 16)
     {"ss_split", {1, 2, 0}},             // 1: one workgroup per channel block; 2: sequence-split
     {"gdn2_kpw4", {1, 0}},               // 1: GDN-2 chunked, 4 key tiles per wave above 128 keys
+    {"gdn2_windowed", {1, 0}},           // 1: GDN-2 chunked, windows of 128 chunks only
 };
 std::atomic<int64_t> g_override[kOverrideCount];
 
