@@ -347,33 +347,43 @@ def cpu_baseline(op, inputs, budget_s):
 
 # ---------------------------------------------------------------------------
 
+def named_op(name):
+    """A named workload of the CPU-sized selective scan or a GDN-2 dispatch
+    boundary as a prepared call: (host inputs, prepare, algorithmic bytes, tokens)."""
+    from xmetai_onnx_plugins import workloads as W
+    import xmetai_onnx_plugins as xp
+    s = W.NAMED[name]
+    if name.startswith("selective_scan"):
+        keys = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+        inp = W.selective_scan_inputs(s, seed=0)
+        prep = lambda d: xp.selective_scan_fn(*(d[k] for k in keys), delta_softplus=s.delta_softplus, prepare=True)
+        nbytes = W.selective_scan_bytes(s)
+    elif name.startswith("gated_deltanet2"):
+        keys = ("q", "k", "v", "g", "beta", "w", "initial_state")
+        inp = W.gated_deltanet2_inputs(s, seed=0)
+        prep = lambda d: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale, prepare=True)
+        nbytes = W.gated_deltanet2_bytes(s)
+    else:
+        raise SystemExit(f"no prepared form for workload {name}")
+    return inp, prep, nbytes, s.batch * s.seqlen
+
+
+EXTRA_CONFIGS = ("selective_scan_b1_d256_l512_n16", "gated_deltanet2_b1_t16384_h8_k256_v256",
+                 "gated_deltanet2_b2_t2048_h4_k320_v64", "gated_deltanet2_b4_t4096_h16_k128_v65")
+
+
 def time_extra_configs(dev, steps, settle_ms):
     """The reference's other configurations (CPU-sized selective scan, GDN-2
     dispatch boundaries): device time only, same inputs and timing as above."""
     import torch
-    from xmetai_onnx_plugins import workloads as W
     import xmetai_onnx_plugins as xp
     out = {}
-    for name in ("selective_scan_b1_d256_l512_n16", "gated_deltanet2_b1_t16384_h8_k256_v256",
-                 "gated_deltanet2_b2_t2048_h4_k320_v64", "gated_deltanet2_b4_t4096_h16_k128_v65"):
-        s = W.NAMED[name]
-        if name.startswith("selective_scan"):
-            keys = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
-            inp = W.selective_scan_inputs(s, seed=0)
-            prep = lambda d, s=s, keys=keys: xp.selective_scan_fn(*(d[k] for k in keys),
-                                                                  delta_softplus=s.delta_softplus, prepare=True)
-            nbytes = W.selective_scan_bytes(s)
-        else:
-            keys = ("q", "k", "v", "g", "beta", "w", "initial_state")
-            inp = W.gated_deltanet2_inputs(s, seed=0)
-            prep = lambda d, s=s, keys=keys: xp.gated_deltanet2_fn(*(d[k] for k in keys), scale=s.scale,
-                                                                   prepare=True)
-            nbytes = W.gated_deltanet2_bytes(s)
+    for name in EXTRA_CONFIGS:
+        inp, prep, nbytes, tokens = named_op(name)
         d = to_device(inp, dev)
         _, per = time_op(dict(prepare=prep), d, steps, 2, settle_ms)
         kernels = xp.last_launches()
         ms = statistics.median(per)
-        tokens = s.batch * s.seqlen
         out[name] = dict(ms_per_call_median=round(ms, 4), tokens_per_s=tokens / (ms / 1e3),
                          achieved_GBps=round(nbytes / (ms / 1e3) / 1e9, 1), algorithmic_bytes=nbytes,
                          kernels=kernels)
@@ -403,8 +413,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip timing the other reference configurations (reported under 'configs')")
+    ap.add_argument("--override", action="append", default=[], metavar="NAME=VALUE",
+                    help="profile modes only: force a kernel variant (xm_set_kernel_override), e.g. gdn2_path=1")
     ap.add_argument("--mode", default="bench",
-                    help="bench | copy | profile-selective_scan | profile-gated_deltanet2 | profile-mamba3_siso")
+                    help="bench | copy | profile-selective_scan | profile-gated_deltanet2 | profile-mamba3_siso | "
+                         "profile-<workload> for one of the other configurations (" + ", ".join(EXTRA_CONFIGS) + ")")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -434,13 +447,22 @@ def main():
         return
 
     import xmetai_onnx_plugins as xp
+    if args.override and not args.mode.startswith("profile-"):
+        raise SystemExit("--override applies to the profile modes only")
     builders = make_ops()
     if args.mode.startswith("profile-"):
         name = args.mode[len("profile-"):]
-        op = builders[name]()
-        d = to_device(op["gen"](), dev)
-        if "device_extra" in op:
-            d.update(op["device_extra"](dev))
+        for ov in args.override:
+            key, _, val = ov.partition("=")
+            xp.set_kernel_override(key, int(val))
+        if name in builders:
+            op = builders[name]()
+            d = to_device(op["gen"](), dev)
+            if "device_extra" in op:
+                d.update(op["device_extra"](dev))
+        else:   # one of the other configurations, by workload name
+            inp, prep, _, _ = named_op(name)
+            op, d = dict(prepare=prep), to_device(inp, dev)
         wall, per = time_op(op, d, args.steps, args.warmup, args.settle_ms)
         log(f"{name}: {statistics.median(per):.3f} ms/call (median of {args.steps})")
         return
