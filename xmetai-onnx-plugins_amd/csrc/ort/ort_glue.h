@@ -10,6 +10,7 @@
 #endif
 #include <onnxruntime_cxx_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -139,6 +140,7 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t min_inputs
     ThrowIfFailed(api, api.KernelContext_GetInputCount(ctx, &n_inputs));
     if (n_inputs < min_inputs || n_inputs > max_inputs) throw std::runtime_error("unexpected number of inputs");
     std::vector<xm_tensor_t> in(n_inputs);
+    size_t n_bound = 0;   // inputs up to the last one the node binds
     for (size_t i = 0; i < n_inputs; ++i) {
         const OrtValue *v = nullptr;
         ThrowIfFailed(api, api.KernelContext_GetInput(ctx, i, &v));
@@ -149,7 +151,12 @@ void ComputeDeviceOp(const OrtApi &api, OrtKernelContext *ctx, size_t min_inputs
             continue;
         }
         in[i] = Describe(api, v);
+        n_bound = i + 1;
     }
+    // Omitted optional inputs at the end (an empty input name in the graph)
+    // read as absent, the same as a node with fewer inputs.
+    n_inputs = std::max(n_bound, min_inputs);
+    in.resize(n_inputs);
     char err[1024];
     int64_t out_shape[XM_MAX_RANK] = {};
     int32_t out_rank = 0;
