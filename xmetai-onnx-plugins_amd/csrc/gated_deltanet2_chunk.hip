@@ -530,11 +530,6 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
-            op = o.qm * xr;   // rows of R' S0 times q_mul
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                if (ii % KS == ks) op = Mfma(o.mt[ii], y[ii], op);   // wave-uniform
-            if constexpr (KS == 1) store_out(t0, op);
             const v4f uk = o.km * u;   // the update's Ut' is unnormalised
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
@@ -542,6 +537,22 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], uk[ii], S[kt]);
             }
+            // Off the chunk's chain (U, then the update): this wave's K slices
+            // of (M T) Y, chosen by selects rather than branches (a branch per
+            // slice split the region and delayed U behind them).
+            op = o.qm * xr;   // rows of R' S0 times q_mul
+#pragma unroll
+            for (int m = 0; m < (4 + KS - 1) / KS; ++m) {
+                const int sel = ks + m * KS;   // wave-uniform; >= 4 for the waves without a slice
+                float ma = 0.0f, ya = 0.0f;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    ma = sel == ii ? o.mt[ii] : ma;
+                    ya = sel == ii ? y[ii] : ya;
+                }
+                if (m * KS < 4) op = Mfma(ma, ya, op);
+            }
+            if constexpr (KS == 1) store_out(t0, op);
             load_ops(min(j + 2, nrun - 1), o);
         };
 
