@@ -527,14 +527,22 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         for (int r = 0; r < 4; ++r) acc[r] = fmaf(ecum4[r], ys[r], fmaf(qk4[r], gam4[r], dval) * vt[r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) acc = Mfma(m[ks], vt[ks], acc);   // + sum_{s<t} M[t][s] v_s
+        float y[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float y = acc[r];
-            if (p.Z != nullptr) y *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
-            // tokens past the end and rows >= P are dropped
-            if constexpr (LONG) BufStF(chunk_rsrc(p.out + vbase, v_stride, c0), ooff[r], y);
-            else BufStF(ro, off(ooff[r], c0 * vs4), y);
+            y[r] = acc[r];
+            if (p.Z != nullptr) y[r] *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            // tokens past the end and rows >= P are dropped
+            if constexpr (LONG) BufStF(chunk_rsrc(p.out + vbase, v_stride, c0), ooff[r], y[r]);
+            else BufStF(ro, off(ooff[r], c0 * vs4), y[r]);
+        }
+        // the four values stay in four registers until every store is issued:
+        // a store's data register rewritten behind it waits for the store to
+        // complete (stores count in vmcnt on gfx950)
+        asm volatile("" ::"v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
     };
 
     const int nch = (T + kC - 1) / kC;
@@ -547,15 +555,18 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // chunk j+2, preparation of chunk j+1.  The last chunk is peeled.
     if (nch > 0 && product_wave) {   // workgroup-uniform: an empty sequence passes its states through
         __syncthreads();
+        // zr is written only by the Z loads: a write in every iteration (its
+        // zeroing) landed on the registers the previous chunk's output stores
+        // read, and waited for those stores to complete (stores count in
+        // vmcnt on gfx950)
+        float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int j = 0; j + 1 < nch; ++j) {
             const int jf = max(j - 1, 0);   // the chunk to finish (from j = 1 on)
-            float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             if (p.Z != nullptr) load_z(jf * kC, zr);
             products(buf(j), par(j));
             if (j > 0 && w < 2) finish(jf * kC, buf(jf), par(jf), zr);
             __syncthreads();
         }
-        float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (p.Z != nullptr && nch > 1) load_z((nch - 2) * kC, zr);
         products(buf(nch - 1), par(nch - 1));
         if (nch > 1 && w < 2) finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
