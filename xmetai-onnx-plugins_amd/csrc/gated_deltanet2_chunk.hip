@@ -432,8 +432,21 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     int vo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) vo[i] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
-    auto rows_bytes = [&](int t0) { return ((min(T - t0, kC) - 1) * HV + dv) * 4; };
+    // Chunk jl of the run starts kC * HV floats after chunk jl - 1 in w, v and
+    // out: the run's first rows are formed once, a chunk adds its offset (no
+    // 64-bit index arithmetic per chunk).  A chunk's rows end after its last
+    // valid token.
     auto token_base = [&](const float *x, int t0) { return x + ((tok0 + t0) * H + h) * dv; };
+    const float *const w_run = token_base(p.w, cs * kC);
+    const float *const v_run = token_base(p.v, cs * kC);
+    float *const out_run = p.out + ((tok0 + cs * kC) * H + h) * dv;
+    const int cstride = kC * HV;
+    const int full_bytes = ((kC - 1) * HV + dv) * 4;
+    auto rows_bytes = [&](int jl) {
+        const int left = T - (cs + jl) * kC;
+        return left >= kC ? full_bytes : ((left - 1) * HV + dv) * 4;
+    };
+    auto chunk_off = [&](int jl) { return static_cast<long long>(jl) * cstride; };
 
     v4f S[KPW];
 #pragma unroll
@@ -460,9 +473,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                 o.e[kt] = BufF4(rblk, lo, sb + (oE + kg * 256) * 4);
                 o.r[kt] = BufF4(rblk, lo, sb + (oR + kg * 256) * 4);
             }
-            const int t0 = (cs + j) * kC;
-            const Rsrc rw = MakeRsrc(token_base(p.w, t0), rows_bytes(t0));
-            const Rsrc rv = MakeRsrc(token_base(p.v, t0), rows_bytes(t0));
+            const Rsrc rw = MakeRsrc(w_run + chunk_off(j), rows_bytes(j));
+            const Rsrc rv = MakeRsrc(v_run + chunk_off(j), rows_bytes(j));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 o.w[i] = BufF(rw, vo[i]);
@@ -491,8 +503,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // 4 with ii % KS == ks); published with the next chunk's E' S0 partials
         // and summed by wave 0, so the output products are spread over the waves.
         v4f op = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto store_out = [&](int t0, const v4f &out) __attribute__((always_inline)) {
-            const Rsrc ro = MakeRsrc(token_base(p.out, t0), rows_bytes(t0));
+        auto store_out = [&](int jl, const v4f &out) __attribute__((always_inline)) {   // chunk jl of the run
+            const Rsrc ro = MakeRsrc(out_run + chunk_off(jl), rows_bytes(jl));
 #pragma unroll
             for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
         };
@@ -503,7 +515,6 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             return out;
         };
         auto step = [&](int j, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
-            const int t0 = (cs + j) * kC;
             v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
@@ -522,7 +533,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                 xe = LdsF4(xp + lane * 4);
 #pragma unroll
                 for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
-                if (ks == 0 && j > 0) store_out(t0 - kC, sum_out(xp));
+                if (ks == 0 && j > 0) store_out(j - 1, sum_out(xp));
             }
             v4f y;   // w, v are zero past the sequence end and dv
 #pragma unroll
@@ -552,7 +563,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                 }
                 if (m * KS < 4) op = Mfma(ma, ya, op);
             }
-            if constexpr (KS == 1) store_out(t0, op);
+            if constexpr (KS == 1) store_out(j, op);
             load_ops(min(j + 2, nrun - 1), o);
         };
 
@@ -576,7 +587,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             float *const xp = sXp + (nrun & 1) * (KS * 512);
             StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);
             __syncthreads();
-            if (ks == 0) store_out((cs + nrun - 1) * kC, sum_out(xp));
+            if (ks == 0) store_out(nrun - 1, sum_out(xp));
             __syncthreads();   // the partial buffers are reused by the workgroup's next run
         }
     }
