@@ -286,9 +286,9 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
                 }
             }
             if constexpr (LPC == 8) {
-                float z = SwapReduce8x4(y);
-                asm volatile("" : "+v"(z));   // keep the reduction ahead of the branch
-                if ((lane & 8) == 0) rY[q4 * 4 + SwapReducedToken(lane)] = z;
+                // lanes c and c + 8 hold the same sum for the same slot: both
+                // write it (no exec-mask region inside the token loop)
+                rY[q4 * 4 + SwapReducedToken(lane)] = SwapReduce8x4(y);
             } else if constexpr (LPC == 4) {
                 rY[q4 * 4 + SwapReducedToken(lane)] = SwapReduce4x4(y);   // every lane: a distinct (channel, token)
             } else {
