@@ -383,7 +383,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
             v += DppF<0x4E>(v);    // quad_perm [2,3,0,1]
             v += DppF<0x141>(v);   // row_half_mirror: the 8 lanes of a half row
             if constexpr (PL == 16) v += DppF<0x128>(v);   // row_ror:8
-            if (pq == 0) bf[L::oQK + w * kC + TPL * tg + s] = v;
+            bf[L::oQK + w * kC + TPL * tg + s] = v;   // every lane of the token group holds the sum
         }
 #pragma unroll
         for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow * kTS + (rtid >> 5) + 2 * NPW * u] = vreg[u];
