@@ -1,7 +1,7 @@
 """Mamba3SisoFn on the GPU vs the fp64 oracle (C restatement), through the
 C ABI, for both kernels (the chunked fp32-MFMA kernel and, with
 the m3_path override, the token-by-token one).  Covers headdim_qk padding (N not a
-multiple of the key tiling), partial angle sets (A < N/2), grouped Q/K heads,
+multiple of the key tiling), headdim_qk above 512 (key-block launches), partial angle sets (A < N/2), grouped Q/K heads,
 the optional D and Z inputs, sequence lengths around the 16-token chunk and
 block, the 32-row workgroups, decay patterns, and the benchmark shape on a
 subset of heads."""
@@ -47,6 +47,12 @@ CASES = {
     "n384_p64_z": M(1, 40, 2, 64, 384, has_z=True),
     "n512_p64_z": M(2, 37, 2, 64, 512, has_z=True),
     "n512_a50_t70": M(1, 70, 1, 40, 512, angles=50),
+    # above 512 keys: one launch per 512-key block, each adding its part of y
+    # (angles inside the first block, crossing into the second, a partial last
+    # block, a shared Q/K head, two row blocks, Z applied by the last launch)
+    "n1024_p16_z_a100": M(1, 45, 2, 16, 1024, has_z=True, angles=100),
+    "n1100_p24_a300_hq1": M(1, 33, 2, 24, 1100, nheads_qk=1, angles=300),
+    "n640_p40_z": M(2, 30, 2, 40, 640, has_z=True),
     "p65_rowblocks": M(2, 35, 2, 65, 32),
     "t100_hq2": M(2, 100, 4, 16, 32, nheads_qk=2),
 }

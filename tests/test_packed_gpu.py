@@ -133,7 +133,7 @@ def test_gdn2_packed_one_sequence_equals_unpacked():
 # Mamba3SisoFn
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n_qk,p_dim,hq", [(16, 8, 1), (64, 33, 2), (128, 64, 2), (256, 24, 2)])
+@pytest.mark.parametrize("n_qk,p_dim,hq", [(16, 8, 1), (64, 33, 2), (128, 64, 2), (256, 24, 2), (768, 16, 2)])
 @pytest.mark.parametrize("with_states", [False, True])
 def test_m3_packed_matches_per_sequence(n_qk, p_dim, hq, with_states, m3_path):
     import torch

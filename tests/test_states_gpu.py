@@ -239,6 +239,7 @@ M3_CASES = {
     "n64_p33_hq1_z": M3(1, 33, 4, 33, 64, nheads_qk=1, has_z=True),
     "n128_a7": M3(1, 40, 2, 64, 128, angles=7),
     "n512_p64": M3(1, 35, 2, 64, 512),
+    "n1100_p16_a300_z": M3(1, 30, 2, 16, 1100, angles=300, has_z=True),   # three key-block launches
     "n130_padded": M3(1, 25, 2, 20, 130),
     "n256": M3(1, 21, 2, 24, 256),
     "p65_rowblocks_t70": M3(2, 70, 2, 65, 32),

@@ -45,8 +45,16 @@
 // along one row of seqlen tokens; a workgroup reads its sequence's offsets
 // (clamped into [0, seqlen]; an inverted range is empty, and an empty
 // sequence passes its states through, its pending look-ahead included).
+//
+// headdim_qk above 512 (KB): the keys are taken in blocks of at most 512, one
+// launch each.  A key's state column, its rotation pair and angle, and its
+// state inputs and outputs depend on no other key; the readout q.S and the
+// unrotated q.k are sums over keys.  So each launch runs the recurrence on its
+// block's keys and adds its part of y to what the earlier launches wrote; the
+// first adds D v, the last applies the Z gate.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 
 #include "mamba3_math.h"
@@ -88,9 +96,14 @@ struct M3Layout {
     static_assert(kBytes <= 160 * 1024, "LDS budget");
 };
 
-template <int KPT>
-__global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) {
+// k0_arg, nk_arg: the key block of this launch; first, last: whether it is
+// the first / last block (KB only: otherwise every key, in one launch).
+template <int KPT, bool KB>
+__global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p, int k0_arg, int nk_arg, int first_arg,
+                                                           int last_arg) {
     using L = M3Layout<KPT>;
+    const int k0 = KB ? k0_arg : 0;                // first key of the block (even)
+    const bool first = !KB || first_arg != 0, last = !KB || last_arg != 0;
     constexpr int PAIRS = L::PAIRS, PB = L::PB, TB = L::TB, SEG = L::SEG, NPS = L::NPS, TVP = L::TVP;
 
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -103,8 +116,10 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
-    const int N = p.n, P = p.p, A = p.a, H = p.nheads;
-    const int half_n = N / 2;
+    const int N = p.n, P = p.p, A = p.a, H = p.nheads;   // N: the full headdim_qk (row strides)
+    const int NK = KB ? nk_arg : N;                        // keys of this launch
+    const int half_n = NK / 2;
+    const int pa0 = k0 / 2;                                // first rotation pair of the block
     const int nrb = (P + kRows - 1) / kRows;
     // the nrb workgroups of one (b,h) prepare the same token vectors: keep them on one XCD
     const int wg = XcdLocalBlock(blockIdx.x, gridDim.x);
@@ -113,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     const int b = bh / H, h = bh % H;
     const int gq = h / (H / p.nheads_qk);
     const int r0 = rb * kRows;
-    const float dval = p.D ? p.D[h] : 0.0f;
+    const float dval = (first && p.D) ? p.D[h] : 0.0f;
     // tokens of sequence b: [tok0, tok0 + T) of its token axis
     int T = p.seqlen;
     size_t tok0 = static_cast<size_t>(b) * T;    // in [B*T] for Q/K/V/Angles/Z
@@ -135,16 +150,16 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     for (int x = 0; x < PB; ++x) {
         const int pr = lane + 64 * x;
         const int pc = min(pr, half_n - 1);
-        const float2 qb = *reinterpret_cast<const float2 *>(p.Q_bias + static_cast<size_t>(h) * N + 2 * pc);
-        const float2 kb = *reinterpret_cast<const float2 *>(p.K_bias + static_cast<size_t>(h) * N + 2 * pc);
+        const float2 qb = *reinterpret_cast<const float2 *>(p.Q_bias + static_cast<size_t>(h) * N + k0 + 2 * pc);
+        const float2 kb = *reinterpret_cast<const float2 *>(p.K_bias + static_cast<size_t>(h) * N + k0 + 2 * pc);
         const bool ok = pr < half_n;
         qbias[x] = ok ? qb : make_float2(0.0f, 0.0f);
         kbias[x] = ok ? kb : make_float2(0.0f, 0.0f);
     }
     // Per-token row bases and strides (elements); token t of this (b,h) is at base + t * stride.
     const size_t q_stride = static_cast<size_t>(p.nheads_qk) * N;
-    const float *qbase = p.Q + (tok0 * p.nheads_qk + gq) * N;
-    const float *kbase = p.K + (tok0 * p.nheads_qk + gq) * N;
+    const float *qbase = p.Q + (tok0 * p.nheads_qk + gq) * N + k0;
+    const float *kbase = p.K + (tok0 * p.nheads_qk + gq) * N + k0;
     const size_t a_stride = static_cast<size_t>(H) * A;
     const float *abase = p.Angles + (tok0 * H + h) * A;
     const size_t v_stride = static_cast<size_t>(H) * P;
@@ -172,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
 #pragma unroll
             for (int x = 0; x < PB; ++x) {
                 const int pr = lane + 64 * x;
-                ang[x][s] = ar[min(pr, A - 1)];
+                ang[x][s] = ar[min(pa0 + pr, A - 1)];
                 const int pc = min(pr, half_n - 1);
                 qv[x][s] = *reinterpret_cast<const float2 *>(qr + 2 * pc);
                 kv[x][s] = *reinterpret_cast<const float2 *>(kr + 2 * pc);
@@ -200,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         const int nt = min(TB, T - t0);
 #pragma unroll
         for (int x = 0; x < PB; ++x) {
-            const bool rot = lane + 64 * x < A;
+            const bool rot = pa0 + lane + 64 * x < A;
             double acc = 0.0;
 #pragma unroll
             for (int s = 0; s < SEG; ++s) {
@@ -231,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
                     const double v = sSeg[w2 * PAIRS + pr];
                     carry = w2 < w ? carry + v : carry;
                 }
-                const bool rot = pr < A;
+                const bool rot = pa0 + pr < A;
                 double th = 0.0;
 #pragma unroll
                 for (int s = 0; s < SEG; ++s) {
@@ -293,12 +308,12 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
     if (p.in_ssm != nullptr && row < P) {
         const float look0 = T > 0 ? dtr[0] * (1.0f - FastSigmoid(trr[0])) : 0.0f;   // stays pending when empty
         const float vl = p.in_v[static_cast<size_t>(bh) * P + row];
-        const float *srow = p.in_ssm + (static_cast<size_t>(bh) * P + row) * N;
-        const float *krow = p.in_k + static_cast<size_t>(bh) * N;
+        const float *srow = p.in_ssm + (static_cast<size_t>(bh) * P + row) * N + k0;
+        const float *krow = p.in_k + static_cast<size_t>(bh) * N + k0;
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             const int key = kg * KPT + j;
-            if (key < N) S[j] = fmaf(vl, krow[key] * look0, srow[key]);
+            if (key < NK) S[j] = fmaf(vl, krow[key] * look0, srow[key]);
         }
     }
 
@@ -362,7 +377,8 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
             if (tt < nt && row < P) {
                 const size_t idx = vbase + static_cast<size_t>(t0 + tt) * v_stride + row;
                 float y = oreg[u];
-                if (p.Z) {
+                if (!first) y += p.out[idx];                 // the earlier key blocks' part
+                if (last && p.Z) {
                     const float z = p.Z[idx];
                     y *= z * FastSigmoid(z);                 // silu gate (reference :155-158)
                 }
@@ -371,7 +387,8 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         }
     };
 
-    if (tid < PAIRS) sCarry[tid] = (p.in_angle != nullptr && tid < A) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + tid]) : 0.0;
+    if (tid < PAIRS)
+        sCarry[tid] = (p.in_angle != nullptr && pa0 + tid < A) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + pa0 + tid]) : 0.0;
     const int nblk = (T + TB - 1) / TB;
     if (T > 0) {   // workgroup-uniform: an empty sequence passes its states through
         load_prep(0);
@@ -396,10 +413,10 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         // the last block's buffers are intact: sK holds its rotated k, the
         // carry of parity nblk % 2 the wrapped angle after its last token
         if (row < P) {
-            float *srow = p.f_ssm + (static_cast<size_t>(bh) * P + row) * N;
+            float *srow = p.f_ssm + (static_cast<size_t>(bh) * P + row) * N + k0;
 #pragma unroll
             for (int j = 0; j < KPT; ++j)
-                if (kg * KPT + j < N) srow[kg * KPT + j] = S[j];
+                if (kg * KPT + j < NK) srow[kg * KPT + j] = S[j];
         }
         if (tid < kRows && r0 + tid < P) {
             const size_t o = static_cast<size_t>(bh) * P + r0 + tid;
@@ -409,25 +426,30 @@ __global__ __launch_bounds__(kThreads) void Mamba3FwdKernel(Mamba3SisoParams p) 
         if (rb == 0) {
             const int tl = T > 0 ? (T - 1) - (nblk - 1) * TB : 0;
             const float *krow = sK + (((nblk - 1) & 1) * TB + tl) * NPS;
-            for (int i = tid; i < N; i += kThreads) {
-                const size_t o = static_cast<size_t>(bh) * N + i;
+            for (int i = tid; i < NK; i += kThreads) {
+                const size_t o = static_cast<size_t>(bh) * N + k0 + i;
                 p.f_k[o] = T > 0 ? krow[L::Pos(i)] : (p.in_k != nullptr ? p.in_k[o] : 0.0f);
             }
-            for (int i = tid; i < A; i += kThreads)
-                p.f_angle[static_cast<size_t>(bh) * A + i] = static_cast<float>(sCarry[(nblk & 1) * PAIRS + i]);
+            for (int i = tid; i < half_n && pa0 + i < A; i += kThreads)
+                p.f_angle[static_cast<size_t>(bh) * A + pa0 + i] = static_cast<float>(sCarry[(nblk & 1) * PAIRS + i]);
         }
     }
 }
 
-template <int KPT>
-void LaunchKPT(const Mamba3SisoParams &p, hipStream_t stream) {
+template <int KPT, bool KB = false>
+void LaunchKPT(const Mamba3SisoParams &p, hipStream_t stream, int k0 = 0, int nk = 0, bool first = true,
+               bool last = true) {
     using L = M3Layout<KPT>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3FwdKernel<KPT>), static_cast<int>(L::kBytes));
-    XM_NOTE_LAUNCH("Mamba3FwdKernel", {}, KPT);
-    hipLaunchKernelGGL((Mamba3FwdKernel<KPT>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), L::kBytes, stream, p);
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3FwdKernel<KPT, KB>), static_cast<int>(L::kBytes));
+    if constexpr (KB) XM_NOTE_LAUNCH("Mamba3FwdKernel", {}, KPT, 1);
+    else XM_NOTE_LAUNCH("Mamba3FwdKernel", {}, KPT);
+    hipLaunchKernelGGL((Mamba3FwdKernel<KPT, KB>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), L::kBytes, stream, p,
+                       k0, nk, first ? 1 : 0, last ? 1 : 0);
 }
+
+constexpr int kKeyBlock = 16 * 32;   // keys per launch above 512 (32 per lane of a 16-lane row)
 
 }  // namespace
 
@@ -443,7 +465,10 @@ void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream_v) {
     else if (kpt <= 12) LaunchKPT<12>(p, stream);
     else if (kpt <= 16) LaunchKPT<16>(p, stream);
     else if (kpt <= 24) LaunchKPT<24>(p, stream);
-    else LaunchKPT<32>(p, stream);
+    else if (kpt <= 32) LaunchKPT<32>(p, stream);
+    else
+        for (int k0 = 0; k0 < p.n; k0 += kKeyBlock)   // stream order: each launch adds to the earlier ones' y
+            LaunchKPT<32, true>(p, stream, k0, std::min(kKeyBlock, p.n - k0), k0 == 0, k0 + kKeyBlock >= p.n);
     XM_LAUNCH_CHECK("Mamba3SisoFn");
 }
 

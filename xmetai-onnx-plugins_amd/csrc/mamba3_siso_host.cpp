@@ -2,12 +2,14 @@
 // Mirrors mamba3_siso_fn_ort.cpp:43-227 of the reference (constructor checks
 // in the same order, ValidateInputs and its messages, ToIntDim, output shape
 // = V.shape) and the launcher's re-checks (mamba3_siso_fwd.cu:177-188).
-// The kernels keep the state in VGPRs and a block of rotated q/k rows in LDS,
-// which bounds headdim_qk at 512 (32 keys per lane of a 16-lane row, 16-token
-// blocks: 155 KiB of LDS).  The reference's limit is its shared-memory budget
-// of P*N + A + 4N + 128 floats (mamba3_siso_fwd.cu:190-207), N = 576 at P = 64
-// on a 160 KiB device; N up to 256 takes the chunked fp32-MFMA kernel, above
-// that the token-by-token kernel.  No scratch.
+// The kernels keep the state in VGPRs and a block of rotated q/k rows in LDS:
+// up to 512 keys in one launch (32 keys per lane of a 16-lane row, 16-token
+// blocks: 155 KiB of LDS), above that one launch per block of 512 keys, each
+// adding its part of the output.  The reference's limit is its shared-memory
+// budget of P*N + A + 4N + 128 floats (mamba3_siso_fwd.cu:190-207), e.g.
+// N = 576 at P = 64 or about 2000 at P = 16 on a 160 KiB device; this layer
+// takes any even headdim_qk.  N up to 256 takes the chunked fp32-MFMA kernel,
+// above that the token-by-token kernel.  No scratch.
 //
 // Widening: has_input_states = 1 and return_final_states = 1, which the
 // reference rejects (:50-55), are accepted.  The states are (ssm [B,H,P,N],
@@ -104,7 +106,6 @@ Plan Validate(const std::vector<View> &in, const IndexView *cu, const xm_mamba3_
     p.nheads = ToIntDim(V.shape[2], "nheads");
     p.p = ToIntDim(V.shape[3], "headdim_v");
     p.a = ToIntDim(Ang.shape[3], "headdim_angles");
-    if (p.n > 512) Unsupported("Mamba3SisoFn supports headdim_qk up to 512");
     p.Q = Q.data;
     p.K = K.data;
     p.V = V.data;
