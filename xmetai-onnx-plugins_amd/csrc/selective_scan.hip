@@ -71,7 +71,8 @@ __device__ __forceinline__ float LaneGroupSum(float x) {
     return x;
 }
 
-// FAST: seqlen % 4 == 0, 16-byte aligned rows and dim_per_group % CPW == 0.
+// FAST: seqlen % 4 == 0, 16-byte aligned rows, dim_per_group % CPW == 0 and a
+// workgroup's rows under 2 GiB.
 // Full tiles then move as float4 with no guards, and the one-tile-ahead
 // prefetch of u/delta/B/C stays in flight through the recurrence.  A ragged
 // last tile (seqlen % 32 != 0) is peeled off the loop and loaded with guards.
@@ -162,14 +163,28 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
     }
 
     // ---- tile loads (global -> registers) ----------------------------------
-    F4 ureg[IPT], dreg[IPT], bcreg[BCPT];
-    auto load_full = [&](int t0) __attribute__((always_inline)) {        // FAST, whole tile in range: no guards
+    // FAST: u, delta and y through raw-buffer descriptors over this
+    // workgroup's CPW rows (under 2 GiB, checked by the host); a lane's byte
+    // offset is fixed, the tile's goes in the scalar operand, so a tile costs
+    // no per-lane address arithmetic.
+    constexpr int EB = static_cast<int>(sizeof(IT));
+    const int rows_bytes = FAST ? CPW * L * EB : 0;
+    const SsRsrc ru = SsRowsRsrc(ub, rows_bytes), rdl = SsRowsRsrc(db, rows_bytes), ryo = SsRowsRsrc(ob, rows_bytes);
+    int voff[IPT];
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+        const int it = min(tid + k * kThreads, ITEMS - 1);   // spare lanes re-read a valid item
+        voff[k] = ((it / kQ4) * L + (it % kQ4) * 4) * EB;
+    }
+    // Two register sets of a tile's loads, used in turn by consecutive full
+    // tiles, so a prefetch lands where it is consumed (no register copies).
+    F4 uA[IPT], dA[IPT], bcA[BCPT], uB[IPT], dB[IPT], bcB[BCPT];
+    auto load_full = [&](int t0, F4 (&ureg)[IPT], F4 (&dreg)[IPT], F4 (&bcreg)[BCPT])
+                         __attribute__((always_inline)) {   // FAST, whole tile in range: no guards
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
-            const int it = min(tid + k * kThreads, ITEMS - 1);   // spare lanes re-read a valid item
-            const int c = it / kQ4, t = t0 + (it % kQ4) * 4;
-            ureg[k] = LoadRow4Fast(ub + static_cast<size_t>(c) * L, t);
-            dreg[k] = LoadRow4Fast(db + static_cast<size_t>(c) * L, t);
+            ureg[k] = SsBufLoad4<IT>(ru, voff[k], t0 * EB);
+            dreg[k] = SsBufLoad4<IT>(rdl, voff[k], t0 * EB);
         }
         if constexpr (NBC > 0) {
             const int per = N * kQ4;
@@ -182,7 +197,8 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
             }
         }
     };
-    auto load_guarded = [&](int t0) __attribute__((always_inline)) {     // any tile: clamped addresses, zero past the ends
+    auto load_guarded = [&](int t0, F4 (&ureg)[IPT], F4 (&dreg)[IPT], F4 (&bcreg)[BCPT])
+                            __attribute__((always_inline)) {   // any tile: clamped addresses, zero past the ends
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
             const int it = tid + k * kThreads;
@@ -205,7 +221,8 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
 
     // ---- phase 1: bias, softplus, delta*u into LDS; keep D*u ----------------
     F4 skip[IPT];
-    auto phase1 = [&](int t0, bool full) __attribute__((always_inline)) {
+    auto phase1 = [&](int t0, bool full, const F4 (&ureg)[IPT], F4 (&dreg)[IPT], const F4 (&bcreg)[BCPT])
+                      __attribute__((always_inline)) {
         // delta' = softplus?(delta + bias): one uniform branch per tile
         if (p.delta_softplus) {
 #pragma unroll
@@ -314,11 +331,12 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
                 F4 acc = skip[k];
                 const float4 x = *reinterpret_cast<const float4 *>(sY + c * kRow + q4 * 4);
                 acc.v[0] += x.x; acc.v[1] += x.y; acc.v[2] += x.z; acc.v[3] += x.w;
-                IT *row = ob + static_cast<size_t>(c) * L;
-                if (FAST && full)
-                    StoreRow4Fast(row, t0 + q4 * 4, acc);
-                else
+                if (FAST && full) {
+                    SsBufStore4<IT>(ryo, voff[k], t0 * EB, acc);
+                } else {
+                    IT *row = ob + static_cast<size_t>(c) * L;
                     StoreRow4(row, t0 + q4 * 4, L, FAST, acc);
+                }
             }
         }
         // sY is rewritten only after the next phase-1 barrier; sDl/sDu/sB/sC
@@ -326,20 +344,27 @@ __global__ __launch_bounds__(kThreads) void SelectiveScanFwdKernel(SelectiveScan
     };
 
     const int nfull = FAST ? L / kTile : 0;   // tiles taken on the unguarded path
-    if (nfull > 0) load_full(0);
-    else load_guarded(0);
-    for (int i = 0; i < nfull; ++i) {
+    if (nfull > 0) load_full(0, uA, dA, bcA);
+    else load_guarded(0, uA, dA, bcA);
+    // a full tile from one register set, prefetching the next tile into the other
+    auto full_tile = [&](int i, F4 (&u)[IPT], F4 (&d)[IPT], F4 (&bc)[BCPT], F4 (&nu)[IPT], F4 (&nd)[IPT],
+                         F4 (&nbc)[BCPT]) __attribute__((always_inline)) {
         const int t0 = i * kTile;
-        phase1(t0, true);
+        phase1(t0, true, u, d, bc);
         __syncthreads();
-        if (i + 1 < nfull) load_full(t0 + kTile);   // prefetch; the tail tile loads after the loop
+        if (i + 1 < nfull) load_full(t0 + kTile, nu, nd, nbc);   // prefetch; the tail tile loads after the loop
         phase2();
         __syncthreads();
         phase3(t0, true);
+    };
+    for (int i = 0; i < nfull; i += 2) {
+        full_tile(i, uA, dA, bcA, uB, dB, bcB);
+        if (i + 1 >= nfull) break;
+        full_tile(i + 1, uB, dB, bcB, uA, dA, bcA);
     }
     for (int t0 = nfull * kTile; t0 < L; t0 += kTile) {   // ragged tail (FAST) or every tile
-        if (t0 > 0 && (FAST || t0 > nfull * kTile)) load_guarded(t0);
-        phase1(t0, false);
+        if (t0 > 0 && (FAST || t0 > nfull * kTile)) load_guarded(t0, uA, dA, bcA);
+        phase1(t0, false, uA, dA, bcA);
         __syncthreads();
         phase2();
         __syncthreads();
@@ -406,7 +431,9 @@ void LaunchLSV(const SelectiveScanParams &p, dim3 grid, hipStream_t stream) {
 template <typename IT, int LPC, int SPL>
 void LaunchLS(const SelectiveScanParams &p, int vec, dim3 grid, hipStream_t stream) {
     constexpr int CPW = kThreads / LPC;
-    if (vec && p.dim_per_group % CPW == 0) LaunchLSV<IT, LPC, SPL, true>(p, grid, stream);
+    // the fast path's row descriptors span a workgroup's CPW rows: under 2 GiB
+    const bool rows_fit = static_cast<long long>(CPW) * p.seqlen * static_cast<long long>(sizeof(IT)) < (1LL << 31);
+    if (vec && rows_fit && p.dim_per_group % CPW == 0) LaunchLSV<IT, LPC, SPL, true>(p, grid, stream);
     else LaunchLSV<IT, LPC, SPL, false>(p, grid, stream);
 }
 

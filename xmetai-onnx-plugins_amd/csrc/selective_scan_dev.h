@@ -107,6 +107,47 @@ __device__ __forceinline__ F4 LoadRow4Guarded(const IT *row, int t, int L, bool 
     return r;
 }
 
+// Four elements at byte offset voff + soff of a raw buffer (a wave-uniform
+// descriptor, a per-lane offset and a wave-uniform one), converted to fp32 /
+// from fp32 (nearest even).  The offsets are in range by construction.
+typedef __amdgpu_buffer_rsrc_t SsRsrc;
+typedef unsigned SsU2 __attribute__((ext_vector_type(2)));
+typedef unsigned SsU4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ SsRsrc SsRowsRsrc(const void *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes, 0x00020000);
+}
+template <typename IT>
+__device__ __forceinline__ F4 SsBufLoad4(SsRsrc r, int voff, int soff) {
+    if constexpr (sizeof(IT) == 4) {
+        const uint4 x = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+        return F4{{__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z), __uint_as_float(x.w)}};
+    } else if constexpr (std::is_same_v<IT, _Float16>) {
+        const h4 x = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+        return F4{{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
+                   static_cast<float>(x[3])}};
+    } else {
+        const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+        return F4{{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u), __uint_as_float(x.y << 16),
+                   __uint_as_float(x.y & 0xffff0000u)}};
+    }
+}
+template <typename IT>
+__device__ __forceinline__ void SsBufStore4(SsRsrc r, int voff, int soff, const F4 &x) {
+    if constexpr (sizeof(IT) == 4) {
+        const SsU4 y{__float_as_uint(x.v[0]), __float_as_uint(x.v[1]), __float_as_uint(x.v[2]), __float_as_uint(x.v[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(y, r, voff, soff, 0);
+    } else if constexpr (std::is_same_v<IT, _Float16>) {
+        h4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = FromF<_Float16>(x.v[e]);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(SsU2, y), r, voff, soff, 0);
+    } else {
+        const unsigned lo = static_cast<uint32_t>(FromF<Bf16>(x.v[0]).bits) | (static_cast<uint32_t>(FromF<Bf16>(x.v[1]).bits) << 16);
+        const unsigned hi = static_cast<uint32_t>(FromF<Bf16>(x.v[2]).bits) | (static_cast<uint32_t>(FromF<Bf16>(x.v[3]).bits) << 16);
+        __builtin_amdgcn_raw_buffer_store_b64(SsU2{lo, hi}, r, voff, soff, 0);
+    }
+}
+
 template <typename IT>
 __device__ __forceinline__ void StoreRow4Fast(IT *row, int t, const F4 &x) {
     if constexpr (sizeof(IT) == 4) {
