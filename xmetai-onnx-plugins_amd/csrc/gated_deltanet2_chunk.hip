@@ -18,18 +18,20 @@
 // no division.  The tail of the sequence is padded with identity tokens
 // (d = 1, zero vectors), which leave the state unchanged.
 //
-// Two kernels per window of up to 128 chunks (2048 tokens):
+// Two kernels per window of chunks (128, or more where 128 MiB of prepared
+// blocks hold more):
 //  * Gdn2ChunkPrepKernel: one wave per (b,h,chunk), all chunks in parallel.
 //    L2 norms, decay products, E, R, Ut, G_15, A, M (MFMA), T (forward
 //    substitution), M T (MFMA), written to scratch in the lane order of the
 //    MFMA operands, so the recurrence reads each with one 16-byte load per
 //    lane.
-//  * Gdn2ChunkRecurKernel: a workgroup owns one (b,h) and CT tiles of 16 value
-//    columns; KS waves split the keys of a column tile (KPW tiles of 16 keys
-//    per wave), the state of a wave being KPW 16x16 accumulator tiles.  Per
-//    chunk: S = G_15 o S + Ut^T U of the previous chunk, partial E S0 and R S0
-//    (MFMA), one barrier, the partials summed, U = T Y and O = R S0 + (M T) Y
-//    (MFMA), O stored.  The state crosses windows through scratch.
+//  * Gdn2ChunkRecurKernel: a workgroup owns one (b,h) and one tile of 16 value
+//    columns; KS waves split the keys (KPW tiles of 16 keys per wave), the
+//    state of a wave being KPW 16x16 accumulator tiles.  Per chunk: partial
+//    E S0 and R S0 (MFMA), one barrier, the partials summed, U = T Y, the
+//    update S = G_15 o S + Ut^T U, and this wave's part of O = R S0 + (M T) Y,
+//    which wave 0 sums and stores after the next chunk's barrier.  The state
+//    crosses windows through scratch.
 // The matrix products use v_mfma_f32_16x16x4_f32 (A[m][k] in lane m+16k, B[k][n]
 // in lane n+16k, D[m][n] in lane n+16(m/4), register m%4); the D layout of the
 // state, of Y and of U serves directly as the B operand of the next product.
