@@ -280,17 +280,20 @@ def test_gdn2_valid_and_scratch():
     # of up to 128 chunks, E, R, Ut tiles (256 floats per 16 keys each), G_15
     # (16 per 16 keys), T and M T (256 each), q and k multipliers (16 each);
     # keys padded to 16 * kpw * ks (kpw = 2 and ks = ceil(tiles / 2) up to 128
-    # keys; 3 tiles x 4 waves for 129-192 keys; 3 tiles x 8 waves for 257-384
-    # keys when the launch has fewer than 128 column-tile workgroups; else
-    # kpw = 4 and ks = ceil(tiles / 4));
+    # keys; 3 tiles x 4 waves for 129-192 keys; 5 tiles x 4 waves for 257-320
+    # keys; for 321-384 keys 3 tiles x 8 waves when the launch has fewer than
+    # 128 column-tile workgroups, else 6 tiles x 4 waves; else kpw = 4 and
+    # ks = ceil(tiles / 4));
     # plus the state carried between windows when there is more than one
     def chunk_scratch(B, T, H, K, V):
         kq = -(-K // 16)
         groups = B * H * -(-V // 16)
         if 8 < kq <= 12:
             kpw, ks = 3, 4
-        elif 16 < kq <= 24 and groups < 128:
-            kpw, ks = 3, 8
+        elif 16 < kq <= 20:
+            kpw, ks = 5, 4
+        elif 20 < kq <= 24:
+            kpw, ks = (3, 8) if groups < 128 else (6, 4)
         elif kq > 8:
             kpw, ks = 4, -(-kq // 4)
         else:
@@ -308,7 +311,7 @@ def test_gdn2_valid_and_scratch():
         return a256(per_block * win) + (a256(B * H * K * V * 4) if win < nch else 0)
     assert scratch == chunk_scratch(2, 5, 3, 16, 8)
     for T, K, V in ((100, 128, 64), (3000, 128, 128), (17, 100, 7), (2049, 256, 16), (2048, 33, 40),
-                    (3000, 512, 64), (40, 300, 16), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8)):
+                    (3000, 512, 64), (40, 300, 16), (40, 352, 16), (40, 352, 352), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8)):
         assert validate("gated_deltanet2", gdn_shapes(T=T, K=K, V=V))[1] == chunk_scratch(2, T, 3, K, V), (T, K, V)
     # packed sequences (headdim_k <= 512) take the fused kernel: no scratch
     # headdim_k > 512: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded

@@ -57,6 +57,8 @@ CASES = {
     "k320_v64": S(2, 40, 2, 320, 64),
     "k352_v20_chunk12": S(1, 37, 2, 352, 20),
     "k384_v16": S(1, 33, 1, 384, 16, per_key_gates=True),
+    # 128 column-tile workgroups: 352 keys take 6 key tiles per wave x 4 waves
+    "k352_v256_h8_six_tiles": S(1, 40, 8, 352, 256, per_key_gates=True),
     "k385_v16": S(1, 19, 1, 385, 16),
     "k448_v40": S(2, 35, 1, 448, 40),
     "k512_v7_perkey": S(1, 12, 1, 512, 7, per_key_gates=True),

@@ -658,24 +658,26 @@ struct ChunkConfig {
 // 65-96 keys measured 11-12% faster).  Fewer splits leave too few
 // waves for the chip (one wave per SIMD at best, and half the SIMDs idle for
 // 4 x 16 heads of 128 x 128): four tiles per wave measured 7-28% slower
-// there.  Above 128 keys, three or four key tiles per wave (at most 512
-// threads keep the register cap at 256; two tiles per wave with 10-16 waves
-// spill), measured 11-22% faster than two tiles per wave for 160-256 keys.
-// A CU has 4 SIMDs, so 5-7 waves put two on some SIMD, whose doubled MFMA
-// work every chunk's barrier waits for: 129-192 keys take 4 waves of 3
-// tiles (3 waves of 4 before: -2 to -9%); 257-384 keys take 8 waves of 3
-// tiles when the launch has fewer column-tile workgroups than half the CUs
-// (2 x 2048 x 4 heads at 320-384 x 64: -7 to -11%), and 4 tiles in
-// ceil(tiles / 4) waves otherwise (the padding to 24 tiles costs more than
-// the imbalance when every CU has work: 4 x 2048 x 32 heads at 320 x 64,
-// +7%).  The gdn2_kpw4 override keeps 4 tiles and ceil(tiles / 4) waves
-// above 128 keys.  `groups`: the launch's column-tile workgroups.
+// there.  Above 128 keys, three to six key tiles per wave (two tiles per
+// wave with 10-16 waves spill), measured 11-22% faster than two tiles per
+// wave for 160-256 keys.  A CU has 4 SIMDs, so 5-7 waves put two on some
+// SIMD, whose doubled MFMA work every chunk's barrier waits for: 129-192
+// keys take 4 waves of 3 tiles (3 waves of 4 before: -2 to -9%); 257-320
+// keys 4 waves of 5 tiles (8 waves of 3 or 5 of 4 before: 2 x 2048 x 4
+// heads at 288-320 x 64 -11%, 4 x 2048 x 32 heads at 320 x 64 -7%);
+// 321-384 keys 8 waves of 3 tiles when the launch has fewer column-tile
+// workgroups than half the CUs (4 waves of 6 tiles: +5% at 2 x 2048 x 4
+// heads), else 4 waves of 6 tiles (-3% against 6 waves of 4 at 4 x 2048 x
+// 16 heads of 384 x 128).  The gdn2_kpw4 override keeps 4 tiles and
+// ceil(tiles / 4) waves above 128 keys.  `groups`: the launch's column-tile
+// workgroups.
 ChunkConfig ChooseChunk(int dk, long long groups) {
     const int kq = (dk + 15) / 16;
     if (kq > 8) {
         if (GetOverride(kOverrideGdn2Kpw4) == 1) return ChunkConfig{4, (kq + 3) / 4};
         if (kq <= 12) return ChunkConfig{3, 4};
-        if (kq > 16 && kq <= 24 && groups < 128) return ChunkConfig{3, 8};
+        if (kq > 16 && kq <= 20) return ChunkConfig{5, 4};
+        if (kq > 20 && kq <= 24) return groups < 128 ? ChunkConfig{3, 8} : ChunkConfig{6, 4};
         return ChunkConfig{4, (kq + 3) / 4};
     }
     ChunkConfig c{kq >= 2 ? 2 : 1, 1};
@@ -712,7 +714,7 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
     if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecur<KPW_, KS_>(p, c0, wn, kq, s_in, s_out, stream);
     XM_GDN2_RECUR(1, 1) XM_GDN2_RECUR(2, 1) XM_GDN2_RECUR(2, 2) XM_GDN2_RECUR(2, 3) XM_GDN2_RECUR(2, 4)
     XM_GDN2_RECUR(3, 4) XM_GDN2_RECUR(3, 8) XM_GDN2_RECUR(4, 3) XM_GDN2_RECUR(4, 4) XM_GDN2_RECUR(4, 5)
-    XM_GDN2_RECUR(4, 6) XM_GDN2_RECUR(4, 7) XM_GDN2_RECUR(4, 8)
+    XM_GDN2_RECUR(4, 6) XM_GDN2_RECUR(4, 7) XM_GDN2_RECUR(4, 8) XM_GDN2_RECUR(5, 4) XM_GDN2_RECUR(6, 4)
 #undef XM_GDN2_RECUR
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }
