@@ -499,7 +499,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // parity, so a wave that runs ahead writes the other buffer, and cannot
         // run two chunks ahead past the next barrier); y = WV - km o E' S0;
         // U = T y; O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut'^T
-        // (km o U).  The operand set then receives chunk j + 2.
+        // (km o U).  The next chunk's operands are loaded as described below.
         // The output of a chunk, O = q_mul o R' S0 + (M T) Y, as this wave's
         // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the
         // 4 with ii % KS == ks); published with the next chunk's E' S0 partials
@@ -516,7 +516,31 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             for (int z = 1; z < KS; ++z) out += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
             return out;
         };
-        auto step = [&](int j, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
+        // Vector loads issued in a burst queue behind each other (the CU's
+        // waves issue them together); placed one after each MFMA of the
+        // products before the barrier, their issue overlaps the products.
+        // Where the operand loads of the next chunk are issued: at the end of
+        // a step, into its own set (chunk j + 2), the loop's back edge sits
+        // between them and the products on every second step; at the head of
+        // a step, into the other set (chunk j + 1, that set consumed by the
+        // previous step), every step interleaves them.  Measured per key
+        // tiling (interleaved A/B): head loads for 4 key tiles per wave and
+        // for 3 x 8 (16k tokens x 8 heads at 256 x 256 1.52 -> 1.42 ms, 2 x
+        // 2048 x 4 heads at 512 x 64 0.336 -> 0.312, at 384 x 64 0.265 ->
+        // 0.253), end-of-step loads elsewhere (head loads: 4 x 4096 x 16
+        // heads at 64 x 64 0.327 -> 0.344, 2 x 2048 x 4 heads at 320 x 64
+        // 0.234 -> 0.244).  With 6 key tiles per wave the interleave measured
+        // 2% slower (4 x 2048 x 16 heads at 384 x 128) and is left out.
+        constexpr bool kHeadLoads = KPW == 4 || (KPW == 3 && KS == 8);
+        auto interleave = [&]() __attribute__((always_inline)) {
+            if constexpr (KPW == 6) return;
+#pragma unroll
+            for (int i = 0; i < 4 * KPW + 12; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // one vector-memory read
+            }
+        };
+        auto step = [&](int j, ChunkOperands<KPW> &o, ChunkOperands<KPW> &nx) __attribute__((always_inline)) {
             v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
@@ -526,10 +550,12 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                     xr = Mfma(o.r[kt][ii], S[kt][ii], xr);
                 }
             }
+            if constexpr (kHeadLoads) load_ops(min(j + 1, nrun - 1), nx);
             if constexpr (KS > 1) {
                 float *const xp = sXp + (j & 1) * (KS * 512);
                 StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
                 StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);   // output partial of chunk j - 1
+                interleave();
                 __syncthreads();
                 // the same summation order in every wave: identical U everywhere
                 xe = LdsF4(xp + lane * 4);
@@ -566,7 +592,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                 if (m * KS < 4) op = Mfma(ma, ya, op);
             }
             if constexpr (KS == 1) store_out(j, op);
-            load_ops(min(j + 2, nrun - 1), o);
+            if constexpr (!kHeadLoads) load_ops(min(j + 2, nrun - 1), o);
         };
 
         // two operand sets in turn, with compile-time roles
@@ -574,15 +600,17 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // prologue would set the loop's wait counts to its own, shorter distances)
         ChunkOperands<KPW> opa, opb;
         load_ops(0, opa);
-        __builtin_amdgcn_sched_barrier(0);
-        load_ops(min(1, nrun - 1), opb);
+        if constexpr (!kHeadLoads) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_ops(min(1, nrun - 1), opb);
+        }
         // each step leaves the loop or goes on to the other set's step: a path
         // from one set's step back to itself (no newer loads outstanding, to the
         // compiler) would take its wait counts to zero
         for (int j = 0;; j += 2) {
-            step(j, opa);
+            step(j, opa, opb);
             if (j + 1 >= nrun) break;
-            step(j + 1, opb);
+            step(j + 1, opb, opa);
             if (j + 2 >= nrun) break;
         }
         if constexpr (KS > 1) {   // output of the last chunk
