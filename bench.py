@@ -64,8 +64,10 @@ def floors_us(name, s, nbytes):
     GDN-2: 4 per state element per token; Mamba-3: decay, readout, update =
     3), at one slot per lane per cycle; where a chunked form runs it is
     reported as valu_sequential_form.  mfma: the fp32 MFMA flops of the
-    16-token chunked forms: GDN-2 (head_k <= 512) 96*K*V + 2560*V per
-    chunk-head (K, V padded to 16); Mamba-3 (N <= 256) 32*(80*N + 512) per
+    16-token chunked forms: GDN-2 (head_k <= 512) 96*K*V + 512*V per
+    chunk-head in the recurrence (E'S, R'S, the update, (M T) Y) and
+    1536*K + 8192 in the preparation (A', M', T^T Ut', M T), K and V padded
+    to 16; Mamba-3 (N <= 256) 32*(80*N + 512) per
     chunk and 32-row block (N padded to 64)."""
     f = {"hbm": nbytes / (HBM_PEAK_GBPS * 1e9) * 1e6}
     if name == "selective_scan":
@@ -75,7 +77,7 @@ def floors_us(name, s, nbytes):
         if s.dk <= 512:
             kp, vp = -(-s.dk // 16) * 16, -(-s.dv // 16) * 16
             chunks = s.batch * s.nheads * -(-s.seqlen // 16)
-            f["mfma"] = chunks * (96 * kp * vp + 2560 * vp) / MFMA_F32_FLOPS * 1e6
+            f["mfma"] = chunks * (96 * kp * vp + 512 * vp + 1536 * kp + 8192) / MFMA_F32_FLOPS * 1e6
     elif name == "mamba3_siso":
         f["valu_sequential_form"] = s.batch * s.seqlen * s.nheads * s.headdim * s.dstate * 3 / VALU_LANE_OPS * 1e6
         if s.dstate <= 256:

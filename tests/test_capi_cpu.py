@@ -300,7 +300,7 @@ def test_gdn2_valid_and_scratch():
             kpw = 2 if kq >= 2 else 1
             ks = -(-kq // kpw)
         kq = kpw * ks
-        block = 3 * kq * 256 + 16 * kq + 512 + 32
+        block = 3 * kq * 256 + 16 * kq + 256 + 32
         nch = -(-T // 16)
         # windows of 128 chunks, or of up to 128 MiB of blocks, balanced in length
         per_block = B * H * block * 4
@@ -360,7 +360,7 @@ def packed_chunk_scratch(N, T, H, K, V):
     window holds chunks [c0, c0 + win) of every sequence (win = min(ceil(T/16),
     128), or every chunk when that costs at most twice the blocks or 512 MiB);
     per head its blocks are at most min(win * N, ceil(T/16) + N), of
-    3*kq*256 + 16*kq + 544 floats each (kq = key tiles, padded to the
+    3*kq*256 + 16*kq + 288 floats each (kq = key tiles, padded to the
     recurrence's key split).  Plus the carried state [N,H,K,V] when a sequence
     can span windows, and the per-window block offsets [windows][N+1] ints;
     each region 256-byte aligned."""
@@ -368,7 +368,7 @@ def packed_chunk_scratch(N, T, H, K, V):
     kq = -(-K // 16)
     kq = 4 * -(-kq // 4) if kq > 8 else (kq if kq < 2 else 2 * -(-kq // 2))
     nch = -(-T // 16)
-    per = H * (3 * kq * 256 + 16 * kq + 544) * 4
+    per = H * (3 * kq * 256 + 16 * kq + 288) * 4
     win = min(nch, 128)
     blocks = a256(per * min(win * N, nch + N))
     if win < nch and a256(per * (nch + N)) <= max(2 * blocks, 512 << 20):

@@ -22,19 +22,19 @@
 // blocks hold more):
 //  * Gdn2ChunkPrepKernel: one wave per (b,h,chunk), all chunks in parallel.
 //    L2 norms, decay products, E, R, Ut, G_15, A, M (MFMA), T (forward
-//    substitution), M T (MFMA), written to scratch in the lane order of the
-//    MFMA operands, so the recurrence reads each with one 16-byte load per
-//    lane.
+//    substitution), M T (MFMA), and Ut~ = T^T Ut (MFMA, so that Ut^T U =
+//    Ut~^T Y), written to scratch in the lane order of the MFMA operands, so
+//    the recurrence reads each with one 16-byte load per lane.
 //  * Gdn2ChunkRecurKernel: a workgroup owns one (b,h) and one tile of 16 value
 //    columns; KS waves split the keys (KPW tiles of 16 keys per wave), the
 //    state of a wave being KPW 16x16 accumulator tiles.  Per chunk: partial
-//    E S0 and R S0 (MFMA), one barrier, the partials summed, U = T Y, the
-//    update S = G_15 o S + Ut^T U, and this wave's part of O = R S0 + (M T) Y,
-//    which wave 0 sums and stores after the next chunk's barrier.  The state
-//    crosses windows through scratch.
+//    E S0 and R S0 (MFMA), one barrier, the partials summed into Y, the update
+//    S = G_15 o S + Ut~^T Y, and this wave's part of O = R S0 + (M T) Y, which
+//    wave 0 sums and stores after the next chunk's barrier.  U itself is never
+//    formed.  The state crosses windows through scratch.
 // The matrix products use v_mfma_f32_16x16x4_f32 (A[m][k] in lane m+16k, B[k][n]
 // in lane n+16k, D[m][n] in lane n+16(m/4), register m%4); the D layout of the
-// state, of Y and of U serves directly as the B operand of the next product.
+// state and of Y serves directly as the B operand of the next product.
 // Numerics differ from the sequential reference by fp32 rounding only; the
 // parity tests bound the difference against the fp64 oracle.
 #include <hip/hip_runtime.h>
@@ -111,13 +111,14 @@ constexpr int kPrepWaves = 4;            // waves (chunk-heads) per prep workgro
 
 // Chunk-head block of the prepared window, in floats, for kq key tiles.  The
 // vectors are unnormalised (q, k in place of qhat, khat); the recurrence
-// applies the per-token multipliers to the rows of E S0, R S0 and U.
+// applies the per-token multipliers to the rows of E S0 and R S0.
 //   E' = beta k G tiles [kq][256], R' = q G tiles [kq][256]: lane l holds
 //     token l%16, keys 4(l/16)..+3 of the tile
-//   Ut' tiles [kq][256] (k prod_{r>t} d_r): lane l holds key l%16, tokens 4(l/16)..+3
-//   G_15 [kq][16]; T [256], M T [256]: lane l holds row l%16, columns 4(l/16)..+3
+//   Ut~ = T^T diag(k_mul) Ut' tiles [kq][256] (Ut' = k prod_{r>t} d_r): lane l
+//     holds key l%16, tokens 4(l/16)..+3
+//   G_15 [kq][16]; M T [256]: lane l holds row l%16, columns 4(l/16)..+3
 //   q and k multipliers [2][16]
-__host__ __device__ constexpr int BlockFloats(int kq) { return 3 * kq * 256 + 16 * kq + 512 + 32; }
+__host__ __device__ constexpr int BlockFloats(int kq) { return 3 * kq * 256 + 16 * kq + 256 + 32; }
 
 __device__ __forceinline__ v4f LdgF4(const float *p) { return *reinterpret_cast<const v4f *>(p); }
 __device__ __forceinline__ void StgF4(float *p, v4f v) { *reinterpret_cast<v4f *>(p) = v; }
@@ -219,8 +220,11 @@ __device__ __forceinline__ void PackedRange(const GatedDeltaNet2Params &p, int b
 // ---------------------------------------------------------------------------
 // Preparation: one wave per (b,h,chunk) of the window
 // ---------------------------------------------------------------------------
+// Dynamic LDS: kPrepWaves * kq * 256 floats, each wave's transposed Ut' tiles
+// kept until T is known.
 __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kq) {
     __shared__ float sw[kPrepWaves][4][kTile];
+    extern __shared__ float prep_dyn[];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int m16 = lane & 15, g4 = lane >> 4;
     const int H = p.nheads;
@@ -258,6 +262,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     float qs = 0.0f, kq2 = 0.0f;
     bool in_range = true;
     v4f al = {0.0f, 0.0f, 0.0f, 0.0f}, mu = al;
+    // this wave's Ut' tiles: lane l holds key l%16, tokens 4(l/16)..+3 (each
+    // lane reads back only its own 16 bytes)
+    float *const ut = prep_dyn + static_cast<size_t>(w) * kq * 256 + lane * 4;
     // one key tile: operand-layout vectors to the block, A' and M' accumulated
     auto tile = [&](int kt, const float (&q)[4], const float (&k)[4], const float (&g)[4], const float (&bt)[4])
                     __attribute__((always_inline)) {
@@ -281,9 +288,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         WaveSync();
         const v4f utA = LdsF4(wTr + m16 * kSP + 4 * g4);
         WaveSync();
+        StF4(ut + kt * 256, utA);
         StgF4(blk + kt * 256 + lane * 4, e);
         StgF4(blk + (kq + kt) * 256 + lane * 4, r);
-        StgF4(blk + (2 * kq + kt) * 256 + lane * 4, utA);
         if (m16 == 0) StgF4(blk + 3 * kq * 256 + kt * 16 + 4 * g4, g15);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         qm *= rsqrtf(qs + kL2EpsC);
         km = rsqrtf(kq2 + kL2EpsC);
     }
-    float *const mul = blk + 3 * kq * 256 + 16 * kq + 512;
+    float *const mul = blk + 3 * kq * 256 + 16 * kq + 256;
     if (g4 == 0) {
         mul[m16] = qm;
         mul[16 + m16] = km;
@@ -373,24 +380,40 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     v4f mt = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) mt = Mfma(mA[ii], tB[ii], mt);
-    StgF4(blk + 3 * kq * 256 + 16 * kq + lane * 4, LdsF4(wT + m16 * kSP + 4 * g4));   // T, A operand
     WaveSync();
 #pragma unroll
     for (int i = 0; i < 4; ++i) wTr[(4 * g4 + i) * kSP + m16] = mt[i];
     WaveSync();
-    StgF4(blk + 3 * kq * 256 + 16 * kq + 256 + lane * 4, LdsF4(wTr + m16 * kSP + 4 * g4));   // M T, A operand
+    StgF4(blk + 3 * kq * 256 + 16 * kq + lane * 4, LdsF4(wTr + m16 * kSP + 4 * g4));   // M T, A operand
+
+    // The update S_C = G_15 o S0 + Ut'^T diag(k_mul) U with U = T Y is
+    // Ut~^T Y, Ut~ = T^T diag(k_mul) Ut': the recurrence updates from Y and
+    // never forms U.  D[s][key] = sum_t T[t][s] k_mul_t Ut'[t][key] on MFMA:
+    // A[s][t] = T^T (tB, lane s + 16k holds T[4k + ii][s]), B[t][key] = the
+    // Ut' tile scaled per token; the D layout (key l%16, tokens 4(l/16)+i) is
+    // the recurrence's A operand.
+    v4f km4;   // k_mul of tokens 4 g4 + ii (every row of lanes holds its token's k_mul)
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) km4[ii] = __shfl(km, 4 * g4 + ii);
+    for (int kt = 0; kt < kq; ++kt) {
+        const v4f b = LdsF4(ut + kt * 256) * km4;
+        v4f d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) d = Mfma(tB[ii], b[ii], d);
+        StgF4(blk + (2 * kq + kt) * 256 + lane * 4, d);
+    }
 }
 
 // ---------------------------------------------------------------------------
 // Recurrence over one window
 // ---------------------------------------------------------------------------
 // The operands of one chunk that a wave needs, in MFMA lane order: its key
-// tiles of E', R', Ut' and G_15, T, M T, the row multipliers and this lane's
+// tiles of E', R', Ut~ and G_15, M T, the row multipliers and this lane's
 // w, v (tokens 4(l/16)+i).
 template <int KPW>
 struct ChunkOperands {
     v4f e[KPW], r[KPW], ut[KPW], g[KPW];
-    v4f t, mt, qm, km;
+    v4f mt, qm, km;
     float w[4], v[4];
 };
 
@@ -416,7 +439,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     using L = RecurLayout<KPW, KS>;
     constexpr int KQ = L::KQ, FB = L::FB;
     constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oG = 3 * KQ * 256;   // block offsets (floats)
-    constexpr int oT = oG + 16 * KQ, oMT = oT + 256, oMul = oT + 512;
+    constexpr int oMT = oG + 16 * KQ, oMul = oMT + 256;
 
     const int H = p.nheads, dk = p.dk, dv = p.dv;
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -483,7 +506,6 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                 o.v[i] = BufF(rv, vo[i]);
             }
             o.km = BufF4(rblk, go, sb + (oMul + 16) * 4);
-            o.t = BufF4(rblk, lo, sb + oT * 4);
             o.qm = BufF4(rblk, go, sb + oMul * 4);
             o.mt = BufF4(rblk, lo, sb + oMT * 4);
 #pragma unroll
@@ -498,8 +520,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // the KS waves (one barrier; the partial buffers alternate by chunk
         // parity, so a wave that runs ahead writes the other buffer, and cannot
         // run two chunks ahead past the next barrier); y = WV - km o E' S0;
-        // U = T y; O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut'^T
-        // (km o U).  The next chunk's operands are loaded as described below.
+        // O = qm o R' S0 + (M T) y (wave 0); S = G_15 o S + Ut~^T y (Ut~ holds
+        // T and k_mul).  The next chunk's operands are loaded as described below.
         // The output of a chunk, O = q_mul o R' S0 + (M T) Y, as this wave's
         // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the
         // 4 with ii % KS == ks); published with the next chunk's E' S0 partials
@@ -535,7 +557,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         auto interleave = [&]() __attribute__((always_inline)) {
             if constexpr (KPW == 6) return;
 #pragma unroll
-            for (int i = 0; i < 4 * KPW + 12; ++i) {
+            for (int i = 0; i < 4 * KPW + 11; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // one vector-memory read
             }
@@ -566,15 +588,12 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             v4f y;   // w, v are zero past the sequence end and dv
 #pragma unroll
             for (int i = 0; i < 4; ++i) y[i] = o.w[i] * o.v[i] - o.km[i] * xe[i];   // rows of E' S0 times k_mul
-            v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) u = Mfma(o.t[ii], y[ii], u);
-            const v4f uk = o.km * u;   // the update's Ut' is unnormalised
+            // S = G_15 o S + Ut~^T Y (Ut~ carries T and k_mul: U is never formed)
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
                 S[kt] *= o.g[kt];
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], uk[ii], S[kt]);
+                for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], y[ii], S[kt]);
             }
             // Off the chunk's chain (U, then the update): this wave's K slices
             // of (M T) Y, chosen by selects rather than branches (a branch per
@@ -712,6 +731,14 @@ ChunkConfig ChooseChunk(int dk, long long groups) {
     const int need = (kq + c.kpw - 1) / c.kpw;
     c.ks = need;
     return c;
+}
+
+// The preparation kernel, with its Ut' tiles' dynamic LDS (up to 128 KiB at
+// 32 key tiles, beside 20 KiB of static LDS).
+void LaunchPrep(int kq, const GatedDeltaNet2Params &p, int c0, int wn, unsigned blocks, hipStream_t stream) {
+    const int dyn = kPrepWaves * kq * 256 * static_cast<int>(sizeof(float));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel), dyn);
+    hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn, kq);
 }
 
 template <int KPW, int KS>
@@ -921,8 +948,7 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
         const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
         if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
         XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
-        hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(static_cast<unsigned>(pblocks)), dim3(64 * kPrepWaves), 0, stream,
-                           q, c0, wn, kq);
+        LaunchPrep(kq, q, c0, wn, static_cast<unsigned>(pblocks), stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
         if (packed)   // the kernel picks each sequence's state buffers itself
             LaunchRecurAny(q, c, c0, wn, kq, nullptr, nullptr, stream);
