@@ -33,7 +33,7 @@ fp32 evaluation order.  For them the test also runs the oracle in fp32 with
 the reference's operation order and each bound becomes max(gate, 8 x that
 fp32 error): the device must be about as accurate as the reference's own
 fp32 recurrence.  Measured (device / fp32 order, row_err): GDN-2 without L2
-norm 3.4e-6 / 1.7e-6; Mamba-3 growth 6.5e-6 / 4.4e-6; long angle runs
+norm 3.2e-6 / 1.7e-6; Mamba-3 growth 6.5e-6 / 4.4e-6; long angle runs
 3.7e-6 / 6.3e-6; GDN-2 hard reset (-200) 3.0e-5 / 1.3e-6, within the base gate.
 """
 
