@@ -262,6 +262,10 @@ int xm_softmax_cpu(const float *in, const int64_t *shape, int32_t rank, int64_t 
  *   "ss_lpc"         1, 2, 4, 8, 16: SelectiveScanFn lanes per channel (d_state <= 16)
  *   "ss_split"       1: SelectiveScanFn channel-block kernel only; 2: the
  *                    sequence-split kernel wherever it applies
+ *   "gdn2_kpw4"      1: chunked GDN-2 above 128 keys with 4 key tiles per wave
+ *   "gdn2_windowed"  1: chunked GDN-2 in windows of 128 chunks
+ *   "gdn2_split"     1: chunked GDN-2 never split along the sequence; 2: split
+ *                    into up to four segments wherever the sequence has 2+ chunks
  * The values are read with one atomic load per launch; a change affects calls
  * made after it.  No counterpart in the reference (its variants are fixed at
  * compile time).  xm_set_kernel_override returns XM_ERR_INVALID_ARGUMENT for

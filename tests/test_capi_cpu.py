@@ -302,6 +302,20 @@ def test_gdn2_valid_and_scratch():
         kq = kpw * ks
         block = 3 * kq * 256 + 16 * kq + 256 + 32
         nch = -(-T // 16)
+        rows, vt, kt = B * H, -(-V // 16), -(-K // 16)
+        # sequence split: rows (vt + kt) <= 160 column tiles and 32+ chunks;
+        # 1 + ceil(768 / (rows (vt + kt))) segments of 16+ chunks; every chunk's
+        # blocks, Psi [B,T,H,KP], Phi [nseg][rows][K][KP] (KP = 16 kt), S0 and
+        # the start states [nseg][rows][K][V]; at most 2 GiB
+        if rows * (vt + kt) <= 160 and nch >= 32 and nch * block * 4 < (1 << 31):
+            nseg = min(1 + max(1, -(-768 // (rows * (vt + kt)))), nch // 16)
+            sc = -(-nch // nseg)
+            nseg = -(-nch // sc)
+            if nseg >= 2:
+                total = (a256(rows * nch * block * 4) + a256(B * T * H * kt * 16 * 4)
+                         + a256(nseg * rows * K * kt * 16 * 4) + 2 * a256(nseg * rows * K * V * 4))
+                if total <= 2 << 30:
+                    return total
         # windows of 128 chunks, or of up to 128 MiB of blocks, balanced in length
         per_block = B * H * block * 4
         win = min(nch, 128)

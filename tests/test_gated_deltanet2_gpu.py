@@ -18,6 +18,7 @@ import pytest
 
 from oracle import cref
 from parity import TOL_GDN2, check, to_dev
+import xmetai_onnx_plugins as xp
 from xmetai_onnx_plugins import TorchAllocator, gated_deltanet2_fn, workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -204,6 +205,47 @@ def test_gdn2_benchmark_shapes(name):
     ref = cref.gated_deltanet2(*(sub[k] for k in KEYS), scale=s.scale, use_qk_l2norm=s.l2norm, dtype=np.float64)
     check(f"gated_deltanet2/{name}_heads", y[b:b + 1, :, hs], ref, TOL_GDN2)
     assert np.isfinite(y).all()
+
+
+# Sequence split (gdn2_split override 2: up to four segments wherever the
+# sequence has two or more chunks): segments after the first run from a zero
+# state beside identity columns, and their outputs are corrected afterwards.
+SPLIT_CASES = {
+    "t50_k100_v48_one_chunk_segments": S(1, 50, 3, 100, 48),
+    "t300_k128_v65": S(1, 300, 2, 128, 65),
+    "t600_k64_v32": S(1, 600, 2, 64, 32),
+    "t1000_k17_v15_nos0": S(2, 1000, 1, 17, 15, initial_state=False),
+    "t700_k320_v20_perkey": S(1, 700, 1, 320, 20, per_key_gates=True),
+    "t520_k512_v7": S(1, 520, 1, 512, 7),
+    "t1025_k256_v256": S(1, 1025, 1, 256, 256),
+    "t40_k128_v128_nol2": S(1, 40, 1, 128, 128, l2norm=False),   # the state grows ~60x a token
+}
+
+
+@pytest.mark.parametrize("name", sorted(SPLIT_CASES))
+def test_gdn2_sequence_split(name, override):
+    s = SPLIT_CASES[name]
+    inp = W.gated_deltanet2_inputs(s, seed=4)
+    override("gdn2_split", 2)
+    got = run_gpu(inp, s)
+    assert any(k.startswith("Gdn2ChunkSplitKernel") for k in xp.last_launches()), xp.last_launches()
+    ref32 = None if s.l2norm else run_ref(inp, s, np.float32)
+    check(f"gated_deltanet2/split_{name}", got, run_ref(inp, s), TOL_GDN2, ref32=ref32)
+
+
+def test_gdn2_sequence_split_selected_for_few_workgroups(override):
+    """A call with few column-tile workgroups and 32+ chunks splits its
+    sequence by itself; gdn2_split = 1 keeps one recurrence over the windows."""
+    s = S(1, 1024, 2, 64, 32)
+    inp = W.gated_deltanet2_inputs(s, seed=5)
+    got = run_gpu(inp, s)
+    assert any(k.startswith("Gdn2ChunkSplitKernel") for k in xp.last_launches()), xp.last_launches()
+    override("gdn2_split", 1)
+    whole = run_gpu(inp, s)
+    assert not any(k.startswith("Gdn2ChunkSplitKernel") for k in xp.last_launches()), xp.last_launches()
+    ref = run_ref(inp, s)
+    check("gated_deltanet2/split_auto", got, ref, TOL_GDN2)
+    check("gated_deltanet2/split_off", whole, ref, TOL_GDN2)
 
 
 def test_gdn2_column_independence_bitwise():

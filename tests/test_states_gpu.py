@@ -145,6 +145,20 @@ def test_gdn2_final_state_parity(name):
     np.testing.assert_array_equal(o, gdn_gpu(inp, s, state=False))   # the state write leaves o alone
 
 
+@pytest.mark.parametrize("shape", [(1, 1500, 2, 96, 40, True), (2, 700, 1, 320, 24, False), (1, 90, 1, 33, 17, True)])
+def test_gdn2_final_state_sequence_split(shape, override):
+    """The final state of a sequence-split call (gdn2_split = 2): the combine
+    kernel's last step, from the initial state or zeros."""
+    b, t, h, k, v, s0 = shape
+    s = S(b, t, h, k, v, initial_state=s0)
+    inp = W.gated_deltanet2_inputs(s, seed=8)
+    override("gdn2_split", 2)
+    o, st = gdn_gpu(inp, s)
+    ref_o, ref_st = gdn_ref(inp, s)
+    check(f"gated_deltanet2_state/split_{b}_{t}_{h}_{k}_{v}/o", o, ref_o, TOL_GDN2)
+    check(f"gated_deltanet2_state/split_{b}_{t}_{h}_{k}_{v}/S", st, ref_st, TOL_GDN2)
+
+
 @pytest.mark.parametrize("name", ["t4100_three_windows", "k448_t2100_window_carry"])
 def test_gdn2_final_state_windows_of_128_chunks(name, override):
     """The final state after 128-chunk windows (gdn2_windowed), the state

@@ -432,10 +432,21 @@ struct RecurLayout {
 // token rows; T: its length; sbase: the row's offset in the [B,H,K,V] states.
 // The state comes from s_in (zeros when null) and goes to s_out (not written
 // when null).  Every wave of the workgroup calls it with the same arguments.
-template <int KPW, int KS>
+// Column tile of a sequence-split run (Gdn2ChunkSplitKernel): tiles below VT
+// are value columns; tile VT + j carries the identity columns 16 j..16 j + 15
+// (keys): WV = 0, initial state I, the output goes to `psi` ([B,T,H,KP] rows,
+// KP = keys padded to 16) and the final state to a [K][KP] transition.  The
+// padded columns start at zero and stay zero, so they are stored as zeros.
+struct SplitTile {
+    int tile;
+    bool ident;
+    float *psi;
+};
+
+template <int KPW, int KS, bool SPLIT = false>
 __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, float *sXp, int h, size_t tok0, int T,
                                              int cs, int cw0, int nrun, int wn, const float *prep_row, size_t sbase,
-                                             const float *s_in, float *s_out) {
+                                             const float *s_in, float *s_out, SplitTile st = {}) {
     using L = RecurLayout<KPW, KS>;
     constexpr int KQ = L::KQ, FB = L::FB;
     constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oG = 3 * KQ * 256;   // block offsets (floats)
@@ -445,9 +456,15 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4;
     const int VT = (dv + 15) / 16;
-    const int vt = XcdLocalBlock(blockIdx.x, gridDim.x) % VT;
+    const int vt = SPLIT ? st.tile : XcdLocalBlock(blockIdx.x, gridDim.x) % VT;
+    const bool ident = SPLIT && st.ident;
     const int col = vt * 16 + (lane & 15);
-    const bool col_ok = col < dv;
+    const bool col_ok = !ident && col < dv;
+    // output column: the value column, or (identity tile) the key it starts as
+    const int kcol = SPLIT ? (vt - VT) * 16 + (lane & 15) : 0;
+    const int ocol = ident ? kcol : col;
+    const bool ocol_ok = ident || col_ok;
+    const int OW = ident ? (dk + 15) / 16 * 16 : dv;   // output row width
     const Rsrc rblk = MakeRsrc(prep_row, wn * FB * 4);   // this head row's prepared blocks of the window
     // byte offsets, from a chunk's first token in [B,T,H,V], of this lane's
     // tokens 4(l/16)+i in its column (out of range for columns past dv); the
@@ -464,7 +481,6 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     auto token_base = [&](const float *x, int t0) { return x + ((tok0 + t0) * H + h) * dv; };
     const float *const w_run = token_base(p.w, cs * kC);
     const float *const v_run = token_base(p.v, cs * kC);
-    float *const out_run = p.out + ((tok0 + cs * kC) * H + h) * dv;
     const int cstride = kC * HV;
     const int full_bytes = ((kC - 1) * HV + dv) * 4;
     auto rows_bytes = [&](int jl) {
@@ -472,6 +488,18 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         return left >= kC ? full_bytes : ((left - 1) * HV + dv) * 4;
     };
     auto chunk_off = [&](int jl) { return static_cast<long long>(jl) * cstride; };
+    // the output rows (O, or psi for an identity tile: rows of OW floats)
+    const int HO = H * OW;
+    int oo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) oo[i] = SPLIT ? (ocol_ok ? ((4 * g4 + i) * HO + ocol) * 4 : kOutOfRange) : vo[i];
+    float *const out_run = (ident ? st.psi : p.out) + ((tok0 + cs * kC) * H + h) * OW;
+    auto out_bytes = [&](int jl) {
+        if constexpr (!SPLIT) return rows_bytes(jl);
+        const int left = min(T - (cs + jl) * kC, kC);
+        return ((left - 1) * HO + OW) * 4;
+    };
+    auto out_off = [&](int jl) { return static_cast<long long>(jl) * (kC * HO); };
 
     v4f S[KPW];
 #pragma unroll
@@ -480,7 +508,9 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int key = kb + i;
-            S[kt][i] = (s_in != nullptr && col_ok && key < dk) ? s_in[sbase + static_cast<size_t>(key) * dv + col] : 0.0f;
+            S[kt][i] = ident ? (key == kcol && key < dk ? 1.0f : 0.0f)
+                             : (s_in != nullptr && col_ok && key < dk) ? s_in[sbase + static_cast<size_t>(key) * dv + col]
+                                                                       : 0.0f;
         }
     }
 
@@ -528,9 +558,9 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // and summed by wave 0, so the output products are spread over the waves.
         v4f op = {0.0f, 0.0f, 0.0f, 0.0f};
         auto store_out = [&](int jl, const v4f &out) __attribute__((always_inline)) {   // chunk jl of the run
-            const Rsrc ro = MakeRsrc(out_run + chunk_off(jl), rows_bytes(jl));
+            const Rsrc ro = MakeRsrc(out_run + out_off(jl), out_bytes(jl));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) BufStF(ro, vo[i], out[i]);
+            for (int i = 0; i < 4; ++i) BufStF(ro, oo[i], out[i]);
         };
         auto sum_out = [&](const float *xp) __attribute__((always_inline)) -> v4f {
             v4f out = LdsF4(xp + 256 + lane * 4);
@@ -640,13 +670,13 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             __syncthreads();   // the partial buffers are reused by the workgroup's next run
         }
     }
-    if (s_out != nullptr && col_ok) {
+    if (s_out != nullptr && ocol_ok) {
 #pragma unroll
         for (int kt = 0; kt < KPW; ++kt) {
             const int kb = (ks * KPW + kt) * 16 + 4 * g4;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (kb + i < dk) s_out[sbase + static_cast<size_t>(kb + i) * dv + col] = S[kt][i];
+                if (kb + i < dk) s_out[sbase + static_cast<size_t>(kb + i) * OW + ocol] = S[kt][i];
         }
     }
 }
@@ -693,6 +723,168 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
         float *out = c0 + nrun == nch ? p.final_state : p.state;
         Gdn2RecurRun<KPW, KS>(p, sXp, h, tok0, T, c0, i0, nrun, wn, prep_row, sbase, in, out);
     }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Sequence split (launches with few column-tile workgroups)
+// ---------------------------------------------------------------------------
+// The state after a run of chunks is affine in the state before it:
+// S_end = Phi S_start + S0 (S0: the run from a zero state), and so are its
+// outputs: O = O0 + Psi S_start.  The chunks are cut into nseg segments of sc;
+// all segments run at once, segment 0 from the initial state and the others
+// from zero, the latter with dk identity columns beside the value columns (WV
+// = 0, state I), whose outputs are Psi and whose final state is Phi.  The
+// combine kernel then steps S_start(s + 1) = Phi_s S_start(s) + S0_s over the
+// segments, and the correction kernel adds Psi_s S_start(s) to their outputs.
+//
+// Workgroup (segment, (b, h), column tile) over VT + KT tiles; segment 0 runs
+// its VT value tiles only.  Value tiles write O0 (O for segment 0) and S0_s
+// ([nseg][B*H][K][V]); identity tiles write Psi ([B,T,H,K], tokens of
+// segments >= 1) and Phi_s ([nseg][B*H][K][K], row = key, column = identity
+// column).
+template <int KPW, int KS>
+__global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Params p, int sc, int nchunks,
+                                                                float *psi, float *phi, float *s0) {
+    using L = RecurLayout<KPW, KS>;
+    __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
+    const int H = p.nheads, VT = (p.dv + 15) / 16, KT = (p.dk + 15) / 16, tiles = VT + KT;
+    const int rows = p.batch * H;
+    const int x = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int tile = x % tiles, row = (x / tiles) % rows, seg = x / tiles / rows;
+    if (seg == 0 && tile >= VT) return;   // whole workgroup
+    const int cs = seg * sc, nrun = min(sc, nchunks - cs);
+    if (nrun <= 0) return;
+    const int b = row / H, h = row % H;
+    const bool ident = tile >= VT;
+    const size_t kv = static_cast<size_t>(p.dk) * p.dv, kp = static_cast<size_t>(p.dk) * KT * 16;
+    const float *s_in = seg == 0 && p.initial_state != nullptr ? p.initial_state + row * kv : nullptr;
+    float *s_out = ident ? phi + (static_cast<size_t>(seg) * rows + row) * kp : s0 + (static_cast<size_t>(seg) * rows + row) * kv;
+    Gdn2RecurRun<KPW, KS, true>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, cs, cs, nrun, nchunks,
+                                p.prepared + static_cast<size_t>(row) * nchunks * L::FB, 0, s_in, s_out,
+                                SplitTile{tile, ident, psi});
+}
+
+// Workgroup ((b, h), value tile), 16 waves: S (keys x 16 columns, keys padded
+// to 16) in LDS, S_start(1) = S0_0; for s >= 1 it stores S_start(s) to sst and
+// forms S_start(s + 1) = Phi_s S_start(s) + S0_s on MFMA, wave w taking the
+// 16-key output tiles w, w + 16; the last one is the final state.  Phi rows
+// (pitch KP, 16-byte aligned) are read 16 bytes a lane, eight key tiles'
+// loads issued before their products.  Dynamic LDS: two buffers of KT * 256
+// floats.
+__global__ __launch_bounds__(1024) void Gdn2SplitCombineKernel(GatedDeltaNet2Params p, int nseg, const float *phi,
+                                                               const float *s0, float *sst) {
+    extern __shared__ float comb[];
+    const int dk = p.dk, dv = p.dv, VT = (dv + 15) / 16, KT = (dk + 15) / 16, KP = KT * 16;
+    const int rows = p.batch * p.nheads;
+    const int row = blockIdx.x / VT, vt = blockIdx.x % VT;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, m16 = lane & 15, g4 = lane >> 4;
+    const size_t kv = static_cast<size_t>(dk) * dv, kp = static_cast<size_t>(dk) * KP;
+    const int col = vt * 16 + m16;
+    float *cur = comb, *nxt = comb + KT * 256;
+    for (int i = tid; i < KT * 256; i += 1024) {
+        const int key = i / 16, c = vt * 16 + i % 16;
+        cur[i] = key < dk && c < dv ? s0[row * kv + static_cast<size_t>(key) * dv + c] : 0.0f;
+    }
+    __syncthreads();
+    for (int s = 1; s < nseg; ++s) {   // workgroup-uniform
+        float *const start = sst + (static_cast<size_t>(s) * rows + row) * kv;
+        for (int i = tid; i < KT * 256; i += 1024) {
+            const int key = i / 16, c = vt * 16 + i % 16;
+            if (key < dk && c < dv) start[static_cast<size_t>(key) * dv + c] = cur[i];
+        }
+        const float *const ph = phi + (static_cast<size_t>(s) * rows + row) * kp;
+        const float *const add = s0 + (static_cast<size_t>(s) * rows + row) * kv;
+        for (int kt = w; kt < KT; kt += 16) {
+            // D[m][n] = S_next[16 kt + m][n]: lane n + 16 (m / 4), register m % 4
+            v4f acc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt * 16 + 4 * g4 + i;
+                acc[i] = key < dk && col < dv ? add[static_cast<size_t>(key) * dv + col] : 0.0f;
+            }
+            const int arow = kt * 16 + m16;   // A[m][k] = Phi[16 kt + m][k], lane m + 16 k
+            const float *const prow = ph + static_cast<size_t>(arow < dk ? arow : 0) * KP + 4 * g4;
+            for (int k0 = 0; k0 < KT; k0 += 8) {
+                v4f a[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    a[u] = arow < dk && k0 + u < KT ? *reinterpret_cast<const v4f *>(prow + (k0 + u) * 16) : z;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (k0 + u >= KT) break;
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii)   // B[k][n] = S[16 kb + 4 k + ii][n]
+                        acc = Mfma(a[u][ii], cur[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nxt[(kt * 16 + 4 * g4 + i) * 16 + m16] = acc[i];
+        }
+        __syncthreads();
+        float *const t = cur;
+        cur = nxt;
+        nxt = t;
+    }
+    if (p.final_state != nullptr) {
+        float *const fs = p.final_state + row * kv;
+        for (int i = tid; i < KT * 256; i += 1024) {
+            const int key = i / 16, c = vt * 16 + i % 16;
+            if (key < dk && c < dv) fs[static_cast<size_t>(key) * dv + c] = cur[i];
+        }
+    }
+}
+
+// O += Psi_s S_start(s) over the tokens of segment s >= 1: workgroup ((b, h),
+// value tile, s), 4 waves taking the segment's chunks in turn, S_start(s)'s
+// column tile staged in LDS.  D[m][n] = sum_k Psi[t0 + m][k] S_start[k][n] on
+// MFMA (A: lane m + 16 k holds Psi[t0 + m][16 kb + 4 k + ii], 16 bytes of a
+// KP-pitch row; B from LDS), added to the output rows.  Dynamic LDS: KT * 256
+// floats.
+__global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int nchunks,
+                                                              const float *psi, const float *sst) {
+    extern __shared__ float sts[];
+    const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
+    const int KP = KT * 16, rows = p.batch * H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, m16 = lane & 15, g4 = lane >> 4;
+    const int x = blockIdx.x;
+    const int vt = x % VT, row = (x / VT) % rows, seg = 1 + x / VT / rows;
+    const int b = row / H, h = row % H;
+    const size_t kv = static_cast<size_t>(dk) * dv;
+    const float *const st = sst + (static_cast<size_t>(seg) * rows + row) * kv;
+    for (int i = tid; i < KT * 256; i += 256) {
+        const int key = i / 16, c = vt * 16 + i % 16;
+        sts[i] = key < dk && c < dv ? st[static_cast<size_t>(key) * dv + c] : 0.0f;
+    }
+    __syncthreads();
+    const int col = vt * 16 + m16;
+    const int c1 = min((seg + 1) * sc, nchunks);
+    for (int c = seg * sc + w; c < c1; c += 4) {   // wave-uniform; no barrier below
+        const int ta = c * kC + m16;   // this lane's A-operand token
+        const float *const prow = psi + ((static_cast<size_t>(b) * T + (ta < T ? ta : T - 1)) * H + h) * KP + 4 * g4;
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k0 = 0; k0 < KT; k0 += 8) {
+            v4f a[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                a[u] = ta < T && k0 + u < KT ? *reinterpret_cast<const v4f *>(prow + (k0 + u) * 16) : z;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (k0 + u >= KT) break;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii)
+                    acc = Mfma(a[u][ii], sts[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = c * kC + 4 * g4 + i;
+            if (t < T && col < dv) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] += acc[i];
+        }
     }
 }
 
@@ -772,6 +964,113 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
     XM_GDN2_RECUR(4, 6) XM_GDN2_RECUR(4, 7) XM_GDN2_RECUR(4, 8) XM_GDN2_RECUR(5, 4) XM_GDN2_RECUR(6, 4)
 #undef XM_GDN2_RECUR
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
+}
+
+template <int KPW, int KS>
+void LaunchSplitRecur(const GatedDeltaNet2Params &p, int nseg, int sc, int nchunks, float *psi, float *phi, float *s0,
+                      hipStream_t stream) {
+    const long long tiles = (p.dv + 15) / 16 + (p.dk + 15) / 16;
+    const long long blocks = static_cast<long long>(nseg) * p.batch * p.nheads * tiles;
+    if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    XM_NOTE_LAUNCH("Gdn2ChunkSplitKernel", {}, KPW, KS);
+    hipLaunchKernelGGL((Gdn2ChunkSplitKernel<KPW, KS>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, stream, p,
+                       sc, nchunks, psi, phi, s0);
+}
+
+void LaunchSplitRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int nseg, int sc, int nchunks, float *psi,
+                         float *phi, float *s0, hipStream_t stream) {
+#define XM_GDN2_SPLIT(KPW_, KS_) \
+    if (c.kpw == KPW_ && c.ks == KS_) return LaunchSplitRecur<KPW_, KS_>(p, nseg, sc, nchunks, psi, phi, s0, stream);
+    XM_GDN2_SPLIT(1, 1) XM_GDN2_SPLIT(2, 1) XM_GDN2_SPLIT(2, 2) XM_GDN2_SPLIT(2, 3) XM_GDN2_SPLIT(2, 4)
+    XM_GDN2_SPLIT(3, 4) XM_GDN2_SPLIT(3, 8) XM_GDN2_SPLIT(4, 3) XM_GDN2_SPLIT(4, 4) XM_GDN2_SPLIT(4, 5)
+    XM_GDN2_SPLIT(4, 6) XM_GDN2_SPLIT(4, 7) XM_GDN2_SPLIT(4, 8) XM_GDN2_SPLIT(5, 4) XM_GDN2_SPLIT(6, 4)
+#undef XM_GDN2_SPLIT
+    throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
+}
+
+// Sequence split of an unpacked call (see Gdn2ChunkSplitKernel): nseg segments
+// of sc chunks, every chunk prepared at once.  Scratch: the prepared blocks
+// of every chunk, Psi ([B,T,H,KP]), Phi ([nseg][B*H][K][KP]), S0 and the
+// segment start states ([nseg][B*H][K][V] each).  Segments >= 1 run their dk
+// identity columns beside the value columns, 1 + dk/dv times the
+// recurrence work, on enough workgroups to fill the chip (about 768 beyond
+// segment 0, segments of at least 16 chunks).  A launch of W0 = B*H*VT
+// column-tile workgroups (at most one per CU) steps each chunk at the
+// latency-bound rate; the split spreads B*H*(VT+KT) tiles' work over the
+// CUs at the throughput rate, so it pays when B*H*(VT+KT) is well under the
+// CU count: taken at <= 160 and 32+ chunks.  At most 2 GiB of scratch.
+struct SplitPlan {
+    int nseg = 0, sc = 0, nchunks = 0;
+    size_t blocks = 0, psi = 0, phi = 0, s0 = 0;
+    size_t total() const { return blocks + psi + phi + 2 * s0; }
+};
+
+SplitPlan PlanSplit(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
+    const int ov = GetOverride(kOverrideGdn2Split);
+    // 128-chunk windows (gdn2_windowed) are the windowed path's test case
+    if (packed || ov == 1 || (ov == 0 && GetOverride(kOverrideGdn2Windowed) == 1)) return SplitPlan{};
+    const long long rows = static_cast<long long>(batch) * nheads;
+    const int VT = (dv + 15) / 16, KT = (dk + 15) / 16;
+    const ChunkConfig c = ChooseChunk(dk, rows * VT);
+    const int nchunks = (seqlen + kC - 1) / kC;
+    const size_t fb = static_cast<size_t>(BlockFloats(c.kpw * c.ks)) * sizeof(float);
+    // the recurrence addresses a row's blocks, and 16 tokens of Psi rows, with
+    // 32-bit byte offsets
+    if (static_cast<size_t>(nchunks) * fb >= (size_t{1} << 31)) return SplitPlan{};
+    if (static_cast<long long>(nheads) * KT * 16 >= (1LL << 25)) return SplitPlan{};
+    int nseg;
+    if (ov == 2) {
+        nseg = std::min(nchunks, 4);
+    } else {
+        if (rows * (VT + KT) > 160 || nchunks < 32) return SplitPlan{};
+        const long long per = rows * (VT + KT);
+        nseg = 1 + static_cast<int>(std::max<long long>(1, (768 + per - 1) / per));
+        nseg = std::min(nseg, nchunks / 16);
+    }
+    if (nseg < 2) return SplitPlan{};
+    SplitPlan sp;
+    sp.sc = (nchunks + nseg - 1) / nseg;
+    sp.nseg = (nchunks + sp.sc - 1) / sp.sc;
+    if (sp.nseg < 2) return SplitPlan{};
+    sp.nchunks = nchunks;
+    sp.blocks = Align256(static_cast<size_t>(rows) * nchunks * fb);
+    sp.psi = Align256(static_cast<size_t>(batch) * seqlen * nheads * KT * 16 * sizeof(float));
+    sp.phi = Align256(static_cast<size_t>(sp.nseg) * rows * dk * KT * 16 * sizeof(float));
+    sp.s0 = Align256(static_cast<size_t>(sp.nseg) * rows * dk * dv * sizeof(float));
+    if (sp.total() > std::min(cap, size_t{2} << 30)) return SplitPlan{};
+    return sp;
+}
+
+void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const SplitPlan &sp, char *base,
+                 hipStream_t stream) {
+    GatedDeltaNet2Params q = p;
+    q.prepared = reinterpret_cast<float *>(base);
+    float *const psi = reinterpret_cast<float *>(base + sp.blocks);
+    float *const phi = reinterpret_cast<float *>(base + sp.blocks + sp.psi);
+    float *const s0 = reinterpret_cast<float *>(base + sp.blocks + sp.psi + sp.phi);
+    float *const sst = reinterpret_cast<float *>(base + sp.blocks + sp.psi + sp.phi + sp.s0);
+    const long long rows = static_cast<long long>(p.batch) * p.nheads;
+    const int VT = (p.dv + 15) / 16, KT = (p.dk + 15) / 16;
+    const long long items = rows * sp.nchunks;
+    const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
+    if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
+    LaunchPrep(c.kpw * c.ks, q, 0, sp.nchunks, static_cast<unsigned>(pblocks), stream);
+    XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
+    LaunchSplitRecurAny(q, c, sp.nseg, sp.sc, sp.nchunks, psi, phi, s0, stream);
+    XM_LAUNCH_CHECK("GatedDeltaNet2Fn split recurrence");
+    const int lds = 2 * KT * 256 * static_cast<int>(sizeof(float));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCombineKernel), lds);
+    XM_NOTE_LAUNCH("Gdn2SplitCombineKernel", {}, );
+    hipLaunchKernelGGL(Gdn2SplitCombineKernel, dim3(static_cast<unsigned>(rows * VT)), dim3(1024), lds, stream, q,
+                       sp.nseg, phi, s0, sst);
+    XM_LAUNCH_CHECK("GatedDeltaNet2Fn split combine");
+    const long long cblocks = rows * VT * (sp.nseg - 1);
+    if (cblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    XM_NOTE_LAUNCH("Gdn2SplitCorrectKernel", {}, );
+    hipLaunchKernelGGL(Gdn2SplitCorrectKernel, dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q,
+                       sp.sc, sp.nchunks, psi, sst);
+    XM_LAUNCH_CHECK("GatedDeltaNet2Fn split correction");
 }
 
 // Scratch of one call for a budget of `cap` bytes: the chunks per window and
@@ -903,6 +1202,8 @@ __global__ __launch_bounds__(256) void Gdn2PackedChunksKernel(GatedDeltaNet2Para
 
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
     if (dk > kGdn2ChunkKeyLimit) return 0;
+    const SplitPlan sp = PlanSplit(batch, seqlen, nheads, dk, dv, packed, cap);
+    if (sp.nseg > 0) return sp.total();
     const WindowPlan w = PlanWindows(batch, seqlen, nheads, dk, dv, packed, cap);
     return w.win == 0 ? SIZE_MAX : w.total();
 }
@@ -920,6 +1221,11 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
     const ChunkConfig c = ChooseChunk(p.dk, static_cast<long long>(p.batch) * p.nheads * ((p.dv + 15) / 16));
     const int kq = c.kpw * c.ks;
     const bool packed = p.cu_seqlens != nullptr;
+    const SplitPlan sp = PlanSplit(p.batch, p.seqlen, p.nheads, p.dk, p.dv, packed, scratch_bytes);
+    if (sp.nseg > 0 && scratch != nullptr) {
+        LaunchSplit(q, c, sp, static_cast<char *>(scratch), stream);
+        return true;
+    }
     const WindowPlan plan = PlanWindows(p.batch, p.seqlen, p.nheads, p.dk, p.dv, packed, scratch_bytes);
     if (plan.win == 0 || plan.total() > scratch_bytes || scratch == nullptr)
         throw Error(XM_ERR_ALLOC, "GatedDeltaNet2Fn: the scratch buffer is smaller than the call needs");

@@ -145,6 +145,7 @@ constexpr OverrideSpec kOverrides[kOverrideCount] = {
     {"ss_split", {1, 2, 0}},             // 1: one workgroup per channel block; 2: sequence-split
     {"gdn2_kpw4", {1, 0}},               // 1: GDN-2 chunked, 4 key tiles per wave above 128 keys
     {"gdn2_windowed", {1, 0}},           // 1: GDN-2 chunked, windows of 128 chunks only
+    {"gdn2_split", {1, 2, 0}},           // GDN-2 chunked: 1 no sequence split, 2 split wherever 2+ chunks
 };
 std::atomic<int64_t> g_override[kOverrideCount];
 
