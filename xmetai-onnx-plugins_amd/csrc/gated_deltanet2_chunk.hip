@@ -765,14 +765,16 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
                                 SplitTile{tile, ident, psi});
 }
 
-// Workgroup ((b, h), value tile), 16 waves: S (keys x 16 columns, keys padded
+// Workgroup ((b, h), value tile), 8 waves: S (keys x 16 columns, keys padded
 // to 16) in LDS, S_start(1) = S0_0; for s >= 1 it stores S_start(s) to sst and
 // forms S_start(s + 1) = Phi_s S_start(s) + S0_s on MFMA, wave w taking the
-// 16-key output tiles w, w + 16; the last one is the final state.  Phi rows
-// (pitch KP, 16-byte aligned) are read 16 bytes a lane, eight key tiles'
-// loads issued before their products.  Dynamic LDS: two buffers of KT * 256
-// floats.
-__global__ __launch_bounds__(1024) void Gdn2SplitCombineKernel(GatedDeltaNet2Params p, int nseg, const float *phi,
+// 16-key output tiles w, w + 8, ...; the last one is the final state.  Phi rows
+// (pitch KP, 16-byte aligned) are read 16 bytes a lane.  A wave's first tile
+// has its first eight key tiles of Phi_{s+1} and its S0_{s+1} values loaded
+// during step s (the steps are serial: each would otherwise wait out its
+// loads); further key tiles are loaded eight at a time.  Dynamic LDS: two
+// buffers of KT * 256 floats.
+__global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Params p, int nseg, const float *phi,
                                                                const float *s0, float *sst) {
     extern __shared__ float comb[];
     const int dk = p.dk, dv = p.dv, VT = (dv + 15) / 16, KT = (dk + 15) / 16, KP = KT * 16;
@@ -782,43 +784,78 @@ __global__ __launch_bounds__(1024) void Gdn2SplitCombineKernel(GatedDeltaNet2Par
     const size_t kv = static_cast<size_t>(dk) * dv, kp = static_cast<size_t>(dk) * KP;
     const int col = vt * 16 + m16;
     float *cur = comb, *nxt = comb + KT * 256;
-    for (int i = tid; i < KT * 256; i += 1024) {
+    for (int i = tid; i < KT * 256; i += 512) {
         const int key = i / 16, c = vt * 16 + i % 16;
         cur[i] = key < dk && c < dv ? s0[row * kv + static_cast<size_t>(key) * dv + c] : 0.0f;
+    }
+    // A[m][k] = Phi_s[16 kt + m][k] (lane m + 16 k, 16 bytes per key tile);
+    // S0_s at the D layout (key 16 kt + 4 (l / 16) + i, column l % 16)
+    auto load_a = [&](int s, int kt, int k0, v4f (&a)[8]) __attribute__((always_inline)) {
+        const int arow = kt * 16 + m16;
+        const float *const prow = phi + (static_cast<size_t>(s) * rows + row) * kp +
+                                  static_cast<size_t>(arow < dk ? arow : 0) * KP + 4 * g4;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+            a[u] = arow < dk && k0 + u < KT ? *reinterpret_cast<const v4f *>(prow + (k0 + u) * 16) : z;
+        }
+    };
+    auto load_add = [&](int s, int kt) __attribute__((always_inline)) -> v4f {
+        const float *const add = s0 + (static_cast<size_t>(s) * rows + row) * kv;
+        v4f r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = kt * 16 + 4 * g4 + i;
+            r[i] = key < dk && col < dv ? add[static_cast<size_t>(key) * dv + col] : 0.0f;
+        }
+        return r;
+    };
+    auto products = [&](v4f acc, const v4f (&a)[8], int k0) __attribute__((always_inline)) -> v4f {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (k0 + u >= KT) break;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)   // B[k][n] = S[16 kb + 4 k + ii][n]
+                acc = Mfma(a[u][ii], cur[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
+        }
+        return acc;
+    };
+    const bool first = w < KT;   // this wave's first tile, kt = w
+    v4f a0[8], a1[8], add0 = {0.0f, 0.0f, 0.0f, 0.0f}, add1 = add0;
+    if (first && nseg > 1) {
+        load_a(1, w, 0, a0);
+        add0 = load_add(1, w);
     }
     __syncthreads();
     for (int s = 1; s < nseg; ++s) {   // workgroup-uniform
         float *const start = sst + (static_cast<size_t>(s) * rows + row) * kv;
-        for (int i = tid; i < KT * 256; i += 1024) {
+        for (int i = tid; i < KT * 256; i += 512) {
             const int key = i / 16, c = vt * 16 + i % 16;
             if (key < dk && c < dv) start[static_cast<size_t>(key) * dv + c] = cur[i];
         }
-        const float *const ph = phi + (static_cast<size_t>(s) * rows + row) * kp;
-        const float *const add = s0 + (static_cast<size_t>(s) * rows + row) * kv;
-        for (int kt = w; kt < KT; kt += 16) {
-            // D[m][n] = S_next[16 kt + m][n]: lane n + 16 (m / 4), register m % 4
-            v4f acc;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kt * 16 + 4 * g4 + i;
-                acc[i] = key < dk && col < dv ? add[static_cast<size_t>(key) * dv + col] : 0.0f;
+        if (first) {
+            if (s + 1 < nseg) {   // the next step's operands, in flight during this one
+                load_a(s + 1, w, 0, a1);
+                add1 = load_add(s + 1, w);
             }
-            const int arow = kt * 16 + m16;   // A[m][k] = Phi[16 kt + m][k], lane m + 16 k
-            const float *const prow = ph + static_cast<size_t>(arow < dk ? arow : 0) * KP + 4 * g4;
+            v4f acc = products(add0, a0, 0);
+            for (int k0 = 8; k0 < KT; k0 += 8) {
+                v4f a[8];
+                load_a(s, w, k0, a);
+                acc = products(acc, a, k0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nxt[(w * 16 + 4 * g4 + i) * 16 + m16] = acc[i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a0[u] = a1[u];
+            add0 = add1;
+        }
+        for (int kt = w + 8; kt < KT; kt += 8) {   // keys beyond 128: further tiles
+            v4f acc = load_add(s, kt);
             for (int k0 = 0; k0 < KT; k0 += 8) {
                 v4f a[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    a[u] = arow < dk && k0 + u < KT ? *reinterpret_cast<const v4f *>(prow + (k0 + u) * 16) : z;
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    if (k0 + u >= KT) break;
-#pragma unroll
-                    for (int ii = 0; ii < 4; ++ii)   // B[k][n] = S[16 kb + 4 k + ii][n]
-                        acc = Mfma(a[u][ii], cur[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
-                }
+                load_a(s, kt, k0, a);
+                acc = products(acc, a, k0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) nxt[(kt * 16 + 4 * g4 + i) * 16 + m16] = acc[i];
@@ -830,7 +867,7 @@ __global__ __launch_bounds__(1024) void Gdn2SplitCombineKernel(GatedDeltaNet2Par
     }
     if (p.final_state != nullptr) {
         float *const fs = p.final_state + row * kv;
-        for (int i = tid; i < KT * 256; i += 1024) {
+        for (int i = tid; i < KT * 256; i += 512) {
             const int key = i / 16, c = vt * 16 + i % 16;
             if (key < dk && c < dv) fs[static_cast<size_t>(key) * dv + c] = cur[i];
         }
@@ -838,53 +875,61 @@ __global__ __launch_bounds__(1024) void Gdn2SplitCombineKernel(GatedDeltaNet2Par
 }
 
 // O += Psi_s S_start(s) over the tokens of segment s >= 1: workgroup ((b, h),
-// value tile, s), 4 waves taking the segment's chunks in turn, S_start(s)'s
-// column tile staged in LDS.  D[m][n] = sum_k Psi[t0 + m][k] S_start[k][n] on
-// MFMA (A: lane m + 16 k holds Psi[t0 + m][16 kb + 4 k + ii], 16 bytes of a
-// KP-pitch row; B from LDS), added to the output rows.  Dynamic LDS: KT * 256
-// floats.
+// value tile, s, four consecutive chunks of the segment), a wave per chunk,
+// S_start(s)'s column tile staged in LDS.  D[m][n] = sum_k Psi[t0 + m][k]
+// S_start[k][n] on MFMA (A: lane m + 16 k holds Psi[t0 + m][16 kb + 4 k + ii],
+// 16 bytes of a KP-pitch row; B from LDS), added to the output rows.
+// Dynamic LDS: KT * 256 floats.
 __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int nchunks,
                                                               const float *psi, const float *sst) {
     extern __shared__ float sts[];
     const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
-    const int KP = KT * 16, rows = p.batch * H;
+    const int KP = KT * 16, rows = p.batch * H, ncg = (sc + 3) / 4;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, m16 = lane & 15, g4 = lane >> 4;
     const int x = blockIdx.x;
-    const int vt = x % VT, row = (x / VT) % rows, seg = 1 + x / VT / rows;
+    const int cg = x % ncg, vt = (x / ncg) % VT, row = (x / ncg / VT) % rows, seg = 1 + x / ncg / VT / rows;
     const int b = row / H, h = row % H;
+    const int c = seg * sc + cg * 4 + w;
+    const bool live = cg * 4 + w < sc && c < nchunks;   // whole wave
+    const int col = vt * 16 + m16;
+    const int ta = c * kC + m16;   // this lane's A-operand token
+    const bool ta_ok = live && ta < T;
+    const float *const prow = psi + ((static_cast<size_t>(b) * T + (ta_ok ? ta : 0)) * H + h) * KP + 4 * g4;
+    v4f a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {   // the first eight key tiles' loads before the staging wait
+        const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+        a[u] = ta_ok && u < KT ? *reinterpret_cast<const v4f *>(prow + u * 16) : z;
+    }
     const size_t kv = static_cast<size_t>(dk) * dv;
     const float *const st = sst + (static_cast<size_t>(seg) * rows + row) * kv;
     for (int i = tid; i < KT * 256; i += 256) {
-        const int key = i / 16, c = vt * 16 + i % 16;
-        sts[i] = key < dk && c < dv ? st[static_cast<size_t>(key) * dv + c] : 0.0f;
+        const int key = i / 16, cc = vt * 16 + i % 16;
+        sts[i] = key < dk && cc < dv ? st[static_cast<size_t>(key) * dv + cc] : 0.0f;
     }
     __syncthreads();
-    const int col = vt * 16 + m16;
-    const int c1 = min((seg + 1) * sc, nchunks);
-    for (int c = seg * sc + w; c < c1; c += 4) {   // wave-uniform; no barrier below
-        const int ta = c * kC + m16;   // this lane's A-operand token
-        const float *const prow = psi + ((static_cast<size_t>(b) * T + (ta < T ? ta : T - 1)) * H + h) * KP + 4 * g4;
-        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int k0 = 0; k0 < KT; k0 += 8) {
-            v4f a[8];
+    if (!live) return;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < KT; k0 += 8) {
+        if (k0 > 0) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-                a[u] = ta < T && k0 + u < KT ? *reinterpret_cast<const v4f *>(prow + (k0 + u) * 16) : z;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (k0 + u >= KT) break;
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii)
-                    acc = Mfma(a[u][ii], sts[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
+                a[u] = ta_ok && k0 + u < KT ? *reinterpret_cast<const v4f *>(prow + (k0 + u) * 16) : z;
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = c * kC + 4 * g4 + i;
-            if (t < T && col < dv) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] += acc[i];
+        for (int u = 0; u < 8; ++u) {
+            if (k0 + u >= KT) break;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+                acc = Mfma(a[u][ii], sts[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
         }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = c * kC + 4 * g4 + i;
+        if (t < T && col < dv) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] += acc[i];
     }
 }
 
@@ -1062,10 +1107,10 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     const int lds = 2 * KT * 256 * static_cast<int>(sizeof(float));
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCombineKernel), lds);
     XM_NOTE_LAUNCH("Gdn2SplitCombineKernel", {}, );
-    hipLaunchKernelGGL(Gdn2SplitCombineKernel, dim3(static_cast<unsigned>(rows * VT)), dim3(1024), lds, stream, q,
+    hipLaunchKernelGGL(Gdn2SplitCombineKernel, dim3(static_cast<unsigned>(rows * VT)), dim3(512), lds, stream, q,
                        sp.nseg, phi, s0, sst);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split combine");
-    const long long cblocks = rows * VT * (sp.nseg - 1);
+    const long long cblocks = rows * VT * (sp.nseg - 1) * ((sp.sc + 3) / 4);
     if (cblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2SplitCorrectKernel", {}, );
     hipLaunchKernelGGL(Gdn2SplitCorrectKernel, dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q,

@@ -205,6 +205,8 @@ GDN2_MAIN = GatedDeltaNet2Shape(batch=4, seqlen=4096, nheads=16, dk=128, dv=128,
 GDN2_LONG = GatedDeltaNet2Shape(batch=1, seqlen=16384, nheads=8, dk=256, dv=256, initial_state=False)
 GDN2_WIDEK = GatedDeltaNet2Shape(batch=2, seqlen=2048, nheads=4, dk=320, dv=64, initial_state=True)
 GDN2_V65 = GatedDeltaNet2Shape(batch=4, seqlen=4096, nheads=16, dk=128, dv=65, initial_state=True)
+# few heads: 32 column-tile workgroups, the sequence-split path
+GDN2_FEW = GatedDeltaNet2Shape(batch=1, seqlen=8192, nheads=4, dk=128, dv=128, initial_state=True)
 M3_MAIN = Mamba3SisoShape(batch=4, seqlen=4096, nheads=32, headdim=64, dstate=128, angles=64,
                           has_d=True, has_z=False)
 
@@ -215,5 +217,6 @@ NAMED = {
     "gated_deltanet2_b1_t16384_h8_k256_v256": GDN2_LONG,
     "gated_deltanet2_b2_t2048_h4_k320_v64": GDN2_WIDEK,
     "gated_deltanet2_b4_t4096_h16_k128_v65": GDN2_V65,
+    "gated_deltanet2_b1_t8192_h4_k128_v128": GDN2_FEW,
     "mamba3_siso_b4_t4096_h32_p64_n128": M3_MAIN,
 }
