@@ -772,8 +772,10 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
 // (pitch KP, 16-byte aligned) are read 16 bytes a lane.  A wave's first tile
 // has its first eight key tiles of Phi_{s+1} and its S0_{s+1} values loaded
 // during step s (the steps are serial: each would otherwise wait out its
-// loads); further key tiles are loaded eight at a time.  Dynamic LDS: two
-// buffers of KT * 256 floats.
+// loads); further key tiles are loaded eight at a time.  S is stored column
+// by column (pitch KP + 4 floats: the 16 columns' rows fall in different
+// banks), so a lane reads its four B-operand keys with one 16-byte LDS read.
+// Dynamic LDS: two buffers of 16 (KP + 4) floats.
 __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Params p, int nseg, const float *phi,
                                                                const float *s0, float *sst) {
     extern __shared__ float comb[];
@@ -783,10 +785,11 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, m16 = lane & 15, g4 = lane >> 4;
     const size_t kv = static_cast<size_t>(dk) * dv, kp = static_cast<size_t>(dk) * KP;
     const int col = vt * 16 + m16;
-    float *cur = comb, *nxt = comb + KT * 256;
+    const int SP = KP + 4;   // LDS pitch of one column of S
+    float *cur = comb, *nxt = comb + 16 * SP;
     for (int i = tid; i < KT * 256; i += 512) {
         const int key = i / 16, c = vt * 16 + i % 16;
-        cur[i] = key < dk && c < dv ? s0[row * kv + static_cast<size_t>(key) * dv + c] : 0.0f;
+        cur[(i % 16) * SP + key] = key < dk && c < dv ? s0[row * kv + static_cast<size_t>(key) * dv + c] : 0.0f;
     }
     // A[m][k] = Phi_s[16 kt + m][k] (lane m + 16 k, 16 bytes per key tile);
     // S0_s at the D layout (key 16 kt + 4 (l / 16) + i, column l % 16)
@@ -814,9 +817,9 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             if (k0 + u >= KT) break;
+            const v4f bs = LdsF4(cur + m16 * SP + (k0 + u) * 16 + 4 * g4);   // B[k][n] = S[16 kb + 4 k + ii][n]
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii)   // B[k][n] = S[16 kb + 4 k + ii][n]
-                acc = Mfma(a[u][ii], cur[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
+            for (int ii = 0; ii < 4; ++ii) acc = Mfma(a[u][ii], bs[ii], acc);
         }
         return acc;
     };
@@ -831,7 +834,7 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
         float *const start = sst + (static_cast<size_t>(s) * rows + row) * kv;
         for (int i = tid; i < KT * 256; i += 512) {
             const int key = i / 16, c = vt * 16 + i % 16;
-            if (key < dk && c < dv) start[static_cast<size_t>(key) * dv + c] = cur[i];
+            if (key < dk && c < dv) start[static_cast<size_t>(key) * dv + c] = cur[(i % 16) * SP + key];
         }
         if (first) {
             if (s + 1 < nseg) {   // the next step's operands, in flight during this one
@@ -844,8 +847,7 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
                 load_a(s, w, k0, a);
                 acc = products(acc, a, k0);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) nxt[(w * 16 + 4 * g4 + i) * 16 + m16] = acc[i];
+            StF4(nxt + m16 * SP + w * 16 + 4 * g4, acc);
 #pragma unroll
             for (int u = 0; u < 8; ++u) a0[u] = a1[u];
             add0 = add1;
@@ -857,8 +859,7 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
                 load_a(s, kt, k0, a);
                 acc = products(acc, a, k0);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) nxt[(kt * 16 + 4 * g4 + i) * 16 + m16] = acc[i];
+            StF4(nxt + m16 * SP + kt * 16 + 4 * g4, acc);
         }
         __syncthreads();
         float *const t = cur;
@@ -869,7 +870,7 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
         float *const fs = p.final_state + row * kv;
         for (int i = tid; i < KT * 256; i += 512) {
             const int key = i / 16, c = vt * 16 + i % 16;
-            if (key < dk && c < dv) fs[static_cast<size_t>(key) * dv + c] = cur[i];
+            if (key < dk && c < dv) fs[static_cast<size_t>(key) * dv + c] = cur[(i % 16) * SP + key];
         }
     }
 }
@@ -878,8 +879,9 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
 // value tile, s, four consecutive chunks of the segment), a wave per chunk,
 // S_start(s)'s column tile staged in LDS.  D[m][n] = sum_k Psi[t0 + m][k]
 // S_start[k][n] on MFMA (A: lane m + 16 k holds Psi[t0 + m][16 kb + 4 k + ii],
-// 16 bytes of a KP-pitch row; B from LDS), added to the output rows.
-// Dynamic LDS: KT * 256 floats.
+// 16 bytes of a KP-pitch row; B from LDS, stored column by column at pitch
+// KP + 4 for 16-byte reads), added to the output rows.  Dynamic LDS:
+// 16 (KP + 4) floats.
 __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int nchunks,
                                                               const float *psi, const float *sst) {
     extern __shared__ float sts[];
@@ -903,9 +905,10 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
     }
     const size_t kv = static_cast<size_t>(dk) * dv;
     const float *const st = sst + (static_cast<size_t>(seg) * rows + row) * kv;
+    const int SP = KP + 4;
     for (int i = tid; i < KT * 256; i += 256) {
         const int key = i / 16, cc = vt * 16 + i % 16;
-        sts[i] = key < dk && cc < dv ? st[static_cast<size_t>(key) * dv + cc] : 0.0f;
+        sts[(i % 16) * SP + key] = key < dk && cc < dv ? st[static_cast<size_t>(key) * dv + cc] : 0.0f;
     }
     __syncthreads();
     if (!live) return;
@@ -921,9 +924,9 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             if (k0 + u >= KT) break;
+            const v4f bs = LdsF4(sts + m16 * SP + (k0 + u) * 16 + 4 * g4);
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                acc = Mfma(a[u][ii], sts[((k0 + u) * 16 + 4 * g4 + ii) * 16 + m16], acc);
+            for (int ii = 0; ii < 4; ++ii) acc = Mfma(a[u][ii], bs[ii], acc);
         }
     }
 #pragma unroll
@@ -1104,8 +1107,9 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
     LaunchSplitRecurAny(q, c, sp.nseg, sp.sc, sp.nchunks, psi, phi, s0, stream);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split recurrence");
-    const int lds = 2 * KT * 256 * static_cast<int>(sizeof(float));
+    const int lds = 2 * 16 * (KT * 16 + 4) * static_cast<int>(sizeof(float));   // two S buffers (combine)
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCombineKernel), lds);
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCorrectKernel), lds / 2);
     XM_NOTE_LAUNCH("Gdn2SplitCombineKernel", {}, );
     hipLaunchKernelGGL(Gdn2SplitCombineKernel, dim3(static_cast<unsigned>(rows * VT)), dim3(512), lds, stream, q,
                        sp.nseg, phi, s0, sst);
