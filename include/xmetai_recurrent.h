@@ -234,7 +234,11 @@ int xm_gated_deltanet2_forward_states(const xm_tensor_t *inputs, size_t n_inputs
  * XM_ERR_UNSUPPORTED before anything is enqueued.  It calls no hipMalloc or
  * hipFree.  Every call on a GPU shares that GPU's array: calls that overlap on
  * one GPU (concurrent streams) race and must be serialised by the caller.
- * Results equal xm_gated_deltanet2_forward's.  output_final_state must be 0. */
+ * Results equal xm_gated_deltanet2_forward's, except where that call splits
+ * the sequence into concurrently run segments (few heads, 32+ chunks) with
+ * more scratch than the array holds: this entry point then steps the
+ * sequence in windows, and the two agree within the fp32 tolerance of two
+ * evaluation orders.  output_final_state must be 0. */
 int xm_gated_deltanet2_forward_noalloc(const xm_tensor_t *inputs, size_t n_inputs,
                                        const xm_gated_deltanet2_attrs_t *attrs, float *out, void *stream,
                                        char *errbuf, size_t errlen);

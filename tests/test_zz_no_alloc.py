@@ -3,7 +3,10 @@ fixed 64 MiB device array instead of an allocator (for callers that cannot
 allocate), called through the C ABI.  Its outputs must equal those of
 xm_gated_deltanet2_forward on the same inputs, on consecutive calls that
 reuse the array (the second smaller than the first), on the chunked path
-with windows shrunk to fit the array, and on the dk > 512 paths."""
+with windows shrunk to fit the array, on the sequence-split path, and on the
+dk > 512 paths; where the allocating call splits the sequence into more
+scratch than the array holds, the two agree within the device-path
+tolerance."""
 
 import ctypes
 
@@ -12,7 +15,7 @@ import pytest
 
 import xmetai_onnx_plugins as xp
 from xmetai_onnx_plugins import _capi, workloads as W
-from parity import to_dev
+from parity import TOL_GPU, check, to_dev
 
 S = W.GatedDeltaNet2Shape
 KEYS = ("q", "k", "v", "g", "beta", "w", "initial_state")
@@ -88,6 +91,23 @@ def test_noalloc_packed_sequences():
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
     assert any(k.startswith("Gdn2ChunkRecurKernel") for k in launched), launched
+
+
+@pytest.mark.gpu
+def test_noalloc_sequence_split():
+    # few heads and 64 chunks: both entry points split the sequence (2 MB of scratch)
+    got, want, launched = run_both(S(1, 1024, 2, 64, 32), seed=6)
+    np.testing.assert_array_equal(got, want)
+    assert any(k.startswith("Gdn2ChunkSplitKernel") for k in launched), launched
+
+
+@pytest.mark.gpu
+def test_noalloc_windows_where_the_split_exceeds_the_array():
+    # 65536 tokens x 2 heads at 128 x 128: the split needs 0.2 GB of prepared
+    # blocks, so the array steps the sequence in windows instead
+    got, want, launched = run_both(S(1, 65536, 2, 128, 128), seed=7)
+    assert not any(k.startswith("Gdn2ChunkSplitKernel") for k in launched), launched
+    check("noalloc/windows_vs_split", got, want, TOL_GPU)
 
 
 @pytest.mark.gpu
