@@ -303,12 +303,12 @@ def test_gdn2_valid_and_scratch():
         block = 3 * kq * 256 + 16 * kq + 256 + 32
         nch = -(-T // 16)
         rows, vt, kt = B * H, -(-V // 16), -(-K // 16)
-        # sequence split: rows (vt + kt) <= 160 column tiles and 32+ chunks;
-        # 1 + ceil(768 / (rows (vt + kt))) segments of 16+ chunks; every chunk's
+        # sequence split: rows (vt + kt) <= 160 column tiles and 64+ chunks;
+        # max(2, min(ceil(chunks / 64), 1 + ceil(1536 / (rows (vt + kt))))) segments; every chunk's
         # blocks, Psi [B,T,H,KP], Phi [nseg][rows][K][KP] (KP = 16 kt), S0 and
         # the start states [nseg][rows][K][V]; at most 2 GiB
-        if rows * (vt + kt) <= 160 and nch >= 32 and nch * block * 4 < (1 << 31):
-            nseg = min(1 + max(1, -(-768 // (rows * (vt + kt)))), nch // 16)
+        if rows * (vt + kt) <= 160 and nch >= 64 and nch * block * 4 < (1 << 31):
+            nseg = max(2, min(-(-nch // 64), 1 + -(-1536 // (rows * (vt + kt)))))
             sc = -(-nch // nseg)
             nseg = -(-nch // sc)
             if nseg >= 2:

@@ -234,7 +234,7 @@ def test_gdn2_sequence_split(name, override):
 
 
 def test_gdn2_sequence_split_selected_for_few_workgroups(override):
-    """A call with few column-tile workgroups and 32+ chunks splits its
+    """A call with few column-tile workgroups and 64+ chunks splits its
     sequence by itself; gdn2_split = 1 keeps one recurrence over the windows."""
     s = S(1, 1024, 2, 64, 32)
     inp = W.gated_deltanet2_inputs(s, seed=5)

@@ -1045,12 +1045,12 @@ void LaunchSplitRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, in
 // of every chunk, Psi ([B,T,H,KP]), Phi ([nseg][B*H][K][KP]), S0 and the
 // segment start states ([nseg][B*H][K][V] each).  Segments >= 1 run their dk
 // identity columns beside the value columns, 1 + dk/dv times the
-// recurrence work, on enough workgroups to fill the chip (about 768 beyond
-// segment 0, segments of at least 16 chunks).  A launch of W0 = B*H*VT
+// recurrence work, in segments of about 64 chunks (at most about 1536
+// workgroups beyond segment 0).  A launch of W0 = B*H*VT
 // column-tile workgroups (at most one per CU) steps each chunk at the
 // latency-bound rate; the split spreads B*H*(VT+KT) tiles' work over the
 // CUs at the throughput rate, so it pays when B*H*(VT+KT) is well under the
-// CU count: taken at <= 160 and 32+ chunks.  At most 2 GiB of scratch.
+// CU count: taken at <= 160 and 64+ chunks.  At most 2 GiB of scratch.
 struct SplitPlan {
     int nseg = 0, sc = 0, nchunks = 0;
     size_t blocks = 0, psi = 0, phi = 0, s0 = 0;
@@ -1074,10 +1074,16 @@ SplitPlan PlanSplit(int batch, int seqlen, int nheads, int dk, int dv, bool pack
     if (ov == 2) {
         nseg = std::min(nchunks, 4);
     } else {
-        if (rows * (VT + KT) > 160 || nchunks < 32) return SplitPlan{};
+        if (rows * (VT + KT) > 160 || nchunks < 64) return SplitPlan{};
+        // segments of about 64 chunks (longer ones leave the recurrence
+        // latency-bound, shorter ones add serial combine steps), at most about
+        // 1536 workgroups beyond segment 0.  Measured at 1 x 8192 x 4 heads
+        // (128 x 128), 1 x 16384 x 16 heads (64 x 64) and 1 x 8192 x 8 heads
+        // (160 x 64), the best of 384 / 768 / 1536 workgroups were 74, 79
+        // and 64 chunks per segment.
         const long long per = rows * (VT + KT);
-        nseg = 1 + static_cast<int>(std::max<long long>(1, (768 + per - 1) / per));
-        nseg = std::min(nseg, nchunks / 16);
+        nseg = std::min((nchunks + 63) / 64, 1 + static_cast<int>((1536 + per - 1) / per));
+        nseg = std::max(nseg, 2);
     }
     if (nseg < 2) return SplitPlan{};
     SplitPlan sp;
