@@ -113,16 +113,28 @@ constexpr int kWindowChunks = 128;       // chunks per prep/recurrence window (2
 size_t Align256(size_t bytes) { return (bytes + 255) / 256 * 256; }
 constexpr int kPrepWaves = 4;            // waves (chunk-heads) per prep workgroup
 
-// Chunk-head block of the prepared window, in floats, for kq key tiles.  The
-// vectors are unnormalised (q, k in place of qhat, khat); the recurrence
-// applies the per-token multipliers to the rows of E S0 and R S0.
+// Chunk-head block of the prepared window, in floats, for a recurrence of ks
+// waves of kpw key tiles (kq = kpw ks).  The vectors are unnormalised (q, k
+// in place of qhat, khat); the recurrence applies the per-token multipliers
+// to the rows of E S0 and R S0.
 //   E' = beta k G tiles [kq][256], R' = q G tiles [kq][256]: lane l holds
 //     token l%16, keys 4(l/16)..+3 of the tile
 //   Ut~ = T^T diag(k_mul) Ut' tiles [kq][256] (Ut' = k prod_{r>t} d_r): lane l
 //     holds key l%16, tokens 4(l/16)..+3
-//   G_15 [kq][16]; M T [256]: lane l holds row l%16, columns 4(l/16)..+3
-//   q and k multipliers [2][16]
-__host__ __device__ constexpr int BlockFloats(int kq) { return 3 * kq * 256 + 16 * kq + 256 + 32; }
+//   M T [256]: lane l holds row l%16, columns 4(l/16)..+3
+//   scalar vectors [ks][ScalarVecs(kpw)][64], one float per lane of recurrence
+//     wave w: lane 16 r + n of vector s holds entry e = 16 s + n of the list
+//     k_mul(4 r + i), q_mul(4 r + i) (i = 0..3), then G_15 of keys
+//     16 (w kpw + kt) + 4 r + i for kt < kpw (kt-major).  The lanes of row r
+//     (the D layout's tokens or keys 4 r..4 r+3) read entry e with a DPP
+//     row broadcast: one 4-byte load per lane brings what four to eight
+//     16-byte loads of 16-lane broadcasts would (a 16-byte load costs the
+//     vector memory path about three times a 4-byte one, whatever its
+//     addresses).
+__host__ __device__ constexpr int ScalarVecs(int kpw) { return (8 + 4 * kpw + 15) / 16; }
+__host__ __device__ constexpr int BlockFloats(int kpw, int ks) {
+    return 3 * kpw * ks * 256 + 256 + ks * ScalarVecs(kpw) * 64;
+}
 
 __device__ __forceinline__ v4f LdgF4(const float *p) { return *reinterpret_cast<const v4f *>(p); }
 __device__ __forceinline__ void StgF4(float *p, v4f v) { *reinterpret_cast<v4f *>(p) = v; }
@@ -225,10 +237,15 @@ __device__ __forceinline__ void PackedRange(const GatedDeltaNet2Params &p, int b
 // Preparation: one wave per (b,h,chunk) of the window
 // ---------------------------------------------------------------------------
 // Dynamic LDS: kPrepWaves * kq * 256 floats, each wave's transposed Ut' tiles
-// kept until T is known.
-__global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kq) {
+// kept until T is known.  kpw, ks: the recurrence's key tiles per wave and
+// waves (kq = kpw ks key tiles), which order the scalar vectors.
+constexpr int kMaxKeyTiles = 32;         // key tiles of the chunked path (dk <= 512)
+__global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kpw,
+                                                                       int ks) {
     __shared__ float sw[kPrepWaves][4][kTile];
+    __shared__ __attribute__((aligned(16))) float sg[kPrepWaves][kMaxKeyTiles * 16];   // G_15 of each key
     extern __shared__ float prep_dyn[];
+    const int kq = kpw * ks;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int m16 = lane & 15, g4 = lane >> 4;
     const int H = p.nheads;
@@ -257,8 +274,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     }
     const bool live = t0 + m16 < T;
     const size_t rowbase = ((tok0 + min(t0 + m16, T - 1)) * H + h) * p.dk;
-    float *const blk = p.prepared + static_cast<size_t>(item) * BlockFloats(kq);
+    float *const blk = p.prepared + static_cast<size_t>(item) * BlockFloats(kpw, ks);
     float *const wTr = sw[w][0], *const wA = sw[w][1], *const wT = sw[w][2], *const wTT = sw[w][3];
+    float *const gsw = sg[w];
 
     // One pass over the key tiles: the unnormalised chunk vectors, the L2
     // norms of token m16, the range of the cumulative decays, and A', M'
@@ -295,7 +313,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         StF4(ut + kt * 256, utA);
         StgF4(blk + kt * 256 + lane * 4, e);
         StgF4(blk + (kq + kt) * 256 + lane * 4, r);
-        if (m16 == 0) StgF4(blk + 3 * kq * 256 + kt * 16 + 4 * g4, g15);
+        if (m16 == 0) StF4(gsw + kt * 16 + 4 * g4, g15);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
             al = Mfma(e[ii], kb[ii], al);
@@ -319,11 +337,6 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         // reference :58-62: q_mul = scale * rsqrt(sum + eps); k_mul = rsqrt(sum + eps)
         qm *= rsqrtf(qs + kL2EpsC);
         km = rsqrtf(kq2 + kL2EpsC);
-    }
-    float *const mul = blk + 3 * kq * 256 + 16 * kq + 256;
-    if (g4 == 0) {
-        mul[m16] = qm;
-        mul[16 + m16] = km;
     }
     if (__all(in_range) && p.pairwise_only == 0) {
         // A[t][s] = k_mul_t k_mul_s A'[t][s], M[t][s] = q_mul_t k_mul_s M'[t][s]
@@ -388,7 +401,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
 #pragma unroll
     for (int i = 0; i < 4; ++i) wTr[(4 * g4 + i) * kSP + m16] = mt[i];
     WaveSync();
-    StgF4(blk + 3 * kq * 256 + 16 * kq + lane * 4, LdsF4(wTr + m16 * kSP + 4 * g4));   // M T, A operand
+    StgF4(blk + 3 * kq * 256 + lane * 4, LdsF4(wTr + m16 * kSP + 4 * g4));   // M T, A operand
 
     // The update S_C = G_15 o S0 + Ut'^T diag(k_mul) U with U = T Y is
     // Ut~^T Y, Ut~ = T^T diag(k_mul) Ut': the recurrence updates from Y and
@@ -406,29 +419,81 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         for (int ii = 0; ii < 4; ++ii) d = Mfma(tB[ii], b[ii], d);
         StgF4(blk + (2 * kq + kt) * 256 + lane * 4, d);
     }
+
+    // The scalar vectors (see BlockFloats): lane 16 r + n of vector s of
+    // recurrence wave v holds entry e = 16 s + n of row r's list.
+    {
+        const int tok = 4 * g4 + (m16 & 3);   // entries e < 8: token 4 r + e % 4
+        const float kmt = __shfl(km, tok), qmt = __shfl(qm, tok);
+        const int nsv = ScalarVecs(kpw);
+        float *const sv = blk + 3 * kq * 256 + 256;
+        for (int v = 0; v < ks; ++v) {
+            for (int sx = 0; sx < nsv; ++sx) {
+                const int e = 16 * sx + m16;
+                float val = e < 4 ? kmt : e < 8 ? qmt : 0.0f;
+                if (e >= 8 && e < 8 + 4 * kpw) val = gsw[(v * kpw + (e - 8) / 4) * 16 + 4 * g4 + (e & 3)];
+                sv[(v * nsv + sx) * 64 + lane] = val;
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
 // Recurrence over one window
 // ---------------------------------------------------------------------------
-// The operands of one chunk that a wave needs, in MFMA lane order: its key
-// tiles of E', R', Ut~ and G_15, M T, the row multipliers and this lane's
-// w, v (tokens 4(l/16)+i).
-template <int KPW>
-struct ChunkOperands {
-    v4f e[KPW], r[KPW], ut[KPW], g[KPW];
-    v4f mt, qm, km;
-    float w[4], v[4];
-};
-
 template <int KPW, int KS>
 struct RecurLayout {
     static constexpr int THREADS = 64 * KS;
     static constexpr int KQ = KPW * KS;
-    static constexpr int FB = BlockFloats(KQ);   // one prepared chunk block
-    // LDS, in floats: [2 chunk parities][KS waves][E' S0, R' S0][256] partials
-    static constexpr int kFloats = KS > 1 ? 2 * KS * 512 : 1;
+    static constexpr int FB = BlockFloats(KPW, KS);   // one prepared chunk block
+    static constexpr int NSV = ScalarVecs(KPW);        // scalar vectors per wave
+    // Token rows i (the D layout's registers) whose w, v a wave loads and
+    // whose (M T) Y slice it forms: i = ks + m KS, m < NM (i < 4).
+    static constexpr int NM = (4 + KS - 1) / KS;
+    // LDS, in floats, per chunk parity: [KS waves][E' S0, output][256]
+    // partials, then W o V [256] (lane l: rows 4(l/16)..+3, column l%16) and
+    // [256] where the waves without a row write (no branch)
+    static constexpr int kPart = KS * 512 + 512;   // W o V, then a spare row slot
+    static constexpr int kFloats = KS > 1 ? 2 * kPart : 1;
 };
+
+// The operands of one chunk that a wave needs, in MFMA lane order: its key
+// tiles of E', R', Ut~, its scalar vectors (k_mul, q_mul, G_15), and for its
+// token rows i = ks + m KS the M T slice (A operand column 4(l/16)+i) and
+// this lane's w, v (token 4(l/16)+i).
+template <int KPW, int KS>
+struct ChunkOperands {
+    using L = RecurLayout<KPW, KS>;
+    v4f e[KPW], r[KPW], ut[KPW];
+    float sc[L::NSV];
+    float mt[L::NM], w[L::NM], v[L::NM];
+};
+
+// Entry E of a wave's scalar list for the lanes of each row (DPP row_newbcast).
+template <int E, int NSV>
+__device__ __forceinline__ float ScalarEntry(const float (&sc)[NSV]) {
+    static_assert(E / 16 < NSV, "scalar entry beyond the wave's vectors");
+    return DppF<0x150 + E % 16>(sc[E / 16]);
+}
+template <int I, int NSV>
+__device__ __forceinline__ float KMul(const float (&sc)[NSV]) { return ScalarEntry<I, NSV>(sc); }
+template <int I, int NSV>
+__device__ __forceinline__ float QMul(const float (&sc)[NSV]) { return ScalarEntry<4 + I, NSV>(sc); }
+template <int KT, int I, int NSV>
+__device__ __forceinline__ float G15(const float (&sc)[NSV]) { return ScalarEntry<8 + 4 * KT + I, NSV>(sc); }
+template <int NSV>
+__device__ __forceinline__ v4f KMulRows(const float (&sc)[NSV]) {
+    return v4f{KMul<0, NSV>(sc), KMul<1, NSV>(sc), KMul<2, NSV>(sc), KMul<3, NSV>(sc)};
+}
+template <int NSV>
+__device__ __forceinline__ v4f QMulRows(const float (&sc)[NSV]) {
+    return v4f{QMul<0, NSV>(sc), QMul<1, NSV>(sc), QMul<2, NSV>(sc), QMul<3, NSV>(sc)};
+}
+// S[kt] = G_15 o S[kt] (keys 16 (ks KPW + kt) + 4 (l/16) + i in register i)
+template <int KPW, int NSV, int... KT>
+__device__ __forceinline__ void DecayState(v4f (&S)[KPW], const float (&sc)[NSV], std::integer_sequence<int, KT...>) {
+    ((S[KT] *= v4f{G15<KT, 0, NSV>(sc), G15<KT, 1, NSV>(sc), G15<KT, 2, NSV>(sc), G15<KT, 3, NSV>(sc)}), ...);
+}
 
 // One (b,h) row's chunks [cs, cs + nrun) of its sequence, whose prepared
 // blocks sit at window-local indices [cw0, cw0 + nrun) of `prep_row` (the row's
@@ -452,9 +517,9 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                                              int cs, int cw0, int nrun, int wn, const float *prep_row, size_t sbase,
                                              const float *s_in, float *s_out, SplitTile st = {}) {
     using L = RecurLayout<KPW, KS>;
-    constexpr int KQ = L::KQ, FB = L::FB;
-    constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oG = 3 * KQ * 256;   // block offsets (floats)
-    constexpr int oMT = oG + 16 * KQ, oMul = oMT + 256;
+    using Ops = ChunkOperands<KPW, KS>;
+    constexpr int KQ = L::KQ, FB = L::FB, NSV = L::NSV, NM = L::NM;
+    constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oMT = 3 * KQ * 256, oSc = oMT + 256;   // block offsets (floats)
 
     const int H = p.nheads, dk = p.dk, dv = p.dv;
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -478,6 +543,16 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     int vo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) vo[i] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
+    // this wave's token rows i = ks + m KS (clamped to 3 where m KS + ks >= 4,
+    // loaded but unused): w, v offsets and the M T slice of the A operand
+    int vl[NM], mo[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        const int i = min(ks + m * KS, 3);
+        vl[m] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
+        mo[m] = (lane * 4 + i) * 4;
+    }
+    const int so = lane * 4 + ks * NSV * 256;   // this wave's scalar vectors
     // Chunk jl of the run starts kC * HV floats after chunk jl - 1 in w, v and
     // out: the run's first rows are formed once, a chunk adds its offset (no
     // 64-bit index arithmetic per chunk).  A chunk's rows end after its last
@@ -523,8 +598,12 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // with a load count that depends on the path, the compiler's wait
         // counts turn conservative and a consumer waits for the newest
         // prefetches too.
-        const int lo = lane * 16, go = g4 * 16;   // a lane's 16 bytes of a tile; a lane group's of a row vector
-        auto load_ops = [&](int j, ChunkOperands<KPW> &o) __attribute__((always_inline)) {
+        const int lo = lane * 16;   // a lane's 16 bytes of a tile
+        // 16-byte loads for the key tiles, 4-byte loads for the rest: w, v
+        // and the M T slice of this wave's rows only (W o V reaches the other
+        // waves through the partial exchange), and the scalar vectors whose
+        // entries a row broadcast hands to the lanes.
+        auto load_ops = [&](int j, Ops &o) __attribute__((always_inline)) {
             const int sb = (cw0 + j) * (FB * 4);
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
@@ -535,17 +614,17 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             const Rsrc rw = MakeRsrc(w_run + chunk_off(j), rows_bytes(j));
             const Rsrc rv = MakeRsrc(v_run + chunk_off(j), rows_bytes(j));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                o.w[i] = BufF(rw, vo[i]);
-                o.v[i] = BufF(rv, vo[i]);
+            for (int m = 0; m < NM; ++m) {
+                o.w[m] = BufF(rw, vl[m]);
+                o.v[m] = BufF(rv, vl[m]);
             }
-            o.km = BufF4(rblk, go, sb + (oMul + 16) * 4);
-            o.qm = BufF4(rblk, go, sb + oMul * 4);
-            o.mt = BufF4(rblk, lo, sb + oMT * 4);
+#pragma unroll
+            for (int x = 0; x < NSV; ++x) o.sc[x] = BufF(rblk, so + x * 256, sb + oSc * 4);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) o.mt[m] = BufF(rblk, mo[m], sb + oMT * 4);
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
                 const int kg = ks * KPW + kt;
-                o.g[kt] = BufF4(rblk, go, sb + (oG + kg * 16) * 4);
                 o.ut[kt] = BufF4(rblk, lo, sb + (oU + kg * 256) * 4);
             }
         };
@@ -588,15 +667,16 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // 0.234 -> 0.244).  With 6 key tiles per wave the interleave measured
         // 2% slower (4 x 2048 x 16 heads at 384 x 128) and is left out.
         constexpr bool kHeadLoads = KPW == 4 || (KPW == 3 && KS == 8);
+        constexpr int kLoads = 3 * KPW + NSV + 3 * NM;   // vector loads of one chunk
         auto interleave = [&]() __attribute__((always_inline)) {
             if constexpr (KPW == 6) return;
 #pragma unroll
-            for (int i = 0; i < 4 * KPW + 11; ++i) {
+            for (int i = 0; i < kLoads; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // one vector-memory read
             }
         };
-        auto step = [&](int j, ChunkOperands<KPW> &o, ChunkOperands<KPW> &nx) __attribute__((always_inline)) {
+        auto step = [&](int j, Ops &o, Ops &nx) __attribute__((always_inline)) {
             v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
@@ -607,42 +687,47 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                 }
             }
             if constexpr (kHeadLoads) load_ops(min(j + 1, nrun - 1), nx);
+            v4f wv;   // W o V of this lane's rows; w, v are zero past the sequence end and dv
             if constexpr (KS > 1) {
-                float *const xp = sXp + (j & 1) * (KS * 512);
+                float *const xp = sXp + (j & 1) * L::kPart;
                 StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
                 StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);   // output partial of chunk j - 1
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {   // this wave's rows of W o V (rows >= 4: a spare slot)
+                    const int i = ks + m * KS;
+                    xp[KS * 512 + (i < 4 ? lane * 4 + i : 256 + lane)] = o.w[m] * o.v[m];
+                }
                 interleave();
                 __syncthreads();
-                // the same summation order in every wave: identical U everywhere
+                // the same summation order in every wave: identical Y everywhere
                 xe = LdsF4(xp + lane * 4);
 #pragma unroll
                 for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
+                wv = LdsF4(xp + KS * 512 + lane * 4);
                 if (ks == 0 && j > 0) store_out(j - 1, sum_out(xp));
-            }
-            v4f y;   // w, v are zero past the sequence end and dv
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) y[i] = o.w[i] * o.v[i] - o.km[i] * xe[i];   // rows of E' S0 times k_mul
+                for (int i = 0; i < 4; ++i) wv[i] = o.w[i] * o.v[i];   // NM = 4: row m is row i
+            }
+            const v4f y = wv - KMulRows(o.sc) * xe;   // rows of E' S0 times k_mul
             // S = G_15 o S + Ut~^T Y (Ut~ carries T and k_mul: U is never formed)
+            DecayState(S, o.sc, std::make_integer_sequence<int, KPW>{});
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
-                S[kt] *= o.g[kt];
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], y[ii], S[kt]);
             }
             // Off the chunk's chain (U, then the update): this wave's K slices
             // of (M T) Y, chosen by selects rather than branches (a branch per
             // slice split the region and delayed U behind them).
-            op = o.qm * xr;   // rows of R' S0 times q_mul
+            op = QMulRows(o.sc) * xr;   // rows of R' S0 times q_mul
 #pragma unroll
-            for (int m = 0; m < (4 + KS - 1) / KS; ++m) {
+            for (int m = 0; m < NM; ++m) {
                 const int sel = ks + m * KS;   // wave-uniform; >= 4 for the waves without a slice
-                float ma = 0.0f, ya = 0.0f;
+                float ya = 0.0f;
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    ma = sel == ii ? o.mt[ii] : ma;
-                    ya = sel == ii ? y[ii] : ya;
-                }
-                if (m * KS < 4) op = Mfma(ma, ya, op);
+                for (int ii = 0; ii < 4; ++ii) ya = sel == ii ? y[ii] : ya;
+                if (m * KS < 4) op = Mfma(sel < 4 ? o.mt[m] : 0.0f, ya, op);
             }
             if constexpr (KS == 1) store_out(j, op);
             if constexpr (!kHeadLoads) load_ops(min(j + 2, nrun - 1), o);
@@ -651,7 +736,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // two operand sets in turn, with compile-time roles
         // (the sets' loads in the same order as in the loop: an interleaved
         // prologue would set the loop's wait counts to its own, shorter distances)
-        ChunkOperands<KPW> opa, opb;
+        Ops opa, opb;
         load_ops(0, opa);
         if constexpr (!kHeadLoads) {
             __builtin_amdgcn_sched_barrier(0);
@@ -667,7 +752,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             if (j + 2 >= nrun) break;
         }
         if constexpr (KS > 1) {   // output of the last chunk
-            float *const xp = sXp + (nrun & 1) * (KS * 512);
+            float *const xp = sXp + (nrun & 1) * L::kPart;
             StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);
             __syncthreads();
             if (ks == 0) store_out(nrun - 1, sum_out(xp));
@@ -979,10 +1064,13 @@ ChunkConfig ChooseChunk(int dk, long long groups) {
 
 // The preparation kernel, with its Ut' tiles' dynamic LDS (up to 128 KiB at
 // 32 key tiles, beside 20 KiB of static LDS).
-void LaunchPrep(int kq, const GatedDeltaNet2Params &p, int c0, int wn, unsigned blocks, hipStream_t stream) {
+void LaunchPrep(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int wn, unsigned blocks,
+                hipStream_t stream) {
+    const int kq = c.kpw * c.ks;
+    if (kq > kMaxKeyTiles) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
     const int dyn = kPrepWaves * kq * 256 * static_cast<int>(sizeof(float));
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel), dyn);
-    hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn, kq);
+    hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn, c.kpw, c.ks);
 }
 
 template <int KPW, int KS>
@@ -1065,7 +1153,7 @@ SplitPlan PlanSplit(int batch, int seqlen, int nheads, int dk, int dv, bool pack
     const int VT = (dv + 15) / 16, KT = (dk + 15) / 16;
     const ChunkConfig c = ChooseChunk(dk, rows * VT);
     const int nchunks = (seqlen + kC - 1) / kC;
-    const size_t fb = static_cast<size_t>(BlockFloats(c.kpw * c.ks)) * sizeof(float);
+    const size_t fb = static_cast<size_t>(BlockFloats(c.kpw, c.ks)) * sizeof(float);
     // the recurrence addresses a row's blocks, and 16 tokens of Psi rows, with
     // 32-bit byte offsets
     if (static_cast<size_t>(nchunks) * fb >= (size_t{1} << 31)) return SplitPlan{};
@@ -1113,7 +1201,7 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
     if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
-    LaunchPrep(c.kpw * c.ks, q, 0, sp.nchunks, static_cast<unsigned>(pblocks), stream);
+    LaunchPrep(c, q, 0, sp.nchunks, static_cast<unsigned>(pblocks), stream);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
     LaunchSplitRecurAny(q, c, sp.nseg, sp.sc, sp.nchunks, psi, phi, s0, stream);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split recurrence");
@@ -1154,7 +1242,7 @@ struct WindowPlan {
 WindowPlan PlanWindows(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
     const ChunkConfig c = ChooseChunk(dk, static_cast<long long>(batch) * nheads * ((dv + 15) / 16));
     const size_t rows = static_cast<size_t>(packed ? 1 : batch) * nheads;
-    const size_t per_block = rows * BlockFloats(c.kpw * c.ks) * sizeof(float);
+    const size_t per_block = rows * BlockFloats(c.kpw, c.ks) * sizeof(float);
     const size_t carry = Align256(static_cast<size_t>(batch) * nheads * dk * dv * sizeof(float));
     const int nchunks = (seqlen + kC - 1) / kC;
     const long long all_blocks = static_cast<long long>(nchunks) + batch;   // packed: every sequence's chunks
@@ -1313,7 +1401,7 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
         const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
         if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
         XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
-        LaunchPrep(kq, q, c0, wn, static_cast<unsigned>(pblocks), stream);
+        LaunchPrep(c, q, c0, wn, static_cast<unsigned>(pblocks), stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
         if (packed)   // the kernel picks each sequence's state buffers itself
             LaunchRecurAny(q, c, c0, wn, kq, nullptr, nullptr, stream);

@@ -30,8 +30,8 @@ __device__ __forceinline__ Rsrc MakeRsrc(const float *base, int bytes) {
 __device__ __forceinline__ v4f BufF4(Rsrc r, int voff, int soff) {
     return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
-__device__ __forceinline__ float BufF(Rsrc r, int voff) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+__device__ __forceinline__ float BufF(Rsrc r, int voff, int soff = 0) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 __device__ __forceinline__ void BufStF(Rsrc r, int voff, float x) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, voff, 0, 0);
