@@ -242,8 +242,7 @@ __device__ __forceinline__ void PackedRange(const GatedDeltaNet2Params &p, int b
 constexpr int kMaxKeyTiles = 32;         // key tiles of the chunked path (dk <= 512)
 __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kpw,
                                                                        int ks) {
-    __shared__ float sw[kPrepWaves][4][kTile];
-    __shared__ __attribute__((aligned(16))) float sg[kPrepWaves][kMaxKeyTiles * 16];   // G_15 of each key
+    __shared__ __attribute__((aligned(16))) float sw[kPrepWaves][4][kTile];
     extern __shared__ float prep_dyn[];
     const int kq = kpw * ks;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -276,7 +275,10 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     const size_t rowbase = ((tok0 + min(t0 + m16, T - 1)) * H + h) * p.dk;
     float *const blk = p.prepared + static_cast<size_t>(item) * BlockFloats(kpw, ks);
     float *const wTr = sw[w][0], *const wA = sw[w][1], *const wT = sw[w][2], *const wTT = sw[w][3];
-    float *const gsw = sg[w];
+    // G_15 of each key, kept until the scalar vectors are written (in wT and
+    // wTT, which T takes over afterwards: 2 kTile >= kMaxKeyTiles * 16)
+    float *const gsw = wT;
+    static_assert(2 * kTile >= kMaxKeyTiles * 16, "G_15 stash");
 
     // One pass over the key tiles: the unnormalised chunk vectors, the L2
     // norms of token m16, the range of the cumulative decays, and A', M'
@@ -338,6 +340,26 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         qm *= rsqrtf(qs + kL2EpsC);
         km = rsqrtf(kq2 + kL2EpsC);
     }
+
+    // The scalar vectors (see BlockFloats): lane 16 r + n of vector s of
+    // recurrence wave v holds entry e = 16 s + n of row r's list.  Written
+    // before the pairwise products and T overwrite the G_15 stash.
+    WaveSync();
+    {
+        const int tok = 4 * g4 + (m16 & 3);   // entries e < 8: token 4 r + e % 4
+        const float kmt = __shfl(km, tok), qmt = __shfl(qm, tok);
+        const int nsv = ScalarVecs(kpw);
+        float *const sv = blk + 3 * kq * 256 + 256;
+        for (int v = 0; v < ks; ++v) {
+            for (int sx = 0; sx < nsv; ++sx) {
+                const int e = 16 * sx + m16;
+                float val = e < 4 ? kmt : e < 8 ? qmt : 0.0f;
+                if (e >= 8 && e < 8 + 4 * kpw) val = gsw[(v * kpw + (e - 8) / 4) * 16 + 4 * g4 + (e & 3)];
+                sv[(v * nsv + sx) * 64 + lane] = val;
+            }
+        }
+    }
+    WaveSync();
     if (__all(in_range) && p.pairwise_only == 0) {
         // A[t][s] = k_mul_t k_mul_s A'[t][s], M[t][s] = q_mul_t k_mul_s M'[t][s]
 #pragma unroll
@@ -418,23 +440,6 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) d = Mfma(tB[ii], b[ii], d);
         StgF4(blk + (2 * kq + kt) * 256 + lane * 4, d);
-    }
-
-    // The scalar vectors (see BlockFloats): lane 16 r + n of vector s of
-    // recurrence wave v holds entry e = 16 s + n of row r's list.
-    {
-        const int tok = 4 * g4 + (m16 & 3);   // entries e < 8: token 4 r + e % 4
-        const float kmt = __shfl(km, tok), qmt = __shfl(qm, tok);
-        const int nsv = ScalarVecs(kpw);
-        float *const sv = blk + 3 * kq * 256 + 256;
-        for (int v = 0; v < ks; ++v) {
-            for (int sx = 0; sx < nsv; ++sx) {
-                const int e = 16 * sx + m16;
-                float val = e < 4 ? kmt : e < 8 ? qmt : 0.0f;
-                if (e >= 8 && e < 8 + 4 * kpw) val = gsw[(v * kpw + (e - 8) / 4) * 16 + 4 * g4 + (e & 3)];
-                sv[(v * nsv + sx) * 64 + lane] = val;
-            }
-        }
     }
 }
 
@@ -827,11 +832,16 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
 // combine kernel then steps S_start(s + 1) = Phi_s S_start(s) + S0_s over the
 // segments, and the correction kernel adds Psi_s S_start(s) to their outputs.
 //
-// Workgroup (segment, (b, h), column tile) over VT + KT tiles; segment 0 runs
-// its VT value tiles only.  Value tiles write O0 (O for segment 0) and S0_s
-// ([nseg][B*H][K][V]); identity tiles write Psi ([B,T,H,K], tokens of
-// segments >= 1) and Phi_s ([nseg][B*H][K][K], row = key, column = identity
-// column).
+// Workgroup ((b, h), segment, column tile): segment 0 runs its VT value tiles,
+// the others VT + KT tiles, VT + (nseg - 1)(VT + KT) workgroups per (b, h) in
+// that order.  Each XCD owns a contiguous range of these logical indices
+// (XcdLocalBlock), so the XCDs get equal shares of the launch and the
+// workgroups of one (b, h), which read the same prepared blocks, share an L2.
+// (Ordered by segment first, the later segments' workgroups crowded onto some
+// XCDs, two to a CU, while segment 0's left others idle.)  Value tiles write
+// O0 (O for segment 0) and S0_s ([nseg][B*H][K][V]); identity tiles write Psi
+// ([B,T,H,K], tokens of segments >= 1) and Phi_s ([nseg][B*H][K][K], row =
+// key, column = identity column).
 template <int KPW, int KS>
 __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Params p, int sc, int nchunks,
                                                                 float *psi, float *phi, float *s0) {
@@ -839,9 +849,12 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
     __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
     const int H = p.nheads, VT = (p.dv + 15) / 16, KT = (p.dk + 15) / 16, tiles = VT + KT;
     const int rows = p.batch * H;
+    const int nseg = (nchunks + sc - 1) / sc;
+    const int per_row = VT + (nseg - 1) * tiles;
     const int x = XcdLocalBlock(blockIdx.x, gridDim.x);
-    const int tile = x % tiles, row = (x / tiles) % rows, seg = x / tiles / rows;
-    if (seg == 0 && tile >= VT) return;   // whole workgroup
+    const int row = x / per_row, rx = x % per_row;
+    const int seg = rx < VT ? 0 : 1 + (rx - VT) / tiles;
+    const int tile = rx < VT ? rx : (rx - VT) % tiles;
     const int cs = seg * sc, nrun = min(sc, nchunks - cs);
     if (nrun <= 0) return;
     const int b = row / H, h = row % H;
@@ -1109,8 +1122,8 @@ void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0,
 template <int KPW, int KS>
 void LaunchSplitRecur(const GatedDeltaNet2Params &p, int nseg, int sc, int nchunks, float *psi, float *phi, float *s0,
                       hipStream_t stream) {
-    const long long tiles = (p.dv + 15) / 16 + (p.dk + 15) / 16;
-    const long long blocks = static_cast<long long>(nseg) * p.batch * p.nheads * tiles;
+    const long long vt = (p.dv + 15) / 16, tiles = vt + (p.dk + 15) / 16;
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * (vt + (nseg - 1) * tiles);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2ChunkSplitKernel", {}, KPW, KS);
     hipLaunchKernelGGL((Gdn2ChunkSplitKernel<KPW, KS>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, stream, p,
@@ -1161,8 +1174,16 @@ SplitPlan PlanSplit(int batch, int seqlen, int nheads, int dk, int dv, bool pack
     int nseg;
     if (ov == 2) {
         nseg = std::min(nchunks, 4);
+    } else if (rows * (VT + KT) > 160) {
+        // Wide keys over few value columns (e.g. 2 x 4 heads at 320 x 64: 32
+        // column-tile workgroups, 192 value and key tiles): two segments when
+        // both fit on the CUs one workgroup each, so the second segment's
+        // identity columns run on CUs the unsplit launch leaves idle and
+        // every CU still steps at most one workgroup.
+        if (nchunks < 64 || rows * VT > 64 || rows * VT + rows * (VT + KT) > 256) return SplitPlan{};
+        nseg = 2;
     } else {
-        if (rows * (VT + KT) > 160 || nchunks < 64) return SplitPlan{};
+        if (nchunks < 64) return SplitPlan{};
         // segments of about 64 chunks (longer ones leave the recurrence
         // latency-bound, shorter ones add serial combine steps), at most about
         // 1536 workgroups beyond segment 0.  Measured at 1 x 8192 x 4 heads
