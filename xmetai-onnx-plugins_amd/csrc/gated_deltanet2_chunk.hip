@@ -78,13 +78,6 @@ __device__ __forceinline__ float RowPrefixMul(float x) {   // prod_{j <= m} x_j
     x *= DppOr<0x118>(1.0f, x);   // row_shr:8
     return x;
 }
-__device__ __forceinline__ float RowPrefixAdd(float x) {   // sum_{j <= m} x_j
-    x += DppOr<0x111>(0.0f, x);
-    x += DppOr<0x112>(0.0f, x);
-    x += DppOr<0x114>(0.0f, x);
-    x += DppOr<0x118>(0.0f, x);
-    return x;
-}
 __device__ __forceinline__ float RowSuffixMulExcl(float x) {   // prod_{j > m} x_j
     x *= DppOr<0x101>(1.0f, x);   // row_shl:1
     x *= DppOr<0x102>(1.0f, x);   // row_shl:2
@@ -168,49 +161,57 @@ __device__ __forceinline__ void LoadKeyTile(const GatedDeltaNet2Params &p, size_
     }
 }
 
-// One token distance D of the pairwise A and M over all key tiles: lane t of
-// each row meets token s = t - D through a row rotation.  Results go to `dst`
-// in the D layout of (t, s): [A: 256][M: 256].
+// Token distance D of the pairwise A and M for one key element: lane t of
+// each row meets token s = t - D through a row rotation.  The decay product
+// prod_{s<r<=t} d_r is exp of the window sum w = sum_{t-D<r<=t} g_r, which
+// this call extends by g_{t-D+1}: a sum of the D terms themselves, not a
+// difference of prefix sums (after a hard reset, say g = -200, two prefix
+// sums near -200 differ by a value whose absolute error is ulp(200)/2, a
+// relative error of 1e-5 in every later product of the chunk).
 template <int D>
-__device__ __forceinline__ void PairStep(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kq, int m16,
-                                         int g4, float qm, float km, float *dst) {
-    float a = 0.0f, mm = 0.0f;
+__device__ __forceinline__ void PairTerm(float g, float kn, float bk, float qq, float &w, float &a, float &mm) {
+    if constexpr (D > 0) w += RowRor<D - 1>(g);
+    const float pd = D == 0 ? 1.0f : __expf(w);
+    const float ks_ = RowRor<D>(kn);
+    a = fmaf(bk * pd, ks_, a);
+    mm = fmaf(qq * pd, ks_, mm);
+}
+
+template <int... Ds>
+__device__ __forceinline__ void PairTerms(std::integer_sequence<int, Ds...>, float g, float kn, float bk, float qq,
+                                          float (&a)[kC], float (&mm)[kC]) {
+    float w = 0.0f;
+    (PairTerm<Ds>(g, kn, bk, qq, w, a[Ds], mm[Ds]), ...);   // D = 0, 1, ..., 15 in turn
+}
+
+// A and M of a chunk whose decays leave the fast range (the whole wave calls
+// it), every token distance at once over one pass of the key tiles.  Results
+// go to `dst` in the D layout of (t, s): [A: 256][M: 256].
+__device__ __forceinline__ void PairwiseAM(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kq,
+                                           float qm, float km, float *dst) {
+    const int lane = threadIdx.x & 63, m16 = lane & 15, g4 = lane >> 4;
+    float a[kC], mm[kC];
+#pragma unroll
+    for (int d = 0; d < kC; ++d) a[d] = mm[d] = 0.0f;
     for (int kt = 0; kt < kq; ++kt) {
         float q[4], k[4], g[4], bt[4];
         LoadKeyTile(p, rowbase, live, kt, g4, q, k, g, bt);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float kn = k[i] * km;
-            const float lg = RowPrefixAdd(g[i]);
-            const float ks_ = RowRor<D>(kn);
-            const float pd = __expf(lg - RowRor<D>(lg));   // prod_{s<r<=t} d_r
-            a = fmaf(bt[i] * kn * pd, ks_, a);
-            mm = fmaf(q[i] * qm * pd, ks_, mm);
+            PairTerms(std::make_integer_sequence<int, kC>{}, g[i], kn, bt[i] * kn, q[i] * qm, a, mm);
         }
     }
-    a = RowsSum4(a);
-    mm = RowsSum4(mm);
-    if (g4 == 0 && m16 >= D) {
-        const int t = m16, s = m16 - D;
-        const int pos = (s + 16 * (t >> 2)) * 4 + (t & 3);
-        dst[pos] = a;
-        dst[256 + pos] = mm;
+#pragma unroll
+    for (int d = 0; d < kC; ++d) {
+        const float ad = RowsSum4(a[d]), md = RowsSum4(mm[d]);
+        if (g4 == 0 && m16 >= d) {
+            const int t = m16, s = m16 - d;
+            const int pos = (s + 16 * (t >> 2)) * 4 + (t & 3);
+            dst[pos] = ad;
+            dst[256 + pos] = md;
+        }
     }
-}
-
-template <int... Ds>
-__device__ __forceinline__ void PairSteps(std::integer_sequence<int, Ds...>, const GatedDeltaNet2Params &p,
-                                          size_t rowbase, bool live, int kq, int m16, int g4, float qm, float km,
-                                          float *dst) {
-    (PairStep<Ds>(p, rowbase, live, kq, m16, g4, qm, km, dst), ...);
-}
-
-// A and M of a chunk whose decays leave the fast range (the whole wave calls
-// it).  Inlined: a call would give every wave a stack frame and its traffic.
-__device__ __forceinline__ void PairwiseAM(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kq,
-                                                     float qm, float km, float *dst) {
-    const int lane = threadIdx.x & 63;
-    PairSteps(std::make_integer_sequence<int, kC>{}, p, rowbase, live, kq, lane & 15, lane >> 4, qm, km, dst);
 }
 
 // Largest b with off[b] <= g (off non-decreasing over [0, n], off[0] = 0 <= g
@@ -285,13 +286,21 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     // (unnormalised A and M) on MFMA, used when every decay product is in range.
     float qs = 0.0f, kq2 = 0.0f;
     bool in_range = true;
-    v4f al = {0.0f, 0.0f, 0.0f, 0.0f}, mu = al;
+    // A' and M' accumulate in four chains (key tile parity x k-step parity),
+    // summed pairwise at the end: the MFMA adds its four products to the
+    // accumulator one fused multiply-add at a time, so one chain over dk keys
+    // is a dk-step rounding chain.  These sums of unnormalised q.k and k.k
+    // products over the keys carry most of the chunked form's rounding error
+    // (the diagonal of M meets each token's own update); the chains cut it to
+    // dk/4 steps plus two.
+    const v4f z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f alc[4] = {z4, z4, z4, z4}, muc[4] = {z4, z4, z4, z4};
     // this wave's Ut' tiles: lane l holds key l%16, tokens 4(l/16)..+3 (each
     // lane reads back only its own 16 bytes)
     float *const ut = prep_dyn + static_cast<size_t>(w) * kq * 256 + lane * 4;
     // one key tile: operand-layout vectors to the block, A' and M' accumulated
-    auto tile = [&](int kt, const float (&q)[4], const float (&k)[4], const float (&g)[4], const float (&bt)[4])
-                    __attribute__((always_inline)) {
+    auto tile = [&](int kt, bool odd, const float (&q)[4], const float (&k)[4], const float (&g)[4],
+                    const float (&bt)[4]) __attribute__((always_inline)) {
         v4f e, r, kb, g15;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -318,8 +327,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         if (m16 == 0) StF4(gsw + kt * 16 + 4 * g4, g15);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
-            al = Mfma(e[ii], kb[ii], al);
-            mu = Mfma(r[ii], kb[ii], mu);
+            const int c = (odd ? 2 : 0) + (ii & 1);
+            alc[c] = Mfma(e[ii], kb[ii], alc[c]);
+            muc[c] = Mfma(r[ii], kb[ii], muc[c]);
         }
     };
     // key tiles in pairs, both loaded before either is used: the two halves of
@@ -329,9 +339,10 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         const bool pair = kt + 1 < kq;   // kq is 1 or even
         LoadKeyTile(p, rowbase, live, kt, g4, q0, k0, g0, b0);
         if (pair) LoadKeyTile(p, rowbase, live, kt + 1, g4, q1, k1, g1, b1);
-        tile(kt, q0, k0, g0, b0);
-        if (pair) tile(kt + 1, q1, k1, g1, b1);
+        tile(kt, false, q0, k0, g0, b0);
+        if (pair) tile(kt + 1, true, q1, k1, g1, b1);
     }
+    v4f al = (alc[0] + alc[1]) + (alc[2] + alc[3]), mu = (muc[0] + muc[1]) + (muc[2] + muc[3]);
     qs = RowsSum4(qs);
     kq2 = RowsSum4(kq2);
     float qm = p.scale, km = 1.0f;
