@@ -233,6 +233,12 @@ const OrtApiBase g_base = {[](uint32_t version) -> const OrtApi * {
                                return version <= ORT_API_VERSION ? &g_api : nullptr;
                            },
                            []() { return "xm-ort-double"; }};
+// A runtime that is older than the headers: tables up to g_max_version only.
+uint32_t g_max_version = ORT_API_VERSION;
+const OrtApiBase g_old_base = {[](uint32_t version) -> const OrtApi * {
+                                   return version <= g_max_version ? &g_api : nullptr;
+                               },
+                               []() { return "xm-ort-double-old"; }};
 OrtSessionOptions g_options;
 bool g_registered = false;
 
@@ -274,6 +280,23 @@ int ortd_register_with_nulls(int null_options, int null_base, char *err, size_t 
     OrtStatus *st = RegisterCustomOps(null_options ? nullptr : &scratch_options, null_base ? nullptr : &g_base);
     if (st == nullptr) return 0;
     Copy(err, errlen, st->msg);
+    delete st;
+    return 1;
+}
+
+// RegisterCustomOps against a runtime that gives API tables up to
+// max_version only (0: none at all): returns 1 with the error status's
+// message and code in err / *code, 0 if it returned null; *domains is the
+// number of operator domains it added.
+int ortd_register_with_max_version(uint32_t max_version, char *err, size_t errlen, int *code, int *domains) {
+    OrtSessionOptions scratch_options;
+    g_max_version = max_version;
+    OrtStatus *st = RegisterCustomOps(&scratch_options, &g_old_base);
+    g_max_version = ORT_API_VERSION;
+    *domains = static_cast<int>(scratch_options.domains.size());
+    if (st == nullptr) return 0;
+    Copy(err, errlen, st->msg);
+    *code = static_cast<int>(st->code);
     delete st;
     return 1;
 }

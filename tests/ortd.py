@@ -38,6 +38,8 @@ def lib():
         l = ctypes.CDLL(LIB)
         l.ortd_register.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
         l.ortd_register_with_nulls.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
+        l.ortd_register_with_max_version.argtypes = [ctypes.c_uint32, ctypes.c_char_p, ctypes.c_size_t,
+                                                     ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
         l.ortd_requested_api_version.restype = ctypes.c_uint32
         l.ortd_domain_name.restype = ctypes.c_char_p
         l.ortd_op_name.restype = ctypes.c_char_p

@@ -55,6 +55,29 @@ def test_register_with_null_arguments():
     assert b"null session options" in err.value
 
 
+def test_register_against_an_older_runtime_fails_with_the_versions():
+    """A runtime whose newest API table is older than the headers the library
+    was built with (GetApi(ORT_API_VERSION) is null) gets an ORT_FAIL status
+    naming both versions from the newest table it does give, and nothing is
+    registered; with no table at all there is nothing to report through."""
+    import ctypes
+    l = ortd.lib()
+    err = ctypes.create_string_buffer(512)
+    code, domains = ctypes.c_int(-1), ctypes.c_int(-1)
+    assert l.ortd_register_with_max_version(16, err, len(err), ctypes.byref(code), ctypes.byref(domains)) == 1
+    msg = err.value.decode()
+    assert code.value == 1   # ORT_FAIL
+    assert domains.value == 0
+    assert "API version 17" in msg and "API version 16 at most" in msg and "xm-ort-double-old" in msg, msg
+    assert l.ortd_register_with_max_version(3, err, len(err), ctypes.byref(code), ctypes.byref(domains)) == 1
+    assert "API version 3 at most" in err.value.decode()
+    assert l.ortd_register_with_max_version(0, err, len(err), ctypes.byref(code), ctypes.byref(domains)) == 0
+    assert domains.value == 0
+    # the build's own version still registers the domain
+    assert l.ortd_register_with_max_version(17, err, len(err), ctypes.byref(code), ctypes.byref(domains)) == 0
+    assert domains.value == 1
+
+
 def _slots(name, t0=FLOAT):
     for _, n, _, ins, outs in ortd.ops():
         if n == name and ins[0][0] == t0:
