@@ -135,6 +135,22 @@ def test_states_entry_needs_a_state_buffer():
     assert (st, msg) == (xp.XM_ERR_INVALID_ARGUMENT, "return_final_states=1 needs four state buffers")
 
 
+def test_gdn2_scratch_follows_the_kernel_that_runs():
+    """The planned scratch is the chunked path's by default and 0 when the
+    gdn2_path override runs the sequential fused kernel (dk <= 512), which
+    takes none; above 512 keys only the LDS-state path runs, with scratch."""
+    import xmetai_onnx_plugins as xp
+    def scratch(T, K, V):
+        return validate("gated_deltanet2", gdn_shapes(T=T, K=K, V=V))[1]
+    assert scratch(300, 128, 64) > 0
+    assert scratch(3000, 512, 64) > 0
+    with xp.kernel_override("gdn2_path", 1):
+        assert scratch(300, 128, 64) == 0
+        assert scratch(3000, 512, 64) == 0
+        assert scratch(3000, 600, 64) > 0
+    assert scratch(300, 128, 64) > 0
+
+
 def test_states_entry_validates_shapes_first():
     bad = ss_shapes()
     bad[1] = (2, 8, 15)
@@ -277,8 +293,9 @@ def test_gdn2_valid_and_scratch():
     a256 = lambda n: (n + 255) // 256 * 256
 
     # headdim_k <= 512 (chunked path): per (b,h) and 16-token chunk of a window
-    # of up to 128 chunks, E, R, Ut tiles (256 floats per 16 keys each), G_15
-    # (16 per 16 keys), T and M T (256 each), q and k multipliers (16 each);
+    # of up to 128 chunks, E, R, Ut tiles (256 floats per 16 keys each), M T
+    # (256), and per recurrence wave ceil((8 + 4 kpw) / 16) scalar vectors of
+    # 64 floats (q and k multipliers, G_15);
     # keys padded to 16 * kpw * ks (kpw = 2 and ks = ceil(tiles / 2) up to 128
     # keys; 3 tiles x 4 waves for 129-192 keys; 5 tiles x 4 waves for 257-320
     # keys; for 321-384 keys 3 tiles x 8 waves when the launch has fewer than
@@ -300,15 +317,18 @@ def test_gdn2_valid_and_scratch():
             kpw = 2 if kq >= 2 else 1
             ks = -(-kq // kpw)
         kq = kpw * ks
-        block = 3 * kq * 256 + 16 * kq + 256 + 32
+        block = 3 * kq * 256 + 256 + ks * (-(-(8 + 4 * kpw) // 16)) * 64
         nch = -(-T // 16)
         rows, vt, kt = B * H, -(-V // 16), -(-K // 16)
-        # sequence split: rows (vt + kt) <= 160 column tiles and 64+ chunks;
-        # max(2, min(ceil(chunks / 64), 1 + ceil(1536 / (rows (vt + kt))))) segments; every chunk's
-        # blocks, Psi [B,T,H,KP], Phi [nseg][rows][K][KP] (KP = 16 kt), S0 and
-        # the start states [nseg][rows][K][V]; at most 2 GiB
-        if rows * (vt + kt) <= 160 and nch >= 64 and nch * block * 4 < (1 << 31):
-            nseg = max(2, min(-(-nch // 64), 1 + -(-1536 // (rows * (vt + kt)))))
+        # sequence split, 64+ chunks: rows (vt + kt) <= 160 column tiles,
+        # max(2, min(ceil(chunks / 64), 1 + ceil(1536 / (rows (vt + kt))))) segments;
+        # above 160, two segments when rows vt <= 64 and rows vt + rows (vt + kt)
+        # <= 256; every chunk's blocks, Psi [B,T,H,KP], Phi [nseg][rows][K][KP]
+        # (KP = 16 kt), S0 and the start states [nseg][rows][K][V]; at most 2 GiB
+        wide = rows * (vt + kt) > 160
+        if (nch >= 64 and nch * block * 4 < (1 << 31)
+                and (not wide or (rows * vt <= 64 and rows * vt + rows * (vt + kt) <= 256))):
+            nseg = 2 if wide else max(2, min(-(-nch // 64), 1 + -(-1536 // (rows * (vt + kt)))))
             sc = -(-nch // nseg)
             nseg = -(-nch // sc)
             if nseg >= 2:
@@ -325,7 +345,8 @@ def test_gdn2_valid_and_scratch():
         return a256(per_block * win) + (a256(B * H * K * V * 4) if win < nch else 0)
     assert scratch == chunk_scratch(2, 5, 3, 16, 8)
     for T, K, V in ((100, 128, 64), (3000, 128, 128), (17, 100, 7), (2049, 256, 16), (2048, 33, 40),
-                    (3000, 512, 64), (40, 300, 16), (40, 352, 16), (40, 352, 352), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8)):
+                    (3000, 512, 64), (40, 300, 16), (40, 352, 16), (40, 352, 352), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8),
+                    (2048, 320, 64), (2048, 384, 64), (2048, 512, 64)):
         assert validate("gated_deltanet2", gdn_shapes(T=T, K=K, V=V))[1] == chunk_scratch(2, T, 3, K, V), (T, K, V)
     # packed sequences (headdim_k <= 512) take the fused kernel: no scratch
     # headdim_k > 512: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded
@@ -379,10 +400,12 @@ def packed_chunk_scratch(N, T, H, K, V):
     can span windows, and the per-window block offsets [windows][N+1] ints;
     each region 256-byte aligned."""
     a256 = lambda x: -(-x // 256) * 256
-    kq = -(-K // 16)
-    kq = 4 * -(-kq // 4) if kq > 8 else (kq if kq < 2 else 2 * -(-kq // 2))
+    kq = -(-K // 16)   # (the key layouts of 16, 64, 128, 256 and 512 keys)
+    kpw = 4 if kq > 8 else (1 if kq < 2 else 2)
+    ks = -(-kq // kpw)
+    kq = kpw * ks
     nch = -(-T // 16)
-    per = H * (3 * kq * 256 + 16 * kq + 288) * 4
+    per = H * (3 * kq * 256 + 256 + ks * (-(-(8 + 4 * kpw) // 16)) * 64) * 4
     win = min(nch, 128)
     blocks = a256(per * min(win * N, nch + N))
     if win < nch and a256(per * (nch + N)) <= max(2 * blocks, 512 << 20):

@@ -112,7 +112,8 @@ def test_noalloc_windows_where_the_split_exceeds_the_array():
 
 @pytest.mark.gpu
 def test_noalloc_without_scratch_needs():
-    # the sequential kernel takes no scratch: nothing is looked up
+    # the sequential kernel (gdn2_path override) takes no scratch: the call
+    # plans 0 bytes (test_capi_cpu checks the size), so the array is not used
     import torch
     s = S(1, 40, 2, 64, 16, initial_state=False)
     with xp.kernel_override("gdn2_path", 1):
@@ -120,6 +121,30 @@ def test_noalloc_without_scratch_needs():
     np.testing.assert_array_equal(got, want)
     assert launched and launched[0].startswith("Gdn2FusedKernel"), launched
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_noalloc_calls_on_two_streams_are_ordered():
+    # A long call on one stream and, right after it with no host wait, another
+    # call on a second stream: both use the one array, so the second waits for
+    # the first's kernels (the device's event) before it overwrites it.  Each
+    # output equals the allocating entry point's, bit for bit.
+    import torch
+    shapes = [S(4, 2100, 16, 128, 64), S(2, 1500, 8, 128, 64)]
+    runs = []
+    for i, s in enumerate(shapes):
+        inp = W.gated_deltanet2_inputs(s, seed=20 + i)
+        d = {k: to_dev(inp[k]) for k in KEYS}
+        ref = xp.gated_deltanet2_fn(*(d[k] for k in KEYS), scale=s.scale, use_qk_l2norm_in_kernel=int(s.l2norm))
+        runs.append((s, d, ref, torch.full_like(ref, float("nan"))))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for (s, d, _, out), st in zip(runs, streams):
+        code, msg = _call_noalloc([xp._desc_from_tensor(d[k]) for k in KEYS], s, out.data_ptr(), st.cuda_stream)
+        assert code == xp.XM_OK, msg
+    torch.cuda.synchronize()
+    for s, _, ref, out in runs:
+        np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
 
 
 def test_noalloc_rejects_calls_beyond_the_array():

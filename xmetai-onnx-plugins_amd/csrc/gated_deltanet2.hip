@@ -663,9 +663,10 @@ LdsPlan PlanLds(int batch, int seqlen, int nheads, int dk, int dv, size_t cap) {
 
 }  // namespace
 
-size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
-    if (dk <= kGdn2ChunkKeyLimit)   // chunked path (packed sequences included)
-        return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv, packed, cap);
+size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap,
+                                  bool allow_split) {
+    if (dk <= kGdn2ChunkKeyLimit && GetOverride(kOverrideGdn2Path) != 1)   // chunked path (packed included)
+        return GatedDeltaNet2ChunkScratchBytes(batch, seqlen, nheads, dk, dv, packed, cap, allow_split);
     if (dk <= kFusedKeyLimit) return 0;   // fused kernel: no scratch
     const LdsPlan l = PlanLds(batch, seqlen, nheads, dk, dv, cap);
     return l.chunk_cap == 0 ? SIZE_MAX : l.total();

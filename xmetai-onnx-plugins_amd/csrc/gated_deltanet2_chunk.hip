@@ -286,21 +286,25 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     // (unnormalised A and M) on MFMA, used when every decay product is in range.
     float qs = 0.0f, kq2 = 0.0f;
     bool in_range = true;
-    // A' and M' accumulate in four chains (key tile parity x k-step parity),
-    // summed pairwise at the end: the MFMA adds its four products to the
-    // accumulator one fused multiply-add at a time, so one chain over dk keys
-    // is a dk-step rounding chain.  These sums of unnormalised q.k and k.k
-    // products over the keys carry most of the chunked form's rounding error
-    // (the diagonal of M meets each token's own update); the chains cut it to
-    // dk/4 steps plus two.
+    // A' and M' are sums over the keys of unnormalised k.k and q.k products,
+    // and they carry most of the chunked form's rounding error (the diagonal
+    // of M meets each token's own update).  The MFMA adds its four products to
+    // the accumulator one fused multiply-add at a time, so a single chain over
+    // dk keys would be a dk-step rounding chain.  Blocked instead: a pair of
+    // key tiles accumulates from zero in two chains of 16 keys (k-step parity),
+    // and the pair's sum is added to the running total once the next pair's
+    // loads are issued (added right after its own products, the wait for them
+    // delayed those loads: 1.7% at 256 keys): about 17 + dk/32 rounding steps
+    // for any dk.
     const v4f z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    v4f alc[4] = {z4, z4, z4, z4}, muc[4] = {z4, z4, z4, z4};
+    v4f al = z4, mu = z4;                     // totals over the key-tile pairs
+    v4f alc[2] = {z4, z4}, muc[2] = {z4, z4};  // the current pair's chains
     // this wave's Ut' tiles: lane l holds key l%16, tokens 4(l/16)..+3 (each
     // lane reads back only its own 16 bytes)
     float *const ut = prep_dyn + static_cast<size_t>(w) * kq * 256 + lane * 4;
     // one key tile: operand-layout vectors to the block, A' and M' accumulated
-    auto tile = [&](int kt, bool odd, const float (&q)[4], const float (&k)[4], const float (&g)[4],
-                    const float (&bt)[4]) __attribute__((always_inline)) {
+    auto tile = [&](int kt, const float (&q)[4], const float (&k)[4], const float (&g)[4], const float (&bt)[4])
+                    __attribute__((always_inline)) {
         v4f e, r, kb, g15;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -327,9 +331,8 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         if (m16 == 0) StF4(gsw + kt * 16 + 4 * g4, g15);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
-            const int c = (odd ? 2 : 0) + (ii & 1);
-            alc[c] = Mfma(e[ii], kb[ii], alc[c]);
-            muc[c] = Mfma(r[ii], kb[ii], muc[c]);
+            alc[ii & 1] = Mfma(e[ii], kb[ii], alc[ii & 1]);
+            muc[ii & 1] = Mfma(r[ii], kb[ii], muc[ii & 1]);
         }
     };
     // key tiles in pairs, both loaded before either is used: the two halves of
@@ -339,10 +342,14 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
         const bool pair = kt + 1 < kq;   // kq is 1 or even
         LoadKeyTile(p, rowbase, live, kt, g4, q0, k0, g0, b0);
         if (pair) LoadKeyTile(p, rowbase, live, kt + 1, g4, q1, k1, g1, b1);
-        tile(kt, false, q0, k0, g0, b0);
-        if (pair) tile(kt + 1, true, q1, k1, g1, b1);
+        al += alc[0] + alc[1];   // the previous pair (zeros at the first)
+        mu += muc[0] + muc[1];
+        alc[0] = alc[1] = muc[0] = muc[1] = z4;
+        tile(kt, q0, k0, g0, b0);
+        if (pair) tile(kt + 1, q1, k1, g1, b1);
     }
-    v4f al = (alc[0] + alc[1]) + (alc[2] + alc[3]), mu = (muc[0] + muc[1]) + (muc[2] + muc[3]);
+    al += alc[0] + alc[1];
+    mu += muc[0] + muc[1];
     qs = RowsSum4(qs);
     kq2 = RowsSum4(kq2);
     float qm = p.scale, km = 1.0f;
@@ -1379,9 +1386,10 @@ __global__ __launch_bounds__(256) void Gdn2PackedChunksKernel(GatedDeltaNet2Para
 
 }  // namespace
 
-size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap) {
+size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed, size_t cap,
+                                       bool allow_split) {
     if (dk > kGdn2ChunkKeyLimit) return 0;
-    const SplitPlan sp = PlanSplit(batch, seqlen, nheads, dk, dv, packed, cap);
+    const SplitPlan sp = allow_split ? PlanSplit(batch, seqlen, nheads, dk, dv, packed, cap) : SplitPlan{};
     if (sp.nseg > 0) return sp.total();
     const WindowPlan w = PlanWindows(batch, seqlen, nheads, dk, dv, packed, cap);
     return w.win == 0 ? SIZE_MAX : w.total();

@@ -104,9 +104,21 @@ Plan Prepare(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet
 void Forward(const xm_tensor_t *inputs, size_t n_inputs, const xm_gated_deltanet2_attrs_t &attrs, float *out,
              float *final_state, void *stream, const xm_allocator_t *alloc) {
     const GatedDeltaNet2Params p = GatedDeltaNet2Plan(inputs, n_inputs, attrs, out, final_state);
-    const size_t bytes = GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv, p.cu_seqlens != nullptr);
+    const bool packed = p.cu_seqlens != nullptr;
+    size_t bytes = GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv, packed);
     Scratch scratch(alloc, stream);
-    void *buf = scratch.Get(bytes);
+    void *buf = scratch.TryGet(bytes);
+    if (buf == nullptr && bytes > 0) {
+        // The sequence split keeps every chunk's blocks at once; when the
+        // allocator refuses that, the windowed plan (a window's blocks plus
+        // the carried state) runs the same call in less.
+        const size_t windowed =
+            GatedDeltaNet2ScratchBytes(p.batch, p.seqlen, p.nheads, p.dk, p.dv, packed, SIZE_MAX, false);
+        if (windowed >= bytes)
+            throw Error(XM_ERR_ALLOC, "scratch allocation of " + std::to_string(bytes) + " bytes failed");
+        bytes = windowed;
+        buf = scratch.Get(bytes);
+    }
     LaunchGatedDeltaNet2(p, buf, bytes, stream);
 }
 

@@ -172,6 +172,7 @@ std::string KernelName(const char *base, std::initializer_list<const char *> typ
 // memory is reused only in stream order, so freeing right after the last
 // launch is safe (reference: gated_deltanet2_fn_ort.cpp:89-111).
 void *DefaultAlloc(size_t bytes, void *stream);
+void *DefaultTryAlloc(size_t bytes, void *stream);   // nullptr when the pool cannot give the bytes
 void DefaultFree(void *ptr, void *stream);
 
 class Scratch {
@@ -189,16 +190,23 @@ public:
         }
     }
     void *Get(size_t bytes) {
+        void *p = TryGet(bytes);
+        if (p == nullptr && bytes > 0)
+            throw Error(XM_ERR_ALLOC, "scratch allocation of " + std::to_string(bytes) + " bytes failed");
+        return p;
+    }
+    // As Get, but nullptr when the allocator refuses the bytes (the caller
+    // may then ask for a smaller layout).
+    void *TryGet(size_t bytes) {
         if (bytes == 0) return nullptr;
         void *p = nullptr;
         if (alloc_ != nullptr) {
             if (alloc_->alloc == nullptr) throw Error(XM_ERR_ALLOC, "scratch allocator has no alloc callback");
             p = alloc_->alloc(alloc_->ctx, bytes);
         } else {
-            p = DefaultAlloc(bytes, stream_);
+            p = DefaultTryAlloc(bytes, stream_);
         }
-        if (p == nullptr) throw Error(XM_ERR_ALLOC, "scratch allocation of " + std::to_string(bytes) + " bytes failed");
-        ptrs_.push_back(p);
+        if (p != nullptr) ptrs_.push_back(p);
         return p;
     }
 

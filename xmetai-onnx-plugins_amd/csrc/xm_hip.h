@@ -15,9 +15,17 @@
     } while (0)
 
 // Reports a failed launch (reference: XM_CUDA_KERNEL_CHECK, cuda_common.h:27-36).
+namespace xm {
+// The HIP error this call's launches left on the thread, consumed; hipSuccess
+// when there is none, or when the pending error is the one the caller had
+// left before the call (ResetLaunches notes it): that one stays for the
+// caller's own check.
+hipError_t TakeLaunchError();
+}  // namespace xm
+
 #define XM_LAUNCH_CHECK(what)                                                                      \
     do {                                                                                           \
-        hipError_t xm_err_ = hipGetLastError();                                                    \
+        hipError_t xm_err_ = ::xm::TakeLaunchError();                                              \
         if (xm_err_ != hipSuccess)                                                                 \
             throw ::xm::Error(XM_ERR_DEVICE, std::string(what) + " kernel launch failed: " + hipGetErrorString(xm_err_)); \
     } while (0)

@@ -93,9 +93,12 @@ GatedDeltaNet2Params GatedDeltaNet2Plan(const xm_tensor_t *inputs, size_t n_inpu
                                         const xm_gated_deltanet2_attrs_t &attrs, float *out, float *final_state);
 // Scratch bytes of one call when at most `cap` bytes are available: the
 // chunked windows and the token chunks of the dk > 512 path shrink to fit.
-// 0 when the call needs none; SIZE_MAX when not even the smallest layout fits.
+// 0 when the call needs none (also when the gdn2_path override runs the
+// sequential kernel); SIZE_MAX when not even the smallest layout fits.
+// allow_split = false: the windowed plan's bytes, never the sequence split's
+// (which keeps every chunk's blocks at once).
 size_t GatedDeltaNet2ScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed,
-                                  size_t cap = SIZE_MAX);
+                                  size_t cap = SIZE_MAX, bool allow_split = true);
 // `scratch` holds `scratch_bytes` bytes; the layout is the one
 // GatedDeltaNet2ScratchBytes chose for cap = scratch_bytes.
 void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_bytes, void *stream);
@@ -107,7 +110,7 @@ void LaunchGatedDeltaNet2(GatedDeltaNet2Params p, void *scratch, size_t scratch_
 // With `packed`, batch is the number of sequences packed along one row of
 // seqlen tokens.
 size_t GatedDeltaNet2ChunkScratchBytes(int batch, int seqlen, int nheads, int dk, int dv, bool packed = false,
-                                       size_t cap = SIZE_MAX);
+                                       size_t cap = SIZE_MAX, bool allow_split = true);
 constexpr int kGdn2ChunkKeyLimit = 512;   // head_k handled by the chunked path
 bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, size_t scratch_bytes, void *stream);
 void LaunchMamba3Siso(const Mamba3SisoParams &p, void *stream);

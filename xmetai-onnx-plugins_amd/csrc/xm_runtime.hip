@@ -50,6 +50,16 @@ void *DefaultAlloc(size_t bytes, void *stream) {
     return p;
 }
 
+void *DefaultTryAlloc(size_t bytes, void *stream) {
+    hipMemPool_t pool = PoolForCurrentDevice();
+    void *p = nullptr;
+    if (hipMallocFromPoolAsync(&p, bytes, pool, static_cast<hipStream_t>(stream)) != hipSuccess) {
+        (void)hipGetLastError();   // this call's own error
+        return nullptr;
+    }
+    return p;
+}
+
 void DefaultFree(void *ptr, void *stream) {
     if (ptr != nullptr) (void)hipFreeAsync(ptr, static_cast<hipStream_t>(stream));
 }
@@ -167,15 +177,23 @@ struct LaunchLog {
     std::string text;
 };
 thread_local LaunchLog t_launches;
+thread_local hipError_t t_entry_error = hipSuccess;   // pending when the current call began
 }  // namespace
 
 void ResetLaunches() {
     t_launches.n = 0;
     // hipGetLastError reports the last error of any runtime call on this
     // thread, including the caller's own (a framework probing devices leaves
-    // one behind).  Clear it so the launch checks of this call see only the
-    // launches it makes.
-    (void)hipGetLastError();
+    // one behind), and clears it.  Note it without clearing: the launch
+    // checks of this call take only an error that differs from it, and the
+    // caller still finds its own.
+    t_entry_error = hipPeekAtLastError();
+}
+
+hipError_t TakeLaunchError() {
+    const hipError_t e = hipPeekAtLastError();
+    if (e == hipSuccess || e == t_entry_error) return hipSuccess;
+    return hipGetLastError();
 }
 
 void NoteLaunch(const char *name) {
