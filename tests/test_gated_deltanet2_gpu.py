@@ -261,3 +261,84 @@ def test_gdn2_column_independence_bitwise():
     sub["initial_state"] = np.ascontiguousarray(inp["initial_state"][..., :65])
     y65 = run_gpu(sub, S(1, 300, 2, 128, 65))
     np.testing.assert_array_equal(y65, y128[..., :65])
+
+
+def test_gdn2_split_scratch_refused_falls_back_to_windows():
+    """An allocator that refuses the sequence split's scratch (every chunk's
+    blocks at once) still gets a successful call: the operator asks again
+    for the windowed plan's bytes, which it grants, and the result matches
+    the oracle."""
+    import torch
+    s = S(1, 4096, 2, 128, 64)   # few heads, 256 chunks: the split is the default plan
+    inp = W.gated_deltanet2_inputs(s, seed=17)
+    split_bytes = xp.validate("gated_deltanet2", [inp[k].shape if inp[k] is not None else None for k in KEYS])[1]
+    base = TorchAllocator()
+    asked = []
+
+    def refusing(ctx, nbytes):
+        asked.append(int(nbytes))
+        return None if nbytes >= split_bytes else base._alloc_cb(ctx, nbytes)
+
+    from xmetai_onnx_plugins import _capi
+    alloc = TorchAllocator()
+    alloc._alloc_cb = _capi.ALLOC_FN(refusing)
+    alloc.struct = _capi.XmAllocator(None, alloc._alloc_cb, base._free_cb)
+    y = gated_deltanet2_fn(*(to_dev(inp[k]) for k in KEYS), scale=s.scale, use_qk_l2norm_in_kernel=s.l2norm,
+                           allocator=alloc)
+    torch.cuda.synchronize()
+    launched = xp.last_launches()
+    assert len(asked) == 2 and asked[0] == split_bytes and asked[1] < split_bytes, asked
+    assert not any(k.startswith("Gdn2ChunkSplitKernel") for k in launched), launched
+    assert any(k.startswith("Gdn2ChunkRecurKernel") for k in launched), launched
+    check("gated_deltanet2/split_refused_windows", y.cpu().numpy(), run_ref(inp, s), TOL_GDN2)
+
+
+# Two value-column tiles per recurrence workgroup (gdn2_ct = 2; built for 33 to
+# 256 keys): the key tiles' operands serve 32 columns, a workgroup's last tile
+# may be past dv (ragged dv), and the state of both tiles crosses windows.
+CT2_CASES = [n for n in sorted(CASES) if 32 < CASES[n].dk <= 256]
+
+
+def _ran_two_tiles():
+    return any(k.startswith("Gdn2ChunkRecurKernel<") and k.split("<")[1].split(",")[2] == "2"
+               for k in xp.last_launches())
+
+
+@pytest.mark.parametrize("name", CT2_CASES)
+def test_gdn2_parity_two_column_tiles(name, override):
+    s = CASES[name]
+    override("gdn2_ct", 2)
+    override("gdn2_split", 1)   # the recurrence kernel itself, not the sequence split
+    inp = W.gated_deltanet2_inputs(s, seed=0)
+    got = run_gpu(inp, s)
+    assert _ran_two_tiles(), xp.last_launches()
+    ref32 = None if s.l2norm else run_ref(inp, s, np.float32)
+    check(f"gated_deltanet2/{name}/ct2", got, run_ref(inp, s), TOL_GDN2, ref32=ref32)
+
+
+@pytest.mark.parametrize("shape", [(1, 2100, 2, 96, 40, True), (2, 4100, 1, 64, 24, False), (1, 2100, 1, 192, 33, True)])
+def test_gdn2_two_column_tiles_window_carry(shape, override):
+    """128-chunk windows (gdn2_windowed): both column tiles' states carried."""
+    b, t, h, k, v, perkey = shape
+    s = S(b, t, h, k, v, per_key_gates=perkey)
+    override("gdn2_ct", 2)
+    override("gdn2_windowed", 1)
+    inp = W.gated_deltanet2_inputs(s, seed=11)
+    got = run_gpu(inp, s)
+    assert _ran_two_tiles(), xp.last_launches()
+    check(f"gated_deltanet2/ct2_windows_{b}_{t}_{h}_{k}_{v}", got, run_ref(inp, s), TOL_GDN2)
+
+
+def test_gdn2_two_column_tiles_equal_one_bitwise(override):
+    """Columns are independent and both layouts sum in the same order: two
+    tiles per workgroup give the one-tile results bit for bit (dv = 65: the
+    third workgroup's second tile is past dv)."""
+    s = S(2, 300, 3, 128, 65)
+    inp = W.gated_deltanet2_inputs(s, seed=12)
+    override("gdn2_split", 1)
+    override("gdn2_ct", 1)
+    one = run_gpu(inp, s)
+    override("gdn2_ct", 2)
+    two = run_gpu(inp, s)
+    assert _ran_two_tiles(), xp.last_launches()
+    np.testing.assert_array_equal(two, one)

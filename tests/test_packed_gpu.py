@@ -254,3 +254,10 @@ def test_m3_packed_uncovered_rows_are_zero(case, m3_path):
                     part[k] = np.ascontiguousarray(x[:, lo:hi])
             ry = cref.mamba3_siso(*(part[k] for k in M3_KEYS), dtype=np.float64)
             check(f"m3_packed_gaps/{case}/{m3_path}/seq{n}", y[:, lo:hi], ry, TOL_M3)
+
+
+@pytest.mark.parametrize("dk,dv", [(64, 40), (128, 65), (256, 20)])
+def test_gdn2_packed_two_column_tiles(dk, dv, override):
+    """Packed sequences through the two-tile recurrence (gdn2_ct = 2)."""
+    override("gdn2_ct", 2)
+    gdn2_packed_check([37, 0, 1, 16, 50, 700], 2, dk, dv, True, "chunk", 13, f"gdn2_packed_ct2/{dk}x{dv}")

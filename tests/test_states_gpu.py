@@ -303,3 +303,17 @@ def test_m3_states_chain(shape, split, m3_path):
     torch.cuda.synchronize()
     check(f"mamba3_state/chain_{split}/y", torch.cat([y1, y2], dim=1).cpu().numpy(), y.cpu().numpy(), TOL_GPU)
     check_m3_states(f"mamba3_state/chain_{split}", [x.cpu().numpy() for x in st2], [x.cpu().numpy() for x in st], TOL_GPU)
+
+
+@pytest.mark.parametrize("name", ["t3_shorter_than_block", "k32_v33_nos0", "k128_v65_partial_wave", "k200_v40",
+                                  "t4100_three_windows"])
+def test_gdn2_final_state_two_column_tiles(name, override):
+    """Final states of both column tiles of a two-tile workgroup (gdn2_ct)."""
+    s = GDN_CASES[name]
+    inp = W.gated_deltanet2_inputs(s, seed=6)
+    override("gdn2_ct", 2)
+    override("gdn2_split", 1)
+    o, st = gdn_gpu(inp, s)
+    ref_o, ref_st = gdn_ref(inp, s)
+    check(f"gated_deltanet2_state/{name}/ct2/o", o, ref_o, TOL_GDN2)
+    check(f"gated_deltanet2_state/{name}/ct2/S", st, ref_st, TOL_GDN2)

@@ -464,7 +464,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
 // ---------------------------------------------------------------------------
 // Recurrence over one window
 // ---------------------------------------------------------------------------
-template <int KPW, int KS>
+// A recurrence workgroup: KS waves of KPW key tiles over CT tiles of 16
+// value columns.
+template <int KPW, int KS, int CT = 1>
 struct RecurLayout {
     static constexpr int THREADS = 64 * KS;
     static constexpr int KQ = KPW * KS;
@@ -473,23 +475,23 @@ struct RecurLayout {
     // Token rows i (the D layout's registers) whose w, v a wave loads and
     // whose (M T) Y slice it forms: i = ks + m KS, m < NM (i < 4).
     static constexpr int NM = (4 + KS - 1) / KS;
-    // LDS, in floats, per chunk parity: [KS waves][E' S0, output][256]
-    // partials, then W o V [256] (lane l: rows 4(l/16)..+3, column l%16) and
-    // [256] where the waves without a row write (no branch)
-    static constexpr int kPart = KS * 512 + 512;   // W o V, then a spare row slot
+    // LDS, in floats, per chunk parity: [KS waves][E' S0, output][CT][256]
+    // partials, then W o V [CT][256] (lane l: rows 4(l/16)..+3, column l%16)
+    // and [256] where the waves without a row write (no branch)
+    static constexpr int kPart = KS * 2 * CT * 256 + CT * 256 + 256;
     static constexpr int kFloats = KS > 1 ? 2 * kPart : 1;
 };
 
 // The operands of one chunk that a wave needs, in MFMA lane order: its key
 // tiles of E', R', Ut~, its scalar vectors (k_mul, q_mul, G_15), and for its
 // token rows i = ks + m KS the M T slice (A operand column 4(l/16)+i) and
-// this lane's w, v (token 4(l/16)+i).
-template <int KPW, int KS>
+// this lane's w, v (token 4(l/16)+i) in each of its CT column tiles.
+template <int KPW, int KS, int CT>
 struct ChunkOperands {
-    using L = RecurLayout<KPW, KS>;
+    using L = RecurLayout<KPW, KS, CT>;
     v4f e[KPW], r[KPW], ut[KPW];
     float sc[L::NSV];
-    float mt[L::NM], w[L::NM], v[L::NM];
+    float mt[L::NM], w[CT][L::NM], v[CT][L::NM];
 };
 
 // Entry E of a wave's scalar list for the lanes of each row (DPP row_newbcast).
@@ -535,44 +537,55 @@ struct SplitTile {
     float *psi;
 };
 
-template <int KPW, int KS, bool SPLIT = false>
+template <int KPW, int KS, int CT = 1, bool SPLIT = false>
 __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, float *sXp, int h, size_t tok0, int T,
                                              int cs, int cw0, int nrun, int wn, const float *prep_row, size_t sbase,
                                              const float *s_in, float *s_out, SplitTile st = {}) {
-    using L = RecurLayout<KPW, KS>;
-    using Ops = ChunkOperands<KPW, KS>;
+    static_assert(!SPLIT || CT == 1, "identity tiles run one column tile per workgroup");
+    using L = RecurLayout<KPW, KS, CT>;
+    using Ops = ChunkOperands<KPW, KS, CT>;
     constexpr int KQ = L::KQ, FB = L::FB, NSV = L::NSV, NM = L::NM;
     constexpr int oE = 0, oR = KQ * 256, oU = 2 * KQ * 256, oMT = 3 * KQ * 256, oSc = oMT + 256;   // block offsets (floats)
 
     const int H = p.nheads, dk = p.dk, dv = p.dv;
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g4 = lane >> 4;
-    const int VT = (dv + 15) / 16;
-    const int vt = SPLIT ? st.tile : XcdLocalBlock(blockIdx.x, gridDim.x) % VT;
+    const int VT = (dv + 15) / 16, VW = (VT + CT - 1) / CT;   // column tiles; workgroups per (b, h)
+    const int vt = SPLIT ? st.tile : XcdLocalBlock(blockIdx.x, gridDim.x) % VW;
     const bool ident = SPLIT && st.ident;
-    const int col = vt * 16 + (lane & 15);
-    const bool col_ok = !ident && col < dv;
-    // output column: the value column, or (identity tile) the key it starts as
+    // this lane's value column in each of the workgroup's CT column tiles
+    int col[CT];
+    bool col_ok[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+        col[c] = (vt * CT + c) * 16 + (lane & 15);
+        col_ok[c] = !ident && col[c] < dv;
+    }
+    // output column (CT = 1 where it differs): the value column, or (identity
+    // tile) the key it starts as
     const int kcol = SPLIT ? (vt - VT) * 16 + (lane & 15) : 0;
-    const int ocol = ident ? kcol : col;
-    const bool ocol_ok = ident || col_ok;
+    const int ocol = ident ? kcol : col[0];
+    const bool ocol_ok = ident || col_ok[0];
     const int OW = ident ? (dk + 15) / 16 * 16 : dv;   // output row width
     const Rsrc rblk = MakeRsrc(prep_row, wn * FB * 4);   // this head row's prepared blocks of the window
     // byte offsets, from a chunk's first token in [B,T,H,V], of this lane's
-    // tokens 4(l/16)+i in its column (out of range for columns past dv); the
+    // tokens 4(l/16)+i in its columns (out of range for columns past dv); the
     // per-chunk descriptors of w, v and out end after the chunk's last valid
     // token, so padded tokens read zeros and are not stored
     const int HV = H * dv;
-    int vo[4];
+    int vo[CT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vo[i] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vo[c][i] = col_ok[c] ? ((4 * g4 + i) * HV + col[c]) * 4 : kOutOfRange;
     // this wave's token rows i = ks + m KS (clamped to 3 where m KS + ks >= 4,
     // loaded but unused): w, v offsets and the M T slice of the A operand
-    int vl[NM], mo[NM];
+    int vl[CT][NM], mo[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         const int i = min(ks + m * KS, 3);
-        vl[m] = col_ok ? ((4 * g4 + i) * HV + col) * 4 : kOutOfRange;
+#pragma unroll
+        for (int c = 0; c < CT; ++c) vl[c][m] = col_ok[c] ? ((4 * g4 + i) * HV + col[c]) * 4 : kOutOfRange;
         mo[m] = (lane * 4 + i) * 4;
     }
     const int so = lane * 4 + ks * NSV * 256;   // this wave's scalar vectors
@@ -592,9 +605,12 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     auto chunk_off = [&](int jl) { return static_cast<long long>(jl) * cstride; };
     // the output rows (O, or psi for an identity tile: rows of OW floats)
     const int HO = H * OW;
-    int oo[4];
+    int oo[CT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) oo[i] = SPLIT ? (ocol_ok ? ((4 * g4 + i) * HO + ocol) * 4 : kOutOfRange) : vo[i];
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            oo[c][i] = SPLIT ? (ocol_ok ? ((4 * g4 + i) * HO + ocol) * 4 : kOutOfRange) : vo[c][i];
     float *const out_run = (ident ? st.psi : p.out) + ((tok0 + cs * kC) * H + h) * OW;
     auto out_bytes = [&](int jl) {
         if constexpr (!SPLIT) return rows_bytes(jl);
@@ -603,18 +619,21 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     };
     auto out_off = [&](int jl) { return static_cast<long long>(jl) * (kC * HO); };
 
-    v4f S[KPW];
+    v4f S[CT][KPW];
 #pragma unroll
-    for (int kt = 0; kt < KPW; ++kt) {
-        const int kb = (ks * KPW + kt) * 16 + 4 * g4;
+    for (int c = 0; c < CT; ++c)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = kb + i;
-            S[kt][i] = ident ? (key == kcol && key < dk ? 1.0f : 0.0f)
-                             : (s_in != nullptr && col_ok && key < dk) ? s_in[sbase + static_cast<size_t>(key) * dv + col]
-                                                                       : 0.0f;
+        for (int kt = 0; kt < KPW; ++kt) {
+            const int kb = (ks * KPW + kt) * 16 + 4 * g4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kb + i;
+                S[c][kt][i] = ident ? (key == kcol && key < dk ? 1.0f : 0.0f)
+                                    : (s_in != nullptr && col_ok[c] && key < dk)
+                                          ? s_in[sbase + static_cast<size_t>(key) * dv + col[c]]
+                                          : 0.0f;
+            }
         }
-    }
 
     if (nrun > 0) {   // workgroup-uniform
         // Loads are issued on every path (chunk indices clamped to the range):
@@ -625,7 +644,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // 16-byte loads for the key tiles, 4-byte loads for the rest: w, v
         // and the M T slice of this wave's rows only (W o V reaches the other
         // waves through the partial exchange), and the scalar vectors whose
-        // entries a row broadcast hands to the lanes.
+        // entries a row broadcast hands to the lanes.  The key tiles serve
+        // the workgroup's CT column tiles.
         auto load_ops = [&](int j, Ops &o) __attribute__((always_inline)) {
             const int sb = (cw0 + j) * (FB * 4);
 #pragma unroll
@@ -637,10 +657,12 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             const Rsrc rw = MakeRsrc(w_run + chunk_off(j), rows_bytes(j));
             const Rsrc rv = MakeRsrc(v_run + chunk_off(j), rows_bytes(j));
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                o.w[m] = BufF(rw, vl[m]);
-                o.v[m] = BufF(rv, vl[m]);
-            }
+            for (int c = 0; c < CT; ++c)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    o.w[c][m] = BufF(rw, vl[c][m]);
+                    o.v[c][m] = BufF(rv, vl[c][m]);
+                }
 #pragma unroll
             for (int x = 0; x < NSV; ++x) o.sc[x] = BufF(rblk, so + x * 256, sb + oSc * 4);
 #pragma unroll
@@ -662,16 +684,21 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the
         // 4 with ii % KS == ks); published with the next chunk's E' S0 partials
         // and summed by wave 0, so the output products are spread over the waves.
-        v4f op = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto store_out = [&](int jl, const v4f &out) __attribute__((always_inline)) {   // chunk jl of the run
+        // Partial c of wave z, kind x (0: E' S0, 1: output) sits at
+        // ((z 2 + x) CT + c) 256 of a parity's buffer.
+        v4f op[CT];
+#pragma unroll
+        for (int c = 0; c < CT; ++c) op[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        auto part = [&](float *xp, int z, int x, int c) { return xp + ((z * 2 + x) * CT + c) * 256 + lane * 4; };
+        auto store_out = [&](int c, int jl, const v4f &out) __attribute__((always_inline)) {   // chunk jl of the run
             const Rsrc ro = MakeRsrc(out_run + out_off(jl), out_bytes(jl));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) BufStF(ro, oo[i], out[i]);
+            for (int i = 0; i < 4; ++i) BufStF(ro, oo[c][i], out[i]);
         };
-        auto sum_out = [&](const float *xp) __attribute__((always_inline)) -> v4f {
-            v4f out = LdsF4(xp + 256 + lane * 4);
+        auto sum_out = [&](float *xp, int c) __attribute__((always_inline)) -> v4f {
+            v4f out = LdsF4(part(xp, 0, 1, c));
 #pragma unroll
-            for (int z = 1; z < KS; ++z) out += LdsF4(xp + (z * 2 + 1) * 256 + lane * 4);
+            for (int z = 1; z < KS; ++z) out += LdsF4(part(xp, z, 1, c));
             return out;
         };
         // Vector loads issued in a burst queue behind each other (the CU's
@@ -690,7 +717,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // 0.234 -> 0.244).  With 6 key tiles per wave the interleave measured
         // 2% slower (4 x 2048 x 16 heads at 384 x 128) and is left out.
         constexpr bool kHeadLoads = KPW == 4 || (KPW == 3 && KS == 8);
-        constexpr int kLoads = 3 * KPW + NSV + 3 * NM;   // vector loads of one chunk
+        constexpr int kLoads = 3 * KPW + NSV + NM + 2 * CT * NM;   // vector loads of one chunk
         auto interleave = [&]() __attribute__((always_inline)) {
             if constexpr (KPW == 6) return;
 #pragma unroll
@@ -700,59 +727,92 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
             }
         };
         auto step = [&](int j, Ops &o, Ops &nx) __attribute__((always_inline)) {
-            v4f xe = {0.0f, 0.0f, 0.0f, 0.0f}, xr = xe;
+            v4f xe[CT], xr[CT];
+#pragma unroll
+            for (int c = 0; c < CT; ++c) xe[c] = xr[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
-                    xe = Mfma(o.e[kt][ii], S[kt][ii], xe);
-                    xr = Mfma(o.r[kt][ii], S[kt][ii], xr);
+#pragma unroll
+                    for (int c = 0; c < CT; ++c) {
+                        xe[c] = Mfma(o.e[kt][ii], S[c][kt][ii], xe[c]);
+                        xr[c] = Mfma(o.r[kt][ii], S[c][kt][ii], xr[c]);
+                    }
                 }
             }
             if constexpr (kHeadLoads) load_ops(min(j + 1, nrun - 1), nx);
-            v4f wv;   // W o V of this lane's rows; w, v are zero past the sequence end and dv
+            v4f wv[CT];   // W o V of this lane's rows; w, v are zero past the sequence end and dv
             if constexpr (KS > 1) {
                 float *const xp = sXp + (j & 1) * L::kPart;
-                StF4(xp + (ks * 2 + 0) * 256 + lane * 4, xe);
-                StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);   // output partial of chunk j - 1
 #pragma unroll
-                for (int m = 0; m < NM; ++m) {   // this wave's rows of W o V (rows >= 4: a spare slot)
+                for (int c = 0; c < CT; ++c) {
+                    StF4(part(xp, ks, 0, c), xe[c]);
+                    StF4(part(xp, ks, 1, c), op[c]);   // output partial of chunk j - 1
+                }
+                float *const xw = xp + KS * 2 * CT * 256;   // W o V [CT][256], then the spare row slot
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {   // this wave's rows of W o V (rows >= 4: the spare slot)
                     const int i = ks + m * KS;
-                    xp[KS * 512 + (i < 4 ? lane * 4 + i : 256 + lane)] = o.w[m] * o.v[m];
+#pragma unroll
+                    for (int c = 0; c < CT; ++c) xw[i < 4 ? c * 256 + lane * 4 + i : CT * 256 + lane] = o.w[c][m] * o.v[c][m];
                 }
                 interleave();
                 __syncthreads();
                 // the same summation order in every wave: identical Y everywhere
-                xe = LdsF4(xp + lane * 4);
 #pragma unroll
-                for (int z = 1; z < KS; ++z) xe += LdsF4(xp + (z * 2) * 256 + lane * 4);
-                wv = LdsF4(xp + KS * 512 + lane * 4);
-                if (ks == 0 && j > 0) store_out(j - 1, sum_out(xp));
+                for (int c = 0; c < CT; ++c) {
+                    xe[c] = LdsF4(part(xp, 0, 0, c));
+#pragma unroll
+                    for (int z = 1; z < KS; ++z) xe[c] += LdsF4(part(xp, z, 0, c));
+                    wv[c] = LdsF4(xw + c * 256 + lane * 4);
+                }
+                if (ks == 0 && j > 0) {
+#pragma unroll
+                    for (int c = 0; c < CT; ++c) store_out(c, j - 1, sum_out(xp, c));
+                }
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) wv[i] = o.w[i] * o.v[i];   // NM = 4: row m is row i
+                for (int c = 0; c < CT; ++c)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) wv[c][i] = o.w[c][i] * o.v[c][i];   // NM = 4: row m is row i
             }
-            const v4f y = wv - KMulRows(o.sc) * xe;   // rows of E' S0 times k_mul
+            v4f y[CT];
+            const v4f km = KMulRows(o.sc);
+#pragma unroll
+            for (int c = 0; c < CT; ++c) y[c] = wv[c] - km * xe[c];   // rows of E' S0 times k_mul
             // S = G_15 o S + Ut~^T Y (Ut~ carries T and k_mul: U is never formed)
-            DecayState(S, o.sc, std::make_integer_sequence<int, KPW>{});
+#pragma unroll
+            for (int c = 0; c < CT; ++c) DecayState(S[c], o.sc, std::make_integer_sequence<int, KPW>{});
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) S[kt] = Mfma(o.ut[kt][ii], y[ii], S[kt]);
+                for (int ii = 0; ii < 4; ++ii) {
+#pragma unroll
+                    for (int c = 0; c < CT; ++c) S[c][kt] = Mfma(o.ut[kt][ii], y[c][ii], S[c][kt]);
+                }
             }
             // Off the chunk's chain (U, then the update): this wave's K slices
             // of (M T) Y, chosen by selects rather than branches (a branch per
             // slice split the region and delayed U behind them).
-            op = QMulRows(o.sc) * xr;   // rows of R' S0 times q_mul
+            const v4f qm = QMulRows(o.sc);
+#pragma unroll
+            for (int c = 0; c < CT; ++c) op[c] = qm * xr[c];   // rows of R' S0 times q_mul
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
                 const int sel = ks + m * KS;   // wave-uniform; >= 4 for the waves without a slice
-                float ya = 0.0f;
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii) ya = sel == ii ? y[ii] : ya;
-                if (m * KS < 4) op = Mfma(sel < 4 ? o.mt[m] : 0.0f, ya, op);
+                for (int c = 0; c < CT; ++c) {
+                    float ya = 0.0f;
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) ya = sel == ii ? y[c][ii] : ya;
+                    if (m * KS < 4) op[c] = Mfma(sel < 4 ? o.mt[m] : 0.0f, ya, op[c]);
+                }
             }
-            if constexpr (KS == 1) store_out(j, op);
+            if constexpr (KS == 1) {
+#pragma unroll
+                for (int c = 0; c < CT; ++c) store_out(c, j, op[c]);
+            }
             if constexpr (!kHeadLoads) load_ops(min(j + 2, nrun - 1), o);
         };
 
@@ -776,19 +836,28 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         }
         if constexpr (KS > 1) {   // output of the last chunk
             float *const xp = sXp + (nrun & 1) * L::kPart;
-            StF4(xp + (ks * 2 + 1) * 256 + lane * 4, op);
+#pragma unroll
+            for (int c = 0; c < CT; ++c) StF4(part(xp, ks, 1, c), op[c]);
             __syncthreads();
-            if (ks == 0) store_out(nrun - 1, sum_out(xp));
+            if (ks == 0) {
+#pragma unroll
+                for (int c = 0; c < CT; ++c) store_out(c, nrun - 1, sum_out(xp, c));
+            }
             __syncthreads();   // the partial buffers are reused by the workgroup's next run
         }
     }
-    if (s_out != nullptr && ocol_ok) {
+    if (s_out != nullptr) {
 #pragma unroll
-        for (int kt = 0; kt < KPW; ++kt) {
-            const int kb = (ks * KPW + kt) * 16 + 4 * g4;
+        for (int c = 0; c < CT; ++c) {
+            const int oc = SPLIT ? ocol : col[c];
+            if (!(SPLIT ? ocol_ok : col_ok[c])) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (kb + i < dk) s_out[sbase + static_cast<size_t>(kb + i) * OW + ocol] = S[kt][i];
+            for (int kt = 0; kt < KPW; ++kt) {
+                const int kb = (ks * KPW + kt) * 16 + 4 * g4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (kb + i < dk) s_out[sbase + static_cast<size_t>(kb + i) * OW + oc] = S[c][kt][i];
+            }
         }
     }
 }
@@ -803,24 +872,24 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 // (p.state); one that ends it writes final_state (if requested), any other
 // the carry, in place: a workgroup reads and writes only its own rows and
 // columns.
-template <int KPW, int KS, bool PACKED>
+template <int KPW, int KS, int CT, bool PACKED>
 __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Params p, int c0, int wn,
                                                                 const float *s_in, float *s_out) {
-    using L = RecurLayout<KPW, KS>;
+    using L = RecurLayout<KPW, KS, CT>;
     __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
     const int H = p.nheads;
-    const int VT = (p.dv + 15) / 16;
-    const int row = XcdLocalBlock(blockIdx.x, gridDim.x) / VT;
+    const int VW = ((p.dv + 15) / 16 + CT - 1) / CT;   // workgroups per (b, h)
+    const int row = XcdLocalBlock(blockIdx.x, gridDim.x) / VW;
     const size_t kv = static_cast<size_t>(p.dk) * p.dv;
     if constexpr (!PACKED) {
         const int b = row / H, h = row % H;
-        Gdn2RecurRun<KPW, KS>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, c0, 0, wn, wn,
-                              p.prepared + static_cast<size_t>(row) * wn * L::FB, static_cast<size_t>(row) * kv,
-                              s_in, s_out);
+        Gdn2RecurRun<KPW, KS, CT>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, c0, 0, wn, wn,
+                                  p.prepared + static_cast<size_t>(row) * wn * L::FB, static_cast<size_t>(row) * kv,
+                                  s_in, s_out);
         return;
     } else {
     const int n = p.batch;
-    const int slots = static_cast<int>(gridDim.x) / (H * VT);
+    const int slots = static_cast<int>(gridDim.x) / (H * VW);
     const int slot = row / H, h = row % H;
     const float *const prep_row = p.prepared + static_cast<size_t>(h) * wn * L::FB;
     for (int b = slot; b < n; b += slots) {   // workgroup-uniform
@@ -833,7 +902,7 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
         const size_t sbase = (static_cast<size_t>(b) * H + h) * kv;
         const float *in = c0 == 0 ? p.initial_state : p.state;
         float *out = c0 + nrun == nch ? p.final_state : p.state;
-        Gdn2RecurRun<KPW, KS>(p, sXp, h, tok0, T, c0, i0, nrun, wn, prep_row, sbase, in, out);
+        Gdn2RecurRun<KPW, KS, CT>(p, sXp, h, tok0, T, c0, i0, nrun, wn, prep_row, sbase, in, out);
     }
     }
 }
@@ -863,7 +932,7 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkRecurKernel(GatedDeltaNet2Pa
 template <int KPW, int KS>
 __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Params p, int sc, int nchunks,
                                                                 float *psi, float *phi, float *s0) {
-    using L = RecurLayout<KPW, KS>;
+    using L = RecurLayout<KPW, KS, 1>;
     __shared__ __attribute__((aligned(16))) float sXp[L::kFloats];
     const int H = p.nheads, VT = (p.dv + 15) / 16, KT = (p.dk + 15) / 16, tiles = VT + KT;
     const int rows = p.batch * H;
@@ -880,7 +949,7 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
     const size_t kv = static_cast<size_t>(p.dk) * p.dv, kp = static_cast<size_t>(p.dk) * KT * 16;
     const float *s_in = seg == 0 && p.initial_state != nullptr ? p.initial_state + row * kv : nullptr;
     float *s_out = ident ? phi + (static_cast<size_t>(seg) * rows + row) * kp : s0 + (static_cast<size_t>(seg) * rows + row) * kv;
-    Gdn2RecurRun<KPW, KS, true>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, cs, cs, nrun, nchunks,
+    Gdn2RecurRun<KPW, KS, 1, true>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, cs, cs, nrun, nchunks,
                                 p.prepared + static_cast<size_t>(row) * nchunks * L::FB, 0, s_in, s_out,
                                 SplitTile{tile, ident, psi});
 }
@@ -1058,6 +1127,7 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
 
 struct ChunkConfig {
     int kpw, ks;
+    int ct = 1;   // value-column tiles per recurrence workgroup
 };
 
 // Up to 128 keys: two key tiles (32 keys) per wave, ks = ceil(tiles / 2)
@@ -1078,7 +1148,7 @@ struct ChunkConfig {
 // 16 heads of 384 x 128).  The gdn2_kpw4 override keeps 4 tiles and
 // ceil(tiles / 4) waves above 128 keys.  `groups`: the launch's column-tile
 // workgroups.
-ChunkConfig ChooseChunk(int dk, long long groups) {
+ChunkConfig ChooseKeyTiling(int dk, long long groups) {
     const int kq = (dk + 15) / 16;
     if (kq > 8) {
         if (GetOverride(kOverrideGdn2Kpw4) == 1) return ChunkConfig{4, (kq + 3) / 4};
@@ -1093,6 +1163,24 @@ ChunkConfig ChooseChunk(int dk, long long groups) {
     return c;
 }
 
+// Recurrence kernels with two column tiles per workgroup are built for these
+// key tilings.
+bool HasTwoTileKernel(const ChunkConfig &c) {
+    return (c.kpw == 2 && c.ks >= 2 && c.ks <= 4) || (c.kpw == 3 && c.ks == 4) || (c.kpw == 4 && c.ks == 4);
+}
+
+// Two column tiles per workgroup share each key tile's loads and partial
+// exchange over twice the MFMA work; taken where the launch still has one
+// workgroup per CU (512+ one-tile workgroups).  With fewer, halving the
+// workgroups idles CUs (16k tokens x 8 heads at 256 x 256: 1.34 -> 2.23 ms;
+// 4 x 4096 x 16 heads at 64 x 64: 0.31 -> 0.41).
+ChunkConfig ChooseChunk(int dk, long long groups) {
+    ChunkConfig c = ChooseKeyTiling(dk, groups);
+    const int64_t ov = GetOverride(kOverrideGdn2Ct);
+    if (HasTwoTileKernel(c) && (ov == 2 || (ov == 0 && groups >= 512))) c.ct = 2;
+    return c;
+}
+
 // The preparation kernel, with its Ut' tiles' dynamic LDS (up to 128 KiB at
 // 32 key tiles, beside 20 KiB of static LDS).
 void LaunchPrep(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int wn, unsigned blocks,
@@ -1104,11 +1192,11 @@ void LaunchPrep(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int
     hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn, c.kpw, c.ks);
 }
 
-template <int KPW, int KS>
+template <int KPW, int KS, int CT>
 void LaunchRecur(const GatedDeltaNet2Params &p, int c0, int wn, int kq, const float *s_in, float *s_out,
                  hipStream_t stream) {
-    if (kq != RecurLayout<KPW, KS>::KQ) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
-    const int vt = (p.dv + 15) / 16;
+    if (kq != RecurLayout<KPW, KS, CT>::KQ) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
+    const int vt = ((p.dv + 15) / 16 + CT - 1) / CT;   // workgroups per (b, h)
     // packed: min(sequences, chunks) slots per (h, column tile); a slot's
     // workgroup takes every slots-th sequence that meets the window
     const long long rows = p.chunk_off != nullptr ? std::min(p.batch, wn) : p.batch;
@@ -1116,23 +1204,25 @@ void LaunchRecur(const GatedDeltaNet2Params &p, int c0, int wn, int kq, const fl
     if (blocks == 0) return;   // no packed sequences
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     if (p.chunk_off != nullptr) {
-        XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS, 1);
-        hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, true>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0,
-                           stream, p, c0, wn, s_in, s_out);
+        XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS, CT, 1);
+        hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, CT, true>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(64 * KS), 0, stream, p, c0, wn, s_in, s_out);
     } else {
-        XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS, 0);
-        hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, false>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0,
-                           stream, p, c0, wn, s_in, s_out);
+        XM_NOTE_LAUNCH("Gdn2ChunkRecurKernel", {}, KPW, KS, CT, 0);
+        hipLaunchKernelGGL((Gdn2ChunkRecurKernel<KPW, KS, CT, false>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(64 * KS), 0, stream, p, c0, wn, s_in, s_out);
     }
 }
 
 void LaunchRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int c0, int wn, int kq, const float *s_in,
                     float *s_out, hipStream_t stream) {
-#define XM_GDN2_RECUR(KPW_, KS_) \
-    if (c.kpw == KPW_ && c.ks == KS_) return LaunchRecur<KPW_, KS_>(p, c0, wn, kq, s_in, s_out, stream);
-    XM_GDN2_RECUR(1, 1) XM_GDN2_RECUR(2, 1) XM_GDN2_RECUR(2, 2) XM_GDN2_RECUR(2, 3) XM_GDN2_RECUR(2, 4)
-    XM_GDN2_RECUR(3, 4) XM_GDN2_RECUR(3, 8) XM_GDN2_RECUR(4, 3) XM_GDN2_RECUR(4, 4) XM_GDN2_RECUR(4, 5)
-    XM_GDN2_RECUR(4, 6) XM_GDN2_RECUR(4, 7) XM_GDN2_RECUR(4, 8) XM_GDN2_RECUR(5, 4) XM_GDN2_RECUR(6, 4)
+#define XM_GDN2_RECUR(KPW_, KS_, CT_)                 \
+    if (c.kpw == KPW_ && c.ks == KS_ && c.ct == CT_) \
+        return LaunchRecur<KPW_, KS_, CT_>(p, c0, wn, kq, s_in, s_out, stream);
+    XM_GDN2_RECUR(1, 1, 1) XM_GDN2_RECUR(2, 1, 1) XM_GDN2_RECUR(2, 2, 1) XM_GDN2_RECUR(2, 3, 1) XM_GDN2_RECUR(2, 4, 1)
+    XM_GDN2_RECUR(3, 4, 1) XM_GDN2_RECUR(3, 8, 1) XM_GDN2_RECUR(4, 3, 1) XM_GDN2_RECUR(4, 4, 1) XM_GDN2_RECUR(4, 5, 1)
+    XM_GDN2_RECUR(4, 6, 1) XM_GDN2_RECUR(4, 7, 1) XM_GDN2_RECUR(4, 8, 1) XM_GDN2_RECUR(5, 4, 1) XM_GDN2_RECUR(6, 4, 1)
+    XM_GDN2_RECUR(2, 2, 2) XM_GDN2_RECUR(2, 3, 2) XM_GDN2_RECUR(2, 4, 2) XM_GDN2_RECUR(3, 4, 2) XM_GDN2_RECUR(4, 4, 2)
 #undef XM_GDN2_RECUR
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
 }

@@ -156,6 +156,7 @@ constexpr OverrideSpec kOverrides[kOverrideCount] = {
     {"gdn2_kpw4", {1, 0}},               // 1: GDN-2 chunked, 4 key tiles per wave above 128 keys
     {"gdn2_windowed", {1, 0}},           // 1: GDN-2 chunked, windows of 128 chunks only
     {"gdn2_split", {1, 2, 0}},           // GDN-2 chunked: 1 no sequence split, 2 split wherever 2+ chunks
+    {"gdn2_ct", {1, 2, 0}},              // GDN-2 chunked: 1 or 2 value-column tiles per recurrence workgroup
 };
 std::atomic<int64_t> g_override[kOverrideCount];
 

@@ -97,7 +97,7 @@ EXPORTED_SYMBOLS = [
 # Kernel-selection overrides (xm_set_kernel_override) and the values each accepts besides 0.
 KERNEL_OVERRIDES = {"gdn2_path": (1,), "gdn2_pairwise": (1,), "gdn2_rows": (1, 2, 4), "m3_path": (1,),
                     "ss_lpc": (1, 2, 4, 8, 16), "ss_split": (1, 2), "gdn2_kpw4": (1,),
-                    "gdn2_windowed": (1,), "gdn2_split": (1, 2)}
+                    "gdn2_windowed": (1,), "gdn2_split": (1, 2), "gdn2_ct": (1, 2)}
 
 
 def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
