@@ -77,9 +77,13 @@ struct M3CLayout {
     static constexpr int TG = 64 / PL;           // token groups (4 rows, or 8 half rows)
     static constexpr int TPL = kC / TG;          // tokens per lane
     static constexpr int VPT = kRows * kC / (64 * NPW);   // V values per preparation thread
-    // Row stride of the [token][key] q^ tile: 4 floats of padding put the 16
-    // rows a 16-lane ds_read_b128 phase touches on distinct banks.
-    static constexpr int QS = NP + 4;
+    // Row stride of the [token][key] q^ tile, 8 floats of padding (NP + 8 is 8
+    // modulo 16): row-strided 16-byte accesses on gfx950 run without bank
+    // conflicts when the row pitch in floats is 8 times an odd number
+    // (measured: pitch 132 doubles both the preparation's paired 8-byte
+    // writes, 15.8 against 7.9 LDS cycles per instruction, and the products'
+    // 16-byte reads, 7.9 against 4.0).
+    static constexpr int QS = NP + 8;
     // one chunk buffer (floats)
     static constexpr int oQ = 0;                      // q^   [kC][QS]
     static constexpr int oKT = oQ + kC * QS;          // k^T  [NP][kTS]
