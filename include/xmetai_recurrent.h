@@ -271,7 +271,9 @@ int xm_softmax_cpu(const float *in, const int64_t *shape, int32_t rank, int64_t 
  *   "gdn2_split"     1: chunked GDN-2 never split along the sequence; 2: split
  *                    into up to four segments wherever the sequence has 2+ chunks
  *   "gdn2_ct"        1, 2: value-column tiles (of 16 columns) per chunked GDN-2
- *                    recurrence workgroup, 2 where such a kernel is built
+ *                    recurrence workgroup, 2 where such a kernel is built (by
+ *                    default 2 where one tile per workgroup would launch more
+ *                    workgroups than the device has CUs)
  * The values are read with one atomic load per launch; a change affects calls
  * made after it.  No counterpart in the reference (its variants are fixed at
  * compile time).  xm_set_kernel_override returns XM_ERR_INVALID_ARGUMENT for

@@ -329,6 +329,20 @@ def test_gdn2_two_column_tiles_window_carry(shape, override):
     check(f"gated_deltanet2/ct2_windows_{b}_{t}_{h}_{k}_{v}", got, run_ref(inp, s), TOL_GDN2)
 
 
+@pytest.mark.parametrize("shape, two", [((4, 40, 16, 128, 65), True),    # 320 one-tile workgroups
+                                         ((4, 40, 12, 128, 128), True),   # 384
+                                         ((2, 40, 16, 128, 128), False),  # 256: one per CU already
+                                         ((4, 40, 16, 64, 64), False)])   # 256
+def test_gdn2_two_column_tiles_by_default_above_one_workgroup_per_cu(shape, two):
+    """Without the override the recurrence takes two column tiles exactly where
+    one tile per workgroup would launch more workgroups than the 256 CUs."""
+    s = S(*shape)
+    inp = W.gated_deltanet2_inputs(s, seed=13)
+    got = run_gpu(inp, s)
+    assert _ran_two_tiles() == two, xp.last_launches()
+    check("gated_deltanet2/ct_default_" + "_".join(map(str, shape)), got, run_ref(inp, s), TOL_GDN2)
+
+
 def test_gdn2_two_column_tiles_equal_one_bitwise(override):
     """Columns are independent and both layouts sum in the same order: two
     tiles per workgroup give the one-tile results bit for bit (dv = 65: the

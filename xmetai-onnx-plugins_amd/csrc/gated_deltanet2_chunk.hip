@@ -44,6 +44,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -1169,15 +1170,34 @@ bool HasTwoTileKernel(const ChunkConfig &c) {
     return (c.kpw == 2 && c.ks >= 2 && c.ks <= 4) || (c.kpw == 3 && c.ks == 4) || (c.kpw == 4 && c.ks == 4);
 }
 
+// CUs of the current device (cached per device).
+int DeviceCus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 // Two column tiles per workgroup share each key tile's loads and partial
-// exchange over twice the MFMA work; taken where the launch still has one
-// workgroup per CU (512+ one-tile workgroups).  With fewer, halving the
-// workgroups idles CUs (16k tokens x 8 heads at 256 x 256: 1.34 -> 2.23 ms;
-// 4 x 4096 x 16 heads at 64 x 64: 0.31 -> 0.41).
+// exchange over twice the MFMA work.  Taken wherever one tile per workgroup
+// would put more workgroups than CUs: a CU stepping two workgroups at once
+// gains about 14% over one, so the doubled CUs set the kernel's time, and
+// half as many two-tile workgroups (one per CU) finish sooner even where some
+// CUs then idle (interleaved A/B, 4 x 4096 heads at 128 keys: 16 heads at
+// dv = 65 0.545 -> 0.520 ms, at dv = 96 0.554 -> 0.520, at dv = 80 0.542 ->
+// 0.534; 12 heads at dv = 128 0.490 -> 0.470).  At or below one workgroup per
+// CU halving them idles CUs (16k tokens x 8 heads at 256 x 256: 1.34 -> 2.23
+// ms; 4 x 4096 x 16 heads at 64 x 64: 0.33 -> 0.41; 2 x 4096 x 16 heads at
+// 128 x 128: 0.325 -> 0.414).
 ChunkConfig ChooseChunk(int dk, long long groups) {
     ChunkConfig c = ChooseKeyTiling(dk, groups);
     const int64_t ov = GetOverride(kOverrideGdn2Ct);
-    if (HasTwoTileKernel(c) && (ov == 2 || (ov == 0 && groups >= 512))) c.ct = 2;
+    if (HasTwoTileKernel(c) && (ov == 2 || (ov == 0 && groups > DeviceCus()))) c.ct = 2;
     return c;
 }
 
