@@ -219,6 +219,7 @@ SPLIT_CASES = {
     "t520_k512_v7": S(1, 520, 1, 512, 7),
     "t1025_k256_v256": S(1, 1025, 1, 256, 256),
     "t40_k128_v128_nol2": S(1, 40, 1, 128, 128, l2norm=False),   # the state grows ~60x a token
+    "t32_k96_v40_two_segments": S(2, 32, 2, 96, 40),   # two segments: no combine step
 }
 
 
@@ -231,6 +232,24 @@ def test_gdn2_sequence_split(name, override):
     assert any(k.startswith("Gdn2ChunkSplitKernel") for k in xp.last_launches()), xp.last_launches()
     ref32 = None if s.l2norm else run_ref(inp, s, np.float32)
     check(f"gated_deltanet2/split_{name}", got, run_ref(inp, s), TOL_GDN2, ref32=ref32)
+
+
+def test_gdn2_two_segment_split_without_combine():
+    """Wide keys over few value columns split into two segments by default;
+    with no final state requested segment 0's final state is segment 1's start
+    and no combine kernel runs.  With the final state the combine forms it."""
+    import torch
+    s = S(2, 1024, 4, 320, 64)
+    inp = W.gated_deltanet2_inputs(s, seed=6)
+    got = run_gpu(inp, s)
+    launched = xp.last_launches()
+    assert any(k.startswith("Gdn2ChunkSplitKernel") for k in launched), launched
+    assert not any(k.startswith("Gdn2SplitCombineKernel") for k in launched), launched
+    check("gated_deltanet2/split_two_segments", got, run_ref(inp, s), TOL_GDN2)
+    y, st = gated_deltanet2_fn(*(to_dev(inp[k]) for k in KEYS), scale=s.scale, output_final_state=True)
+    torch.cuda.synchronize()
+    assert any(k.startswith("Gdn2SplitCombineKernel") for k in xp.last_launches()), xp.last_launches()
+    np.testing.assert_array_equal(y.cpu().numpy(), got)
 
 
 def test_gdn2_sequence_split_selected_for_few_workgroups(override):

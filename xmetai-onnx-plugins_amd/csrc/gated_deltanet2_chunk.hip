@@ -958,7 +958,8 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
 // Workgroup ((b, h), value tile), 8 waves: S (keys x 16 columns, keys padded
 // to 16) in LDS, S_start(1) = S0_0; for s >= 1 it stores S_start(s) to sst and
 // forms S_start(s + 1) = Phi_s S_start(s) + S0_s on MFMA, wave w taking the
-// 16-key output tiles w, w + 8, ...; the last one is the final state.  Phi rows
+// 16-key output tiles w, w + 8, ...; the last one is the final state, formed
+// only when it is requested.  Phi rows
 // (pitch KP, 16-byte aligned) are read 16 bytes a lane.  A wave's first tile
 // has its first eight key tiles of Phi_{s+1} and its S0_{s+1} values loaded
 // during step s (the steps are serial: each would otherwise wait out its
@@ -1014,8 +1015,10 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
         return acc;
     };
     const bool first = w < KT;   // this wave's first tile, kt = w
+    // the products of step s form S_start(s + 1): the last one only for the final state
+    const int nprod = p.final_state != nullptr ? nseg : nseg - 1;
     v4f a0[8], a1[8], add0 = {0.0f, 0.0f, 0.0f, 0.0f}, add1 = add0;
-    if (first && nseg > 1) {
+    if (first && nprod > 1) {
         load_a(1, w, 0, a0);
         add0 = load_add(1, w);
     }
@@ -1026,8 +1029,9 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
             const int key = i / 16, c = vt * 16 + i % 16;
             if (key < dk && c < dv) start[static_cast<size_t>(key) * dv + c] = cur[(i % 16) * SP + key];
         }
+        if (s >= nprod) break;   // workgroup-uniform: no final state wanted
         if (first) {
-            if (s + 1 < nseg) {   // the next step's operands, in flight during this one
+            if (s + 1 < nprod) {   // the next step's operands, in flight during this one
                 load_a(s + 1, w, 0, a1);
                 add1 = load_add(s + 1, w);
             }
@@ -1072,8 +1076,11 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
 // 16 bytes of a KP-pitch row; B from LDS, stored column by column at pitch
 // KP + 4 for 16-byte reads), added to the output rows.  Dynamic LDS:
 // 16 (KP + 4) floats.
+// s1 (or null): segment 1's start state at the row's [K][V] of s1, in place
+// of sst (a split in two segments with no final state has no combine step:
+// segment 0's final state is segment 1's start).
 __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int nchunks,
-                                                              const float *psi, const float *sst) {
+                                                              const float *psi, const float *sst, const float *s1) {
     extern __shared__ float sts[];
     const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
     const int KP = KT * 16, rows = p.batch * H, ncg = (sc + 3) / 4;
@@ -1094,7 +1101,8 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
         a[u] = ta_ok && u < KT ? *reinterpret_cast<const v4f *>(prow + u * 16) : z;
     }
     const size_t kv = static_cast<size_t>(dk) * dv;
-    const float *const st = sst + (static_cast<size_t>(seg) * rows + row) * kv;
+    const float *const st = seg == 1 && s1 != nullptr ? s1 + static_cast<size_t>(row) * kv
+                                                      : sst + (static_cast<size_t>(seg) * rows + row) * kv;
     const int SP = KP + 4;
     for (int i = tid; i < KT * 256; i += 256) {
         const int key = i / 16, cc = vt * 16 + i % 16;
@@ -1357,15 +1365,20 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     const int lds = 2 * 16 * (KT * 16 + 4) * static_cast<int>(sizeof(float));   // two S buffers (combine)
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCombineKernel), lds);
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCorrectKernel), lds / 2);
-    XM_NOTE_LAUNCH("Gdn2SplitCombineKernel", {}, );
-    hipLaunchKernelGGL(Gdn2SplitCombineKernel, dim3(static_cast<unsigned>(rows * VT)), dim3(512), lds, stream, q,
-                       sp.nseg, phi, s0, sst);
-    XM_LAUNCH_CHECK("GatedDeltaNet2Fn split combine");
+    // two segments with no final state: segment 0's final state (in s0) is
+    // segment 1's start, and there is nothing to combine
+    const bool direct = sp.nseg == 2 && p.final_state == nullptr;
+    if (!direct) {
+        XM_NOTE_LAUNCH("Gdn2SplitCombineKernel", {}, );
+        hipLaunchKernelGGL(Gdn2SplitCombineKernel, dim3(static_cast<unsigned>(rows * VT)), dim3(512), lds, stream, q,
+                           sp.nseg, phi, s0, sst);
+        XM_LAUNCH_CHECK("GatedDeltaNet2Fn split combine");
+    }
     const long long cblocks = rows * VT * (sp.nseg - 1) * ((sp.sc + 3) / 4);
     if (cblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2SplitCorrectKernel", {}, );
     hipLaunchKernelGGL(Gdn2SplitCorrectKernel, dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q,
-                       sp.sc, sp.nchunks, psi, sst);
+                       sp.sc, sp.nchunks, psi, sst, direct ? s0 : nullptr);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split correction");
 }
 
