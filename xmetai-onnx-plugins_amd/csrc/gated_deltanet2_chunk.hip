@@ -955,6 +955,33 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
                                 SplitTile{tile, ident, psi});
 }
 
+// Stages column tile vt of a [dk][dv] state (row base src, workgroup-uniform)
+// in LDS column by column at pitch SP, keys padded to 16 KT with zeros: NT
+// threads, each with B loads in flight before their LDS writes (one load,
+// wait and write per element serialises the loads' latency: 20 of them at
+// 320 keys).  Byte offsets are 32-bit (a state row is under 2 GiB), so each
+// load takes one offset register beside the uniform base.
+template <int NT, int B>
+__device__ __forceinline__ void StageStateTile(float *dst, const float *src, int dk, int dv, int vt, int KT, int SP,
+                                               int tid) {
+    const int n = KT * 256, c = vt * 16 + tid % 16;
+    const char *const base = reinterpret_cast<const char *>(src);
+    for (int i0 = 0; i0 < n; i0 += B * NT) {
+        float v[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int i = i0 + u * NT + tid, key = i / 16;
+            const unsigned off = static_cast<unsigned>(key * dv + c) * 4u;
+            v[u] = i < n && key < dk && c < dv ? *reinterpret_cast<const float *>(base + off) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int i = i0 + u * NT + tid;
+            if (i < n) dst[(tid % 16) * SP + i / 16] = v[u];
+        }
+    }
+}
+
 // Workgroup ((b, h), value tile), 8 waves: S (keys x 16 columns, keys padded
 // to 16) in LDS, S_start(1) = S0_0; for s >= 1 it stores S_start(s) to sst and
 // forms S_start(s + 1) = Phi_s S_start(s) + S0_s on MFMA, wave w taking the
@@ -978,10 +1005,7 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
     const int col = vt * 16 + m16;
     const int SP = KP + 4;   // LDS pitch of one column of S
     float *cur = comb, *nxt = comb + 16 * SP;
-    for (int i = tid; i < KT * 256; i += 512) {
-        const int key = i / 16, c = vt * 16 + i % 16;
-        cur[(i % 16) * SP + key] = key < dk && c < dv ? s0[row * kv + static_cast<size_t>(key) * dv + c] : 0.0f;
-    }
+    StageStateTile<512, 8>(cur, s0 + row * kv, dk, dv, vt, KT, SP, tid);
     // A[m][k] = Phi_s[16 kt + m][k] (lane m + 16 k, 16 bytes per key tile);
     // S0_s at the D layout (key 16 kt + 4 (l / 16) + i, column l % 16)
     auto load_a = [&](int s, int kt, int k0, v4f (&a)[8]) __attribute__((always_inline)) {
@@ -1079,6 +1103,10 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
 // s1 (or null): segment 1's start state at the row's [K][V] of s1, in place
 // of sst (a split in two segments with no final state has no combine step:
 // segment 0's final state is segment 1's start).
+// SB: state loads in flight per thread while staging.  16 takes the kernel
+// from 50 to 112 VGPRs (4 waves per SIMD instead of 8): worth it only where
+// every workgroup is resident at once and each waits out its own staging.
+template <int SB>
 __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int nchunks,
                                                               const float *psi, const float *sst, const float *s1) {
     extern __shared__ float sts[];
@@ -1100,14 +1128,18 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
         const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
         a[u] = ta_ok && u < KT ? *reinterpret_cast<const v4f *>(prow + u * 16) : z;
     }
+    float *const orow = p.out + ((static_cast<size_t>(b) * T + c * kC + 4 * g4) * H + h) * dv + col;
+    float o[4];   // the output values the products add to, loaded with the first operands
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = c * kC + 4 * g4 + i;
+        o[i] = live && t < T && col < dv ? orow[static_cast<size_t>(i) * H * dv] : 0.0f;
+    }
     const size_t kv = static_cast<size_t>(dk) * dv;
     const float *const st = seg == 1 && s1 != nullptr ? s1 + static_cast<size_t>(row) * kv
                                                       : sst + (static_cast<size_t>(seg) * rows + row) * kv;
     const int SP = KP + 4;
-    for (int i = tid; i < KT * 256; i += 256) {
-        const int key = i / 16, cc = vt * 16 + i % 16;
-        sts[(i % 16) * SP + key] = key < dk && cc < dv ? st[static_cast<size_t>(key) * dv + cc] : 0.0f;
-    }
+    StageStateTile<256, SB>(sts, st, dk, dv, vt, KT, SP, tid);
     __syncthreads();
     if (!live) return;
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1130,7 +1162,7 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = c * kC + 4 * g4 + i;
-        if (t < T && col < dv) p.out[((static_cast<size_t>(b) * T + t) * H + h) * dv + col] += acc[i];
+        if (t < T && col < dv) orow[static_cast<size_t>(i) * H * dv] = o[i] + acc[i];
     }
 }
 
@@ -1364,7 +1396,8 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split recurrence");
     const int lds = 2 * 16 * (KT * 16 + 4) * static_cast<int>(sizeof(float));   // two S buffers (combine)
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCombineKernel), lds);
-    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCorrectKernel), lds / 2);
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCorrectKernel<1>), lds / 2);
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCorrectKernel<16>), lds / 2);
     // two segments with no final state: segment 0's final state (in s0) is
     // segment 1's start, and there is nothing to combine
     const bool direct = sp.nseg == 2 && p.final_state == nullptr;
@@ -1377,8 +1410,11 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     const long long cblocks = rows * VT * (sp.nseg - 1) * ((sp.sc + 3) / 4);
     if (cblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2SplitCorrectKernel", {}, );
-    hipLaunchKernelGGL(Gdn2SplitCorrectKernel, dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q,
-                       sp.sc, sp.nchunks, psi, sst, direct ? s0 : nullptr);
+    // at most four 4-wave workgroups per CU: all resident at once with 112 VGPRs
+    const bool overlap = cblocks <= 4LL * DeviceCus();
+    hipLaunchKernelGGL(overlap ? Gdn2SplitCorrectKernel<16> : Gdn2SplitCorrectKernel<1>,
+                       dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q, sp.sc, sp.nchunks, psi,
+                       sst, direct ? s0 : nullptr);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split correction");
 }
 
