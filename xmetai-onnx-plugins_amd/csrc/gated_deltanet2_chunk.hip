@@ -135,31 +135,54 @@ __device__ __forceinline__ void StgF4(float *p, v4f v) { *reinterpret_cast<v4f *
 
 // Raw inputs of one key tile of one chunk in operand layout (lane m + 16g:
 // token t0 + m, keys kt*16 + 4g + i), zero past the ends.
-__device__ __forceinline__ void LoadKeyTile(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kt,
-                                            int g4, float (&q)[4], float (&k)[4], float (&g)[4], float (&bt)[4]) {
+// One key tile's q, k, g and beta for this lane (keys 16 kt + 4 g4 + i, the
+// token of rowbase) as loaded: addresses clamped into the row, values not yet
+// masked, so the loads can be issued well before their use.  VEC4: the
+// caller knows that p.vec4_keys holds (no branch between the two forms, whose
+// different load counts would make the loop's wait counts conservative).
+struct KeyTileRaw {
+    v4f q, k, g, b;
+};
+template <bool VEC4 = false>
+__device__ __forceinline__ KeyTileRaw LoadKeyTileRaw(const GatedDeltaNet2Params &p, size_t rowbase, int kt, int g4) {
     const int k0 = kt * 16 + 4 * g4;
-    if (p.vec4_keys) {
+    KeyTileRaw r;
+    if (VEC4 || p.vec4_keys) {
         const size_t at = rowbase + min(k0, p.dk - 4);
-        const v4f q4 = LdgF4(p.q + at), k4 = LdgF4(p.k + at), g4v = LdgF4(p.g + at), b4 = LdgF4(p.beta + at);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool ok = live && k0 + i < p.dk;
-            q[i] = ok ? q4[i] : 0.0f;
-            k[i] = ok ? k4[i] : 0.0f;
-            g[i] = ok ? g4v[i] : 0.0f;
-            bt[i] = ok ? b4[i] : 0.0f;
-        }
+        r.q = LdgF4(p.q + at);
+        r.k = LdgF4(p.k + at);
+        r.g = LdgF4(p.g + at);
+        r.b = LdgF4(p.beta + at);
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const bool ok = live && k0 + i < p.dk;
             const size_t at = rowbase + min(k0 + i, p.dk - 1);
-            q[i] = ok ? p.q[at] : 0.0f;
-            k[i] = ok ? p.k[at] : 0.0f;
-            g[i] = ok ? p.g[at] : 0.0f;
-            bt[i] = ok ? p.beta[at] : 0.0f;
+            r.q[i] = p.q[at];
+            r.k[i] = p.k[at];
+            r.g[i] = p.g[at];
+            r.b[i] = p.beta[at];
         }
     }
+    return r;
+}
+
+// Zeros for padded keys and dead tokens.
+__device__ __forceinline__ void MaskKeyTile(const KeyTileRaw &r, bool live, int dk, int kt, int g4, float (&q)[4],
+                                            float (&k)[4], float (&g)[4], float (&bt)[4]) {
+    const int k0 = kt * 16 + 4 * g4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool ok = live && k0 + i < dk;
+        q[i] = ok ? r.q[i] : 0.0f;
+        k[i] = ok ? r.k[i] : 0.0f;
+        g[i] = ok ? r.g[i] : 0.0f;
+        bt[i] = ok ? r.b[i] : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void LoadKeyTile(const GatedDeltaNet2Params &p, size_t rowbase, bool live, int kt,
+                                            int g4, float (&q)[4], float (&k)[4], float (&g)[4], float (&bt)[4]) {
+    MaskKeyTile(LoadKeyTileRaw(p, rowbase, kt, g4), live, p.dk, kt, g4, q, k, g, bt);
 }
 
 // Token distance D of the pairwise A and M for one key element: lane t of
@@ -241,7 +264,11 @@ __device__ __forceinline__ void PackedRange(const GatedDeltaNet2Params &p, int b
 // Dynamic LDS: kPrepWaves * kq * 256 floats, each wave's transposed Ut' tiles
 // kept until T is known.  kpw, ks: the recurrence's key tiles per wave and
 // waves (kq = kpw ks key tiles), which order the scalar vectors.
+// AHEAD: each pair of key tiles' loads issued one pair early, before the
+// previous pair's work (32 more VGPRs; 16-byte key loads only, p.vec4_keys);
+// the arithmetic is the same.
 constexpr int kMaxKeyTiles = 32;         // key tiles of the chunked path (dk <= 512)
+template <bool AHEAD>
 __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kpw,
                                                                        int ks) {
     __shared__ __attribute__((aligned(16))) float sw[kPrepWaves][4][kTile];
@@ -338,16 +365,32 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     };
     // key tiles in pairs, both loaded before either is used: the two halves of
     // a 128-byte line of each token row are requested together
+    // (AHEAD: raw values carried over, masked at their use, so that no select
+    // waits for them early)
+    // and issued on every pass, past the last pair too (key addresses are
+    // clamped into the token's row), so the loop's wait counts are exact)
+    KeyTileRaw cur[2], nxt[2];
+    auto load_pair = [&](int kt, KeyTileRaw (&x)[2]) __attribute__((always_inline)) {
+        x[0] = LoadKeyTileRaw<AHEAD>(p, rowbase, kt, g4);
+        if (AHEAD || kt + 1 < kq) x[1] = LoadKeyTileRaw<AHEAD>(p, rowbase, kt + 1, g4);
+    };
+    if (AHEAD) load_pair(0, cur);
     for (int kt = 0; kt < kq; kt += 2) {
+        const bool pair = kt + 1 < kq;   // kq is 1 or even (AHEAD: even)
+        if (!AHEAD) load_pair(kt, cur);
+        else load_pair(kt + 2, nxt);
         float q0[4], k0[4], g0[4], b0[4], q1[4], k1[4], g1[4], b1[4];
-        const bool pair = kt + 1 < kq;   // kq is 1 or even
-        LoadKeyTile(p, rowbase, live, kt, g4, q0, k0, g0, b0);
-        if (pair) LoadKeyTile(p, rowbase, live, kt + 1, g4, q1, k1, g1, b1);
+        MaskKeyTile(cur[0], live, p.dk, kt, g4, q0, k0, g0, b0);
+        if (pair) MaskKeyTile(cur[1], live, p.dk, kt + 1, g4, q1, k1, g1, b1);
         al += alc[0] + alc[1];   // the previous pair (zeros at the first)
         mu += muc[0] + muc[1];
         alc[0] = alc[1] = muc[0] = muc[1] = z4;
         tile(kt, q0, k0, g0, b0);
         if (pair) tile(kt + 1, q1, k1, g1, b1);
+        if (AHEAD) {
+            cur[0] = nxt[0];
+            cur[1] = nxt[1];
+        }
     }
     al += alc[0] + alc[1];
     mu += muc[0] + muc[1];
@@ -1248,8 +1291,18 @@ void LaunchPrep(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int
     const int kq = c.kpw * c.ks;
     if (kq > kMaxKeyTiles) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
     const int dyn = kPrepWaves * kq * 256 * static_cast<int>(sizeof(float));
-    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel), dyn);
-    hipLaunchKernelGGL(Gdn2ChunkPrepKernel, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn, c.kpw, c.ks);
+    // Loads one pair ahead where the Ut' stash in LDS already limits the CU to
+    // at most three workgroups (kq > 4); at up to 64 keys the extra registers
+    // would take it from four to three.
+    if (kq > 4 && p.vec4_keys) {
+        EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel<true>), dyn);
+        hipLaunchKernelGGL(Gdn2ChunkPrepKernel<true>, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn,
+                           c.kpw, c.ks);
+    } else {
+        EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel<false>), dyn);
+        hipLaunchKernelGGL(Gdn2ChunkPrepKernel<false>, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn,
+                           c.kpw, c.ks);
+    }
 }
 
 template <int KPW, int KS, int CT>
