@@ -655,6 +655,17 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             oo[c][i] = SPLIT ? (ocol_ok ? ((4 * g4 + i) * HO + ocol) * 4 : kOutOfRange) : vo[c][i];
+    // this wave's output rows i = ks + m KS (kOutOfRange for i >= 4: the
+    // store is dropped)
+    int ol[CT][NM];
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const int i = ks + m * KS;
+            const bool ok = i < 4 && (SPLIT ? ocol_ok : col_ok[c]);
+            ol[c][m] = ok ? ((4 * g4 + i) * HO + (SPLIT ? ocol : col[c])) * 4 : kOutOfRange;
+        }
     float *const out_run = (ident ? st.psi : p.out) + ((tok0 + cs * kC) * H + h) * OW;
     auto out_bytes = [&](int jl) {
         if constexpr (!SPLIT) return rows_bytes(jl);
@@ -727,7 +738,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         // The output of a chunk, O = q_mul o R' S0 + (M T) Y, as this wave's
         // partial: its keys of R' S0 and its K slices of (M T) Y (the ii of the
         // 4 with ii % KS == ks); published with the next chunk's E' S0 partials
-        // and summed by wave 0, so the output products are spread over the waves.
+        // and summed row by row across the waves, so the output products and
+        // their reduction are spread over the waves.
         // Partial c of wave z, kind x (0: E' S0, 1: output) sits at
         // ((z 2 + x) CT + c) 256 of a parity's buffer.
         v4f op[CT];
@@ -739,11 +751,35 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
             for (int i = 0; i < 4; ++i) BufStF(ro, oo[c][i], out[i]);
         };
-        auto sum_out = [&](float *xp, int c) __attribute__((always_inline)) -> v4f {
+        // The output of chunk jl from the waves' partials, added in wave order.
+        // kSpreadOut: wave ks sums and stores token rows i = ks + m KS, so that
+        // no wave carries the whole reduction between two barriers; else wave
+        // 0 sums and stores every row.  Interleaved A/B, spread against wave 0:
+        // sequence-split runs 2 x 2048 x 4 heads at 320 x 64 0.1415 -> 0.1391 ms,
+        // 1 x 8192 x 4 heads 0.1563 -> 0.1517; two waves per tile 4 x 4096 x 16
+        // heads at 64 x 64 0.3092 -> 0.3015; but four waves per tile (unsplit)
+        // 4 x 4096 x 16 heads at 128 x 128 0.5113 -> 0.5208, 16k x 8 heads at
+        // 256 x 256 1.2884 -> 1.3057, 8 x 2048 x 16 heads 0.4529 -> 0.4663.
+        constexpr bool kSpreadOut = SPLIT || KS <= 3;
+        auto sum_out = [&](float *xp, int c) __attribute__((always_inline)) -> v4f {   // wave 0's form
             v4f out = LdsF4(part(xp, 0, 1, c));
 #pragma unroll
             for (int z = 1; z < KS; ++z) out += LdsF4(part(xp, z, 1, c));
             return out;
+        };
+        auto sum_store_out = [&](float *xp, int jl) __attribute__((always_inline)) {   // the spread form
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
+                const Rsrc ro = MakeRsrc(out_run + out_off(jl), out_bytes(jl));
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    const int i = min(ks + m * KS, 3);   // rows >= 4: read row 3, store dropped
+                    float out = part(xp, 0, 1, c)[i];
+#pragma unroll
+                    for (int z = 1; z < KS; ++z) out += part(xp, z, 1, c)[i];
+                    BufStF(ro, ol[c][m], out);
+                }
+            }
         };
         // Vector loads issued in a burst queue behind each other (the CU's
         // waves issue them together); placed one after each MFMA of the
@@ -811,7 +847,9 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
                     for (int z = 1; z < KS; ++z) xe[c] += LdsF4(part(xp, z, 0, c));
                     wv[c] = LdsF4(xw + c * 256 + lane * 4);
                 }
-                if (ks == 0 && j > 0) {
+                if constexpr (kSpreadOut) {
+                    if (j > 0) sum_store_out(xp, j - 1);
+                } else if (ks == 0 && j > 0) {
 #pragma unroll
                     for (int c = 0; c < CT; ++c) store_out(c, j - 1, sum_out(xp, c));
                 }
@@ -883,7 +921,9 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
             for (int c = 0; c < CT; ++c) StF4(part(xp, ks, 1, c), op[c]);
             __syncthreads();
-            if (ks == 0) {
+            if constexpr (kSpreadOut) {
+                sum_store_out(xp, nrun - 1);
+            } else if (ks == 0) {
 #pragma unroll
                 for (int c = 0; c < CT; ++c) store_out(c, nrun - 1, sum_out(xp, c));
             }
