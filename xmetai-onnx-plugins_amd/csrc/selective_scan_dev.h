@@ -111,6 +111,9 @@ __device__ __forceinline__ F4 LoadRow4Guarded(const IT *row, int t, int L, bool 
 // descriptor, a per-lane offset and a wave-uniform one), converted to fp32 /
 // from fp32 (nearest even).  The offsets are in range by construction.
 typedef __amdgpu_buffer_rsrc_t SsRsrc;
+// A per-lane offset beyond any descriptor size used here: a store there is
+// dropped (the bounds check of a raw buffer).
+constexpr int kSsDropOffset = static_cast<int>(0x80000000u);
 typedef unsigned SsU2 __attribute__((ext_vector_type(2)));
 typedef unsigned SsU4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ SsRsrc SsRowsRsrc(const void *base, int bytes) {
