@@ -494,14 +494,33 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // MFMA work covers the latency.
     const Rsrc rz = MakeRsrc(p.Z != nullptr ? p.Z + vbase : p.out, p.Z != nullptr ? seq_bytes(v_stride) : 0);
     const Rsrc ro = MakeRsrc(p.out + vbase, seq_bytes(v_stride));
+    const Rsrc rnone = MakeRsrc(p.out, 0);   // every access dropped
+    // Issued whether or not there is a Z (then every load reads zero): paths
+    // with and without the loads would leave the compiler's wait counts at
+    // the smaller one.
     auto load_z = [&](int c0, float (&zr)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            if constexpr (LONG) zr[r] = BufF(chunk_rsrc(p.Z + vbase, v_stride, c0), ooff[r]);
+            if constexpr (LONG) zr[r] = BufF(p.Z != nullptr ? chunk_rsrc(p.Z + vbase, v_stride, c0) : rnone, ooff[r]);
             else zr[r] = BufF(rz, off(ooff[r], c0 * vs4));
         }
     };
-    auto finish = [&](int c0, const float *bf, const float *pp, const float (&zr)[4]) __attribute__((always_inline)) {
+    // y of chunk c0 (tokens past the end and rows >= P are dropped), or with
+    // ok false nothing: every wave issues the same four stores in every
+    // iteration, so the wait counts do not fall to those of a path without
+    // them.  The values stay in their four registers until every store is
+    // issued: a store's data register rewritten behind it waits for the store
+    // to complete (stores count in vmcnt on gfx950).
+    auto store_y = [&](int c0, const float (&y)[4], bool ok) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (LONG) BufStF(ok ? chunk_rsrc(p.out + vbase, v_stride, c0) : rnone, ooff[r], y[r]);
+            else BufStF(ro, ok ? off(ooff[r], c0 * vs4) : kOutOfRange, y[r]);
+        }
+        asm volatile("" ::"v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
+    };
+    auto finish = [&](const float *bf, const float *pp, const float (&zr)[4], float (&y)[4])
+                      __attribute__((always_inline)) {
         const int pt = w;
         v4f g = LdsF4(pp + lane * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
         v4f qk4 = LdsF4(bf + L::oQK + 4 * g4);
@@ -531,22 +550,11 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         for (int r = 0; r < 4; ++r) acc[r] = fmaf(ecum4[r], ys[r], fmaf(qk4[r], gam4[r], dval) * vt[r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) acc = Mfma(m[ks], vt[ks], acc);   // + sum_{s<t} M[t][s] v_s
-        float y[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             y[r] = acc[r];
             if (p.Z != nullptr) y[r] *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            // tokens past the end and rows >= P are dropped
-            if constexpr (LONG) BufStF(chunk_rsrc(p.out + vbase, v_stride, c0), ooff[r], y[r]);
-            else BufStF(ro, off(ooff[r], c0 * vs4), y[r]);
-        }
-        // the four values stay in four registers until every store is issued:
-        // a store's data register rewritten behind it waits for the store to
-        // complete (stores count in vmcnt on gfx950)
-        asm volatile("" ::"v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
     };
 
     const int nch = (T + kC - 1) / kC;
@@ -559,26 +567,44 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // chunk j+2, preparation of chunk j+1.  The last chunk is peeled.
     if (nch > 0 && product_wave) {   // workgroup-uniform: an empty sequence passes its states through
         __syncthreads();
-        // zr is written only by the Z loads: a write in every iteration (its
-        // zeroing) landed on the registers the previous chunk's output stores
-        // read, and waited for those stores to complete (stores count in
-        // vmcnt on gfx950)
-        float zr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int j = 0; j + 1 < nch; ++j) {
-            const int jf = max(j - 1, 0);   // the chunk to finish (from j = 1 on)
-            if (p.Z != nullptr) load_z(jf * kC, zr);
+        // Z of chunk j is loaded in iteration j (before its products) into
+        // the register set of j's parity and gated in iteration j + 1, where
+        // chunk j is finished.  Loaded in the finishing iteration itself, it
+        // came after the previous chunk's output stores, and the wait for it
+        // (stores count in vmcnt on gfx950) waited for those stores to
+        // complete.  The sets are written only by the Z loads: a zeroing in
+        // every iteration landed on registers the previous stores read.
+        float za[4] = {0.0f, 0.0f, 0.0f, 0.0f}, zb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // zl: the set for chunk j's Z; zu: chunk j - 1's, finished here
+        auto step = [&](int j, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
+            load_z(j * kC, zl);
             products(buf(j), par(j));
-            if (j > 0 && w < 2) finish(jf * kC, buf(jf), par(jf), zr);
+            const bool fin = j > 0 && w < 2;
+            float y[4] = {zu[0], zu[1], zu[2], zu[3]};   // stored only where fin
+            if (fin) finish(buf(j - 1), par(j - 1), zu, y);
+            store_y((j - 1) * kC, y, fin);
+        };
+        auto iter = [&](int j, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
+            step(j, zl, zu);
             __syncthreads();
+        };
+        for (int j = 0; j + 1 < nch; j += 2) {   // unrolled by two for the sets
+            iter(j, za, zb);
+            if (j + 2 >= nch) break;
+            iter(j + 1, zb, za);
         }
-        if (p.Z != nullptr && nch > 1) load_z((nch - 2) * kC, zr);
-        products(buf(nch - 1), par(nch - 1));
-        if (nch > 1 && w < 2) finish((nch - 2) * kC, buf(nch - 2), par(nch - 2), zr);
-        __syncthreads();
-        if (w < 2) {
-            if (p.Z != nullptr) load_z((nch - 1) * kC, zr);
-            finish((nch - 1) * kC, buf(nch - 1), par(nch - 1), zr);
-        }
+        auto last = [&](float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
+            const int j = nch - 1;
+            step(j, zl, zu);
+            __syncthreads();
+            if (w < 2) {
+                float y[4];
+                finish(buf(j), par(j), zl, y);
+                store_y(j * kC, y, true);
+            }
+        };
+        if ((nch - 1) & 1) last(zb, za);
+        else last(za, zb);
     } else if (nch > 0) {
         load_prep(0, raw0);
         if constexpr (DB) load_prep(min(1, nch - 1) * kC, raw1);
