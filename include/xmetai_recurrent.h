@@ -269,7 +269,9 @@ int xm_softmax_cpu(const float *in, const int64_t *shape, int32_t rank, int64_t 
  *   "gdn2_kpw4"      1: chunked GDN-2 above 128 keys with 4 key tiles per wave
  *   "gdn2_windowed"  1: chunked GDN-2 in windows of 128 chunks
  *   "gdn2_split"     1: chunked GDN-2 never split along the sequence; 2: split
- *                    into up to four segments wherever the sequence has 2+ chunks
+ *                    into up to four segments wherever the sequence has 2+ chunks;
+ *                    3: two unequal segments, the second two column tiles per
+ *                    workgroup (where such a kernel is built, 2+ chunks)
  *   "gdn2_ct"        1, 2: value-column tiles (of 16 columns) per chunked GDN-2
  *                    recurrence workgroup, 2 where such a kernel is built (by
  *                    default 2 where one tile per workgroup would launch more

@@ -234,6 +234,49 @@ def test_gdn2_sequence_split(name, override):
     check(f"gated_deltanet2/split_{name}", got, run_ref(inp, s), TOL_GDN2, ref32=ref32)
 
 
+# Two unequal segments, the second at two column tiles per workgroup
+# (gdn2_split override 3; key tilings with a two-tile kernel, up to 256 keys).
+# Odd value-tile counts leave the last value pair half empty, odd key-tile
+# counts the last identity pair (its second tile past the padded keys stores
+# nothing).
+SPLIT2_CASES = {
+    "t50_k100_v48": S(1, 50, 3, 100, 48),
+    "t300_k128_v65_odd_value_tiles": S(1, 300, 2, 128, 65),
+    "t600_k64_v32": S(1, 600, 2, 64, 32),
+    "t1000_k40_v15_odd_key_tiles_nos0": S(2, 1000, 1, 40, 15, initial_state=False),
+    "t700_k160_v48_perkey": S(1, 700, 1, 160, 48, per_key_gates=True),
+    "t1025_k256_v256": S(1, 1025, 1, 256, 256),
+    "t40_k128_v128_nol2": S(1, 40, 1, 128, 128, l2norm=False),
+    "t17_k33_v17_two_chunks": S(1, 17, 2, 33, 17),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SPLIT2_CASES))
+def test_gdn2_two_tile_split(name, override):
+    s = SPLIT2_CASES[name]
+    inp = W.gated_deltanet2_inputs(s, seed=12)
+    override("gdn2_split", 3)
+    got = run_gpu(inp, s)
+    assert any(k.startswith("Gdn2ChunkSplit2Kernel") for k in xp.last_launches()), xp.last_launches()
+    ref32 = None if s.l2norm else run_ref(inp, s, np.float32)
+    check(f"gated_deltanet2/split2_{name}", got, run_ref(inp, s), TOL_GDN2, ref32=ref32)
+
+
+def test_gdn2_two_tile_split_selected_for_wide_heads():
+    """1 x 8 heads at 256 x 256 (128 value-tile workgroups, too many value and
+    key tiles for a second segment at one tile each) takes the two-tile split
+    by itself; the first and last heads are checked over the whole sequence."""
+    s = S(1, 2048, 8, 256, 256, initial_state=False)
+    inp = W.gated_deltanet2_inputs(s, seed=13)
+    y = run_gpu(inp, s)
+    launched = xp.last_launches()
+    assert any(k.startswith("Gdn2ChunkSplit2Kernel") for k in launched), launched
+    assert not any(k.startswith("Gdn2SplitCombineKernel") for k in launched), launched
+    sub = _head_subset(inp, 0, [0, 7])
+    ref = cref.gated_deltanet2(*(sub[k] for k in KEYS), scale=s.scale, use_qk_l2norm=s.l2norm, dtype=np.float64)
+    check("gated_deltanet2/split2_auto_heads", y[:, :, [0, 7]], ref, TOL_GDN2)
+
+
 def test_gdn2_two_segment_split_without_combine():
     """Wide keys over few value columns split into two segments by default;
     with no final state requested segment 0's final state is segment 1's start

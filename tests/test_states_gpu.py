@@ -19,6 +19,7 @@ import pytest
 from oracle import cref
 from parity import TOL_GPU, TOL_GDN2, TOL_M3, TOL_SS, check, to_dev
 from xmetai_onnx_plugins import gated_deltanet2_fn, mamba3_siso_fn, selective_scan_fn, workloads as W
+import xmetai_onnx_plugins as xp
 
 pytestmark = pytest.mark.gpu
 
@@ -145,18 +146,24 @@ def test_gdn2_final_state_parity(name):
     np.testing.assert_array_equal(o, gdn_gpu(inp, s, state=False))   # the state write leaves o alone
 
 
-@pytest.mark.parametrize("shape", [(1, 1500, 2, 96, 40, True), (2, 700, 1, 320, 24, False), (1, 90, 1, 33, 17, True)])
-def test_gdn2_final_state_sequence_split(shape, override):
-    """The final state of a sequence-split call (gdn2_split = 2): the combine
-    kernel's last step, from the initial state or zeros."""
+@pytest.mark.parametrize("shape,mode", [((1, 1500, 2, 96, 40, True), 2), ((2, 700, 1, 320, 24, False), 2),
+                                        ((1, 90, 1, 33, 17, True), 2), ((1, 1500, 2, 96, 40, True), 3),
+                                        ((2, 700, 1, 256, 24, False), 3), ((1, 90, 1, 40, 17, True), 3)])
+def test_gdn2_final_state_sequence_split(shape, mode, override):
+    """The final state of a sequence-split call (gdn2_split = 2: up to four
+    equal segments; 3: two unequal segments, the second two tiles per
+    workgroup): the combine kernel's last step, from the initial state or
+    zeros."""
     b, t, h, k, v, s0 = shape
     s = S(b, t, h, k, v, initial_state=s0)
     inp = W.gated_deltanet2_inputs(s, seed=8)
-    override("gdn2_split", 2)
+    override("gdn2_split", mode)
     o, st = gdn_gpu(inp, s)
+    kernel = "Gdn2ChunkSplit2Kernel" if mode == 3 else "Gdn2ChunkSplitKernel"
+    assert any(x.startswith(kernel) for x in xp.last_launches()), xp.last_launches()
     ref_o, ref_st = gdn_ref(inp, s)
-    check(f"gated_deltanet2_state/split_{b}_{t}_{h}_{k}_{v}/o", o, ref_o, TOL_GDN2)
-    check(f"gated_deltanet2_state/split_{b}_{t}_{h}_{k}_{v}/S", st, ref_st, TOL_GDN2)
+    check(f"gated_deltanet2_state/split{mode}_{b}_{t}_{h}_{k}_{v}/o", o, ref_o, TOL_GDN2)
+    check(f"gated_deltanet2_state/split{mode}_{b}_{t}_{h}_{k}_{v}/S", st, ref_st, TOL_GDN2)
 
 
 @pytest.mark.parametrize("name", ["t4100_three_windows", "k448_t2100_window_carry"])

@@ -570,11 +570,14 @@ __device__ __forceinline__ void DecayState(v4f (&S)[KPW], const float (&sc)[NSV]
 // token rows; T: its length; sbase: the row's offset in the [B,H,K,V] states.
 // The state comes from s_in (zeros when null) and goes to s_out (not written
 // when null).  Every wave of the workgroup calls it with the same arguments.
-// Column tile of a sequence-split run (Gdn2ChunkSplitKernel): tiles below VT
-// are value columns; tile VT + j carries the identity columns 16 j..16 j + 15
-// (keys): WV = 0, initial state I, the output goes to `psi` ([B,T,H,KP] rows,
-// KP = keys padded to 16) and the final state to a [K][KP] transition.  The
-// padded columns start at zero and stay zero, so they are stored as zeros.
+// Column tiles of a sequence-split run (Gdn2ChunkSplitKernel,
+// Gdn2ChunkSplit2Kernel), in units of the workgroup's CT tiles: with VW =
+// ceil(VT / CT), units below VW are value columns; unit VW + j carries the
+// identity columns 16 (CT j + c)..+15 (keys) in its tile c: WV = 0, initial
+// state I, the output goes to `psi` ([B,T,H,KP] rows, KP = keys padded to
+// 16) and the final state to a [K][KP] transition.  The padded columns start
+// at zero and stay zero, so they are stored as zeros; identity tiles past KP
+// (the second tile of the last unit when ceil(dk / 16) is odd) store nothing.
 struct SplitTile {
     int tile;
     bool ident;
@@ -585,7 +588,6 @@ template <int KPW, int KS, int CT = 1, bool SPLIT = false>
 __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, float *sXp, int h, size_t tok0, int T,
                                              int cs, int cw0, int nrun, int wn, const float *prep_row, size_t sbase,
                                              const float *s_in, float *s_out, SplitTile st = {}) {
-    static_assert(!SPLIT || CT == 1, "identity tiles run one column tile per workgroup");
     using L = RecurLayout<KPW, KS, CT>;
     using Ops = ChunkOperands<KPW, KS, CT>;
     constexpr int KQ = L::KQ, FB = L::FB, NSV = L::NSV, NM = L::NM;
@@ -605,12 +607,17 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
         col[c] = (vt * CT + c) * 16 + (lane & 15);
         col_ok[c] = !ident && col[c] < dv;
     }
-    // output column (CT = 1 where it differs): the value column, or (identity
-    // tile) the key it starts as
-    const int kcol = SPLIT ? (vt - VT) * 16 + (lane & 15) : 0;
-    const int ocol = ident ? kcol : col[0];
-    const bool ocol_ok = ident || col_ok[0];
+    // output column of each tile: the value column, or (identity tile) the
+    // key it starts as
     const int OW = ident ? (dk + 15) / 16 * 16 : dv;   // output row width
+    int kcol[CT], ocol[CT];
+    bool ocol_ok[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+        kcol[c] = SPLIT ? ((vt - VW) * CT + c) * 16 + (lane & 15) : 0;
+        ocol[c] = ident ? kcol[c] : col[c];
+        ocol_ok[c] = ident ? kcol[c] < OW : col_ok[c];
+    }
     const Rsrc rblk = MakeRsrc(prep_row, wn * FB * 4);   // this head row's prepared blocks of the window
     // byte offsets, from a chunk's first token in [B,T,H,V], of this lane's
     // tokens 4(l/16)+i in its columns (out of range for columns past dv); the
@@ -654,7 +661,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     for (int c = 0; c < CT; ++c)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            oo[c][i] = SPLIT ? (ocol_ok ? ((4 * g4 + i) * HO + ocol) * 4 : kOutOfRange) : vo[c][i];
+            oo[c][i] = SPLIT ? (ocol_ok[c] ? ((4 * g4 + i) * HO + ocol[c]) * 4 : kOutOfRange) : vo[c][i];
     // this wave's output rows i = ks + m KS (kOutOfRange for i >= 4: the
     // store is dropped)
     int ol[CT][NM];
@@ -663,8 +670,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             const int i = ks + m * KS;
-            const bool ok = i < 4 && (SPLIT ? ocol_ok : col_ok[c]);
-            ol[c][m] = ok ? ((4 * g4 + i) * HO + (SPLIT ? ocol : col[c])) * 4 : kOutOfRange;
+            const bool ok = i < 4 && ocol_ok[c];
+            ol[c][m] = ok ? ((4 * g4 + i) * HO + ocol[c]) * 4 : kOutOfRange;
         }
     float *const out_run = (ident ? st.psi : p.out) + ((tok0 + cs * kC) * H + h) * OW;
     auto out_bytes = [&](int jl) {
@@ -683,7 +690,7 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = kb + i;
-                S[c][kt][i] = ident ? (key == kcol && key < dk ? 1.0f : 0.0f)
+                S[c][kt][i] = ident ? (key == kcol[c] && key < dk ? 1.0f : 0.0f)
                                     : (s_in != nullptr && col_ok[c] && key < dk)
                                           ? s_in[sbase + static_cast<size_t>(key) * dv + col[c]]
                                           : 0.0f;
@@ -933,8 +940,8 @@ __device__ __forceinline__ void Gdn2RecurRun(const GatedDeltaNet2Params &p, floa
     if (s_out != nullptr) {
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
-            const int oc = SPLIT ? ocol : col[c];
-            if (!(SPLIT ? ocol_ok : col_ok[c])) continue;
+            const int oc = ocol[c];
+            if (!ocol_ok[c]) continue;
 #pragma unroll
             for (int kt = 0; kt < KPW; ++kt) {
                 const int kb = (ks * KPW + kt) * 16 + 4 * g4;
@@ -1036,6 +1043,47 @@ __global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplitKernel(GatedDeltaNet2Pa
     Gdn2RecurRun<KPW, KS, 1, true>(p, sXp, h, static_cast<size_t>(b) * p.seqlen, p.seqlen, cs, cs, nrun, nchunks,
                                 p.prepared + static_cast<size_t>(row) * nchunks * L::FB, 0, s_in, s_out,
                                 SplitTile{tile, ident, psi});
+}
+
+// Two unequal segments for launches whose value tiles fill at most half the
+// CUs and whose identity tiles are too many for one more workgroup per CU at
+// one tile each (e.g. 1 x 8 heads at 256 x 256: 128 value tiles, 256 value and
+// key tiles in a second segment).  Segment 0, chunks [0, sc), runs its VT value
+// tiles one per workgroup; segment 1, chunks [sc, nchunks), runs its value and
+// identity tiles two per workgroup (ceil(VT / 2) + ceil(KT / 2) workgroups),
+// which steps a chunk in about 1.6 times segment 0's time when both run.  So
+// segment 0 is the longer one, and the launch has one workgroup per CU for
+// both.  Workgroups per (b, h): segment 0's tiles, then segment 1's pairs;
+// outputs as in Gdn2ChunkSplitKernel with nseg = 2.
+template <int KPW, int KS>
+__global__ __launch_bounds__(64 * KS) void Gdn2ChunkSplit2Kernel(GatedDeltaNet2Params p, int sc, int nchunks,
+                                                                 float *psi, float *phi, float *s0) {
+    using L1 = RecurLayout<KPW, KS, 1>;
+    using L2 = RecurLayout<KPW, KS, 2>;
+    static_assert(L1::FB == L2::FB && L1::kFloats <= L2::kFloats, "one block layout, the two-tile partials");
+    __shared__ __attribute__((aligned(16))) float sXp[L2::kFloats];
+    const int H = p.nheads, VT = (p.dv + 15) / 16, KT = (p.dk + 15) / 16;
+    const int VP = (VT + 1) / 2, per_row = VT + VP + (KT + 1) / 2;
+    const int rows = p.batch * H;
+    const int x = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int row = x / per_row, rx = x % per_row;
+    const int b = row / H, h = row % H;
+    const size_t kv = static_cast<size_t>(p.dk) * p.dv, kp = static_cast<size_t>(p.dk) * KT * 16;
+    const float *const prep_row = p.prepared + static_cast<size_t>(row) * nchunks * L1::FB;
+    const size_t tok0 = static_cast<size_t>(b) * p.seqlen;
+    if (rx < VT) {   // workgroup-uniform
+        const float *s_in = p.initial_state != nullptr ? p.initial_state + row * kv : nullptr;
+        Gdn2RecurRun<KPW, KS, 1, true>(p, sXp, h, tok0, p.seqlen, 0, 0, min(sc, nchunks), nchunks, prep_row, 0, s_in,
+                                       s0 + static_cast<size_t>(row) * kv, SplitTile{rx, false, psi});
+    } else {
+        const int nrun = nchunks - sc;
+        if (nrun <= 0) return;
+        const int u = rx - VT;
+        const bool ident = u >= VP;
+        float *s_out = ident ? phi + (static_cast<size_t>(rows) + row) * kp : s0 + (static_cast<size_t>(rows) + row) * kv;
+        Gdn2RecurRun<KPW, KS, 2, true>(p, sXp, h, tok0, p.seqlen, sc, sc, nrun, nchunks, prep_row, 0, nullptr, s_out,
+                                       SplitTile{u, ident, psi});
+    }
 }
 
 // Stages column tile vt of a [dk][dv] state (row base src, workgroup-uniform)
@@ -1176,9 +1224,10 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
     }
 }
 
-// O += Psi_s S_start(s) over the tokens of segment s >= 1: workgroup ((b, h),
-// value tile, s, four consecutive chunks of the segment), a wave per chunk,
-// S_start(s)'s column tile staged in LDS.  D[m][n] = sum_k Psi[t0 + m][k]
+// O += Psi_s S_start(s) over the tokens of segment s >= 1 (chunks [s sc,
+// min((s + 1) sc, nchunks))): workgroup ((b, h), value tile, s, four
+// consecutive chunks of the segment; ncg such groups per segment), a wave per
+// chunk, S_start(s)'s column tile staged in LDS.  D[m][n] = sum_k Psi[t0 + m][k]
 // S_start[k][n] on MFMA (A: lane m + 16 k holds Psi[t0 + m][16 kb + 4 k + ii],
 // 16 bytes of a KP-pitch row; B from LDS, stored column by column at pitch
 // KP + 4 for 16-byte reads), added to the output rows.  Dynamic LDS:
@@ -1190,14 +1239,19 @@ __global__ __launch_bounds__(512) void Gdn2SplitCombineKernel(GatedDeltaNet2Para
 // from 50 to 112 VGPRs (4 waves per SIMD instead of 8): worth it only where
 // every workgroup is resident at once and each waits out its own staging.
 template <int SB>
-__global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int nchunks,
+__global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Params p, int sc, int ncg, int nchunks,
                                                               const float *psi, const float *sst, const float *s1) {
     extern __shared__ float sts[];
     const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
-    const int KP = KT * 16, rows = p.batch * H, ncg = (sc + 3) / 4;
+    const int KP = KT * 16, rows = p.batch * H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, m16 = lane & 15, g4 = lane >> 4;
-    const int x = blockIdx.x;
-    const int cg = x % ncg, vt = (x / ncg) % VT, row = (x / ncg / VT) % rows, seg = 1 + x / ncg / VT / rows;
+    // value tile fastest, each XCD a contiguous range: the VT workgroups of
+    // one group of chunks run together on one XCD and read its Psi rows
+    // through one L2 (ordered chunk group first, a Psi row was fetched once per
+    // value tile: 1 x 16384 x 8 heads at 256 x 256 with the two-tile split,
+    // 1.188 -> 1.171 ms, interleaved A/B)
+    const int x = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int vt = x % VT, cg = (x / VT) % ncg, row = (x / VT / ncg) % rows, seg = 1 + x / VT / ncg / rows;
     const int b = row / H, h = row % H;
     const int c = seg * sc + cg * 4 + w;
     const bool live = cg * 4 + w < sc && c < nchunks;   // whole wave
@@ -1246,6 +1300,103 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
     for (int i = 0; i < 4; ++i) {
         const int t = c * kC + 4 * g4 + i;
         if (t < T && col < dv) orow[static_cast<size_t>(i) * H * dv] = o[i] + acc[i];
+    }
+}
+
+// O += Psi S_start(1) over segment 1 of a two-segment split (chunks [c0,
+// nchunks)), with KTM >= ceil(dk / 16) key tiles (KTM a multiple of 8): each
+// wave owns a ((b, h), block of cpw chunks, value tile) item, value tile
+// fastest (in XCD-local order the value tiles of one chunk block run together
+// and read its Psi rows through one L2).  The wave holds the value tile of
+// S_start (st: [K][V] per (b, h)) in VGPRs as MFMA B operands (lane l: keys
+// 16 kt + 4 (l / 16) + ii, column l % 16) and streams its chunks: D[m][n] =
+// sum_k Psi[t0 + m][k] S_start[k][n] (A: lane m + 16 k holds Psi[t0 + m][16 kt
+// + 4 k + ii]), added to the output rows.  Psi and output rows go through
+// per-chunk raw-buffer descriptors that end after the chunk's last valid
+// token (fixed 32-bit lane offsets, zeros past the end, no address
+// arithmetic per load); a chunk's second half of key tiles multiplies while
+// the next chunk's first half and output values load; the MFMAs alternate
+// over four accumulators (four independent chains).  No LDS, no barrier.
+// The host keeps H KP and H dv under 2^25 and dk dv under 2^29.
+template <int KTM>
+__global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2Params p, int c0, int ncb, int cpw,
+                                                                 int nchunks, const float *psi, const float *st) {
+    static_assert(KTM % 8 == 0, "two halves of whole MFMA groups");
+    constexpr int HT = KTM / 2;
+    const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
+    const int KP = KT * 16, rows = p.batch * H;
+    const int lane = threadIdx.x & 63, m16 = lane & 15, g4 = lane >> 4;
+    const long long item = static_cast<long long>(XcdLocalBlock(blockIdx.x, gridDim.x)) * 4 + (threadIdx.x >> 6);
+    const int vt = static_cast<int>(item % VT);
+    const long long rc = item / VT;
+    const int cb = static_cast<int>(rc % ncb), row = static_cast<int>(rc / ncb);
+    if (row >= rows) return;   // whole wave: the last workgroup's spare waves
+    const int b = row / H, h = row % H;
+    const int col = vt * 16 + m16;
+    const bool col_ok = col < dv;
+    const Rsrc rs = MakeRsrc(st + static_cast<size_t>(row) * dk * dv, dk * dv * 4);
+    float S[KTM][4];
+#pragma unroll
+    for (int kt = 0; kt < KTM; ++kt)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int key = 16 * kt + 4 * g4 + ii;
+            S[kt][ii] = BufF(rs, key < dk && col_ok ? (key * dv + col) * 4 : kOutOfRange);
+        }
+    const int cbeg = c0 + cb * cpw, cend = min(cbeg + cpw, nchunks);
+    const int HKP4 = H * KP * 4, HD4 = H * dv * 4;
+    // lane offsets: A operands of key tile kt (out of range past the key
+    // tiles: the padded tiles of KTM are zeros, not a neighbour row's values)
+    int pk[KTM];
+#pragma unroll
+    for (int kt = 0; kt < KTM; ++kt) pk[kt] = kt < KT ? m16 * HKP4 + (16 * kt + 4 * g4) * 4 : kOutOfRange;
+    int oo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) oo[i] = col_ok ? (4 * g4 + i) * HD4 + col * 4 : kOutOfRange;
+    auto rows_rsrc = [&](const float *x, int w, int c) __attribute__((always_inline)) {   // chunk c's token rows of width w
+        c = min(c, nchunks - 1);
+        const int left = min(T - c * kC, kC);
+        return MakeRsrc(x + ((static_cast<size_t>(b) * T + c * kC) * H + h) * w, ((left - 1) * H * w + w) * 4);
+    };
+    auto load_half = [&](const Rsrc &r, int k0, v4f (&a)[HT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < HT; ++u) a[u] = BufF4(r, pk[k0 + u], 0);
+    };
+    v4f a0[HT], a1[HT];
+    float o[4];
+    {
+        const Rsrc rp = rows_rsrc(psi, KP, cbeg), ro = rows_rsrc(p.out, dv, cbeg);
+        load_half(rp, 0, a0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = BufF(ro, oo[i]);
+    }
+    for (int c = cbeg; c < cend; ++c) {
+        const Rsrc rp = rows_rsrc(psi, KP, c), ro = rows_rsrc(p.out, dv, c);
+        load_half(rp, HT, a1);
+        v4f acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < HT; ++u)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) acc[ii] = Mfma(a0[u][ii], S[u][ii], acc[ii]);
+        // the next chunk's first half and output values (clamped to the last
+        // chunk: loaded, unused)
+        const Rsrc rpn = rows_rsrc(psi, KP, c + 1), ron = rows_rsrc(p.out, dv, c + 1);
+        load_half(rpn, 0, a0);
+        float on[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) on[i] = BufF(ron, oo[i]);
+#pragma unroll
+        for (int u = 0; u < HT; ++u)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) acc[ii] = Mfma(a1[u][ii], S[HT + u][ii], acc[ii]);
+        const v4f d = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            BufStF(ro, oo[i], o[i] + d[i]);
+            o[i] = on[i];
+        }
     }
 }
 
@@ -1391,6 +1542,17 @@ void LaunchSplitRecur(const GatedDeltaNet2Params &p, int nseg, int sc, int nchun
                        sc, nchunks, psi, phi, s0);
 }
 
+template <int KPW, int KS>
+void LaunchSplit2Recur(const GatedDeltaNet2Params &p, int sc, int nchunks, float *psi, float *phi, float *s0,
+                       hipStream_t stream) {
+    const long long vt = (p.dv + 15) / 16, kt = (p.dk + 15) / 16;
+    const long long blocks = static_cast<long long>(p.batch) * p.nheads * (vt + (vt + 1) / 2 + (kt + 1) / 2);
+    if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    XM_NOTE_LAUNCH("Gdn2ChunkSplit2Kernel", {}, KPW, KS);
+    hipLaunchKernelGGL((Gdn2ChunkSplit2Kernel<KPW, KS>), dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, stream,
+                       p, sc, nchunks, psi, phi, s0);
+}
+
 void LaunchSplitRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int nseg, int sc, int nchunks, float *psi,
                          float *phi, float *s0, hipStream_t stream) {
 #define XM_GDN2_SPLIT(KPW_, KS_) \
@@ -1400,6 +1562,15 @@ void LaunchSplitRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, in
     XM_GDN2_SPLIT(4, 6) XM_GDN2_SPLIT(4, 7) XM_GDN2_SPLIT(4, 8) XM_GDN2_SPLIT(5, 4) XM_GDN2_SPLIT(6, 4)
 #undef XM_GDN2_SPLIT
     throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no chunk kernel for this key tiling");
+}
+
+void LaunchSplit2RecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, int sc, int nchunks, float *psi,
+                          float *phi, float *s0, hipStream_t stream) {
+#define XM_GDN2_SPLIT2(KPW_, KS_) \
+    if (c.kpw == KPW_ && c.ks == KS_) return LaunchSplit2Recur<KPW_, KS_>(p, sc, nchunks, psi, phi, s0, stream);
+    XM_GDN2_SPLIT2(2, 2) XM_GDN2_SPLIT2(2, 3) XM_GDN2_SPLIT2(2, 4) XM_GDN2_SPLIT2(3, 4) XM_GDN2_SPLIT2(4, 4)
+#undef XM_GDN2_SPLIT2
+    throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn: no two-tile split kernel for this key tiling");
 }
 
 // Sequence split of an unpacked call (see Gdn2ChunkSplitKernel): nseg segments
@@ -1415,6 +1586,7 @@ void LaunchSplitRecurAny(const GatedDeltaNet2Params &p, const ChunkConfig &c, in
 // CU count: taken at <= 160 and 64+ chunks.  At most 2 GiB of scratch.
 struct SplitPlan {
     int nseg = 0, sc = 0, nchunks = 0;
+    bool two_tile = false;   // Gdn2ChunkSplit2Kernel: nseg = 2, segment 0 = chunks [0, sc)
     size_t blocks = 0, psi = 0, phi = 0, s0 = 0;
     size_t total() const { return blocks + psi + phi + 2 * s0; }
 };
@@ -1433,16 +1605,31 @@ SplitPlan PlanSplit(int batch, int seqlen, int nheads, int dk, int dv, bool pack
     if (static_cast<size_t>(nchunks) * fb >= (size_t{1} << 31)) return SplitPlan{};
     if (static_cast<long long>(nheads) * KT * 16 >= (1LL << 25)) return SplitPlan{};
     int nseg;
+    bool two_tile = false;
     if (ov == 2) {
         nseg = std::min(nchunks, 4);
+    } else if (ov == 3) {
+        if (!HasTwoTileKernel(c) || nchunks < 2) return SplitPlan{};
+        nseg = 2;
+        two_tile = true;
     } else if (rows * (VT + KT) > 160) {
         // Wide keys over few value columns (e.g. 2 x 4 heads at 320 x 64: 32
         // column-tile workgroups, 192 value and key tiles): two segments when
         // both fit on the CUs one workgroup each, so the second segment's
         // identity columns run on CUs the unsplit launch leaves idle and
         // every CU still steps at most one workgroup.
-        if (nchunks < 64 || rows * VT > 64 || rows * VT + rows * (VT + KT) > 256) return SplitPlan{};
-        nseg = 2;
+        if (nchunks < 64) return SplitPlan{};
+        if (rows * VT <= 64 && rows * VT + rows * (VT + KT) <= 256) {
+            nseg = 2;
+        } else if (HasTwoTileKernel(c) && rows * (VT + (VT + 1) / 2 + (KT + 1) / 2) <= DeviceCus()) {
+            // Too many tiles for that, but segment 1 at two tiles per
+            // workgroup still fits beside segment 0 (e.g. 1 x 8 heads at
+            // 256 x 256: 128 + 128 workgroups): Gdn2ChunkSplit2Kernel.
+            nseg = 2;
+            two_tile = true;
+        } else {
+            return SplitPlan{};
+        }
     } else {
         if (nchunks < 64) return SplitPlan{};
         // segments of about 64 chunks (longer ones leave the recurrence
@@ -1457,8 +1644,20 @@ SplitPlan PlanSplit(int batch, int seqlen, int nheads, int dk, int dv, bool pack
     }
     if (nseg < 2) return SplitPlan{};
     SplitPlan sp;
-    sp.sc = (nchunks + nseg - 1) / nseg;
-    sp.nseg = (nchunks + sp.sc - 1) / sp.sc;
+    if (two_tile) {
+        // Segment 0 takes 8 / 13 of the chunks (lengths 1.6 : 1).  Run side
+        // by side, a two-tile segment-1 step measured about 1.6 times a
+        // one-tile segment-0 step (2.1 against 1.3 us at 1 x 16384 x 8 heads,
+        // 256 x 256; each alone: 1.97 against 1.05).  Interleaved A/B of the
+        // segment-0 share there: 1.5 : 1 1.184 ms, 1.6 : 1 1.151, 1.7 : 1
+        // 1.162, 2.0 : 1 1.213.
+        sp.two_tile = true;
+        sp.nseg = 2;
+        sp.sc = std::min(nchunks - 1, std::max(1, static_cast<int>((static_cast<long long>(nchunks) * 8 + 6) / 13)));
+    } else {
+        sp.sc = (nchunks + nseg - 1) / nseg;
+        sp.nseg = (nchunks + sp.sc - 1) / sp.sc;
+    }
     if (sp.nseg < 2) return SplitPlan{};
     sp.nchunks = nchunks;
     sp.blocks = Align256(static_cast<size_t>(rows) * nchunks * fb);
@@ -1485,7 +1684,8 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
     LaunchPrep(c, q, 0, sp.nchunks, static_cast<unsigned>(pblocks), stream);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
-    LaunchSplitRecurAny(q, c, sp.nseg, sp.sc, sp.nchunks, psi, phi, s0, stream);
+    if (sp.two_tile) LaunchSplit2RecurAny(q, c, sp.sc, sp.nchunks, psi, phi, s0, stream);
+    else LaunchSplitRecurAny(q, c, sp.nseg, sp.sc, sp.nchunks, psi, phi, s0, stream);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split recurrence");
     const int lds = 2 * 16 * (KT * 16 + 4) * static_cast<int>(sizeof(float));   // two S buffers (combine)
     EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2SplitCombineKernel), lds);
@@ -1500,13 +1700,33 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
                            sp.nseg, phi, s0, sst);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn split combine");
     }
-    const long long cblocks = rows * VT * (sp.nseg - 1) * ((sp.sc + 3) / 4);
+    if (sp.two_tile && KT <= 16 && static_cast<long long>(p.nheads) * p.dv < (1LL << 25) &&
+        static_cast<long long>(p.dk) * p.dv < (1LL << 29)) {
+        // segment 1 of two, the state in each wave's registers: blocks of cpw
+        // chunks, about 8 waves per CU
+        const int n1 = sp.nchunks - sp.sc;
+        const long long per = rows * VT;
+        const int cpw = static_cast<int>(std::max(1LL, std::min(32LL, per * n1 / (8LL * DeviceCus()))));
+        const int ncb = (n1 + cpw - 1) / cpw;
+        const long long items = per * ncb, wblocks = (items + 3) / 4;
+        if (wblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+        const float *const st1 = direct ? s0 : sst + static_cast<size_t>(rows) * p.dk * p.dv;
+        XM_NOTE_LAUNCH("Gdn2SplitCorrectRegKernel", {}, );
+        hipLaunchKernelGGL(KT <= 8 ? Gdn2SplitCorrectRegKernel<8> : Gdn2SplitCorrectRegKernel<16>,
+                           dim3(static_cast<unsigned>(wblocks)), dim3(256), 0, stream, q, sp.sc, ncb, cpw, sp.nchunks,
+                           psi, st1);
+        XM_LAUNCH_CHECK("GatedDeltaNet2Fn split correction");
+        return;
+    }
+    // groups of four chunks per segment s >= 1 (segment 1 of two is the shorter)
+    const int ncg = (std::min(sp.sc, sp.nchunks - sp.sc) + 3) / 4;
+    const long long cblocks = rows * VT * (sp.nseg - 1) * ncg;
     if (cblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2SplitCorrectKernel", {}, );
     // at most four 4-wave workgroups per CU: all resident at once with 112 VGPRs
     const bool overlap = cblocks <= 4LL * DeviceCus();
     hipLaunchKernelGGL(overlap ? Gdn2SplitCorrectKernel<16> : Gdn2SplitCorrectKernel<1>,
-                       dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q, sp.sc, sp.nchunks, psi,
+                       dim3(static_cast<unsigned>(cblocks)), dim3(256), lds / 2, stream, q, sp.sc, ncg, sp.nchunks, psi,
                        sst, direct ? s0 : nullptr);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn split correction");
 }

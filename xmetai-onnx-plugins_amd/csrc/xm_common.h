@@ -147,7 +147,7 @@ enum Override {
     kOverrideSsSplit,        // selective scan: 1 channel blocks only, 2 sequence-split
     kOverrideGdn2Kpw4,       // 1: GDN-2 chunked recurrence above 128 keys with 4 key tiles per wave, ceil(tiles/4) waves
     kOverrideGdn2Windowed,   // 1: GDN-2 chunked path in windows of 128 chunks (not sized to 128 MiB / one packed window)
-    kOverrideGdn2Split,      // GDN-2 chunked path: 1 never split the sequence, 2 split it wherever it has 2+ chunks
+    kOverrideGdn2Split,      // GDN-2 chunked path: 1 never split the sequence, 2 split it wherever it has 2+ chunks, 3 two unequal segments (the second two tiles per workgroup)
     kOverrideGdn2Ct,         // GDN-2 chunked recurrence: value-column tiles per workgroup (1 or 2)
     kOverrideCount
 };

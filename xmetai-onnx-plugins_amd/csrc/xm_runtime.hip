@@ -155,7 +155,8 @@ constexpr OverrideSpec kOverrides[kOverrideCount] = {
     {"ss_split", {1, 2, 0}},             // 1: one workgroup per channel block; 2: sequence-split
     {"gdn2_kpw4", {1, 0}},               // 1: GDN-2 chunked, 4 key tiles per wave above 128 keys
     {"gdn2_windowed", {1, 0}},           // 1: GDN-2 chunked, windows of 128 chunks only
-    {"gdn2_split", {1, 2, 0}},           // GDN-2 chunked: 1 no sequence split, 2 split wherever 2+ chunks
+    {"gdn2_split", {1, 2, 3, 0}},        // GDN-2 chunked: 1 no sequence split, 2 split wherever 2+ chunks,
+                                         // 3 two unequal segments, the second at two tiles per workgroup
     {"gdn2_ct", {1, 2, 0}},              // GDN-2 chunked: 1 or 2 value-column tiles per recurrence workgroup
 };
 std::atomic<int64_t> g_override[kOverrideCount];
