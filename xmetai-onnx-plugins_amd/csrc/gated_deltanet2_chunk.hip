@@ -105,7 +105,7 @@ __device__ __forceinline__ float RowRor(float x) {
 constexpr int kWindowChunks = 128;       // chunks per prep/recurrence window (2048 tokens)
 
 size_t Align256(size_t bytes) { return (bytes + 255) / 256 * 256; }
-constexpr int kPrepWaves = 4;            // waves (chunk-heads) per prep workgroup
+constexpr int kPrepWaves = 4;            // waves (chunk-heads) per prep workgroup (2 above 128 keys, see LaunchPrep)
 
 // Chunk-head block of the prepared window, in floats, for a recurrence of ks
 // waves of kpw key tiles (kq = kpw ks).  The vectors are unnormalised (q, k
@@ -261,17 +261,17 @@ __device__ __forceinline__ void PackedRange(const GatedDeltaNet2Params &p, int b
 // ---------------------------------------------------------------------------
 // Preparation: one wave per (b,h,chunk) of the window
 // ---------------------------------------------------------------------------
-// Dynamic LDS: kPrepWaves * kq * 256 floats, each wave's transposed Ut' tiles
+// PW waves (chunk-heads) per workgroup.
+// Dynamic LDS: PW * kq * 256 floats, each wave's transposed Ut' tiles
 // kept until T is known.  kpw, ks: the recurrence's key tiles per wave and
 // waves (kq = kpw ks key tiles), which order the scalar vectors.
 // AHEAD: each pair of key tiles' loads issued one pair early, before the
 // previous pair's work (32 more VGPRs; 16-byte key loads only, p.vec4_keys);
 // the arithmetic is the same.
 constexpr int kMaxKeyTiles = 32;         // key tiles of the chunked path (dk <= 512)
-template <bool AHEAD>
-__global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kpw,
-                                                                       int ks) {
-    __shared__ __attribute__((aligned(16))) float sw[kPrepWaves][4][kTile];
+template <bool AHEAD, int PW>
+__global__ __launch_bounds__(64 * PW) void Gdn2ChunkPrepKernel(GatedDeltaNet2Params p, int c0, int wn, int kpw, int ks) {
+    __shared__ __attribute__((aligned(16))) float sw[PW][4][kTile];
     extern __shared__ float prep_dyn[];
     const int kq = kpw * ks;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void Gdn2ChunkPrepKernel(GatedDelt
     // blocks [chunk_off[b], chunk_off[b + 1]) of the row
     const bool packed = p.chunk_off != nullptr;
     const long long rows = packed ? H : static_cast<long long>(p.batch) * H;
-    const long long item = static_cast<long long>(blockIdx.x) * kPrepWaves + w;
+    const long long item = static_cast<long long>(blockIdx.x) * PW + w;
     if (item >= rows * wn) return;   // whole wave; no workgroup barrier here
     const int row = static_cast<int>(item / wn), cw = static_cast<int>(item % wn);
     int h, T, t0;
@@ -1304,36 +1304,43 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
 }
 
 // O += Psi S_start(1) over segment 1 of a two-segment split (chunks [c0,
-// nchunks)), with KTM >= ceil(dk / 16) key tiles (KTM a multiple of 8): each
-// wave owns a ((b, h), block of cpw chunks, value tile) item, value tile
-// fastest (in XCD-local order the value tiles of one chunk block run together
-// and read its Psi rows through one L2).  The wave holds the value tile of
-// S_start (st: [K][V] per (b, h)) in VGPRs as MFMA B operands (lane l: keys
-// 16 kt + 4 (l / 16) + ii, column l % 16) and streams its chunks: D[m][n] =
-// sum_k Psi[t0 + m][k] S_start[k][n] (A: lane m + 16 k holds Psi[t0 + m][16 kt
-// + 4 k + ii]), added to the output rows.  Psi and output rows go through
-// per-chunk raw-buffer descriptors that end after the chunk's last valid
-// token (fixed 32-bit lane offsets, zeros past the end, no address
-// arithmetic per load); a chunk's second half of key tiles multiplies while
-// the next chunk's first half and output values load; the MFMAs alternate
-// over four accumulators (four independent chains).  No LDS, no barrier.
-// The host keeps H KP and H dv under 2^25 and dk dv under 2^29.
+// nchunks)), with KTM >= ceil(dk / 16) key tiles: workgroup ((b, h), block of
+// cpw chunks, group of four value tiles), value-tile group fastest (in
+// XCD-local order the groups of one chunk block run together and read its Psi
+// rows through one L2).  Wave w holds value tile 4 g + w of S_start (st: [K][V]
+// per (b, h)) in VGPRs as MFMA B operands (lane l: keys 16 kt + 4 (l / 16) +
+// ii, column l % 16).  Per chunk the workgroup stages the chunk's Psi tile (16
+// token rows of KP keys) in LDS once, and each wave multiplies it by its
+// state tile: D[m][n] = sum_k Psi[t0 + m][k] S_start[k][n] (A: lane m + 16 k
+// reads Psi[t0 + m][16 kt + 4 k + ii]), added to the output rows.  Read from
+// L2 by every wave (16 KB per 64 MFMAs), the A operands held the CU's vector
+// memory path at its limit: 117 us at 1 x 16384 x 8 heads, 256 x 256.  Psi
+// and output rows go through per-chunk raw-buffer descriptors that end after
+// the chunk's last valid token (zeros past it; keys past KP read as zeros);
+// the next chunk's tile loads into registers while a chunk multiplies, and
+// goes to the other of two LDS buffers (one barrier per chunk).  The MFMAs
+// alternate over four accumulators.  LDS rows at a pitch of KTM 16 + 8
+// floats (8 x odd: row-strided 16-byte reads without bank conflicts).  The
+// host keeps H KP and H dv under 2^25 and dk dv under 2^29.
 template <int KTM>
 __global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2Params p, int c0, int ncb, int cpw,
                                                                  int nchunks, const float *psi, const float *st) {
-    static_assert(KTM % 8 == 0, "two halves of whole MFMA groups");
-    constexpr int HT = KTM / 2;
+    constexpr int PS = KTM * 16 + 8;   // LDS row pitch (floats)
+    constexpr int NV = KTM / 4;        // 16-byte loads per thread per tile
+    __shared__ __attribute__((aligned(16))) float sa[2][kC * PS];
     const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
-    const int KP = KT * 16, rows = p.batch * H;
-    const int lane = threadIdx.x & 63, m16 = lane & 15, g4 = lane >> 4;
-    const long long item = static_cast<long long>(XcdLocalBlock(blockIdx.x, gridDim.x)) * 4 + (threadIdx.x >> 6);
-    const int vt = static_cast<int>(item % VT);
-    const long long rc = item / VT;
+    const int KP = KT * 16, VG = (VT + 3) / 4;
+    const int tid = threadIdx.x, lane = tid & 63, m16 = lane & 15, g4 = lane >> 4;
+    // wave-uniform (readfirstlane): descriptors built from a lane-varying
+    // value would put every buffer load in a waterfall loop
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
+    const long long x = XcdLocalBlock(blockIdx.x, gridDim.x);
+    const int vg = static_cast<int>(x % VG);
+    const long long rc = x / VG;
     const int cb = static_cast<int>(rc % ncb), row = static_cast<int>(rc / ncb);
-    if (row >= rows) return;   // whole wave: the last workgroup's spare waves
     const int b = row / H, h = row % H;
-    const int col = vt * 16 + m16;
-    const bool col_ok = col < dv;
+    const int col = (4 * vg + wave) * 16 + m16;
+    const bool col_ok = col < dv;   // false in every lane of a wave past the value tiles: zeros, stores dropped
     const Rsrc rs = MakeRsrc(st + static_cast<size_t>(row) * dk * dv, dk * dv * 4);
     float S[KTM][4];
 #pragma unroll
@@ -1343,60 +1350,65 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2P
             const int key = 16 * kt + 4 * g4 + ii;
             S[kt][ii] = BufF(rs, key < dk && col_ok ? (key * dv + col) * 4 : kOutOfRange);
         }
-    const int cbeg = c0 + cb * cpw, cend = min(cbeg + cpw, nchunks);
+    const int cbeg = c0 + cb * cpw, cend = min(cbeg + cpw, nchunks);   // workgroup-uniform
     const int HKP4 = H * KP * 4, HD4 = H * dv * 4;
-    // lane offsets: A operands of key tile kt (out of range past the key
-    // tiles: the padded tiles of KTM are zeros, not a neighbour row's values)
-    int pk[KTM];
+    // staging: thread t copies floats 16 KTM / 16 (t % 16) .. + KTM - 1 of
+    // token row t / 16 (keys past KP out of range: zeros)
+    const int srow = tid >> 4, sseg = (tid & 15) * KTM;
+    int so[NV];
 #pragma unroll
-    for (int kt = 0; kt < KTM; ++kt) pk[kt] = kt < KT ? m16 * HKP4 + (16 * kt + 4 * g4) * 4 : kOutOfRange;
+    for (int v = 0; v < NV; ++v) so[v] = sseg + 4 * v < KP ? srow * HKP4 + (sseg + 4 * v) * 4 : kOutOfRange;
     int oo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) oo[i] = col_ok ? (4 * g4 + i) * HD4 + col * 4 : kOutOfRange;
-    auto rows_rsrc = [&](const float *x, int w, int c) __attribute__((always_inline)) {   // chunk c's token rows of width w
-        c = min(c, nchunks - 1);
+    auto rows_rsrc = [&](const float *xr, int w, int c) __attribute__((always_inline)) {   // chunk c's token rows of width w
+        c = __builtin_amdgcn_readfirstlane(min(c, nchunks - 1));
         const int left = min(T - c * kC, kC);
-        return MakeRsrc(x + ((static_cast<size_t>(b) * T + c * kC) * H + h) * w, ((left - 1) * H * w + w) * 4);
+        return MakeRsrc(xr + ((static_cast<size_t>(b) * T + c * kC) * H + h) * w, ((left - 1) * H * w + w) * 4);
     };
-    auto load_half = [&](const Rsrc &r, int k0, v4f (&a)[HT]) __attribute__((always_inline)) {
+    v4f pre[NV];
+    auto gload = [&](int c) __attribute__((always_inline)) {   // chunk c's Psi tile (clamped to the last chunk)
+        const Rsrc rp = rows_rsrc(psi, KP, c);
 #pragma unroll
-        for (int u = 0; u < HT; ++u) a[u] = BufF4(r, pk[k0 + u], 0);
+        for (int v = 0; v < NV; ++v) pre[v] = BufF4(rp, so[v], 0);
     };
-    v4f a0[HT], a1[HT];
-    float o[4];
-    {
-        const Rsrc rp = rows_rsrc(psi, KP, cbeg), ro = rows_rsrc(p.out, dv, cbeg);
-        load_half(rp, 0, a0);
+    auto lstore = [&](float *buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) StF4(buf + srow * PS + sseg + 4 * v, pre[v]);
+    };
+    auto oload = [&](int c, float (&o)[4]) __attribute__((always_inline)) {
+        const Rsrc ro = rows_rsrc(p.out, dv, c);
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = BufF(ro, oo[i]);
-    }
+    };
+    gload(cbeg);
+    lstore(sa[0]);
+    float o[4];
+    oload(cbeg, o);
+    __syncthreads();
     for (int c = cbeg; c < cend; ++c) {
-        const Rsrc rp = rows_rsrc(psi, KP, c), ro = rows_rsrc(p.out, dv, c);
-        load_half(rp, HT, a1);
+        float *const cur = sa[(c - cbeg) & 1];
+        gload(c + 1);
+        float on[4];
+        oload(c + 1, on);
         v4f acc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < HT; ++u)
+        for (int kt = 0; kt < KTM; ++kt) {
+            const v4f a = LdsF4(cur + m16 * PS + 16 * kt + 4 * g4);
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) acc[ii] = Mfma(a0[u][ii], S[u][ii], acc[ii]);
-        // the next chunk's first half and output values (clamped to the last
-        // chunk: loaded, unused)
-        const Rsrc rpn = rows_rsrc(psi, KP, c + 1), ron = rows_rsrc(p.out, dv, c + 1);
-        load_half(rpn, 0, a0);
-        float on[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) on[i] = BufF(ron, oo[i]);
-#pragma unroll
-        for (int u = 0; u < HT; ++u)
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) acc[ii] = Mfma(a1[u][ii], S[HT + u][ii], acc[ii]);
-        const v4f d = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            BufStF(ro, oo[i], o[i] + d[i]);
-            o[i] = on[i];
+            for (int ii = 0; ii < 4; ++ii) acc[ii] = Mfma(a[ii], S[kt][ii], acc[ii]);
         }
+        const v4f d = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        const Rsrc ro = rows_rsrc(p.out, dv, c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) BufStF(ro, oo[i], o[i] + d[i]);
+        // the other buffer was last read in iteration c - 1, before its barrier
+        lstore(sa[((c - cbeg) & 1) ^ 1]);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = on[i];
     }
 }
 
@@ -1477,22 +1489,40 @@ ChunkConfig ChooseChunk(int dk, long long groups) {
 
 // The preparation kernel, with its Ut' tiles' dynamic LDS (up to 128 KiB at
 // 32 key tiles, beside 20 KiB of static LDS).
-void LaunchPrep(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int wn, unsigned blocks,
+template <bool AHEAD, int PW>
+void LaunchPrepWaves(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int wn, long long items,
+                     hipStream_t stream) {
+    const long long blocks = (items + PW - 1) / PW;
+    if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
+    const int dyn = PW * c.kpw * c.ks * 256 * static_cast<int>(sizeof(float));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel<AHEAD, PW>), dyn);
+    hipLaunchKernelGGL((Gdn2ChunkPrepKernel<AHEAD, PW>), dim3(static_cast<unsigned>(blocks)), dim3(64 * PW), dyn, stream,
+                       p, c0, wn, c.kpw, c.ks);
+}
+
+void LaunchPrep(const ChunkConfig &c, const GatedDeltaNet2Params &p, int c0, int wn, long long items,
                 hipStream_t stream) {
     const int kq = c.kpw * c.ks;
     if (kq > kMaxKeyTiles) throw Error(XM_ERR_DEVICE, "GatedDeltaNet2Fn chunk configuration mismatch");
-    const int dyn = kPrepWaves * kq * 256 * static_cast<int>(sizeof(float));
     // Loads one pair ahead where the Ut' stash in LDS already limits the CU to
     // at most three workgroups (kq > 4); at up to 64 keys the extra registers
     // would take it from four to three.
-    if (kq > 4 && p.vec4_keys) {
-        EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel<true>), dyn);
-        hipLaunchKernelGGL(Gdn2ChunkPrepKernel<true>, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn,
-                           c.kpw, c.ks);
+    const bool ahead = kq > 4 && p.vec4_keys;
+    // Above 128 keys the Ut' stash (kq KiB per wave) holds a four-wave
+    // workgroup to one per CU; two-wave workgroups fit three per CU (256
+    // keys: 6 waves per CU against 4).  Only for launches of 16+ chunk-heads
+    // per CU: with fewer, up to three land on some CUs and leave others
+    // short.  Interleaved A/B: 1 x 16384 x 8 heads at 256 x 256 (8192 chunk-
+    // heads) 1.189 -> 1.166 ms; 2 x 2048 x 4 heads at 320 x 64 (1024) 0.1383 ->
+    // 0.1440 with two waves; at 128 keys 0.517 -> 0.519 (VGPRs already bound
+    // occupancy there).
+    const bool two = kq > 8 && items >= 16LL * DeviceCus();
+    if (ahead) {
+        if (two) LaunchPrepWaves<true, 2>(c, p, c0, wn, items, stream);
+        else LaunchPrepWaves<true, kPrepWaves>(c, p, c0, wn, items, stream);
     } else {
-        EnsureDynamicLds(reinterpret_cast<const void *>(&Gdn2ChunkPrepKernel<false>), dyn);
-        hipLaunchKernelGGL(Gdn2ChunkPrepKernel<false>, dim3(blocks), dim3(64 * kPrepWaves), dyn, stream, p, c0, wn,
-                           c.kpw, c.ks);
+        if (two) LaunchPrepWaves<false, 2>(c, p, c0, wn, items, stream);
+        else LaunchPrepWaves<false, kPrepWaves>(c, p, c0, wn, items, stream);
     }
 }
 
@@ -1678,11 +1708,8 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     float *const sst = reinterpret_cast<float *>(base + sp.blocks + sp.psi + sp.phi + sp.s0);
     const long long rows = static_cast<long long>(p.batch) * p.nheads;
     const int VT = (p.dv + 15) / 16, KT = (p.dk + 15) / 16;
-    const long long items = rows * sp.nchunks;
-    const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
-    if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
-    LaunchPrep(c, q, 0, sp.nchunks, static_cast<unsigned>(pblocks), stream);
+    LaunchPrep(c, q, 0, sp.nchunks, rows * sp.nchunks, stream);
     XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
     if (sp.two_tile) LaunchSplit2RecurAny(q, c, sp.sc, sp.nchunks, psi, phi, s0, stream);
     else LaunchSplitRecurAny(q, c, sp.nseg, sp.sc, sp.nchunks, psi, phi, s0, stream);
@@ -1703,12 +1730,14 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
     if (sp.two_tile && KT <= 16 && static_cast<long long>(p.nheads) * p.dv < (1LL << 25) &&
         static_cast<long long>(p.dk) * p.dv < (1LL << 29)) {
         // segment 1 of two, the state in each wave's registers: blocks of cpw
-        // chunks, about 8 waves per CU
+        // chunks, about two workgroups per CU
         const int n1 = sp.nchunks - sp.sc;
-        const long long per = rows * VT;
-        const int cpw = static_cast<int>(std::max(1LL, std::min(32LL, per * n1 / (8LL * DeviceCus()))));
+        const long long vg = (VT + 3) / 4;
+        // (1 x 16384 x 8 heads at 256 x 256: 24 chunks per workgroup; 4, 8
+        // and 12 measured the same)
+        const int cpw = static_cast<int>(std::max(1LL, std::min(32LL, rows * vg * n1 / (2LL * DeviceCus()))));
         const int ncb = (n1 + cpw - 1) / cpw;
-        const long long items = per * ncb, wblocks = (items + 3) / 4;
+        const long long wblocks = rows * vg * ncb;
         if (wblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
         const float *const st1 = direct ? s0 : sst + static_cast<size_t>(rows) * p.dk * p.dv;
         XM_NOTE_LAUNCH("Gdn2SplitCorrectRegKernel", {}, );
@@ -1909,11 +1938,8 @@ bool LaunchGatedDeltaNet2Chunked(const GatedDeltaNet2Params &p, void *scratch, s
         if (packed) q.chunk_off = offs + static_cast<size_t>(c0 / win) * (p.batch + 1);
         const int wn = packed ? plan.slots : std::min(win, nchunks - c0);
         const bool first = c0 == 0, last = c0 + wn >= nchunks;
-        const long long items = static_cast<long long>(heads) * wn;
-        const long long pblocks = (items + kPrepWaves - 1) / kPrepWaves;
-        if (pblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
         XM_NOTE_LAUNCH("Gdn2ChunkPrepKernel", {}, );
-        LaunchPrep(c, q, c0, wn, static_cast<unsigned>(pblocks), stream);
+        LaunchPrep(c, q, c0, wn, static_cast<long long>(heads) * wn, stream);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn chunk preparation");
         if (packed)   // the kernel picks each sequence's state buffers itself
             LaunchRecurAny(q, c, c0, wn, kq, nullptr, nullptr, stream);
