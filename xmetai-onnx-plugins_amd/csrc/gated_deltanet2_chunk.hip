@@ -1303,13 +1303,15 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
     }
 }
 
-// O += Psi S_start(1) over segment 1 of a two-segment split (chunks [c0,
-// nchunks)), with KTM >= ceil(dk / 16) key tiles: workgroup ((b, h), block of
-// cpw chunks, group of four value tiles), value-tile group fastest (in
-// XCD-local order the groups of one chunk block run together and read its Psi
-// rows through one L2).  Wave w holds value tile 4 g + w of S_start (st: [K][V]
-// per (b, h)) in VGPRs as MFMA B operands (lane l: keys 16 kt + 4 (l / 16) +
-// ii, column l % 16).  Per chunk the workgroup stages the chunk's Psi tile (16
+// O += Psi S_start(s) over the chunks [s sc, min((s + 1) sc, nchunks)) of
+// every segment s >= 1, with KTM >= ceil(dk / 16) key tiles: workgroup (s,
+// (b, h), block of cpw chunks of the segment, group of four value tiles),
+// value-tile group fastest (in XCD-local order the groups of one chunk block
+// run together and read its Psi rows through one L2); ncb blocks per segment.
+// S_start(s) is at sst's [s][B*H][K][V], or for s = 1 at s1 when given (two
+// segments with no final state: segment 0's final state is segment 1's
+// start).  Wave w holds value tile 4 g + w of S_start(s) in VGPRs as MFMA B
+// operands (lane l: keys 16 kt + 4 (l / 16) + ii, column l % 16).  Per chunk the workgroup stages the chunk's Psi tile (16
 // token rows of KP keys) in LDS once, and each wave multiplies it by its
 // state tile: D[m][n] = sum_k Psi[t0 + m][k] S_start[k][n] (A: lane m + 16 k
 // reads Psi[t0 + m][16 kt + 4 k + ii]), added to the output rows.  Read from
@@ -1323,13 +1325,14 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectKernel(GatedDeltaNet2Para
 // floats (8 x odd: row-strided 16-byte reads without bank conflicts).  The
 // host keeps H KP and H dv under 2^25 and dk dv under 2^29.
 template <int KTM>
-__global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2Params p, int c0, int ncb, int cpw,
-                                                                 int nchunks, const float *psi, const float *st) {
+__global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2Params p, int sc, int ncb, int cpw,
+                                                                 int nchunks, const float *psi, const float *sst,
+                                                                 const float *s1) {
     constexpr int PS = KTM * 16 + 8;   // LDS row pitch (floats)
     constexpr int NV = KTM / 4;        // 16-byte loads per thread per tile
     __shared__ __attribute__((aligned(16))) float sa[2][kC * PS];
     const int dk = p.dk, dv = p.dv, H = p.nheads, T = p.seqlen, VT = (dv + 15) / 16, KT = (dk + 15) / 16;
-    const int KP = KT * 16, VG = (VT + 3) / 4;
+    const int KP = KT * 16, VG = (VT + 3) / 4, rows = p.batch * H;
     const int tid = threadIdx.x, lane = tid & 63, m16 = lane & 15, g4 = lane >> 4;
     // wave-uniform (readfirstlane): descriptors built from a lane-varying
     // value would put every buffer load in a waterfall loop
@@ -1337,11 +1340,14 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2P
     const long long x = XcdLocalBlock(blockIdx.x, gridDim.x);
     const int vg = static_cast<int>(x % VG);
     const long long rc = x / VG;
-    const int cb = static_cast<int>(rc % ncb), row = static_cast<int>(rc / ncb);
+    const int cb = static_cast<int>(rc % ncb), row = static_cast<int>(rc / ncb % rows);
+    const int seg = 1 + static_cast<int>(rc / ncb / rows);
     const int b = row / H, h = row % H;
     const int col = (4 * vg + wave) * 16 + m16;
+    const size_t kv = static_cast<size_t>(dk) * dv;
+    const float *const st = (seg == 1 && s1 != nullptr ? s1 : sst + static_cast<size_t>(seg) * rows * kv) + row * kv;
     const bool col_ok = col < dv;   // false in every lane of a wave past the value tiles: zeros, stores dropped
-    const Rsrc rs = MakeRsrc(st + static_cast<size_t>(row) * dk * dv, dk * dv * 4);
+    const Rsrc rs = MakeRsrc(st, dk * dv * 4);
     float S[KTM][4];
 #pragma unroll
     for (int kt = 0; kt < KTM; ++kt)
@@ -1350,14 +1356,15 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2P
             const int key = 16 * kt + 4 * g4 + ii;
             S[kt][ii] = BufF(rs, key < dk && col_ok ? (key * dv + col) * 4 : kOutOfRange);
         }
-    const int cbeg = c0 + cb * cpw, cend = min(cbeg + cpw, nchunks);   // workgroup-uniform
+    const int cbeg = seg * sc + cb * cpw, cend = min(min(cbeg + cpw, (seg + 1) * sc), nchunks);   // workgroup-uniform
     const int HKP4 = H * KP * 4, HD4 = H * dv * 4;
-    // staging: thread t copies floats 16 KTM / 16 (t % 16) .. + KTM - 1 of
-    // token row t / 16 (keys past KP out of range: zeros)
-    const int srow = tid >> 4, sseg = (tid & 15) * KTM;
+    // staging: thread t copies the 16-byte pieces 16 v + t % 16 (v < NV) of
+    // token row t / 16, so the 16 threads of a row read 256 contiguous bytes
+    // and write them to 64 distinct banks (keys past KP out of range: zeros)
+    const int srow = tid >> 4, sseg = (tid & 15) * 4;
     int so[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) so[v] = sseg + 4 * v < KP ? srow * HKP4 + (sseg + 4 * v) * 4 : kOutOfRange;
+    for (int v = 0; v < NV; ++v) so[v] = sseg + 64 * v < KP ? srow * HKP4 + (sseg + 64 * v) * 4 : kOutOfRange;
     int oo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) oo[i] = col_ok ? (4 * g4 + i) * HD4 + col * 4 : kOutOfRange;
@@ -1374,7 +1381,7 @@ __global__ __launch_bounds__(256) void Gdn2SplitCorrectRegKernel(GatedDeltaNet2P
     };
     auto lstore = [&](float *buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int v = 0; v < NV; ++v) StF4(buf + srow * PS + sseg + 4 * v, pre[v]);
+        for (int v = 0; v < NV; ++v) StF4(buf + srow * PS + sseg + 64 * v, pre[v]);
     };
     auto oload = [&](int c, float (&o)[4]) __attribute__((always_inline)) {
         const Rsrc ro = rows_rsrc(p.out, dv, c);
@@ -1727,28 +1734,33 @@ void LaunchSplit(const GatedDeltaNet2Params &p, const ChunkConfig &c, const Spli
                            sp.nseg, phi, s0, sst);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn split combine");
     }
-    if (sp.two_tile && KT <= 16 && static_cast<long long>(p.nheads) * p.dv < (1LL << 25) &&
+    // the longest segment s >= 1 (segment 1 of two is the shorter)
+    const int seglen = sp.nseg == 2 ? std::min(sp.sc, sp.nchunks - sp.sc) : sp.sc;
+    if (KT <= 32 && static_cast<long long>(p.nheads) * p.dv < (1LL << 25) &&
         static_cast<long long>(p.dk) * p.dv < (1LL << 29)) {
-        // segment 1 of two, the state in each wave's registers: blocks of cpw
-        // chunks, about two workgroups per CU
-        const int n1 = sp.nchunks - sp.sc;
+        // the state in each wave's registers: blocks of cpw chunks, about two
+        // workgroups per CU (1 x 16384 x 8 heads at 256 x 256: 24 chunks per
+        // workgroup; 4, 8 and 12 measured the same).  Against the staged
+        // kernel below (interleaved A/B): 1 x 16384 x 8 heads at 256 x 256
+        // 1.143 -> 1.082 ms, 1 x 8192 x 4 heads at 128 x 128 0.1507 ->
+        // 0.1423, 2 x 2048 x 4 heads at 320 x 64 0.1379 -> 0.1358.  The staged
+        // kernel remains for states or output rows past the 32-bit offsets.
         const long long vg = (VT + 3) / 4;
-        // (1 x 16384 x 8 heads at 256 x 256: 24 chunks per workgroup; 4, 8
-        // and 12 measured the same)
-        const int cpw = static_cast<int>(std::max(1LL, std::min(32LL, rows * vg * n1 / (2LL * DeviceCus()))));
-        const int ncb = (n1 + cpw - 1) / cpw;
-        const long long wblocks = rows * vg * ncb;
+        const int cpw = static_cast<int>(
+            std::max(1LL, std::min<long long>(std::min(32, seglen), rows * vg * (sp.nchunks - sp.sc) / (2LL * DeviceCus()))));
+        const int ncb = (seglen + cpw - 1) / cpw;
+        const long long wblocks = static_cast<long long>(sp.nseg - 1) * rows * vg * ncb;
         if (wblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
-        const float *const st1 = direct ? s0 : sst + static_cast<size_t>(rows) * p.dk * p.dv;
         XM_NOTE_LAUNCH("Gdn2SplitCorrectRegKernel", {}, );
-        hipLaunchKernelGGL(KT <= 8 ? Gdn2SplitCorrectRegKernel<8> : Gdn2SplitCorrectRegKernel<16>,
-                           dim3(static_cast<unsigned>(wblocks)), dim3(256), 0, stream, q, sp.sc, ncb, cpw, sp.nchunks,
-                           psi, st1);
+        auto kern = KT <= 8 ? Gdn2SplitCorrectRegKernel<8> : KT <= 16 ? Gdn2SplitCorrectRegKernel<16>
+                  : KT <= 24 ? Gdn2SplitCorrectRegKernel<24> : Gdn2SplitCorrectRegKernel<32>;
+        hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(wblocks)), dim3(256), 0, stream, q, sp.sc, ncb, cpw,
+                           sp.nchunks, psi, sst, direct ? s0 : nullptr);
         XM_LAUNCH_CHECK("GatedDeltaNet2Fn split correction");
         return;
     }
-    // groups of four chunks per segment s >= 1 (segment 1 of two is the shorter)
-    const int ncg = (std::min(sp.sc, sp.nchunks - sp.sc) + 3) / 4;
+    // groups of four chunks per segment s >= 1
+    const int ncg = (seglen + 3) / 4;
     const long long cblocks = rows * VT * (sp.nseg - 1) * ncg;
     if (cblocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "GatedDeltaNet2Fn launch exceeds the grid limit");
     XM_NOTE_LAUNCH("Gdn2SplitCorrectKernel", {}, );
