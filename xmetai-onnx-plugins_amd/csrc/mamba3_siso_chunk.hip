@@ -65,7 +65,17 @@ using namespace m3;
 constexpr int kC = 16;          // tokens per chunk
 constexpr int kRows = 32;       // state rows per workgroup (two 16-row tiles)
 constexpr int kBufs = 3;        // chunk buffers: preparing j+1, products of j, finishing j-1
-constexpr int kTS = kC + 4;     // row stride (floats) of the [key][token] and [row][token] tiles
+// Row stride (floats) of the [key][token] k^T and [row][token] V^T tiles.
+// LDS bank conflicts of the kernel's access patterns, measured per access on
+// gfx950 (SQ_LDS_BANK_CONFLICT of a probe issuing each pattern), pitch 20
+// against 24: V^T 4-byte stores, 32 rows x 2 tokens per wave, 6 and 14 (8
+// rows x 8 tokens: 0 at 24); 16-byte reads of 16 rows x 4 tokens 4 and 0;
+// k^T 8-byte stores, 8 pair rows x 8 token pairs per wave, 4 and 12, 0 with
+// the k^T tile's 4-token groups XOR-swizzled by (row >> 2) & 3 (KtCol).
+constexpr int kTS = kC + 8;
+// Physical column of token t in row r of the k^T tile: its 4-token group
+// XOR (r >> 2) & 3, so a group's 4 tokens stay contiguous for 16-byte reads.
+__device__ __forceinline__ int KtCol(int r, int t) { return (((t >> 2) ^ ((r >> 2) & 3)) << 2) | (t & 3); }
 
 template <int KBW, int NW, int NPW>   // 16-key blocks per product wave, product waves, preparation waves
 struct M3CLayout {
@@ -93,14 +103,21 @@ struct M3CLayout {
     static constexpr int oW = oEcum + kC;             // w_t = gamma_t + look_t
     static constexpr int oGam = oW + kC;              // gamma_t
     static constexpr int oQK = oGam + kC;             // partial q.k per preparation wave [NPW][kC]
-    static constexpr int kBuf = oQK + NPW * kC;
+    static constexpr int oK = oQK + NPW * kC;         // k^   [kC][QS] (KCOPY)
     // partial products per parity: [NW][3 tiles: G^T, Y rows 0-15, Y rows 16-31][64 lanes][4]
-    static constexpr int oPart = kBufs * kBuf;
     static constexpr int kPart = NW * 3 * 64 * 4;
+    // k^ also in [token][key] order where LDS holds it (up to 128 keys): the
+    // G^T product's A operands then come as one 16-byte read per key block
+    // (the q^ tile's conflict-free pattern) instead of four 4-byte reads of k^T
+    // (2 conflict cycles each)
+    static constexpr bool KCOPY = sizeof(float) * (kBufs * (oK + kC * QS) + 2 * kPart) <= 160 * 1024;
+    static constexpr int kBuf = oK + (KCOPY ? kC * QS : 0);
+    static constexpr int oPart = kBufs * kBuf;
     static constexpr size_t kBytes = sizeof(float) * (oPart + 2 * kPart);
     static_assert(kBuf % 4 == 0 && QS % 4 == 0 && kTS % 4 == 0, "16-byte aligned tiles");
     static_assert(kBytes <= 160 * 1024, "LDS budget");
     static_assert(PPW % 8 == 0 && PB * PL == PPW && TPL * TG == kC && VPT * 64 * NPW == kRows * kC, "lane mapping");
+    static_assert(VPT * NPW == 8 && kRows == 32 && kC == 16, "V^T: 4 row blocks x 2 token blocks of 8 x 8");
 };
 
 // Cross-row moves of one fp64 value per lane with the gfx950 lane-swap
@@ -181,7 +198,6 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool product_wave = wave < NW;
     const int w = product_wave ? wave : wave - NW;   // index within the role
-    const int rtid = product_wave ? tid : tid - 64 * NW;   // thread index within the role
     const int i16 = lane & 15, g4 = lane >> 4;
     const int N = p.n, P = p.p, A = p.a, H = p.nheads;
     const int half_n = N / 2;
@@ -246,11 +262,16 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
             aoff[x][s] = rot ? ((TPL * tg + s) * static_cast<int>(a_stride) + pr[x]) * 4 : kOutOfRange;
         }
     }
-    const int vrow = rtid & 31;
-    int voff[VPT];
+    // V values: block w + NPW u of 8 rows x 8 tokens (row block % 4, token
+    // block / 4), lane l: row l / 8, token l % 8 of the block
+    int vrow[VPT], vtok[VPT], voff[VPT];
 #pragma unroll
-    for (int u = 0; u < VPT; ++u)
-        voff[u] = r0 + vrow < P ? (((rtid >> 5) + 2 * NPW * u) * static_cast<int>(v_stride) + r0 + vrow) * 4 : kOutOfRange;
+    for (int u = 0; u < VPT; ++u) {
+        const int blk = w + NPW * u;
+        vrow[u] = 8 * (blk % 4) + (lane >> 3);
+        vtok[u] = 8 * (blk / 4) + (lane & 7);
+        voff[u] = r0 + vrow[u] < P ? (vtok[u] * static_cast<int>(v_stride) + r0 + vrow[u]) * 4 : kOutOfRange;
+    }
     // One descriptor per tensor, fixed for the whole sequence: it ends at the
     // sequence's last token, so a token past the end is out of range.  A
     // chunk's token offset goes into the per-lane offset (the range check
@@ -359,13 +380,16 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
                     make_float2(q.x * c - q.y * sn, q.x * sn + q.y * c);
                 kc0[s] = k.x * c - k.y * sn;
                 kc1[s] = k.x * sn + k.y * c;
+                if constexpr (L::KCOPY)
+                    *reinterpret_cast<float2 *>(bf + L::oK + (TPL * tg + s) * QS + 2 * pr[x]) = make_float2(kc0[s], kc1[s]);
             }
+            const int r0k = 2 * pr[x], r1k = 2 * pr[x] + 1;   // this lane's tokens stay in one swizzled group
             if constexpr (TPL == 4) {
-                StF4(bf + L::oKT + (2 * pr[x]) * kTS + 4 * tg, v4f{kc0[0], kc0[1], kc0[2], kc0[3]});
-                StF4(bf + L::oKT + (2 * pr[x] + 1) * kTS + 4 * tg, v4f{kc1[0], kc1[1], kc1[2], kc1[3]});
+                StF4(bf + L::oKT + r0k * kTS + KtCol(r0k, 4 * tg), v4f{kc0[0], kc0[1], kc0[2], kc0[3]});
+                StF4(bf + L::oKT + r1k * kTS + KtCol(r1k, 4 * tg), v4f{kc1[0], kc1[1], kc1[2], kc1[3]});
             } else {
-                *reinterpret_cast<float2 *>(bf + L::oKT + (2 * pr[x]) * kTS + TPL * tg) = make_float2(kc0[0], kc0[1]);
-                *reinterpret_cast<float2 *>(bf + L::oKT + (2 * pr[x] + 1) * kTS + TPL * tg) = make_float2(kc1[0], kc1[1]);
+                *reinterpret_cast<float2 *>(bf + L::oKT + r0k * kTS + KtCol(r0k, TPL * tg)) = make_float2(kc0[0], kc0[1]);
+                *reinterpret_cast<float2 *>(bf + L::oKT + r1k * kTS + KtCol(r1k, TPL * tg)) = make_float2(kc1[0], kc1[1]);
             }
             // the chunk's last token
             if constexpr (PL == 16) {
@@ -390,7 +414,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
             bf[L::oQK + w * kC + TPL * tg + s] = v;   // every lane of the token group holds the sum
         }
 #pragma unroll
-        for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow * kTS + (rtid >> 5) + 2 * NPW * u] = vreg[u];
+        for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow[u] * kTS + vtok[u]] = vreg[u];
         if (w == NPW - 1) {
             const float gam = r.sdt * FastSigmoid(r.strap);
             const float look = r.sdt1 * (1.0f - FastSigmoid(r.strap1));   // zero DT past the end
@@ -433,11 +457,15 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         for (int kb = 0; kb < KBW; ++kb) {
             const int nb0 = 16 * (KBW * w + kb);
             const v4f q4 = LdsF4(bf + L::oQ + i16 * QS + nb0 + 4 * g4);
-            const v4f t4 = LdsF4(bf + L::oKT + (nb0 + i16) * kTS + 4 * g4);
+            const v4f t4 = LdsF4(bf + L::oKT + (nb0 + i16) * kTS + KtCol(nb0 + i16, 4 * g4));
+            v4f k4;
+            if constexpr (L::KCOPY) k4 = LdsF4(bf + L::oK + i16 * QS + nb0 + 4 * g4);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
+                const int kr = nb0 + 4 * g4 + ks;
                 qa[kb][ks] = q4[ks];                                       // q^[t = i16][key nb0 + 4 g4 + ks]
-                ka[kb][ks] = bf[L::oKT + (nb0 + 4 * g4 + ks) * kTS + i16];  // k^[s = i16][same key]
+                if constexpr (L::KCOPY) ka[kb][ks] = k4[ks];               // k^[s = i16][same key]
+                else ka[kb][ks] = bf[L::oKT + kr * kTS + KtCol(kr, i16)];
                 kt[kb][ks] = t4[ks];                                       // k^[s = 4 g4 + ks][key nb0 + i16]
             }
         }
@@ -657,7 +685,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
             const float *kt = smem + ((nch > 0 ? nch - 1 : 0) % kBufs) * L::kBuf + L::oKT;
             for (int i = tid; i < N; i += NT) {
                 const size_t o = static_cast<size_t>(bh) * N + i;
-                p.f_k[o] = T > 0 ? kt[i * kTS + tl] : (p.in_k != nullptr ? p.in_k[o] : 0.0f);
+                p.f_k[o] = T > 0 ? kt[i * kTS + KtCol(i, tl)] : (p.in_k != nullptr ? p.in_k[o] : 0.0f);
             }
         }
     }
