@@ -9,7 +9,8 @@ Covered: SelectiveScanFn in fp32, fp16 and bf16 (descriptor chosen by the
 data type) with the last state; GatedDeltaNet2Fn with the initial and final
 state, packed sequences (input 7) and the trailing optional input omitted;
 Mamba3SisoFn with D, Z, the input states (inputs 11-14) and the four final
-states.
+states; nodes with exactly the reference's inputs and outputs (the optional
+tails absent).
 
 Reference: selective_scan_fn_ort.cpp:58-150, gated_deltanet2_fn_ort.cpp:66-142,
 mamba3_siso_fn_ort.cpp:61-145 (Compute), ort_common.h:74-101 (tensor views)."""
@@ -181,3 +182,28 @@ def test_mamba3_with_input_and_final_states():
             two_pi = 2.0 * float(np.float32(np.pi))
             g = r + (np.mod(g - r + two_pi / 2, two_pi) - two_pi / 2)
         check(f"ort/mamba3/{name}", g, r, TOL_M3)
+
+
+def test_reference_arity_nodes():
+    """Nodes with exactly the reference's inputs and outputs (GatedDeltaNet2Fn
+    7 inputs and 1 output, gated_deltanet2_fn_ort.cpp; Mamba3SisoFn 11 inputs
+    and 1 output, mamba3_siso_fn_ort.cpp): the optional tails this layer
+    declares beyond them (cu_seqlens, the states) read as absent, and the
+    outputs equal the direct C ABI call bit for bit."""
+    s = W.GatedDeltaNet2Shape(2, 50, 3, 48, 20)
+    inp = W.gated_deltanet2_inputs(s, seed=41)
+    dev = [to_dev(inp[k]) for k in GDN_KEYS]
+    assert len(dev) == 7
+    (o,), _ = ortd.run("GatedDeltaNet2Fn", dev, [like((2, 50, 3, 20))], floats={"scale": s.scale},
+                       stream=stream(), scratch=scratch())
+    o, do = done(o, xp.gated_deltanet2_fn(*dev, scale=s.scale))
+    np.testing.assert_array_equal(o, do)
+
+    m = W.Mamba3SisoShape(1, 40, 2, 16, 32, has_z=True)
+    minp = W.mamba3_siso_inputs(m, seed=42)
+    mdev = [to_dev(minp[k]) for k in M3_KEYS]
+    assert len(mdev) == 11
+    (y,), _ = ortd.run("Mamba3SisoFn", mdev, [like((1, 40, 2, 16))],
+                       ints={"chunk_size": 64, "has_d": 1, "has_z": 1}, stream=stream(), scratch=scratch())
+    y, dy = done(y, xp.mamba3_siso_fn(*mdev))
+    np.testing.assert_array_equal(y, dy)
