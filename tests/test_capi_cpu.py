@@ -323,11 +323,15 @@ def test_gdn2_valid_and_scratch():
         # sequence split, 64+ chunks: rows (vt + kt) <= 160 column tiles,
         # max(2, min(ceil(chunks / 64), 1 + ceil(1536 / (rows (vt + kt))))) segments;
         # above 160, two segments when rows vt <= 64 and rows vt + rows (vt + kt)
-        # <= 256; every chunk's blocks, Psi [B,T,H,KP], Phi [nseg][rows][K][KP]
-        # (KP = 16 kt), S0 and the start states [nseg][rows][K][V]; at most 2 GiB
+        # <= 256, or (two-tile split: a two-tile kernel for the key tiling, up to
+        # 256 keys) when rows (vt + ceil(vt / 2) + ceil(kt / 2)) <= 256 CUs; every
+        # chunk's blocks, Psi [B,T,H,KP], Phi [nseg][rows][K][KP] (KP = 16 kt), S0
+        # and the start states [nseg][rows][K][V]; at most 2 GiB
         wide = rows * (vt + kt) > 160
+        two_tile = (kpw, ks) in ((2, 2), (2, 3), (2, 4), (3, 4), (4, 4))
         if (nch >= 64 and nch * block * 4 < (1 << 31)
-                and (not wide or (rows * vt <= 64 and rows * vt + rows * (vt + kt) <= 256))):
+                and (not wide or (rows * vt <= 64 and rows * vt + rows * (vt + kt) <= 256)
+                     or (two_tile and rows * (vt + -(-vt // 2) + -(-kt // 2)) <= 256))):
             nseg = 2 if wide else max(2, min(-(-nch // 64), 1 + -(-1536 // (rows * (vt + kt)))))
             sc = -(-nch // nseg)
             nseg = -(-nch // sc)
@@ -346,7 +350,9 @@ def test_gdn2_valid_and_scratch():
     assert scratch == chunk_scratch(2, 5, 3, 16, 8)
     for T, K, V in ((100, 128, 64), (3000, 128, 128), (17, 100, 7), (2049, 256, 16), (2048, 33, 40),
                     (3000, 512, 64), (40, 300, 16), (40, 352, 16), (40, 352, 352), (33, 385, 8), (50, 129, 8), (50, 150, 8), (50, 192, 8), (50, 80, 8), (50, 96, 8), (50, 48, 8),
-                    (2048, 320, 64), (2048, 384, 64), (2048, 512, 64)):
+                    (2048, 320, 64), (2048, 384, 64), (2048, 512, 64),
+                    (2048, 256, 256), (2048, 200, 240), (1024, 256, 256), (1008, 256, 256),
+                    (2048, 320, 256), (2048, 128, 640)):
         assert validate("gated_deltanet2", gdn_shapes(T=T, K=K, V=V))[1] == chunk_scratch(2, T, 3, K, V), (T, K, V)
     # packed sequences (headdim_k <= 512) take the fused kernel: no scratch
     # headdim_k > 512: prepared chunk of B*H*min(T,1024) rows (4 vectors x K padded
