@@ -35,7 +35,9 @@
 // Launches with few column tiles (few heads) split the sequence instead:
 // every segment runs at once, the later ones from a zero state beside
 // identity columns that give their transition and output map, and a combine
-// and a correction kernel finish the result (Gdn2ChunkSplitKernel below).
+// and a correction kernel finish the result (Gdn2ChunkSplitKernel below; two
+// unequal segments with the second at two column tiles per workgroup in
+// Gdn2ChunkSplit2Kernel; the correction in Gdn2SplitCorrectRegKernel).
 // The matrix products use v_mfma_f32_16x16x4_f32 (A[m][k] in lane m+16k, B[k][n]
 // in lane n+16k, D[m][n] in lane n+16(m/4), register m%4); the D layout of the
 // state and of Y serves directly as the B operand of the next product.
