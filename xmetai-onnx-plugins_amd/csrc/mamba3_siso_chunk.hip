@@ -13,14 +13,15 @@
 //   S_next = e^{cum_15} S_prev + sum_s e^{cum_15 - cum_s} w_s v_s (x) k^_s
 // (equal to the token-by-token recurrence in exact arithmetic).
 //
-// A workgroup of 8 waves owns one (b,h) and 32 state rows (two 16-row
-// tiles) and walks the chunks in order.  Waves 0-3 (product waves) form the
-// matrix products and keep S^T in MFMA accumulator layout: product wave w
-// holds the key blocks [KBW w, KBW (w+1)) of 16 keys; product waves 0 and 1
-// also finish the previous chunk.  Waves 4-7 (preparation waves) prepare the
-// next chunk.  Each SIMD runs
-// one wave of each kind, so the preparation's VALU work and the products'
-// MFMA work overlap.  Per chunk, with
+// A workgroup of 8 waves (12 up to 128 keys) owns one (b,h) and 32 state
+// rows (two 16-row tiles) and walks the chunks in order.  Waves 0-3 (product
+// waves) form the matrix products and keep S^T in MFMA accumulator layout:
+// product wave w holds the key blocks [KBW w, KBW (w+1)) of 16 keys; product
+// waves 0 and 1 also finish the previous chunk, with the decay mask and the
+// q.k sum that product waves 2 and 3 form for them (and, from 192 keys, the
+// whole G^T).  The other waves (preparation waves) prepare the next chunk.
+// Each SIMD runs one product wave and one or two preparation waves, so the
+// preparation's VALU work and the products' MFMA work overlap.  Per chunk, with
 // v_mfma_f32_16x16x4_f32 (A[m][k] in lane m+16k, B[k][n] in lane n+16k,
 // D[m][n] in lane n+16(m/4), register m%4):
 //   G^T = K^ Q^T   over the wave's keys    (partial, summed across the waves)
@@ -103,7 +104,13 @@ struct M3CLayout {
     static constexpr int oW = oEcum + kC;             // w_t = gamma_t + look_t
     static constexpr int oGam = oW + kC;              // gamma_t
     static constexpr int oQK = oGam + kC;             // partial q.k per preparation wave [NPW][kC]
-    static constexpr int oK = oQK + NPW * kC;         // k^   [kC][QS] (KCOPY)
+    // formed once per chunk for both finishing waves, by product waves 2 and 3
+    // while the chunk's products run: the decay mask L_ts = e^{cum_t - cum_s}
+    // w_s in the finishing MFMA's A layout (lane t + 16 g, register k: s = 4 g
+    // + k; s >= t selected away at use) and the sum of the q.k partials
+    static constexpr int oLm = oQK + NPW * kC;        // [64 lanes][4]
+    static constexpr int oQKT = oLm + 256;            // q.k [kC]
+    static constexpr int oK = oQKT + kC;              // k^   [kC][QS] (KCOPY)
     // partial products per parity: [NW][3 tiles: G^T, Y rows 0-15, Y rows 16-31][64 lanes][4]
     static constexpr int kPart = NW * 3 * 64 * 4;
     // k^ also in [token][key] order where LDS holds it (up to 128 keys): the
@@ -187,6 +194,7 @@ __device__ __forceinline__ float RowInclusiveScan16(float x) {
 template <int KBW, int NW, int NPW, bool LONG>
 __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     using L = M3CLayout<KBW, NW, NPW>;
+    static_assert(NW == 4, "product waves 0 and 1 finish, 2 and 3 take shared work off them");
     constexpr int NT = L::NT;
     constexpr int PPW = L::PPW, PL = L::PL, PB = L::PB, TPL = L::TPL, VPT = L::VPT, QS = L::QS;
 
@@ -451,23 +459,40 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     }
 
     // ---- products of one chunk: partial G^T and Y to LDS, then the state update
+    // G^T = K Q^T is summed over all keys: the finishing waves 0 and 1 form it
+    // over the first GK0 of their key blocks only, waves 2 and 3 over theirs
+    // and the remaining GX of wave w - 2's.  Measured (4 x 4096 x 32 heads,
+    // 2 x at 192 and 256 keys): up to 128 keys nothing moves (one block
+    // moved: 0.398 -> 0.421 ms, both: 0.431); at 192 and 256 keys, where the
+    // k^ copy does not fit and the A operands come as 4-byte k^T reads, all
+    // of them move (0.711 -> 0.656, 0.822 -> 0.795 ms; one of three or two of
+    // four: 0.659, 0.806).
+    constexpr int GK0 = KBW <= 2 ? KBW : 0, GX = KBW - GK0;
+    auto load_qk = [&](const float *bf, int nb0, float (&q)[4], float (&k)[4]) __attribute__((always_inline)) {
+        const v4f q4 = LdsF4(bf + L::oQ + i16 * QS + nb0 + 4 * g4);
+        v4f k4;
+        if constexpr (L::KCOPY) k4 = LdsF4(bf + L::oK + i16 * QS + nb0 + 4 * g4);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int kr = nb0 + 4 * g4 + ks;
+            q[ks] = q4[ks];                                       // q^[t = i16][key nb0 + 4 g4 + ks]
+            if constexpr (L::KCOPY) k[ks] = k4[ks];               // k^[s = i16][same key]
+            else k[ks] = bf[L::oKT + kr * kTS + KtCol(kr, i16)];
+        }
+    };
     auto products = [&](const float *bf, float *pp) __attribute__((always_inline)) {
-        float qa[KBW][4], ka[KBW][4], kt[KBW][4];
+        float qa[KBW][4], ka[KBW][4], kt[KBW][4], qx[GX > 0 ? GX : 1][4], kx[GX > 0 ? GX : 1][4];
 #pragma unroll
         for (int kb = 0; kb < KBW; ++kb) {
             const int nb0 = 16 * (KBW * w + kb);
-            const v4f q4 = LdsF4(bf + L::oQ + i16 * QS + nb0 + 4 * g4);
+            load_qk(bf, nb0, qa[kb], ka[kb]);
             const v4f t4 = LdsF4(bf + L::oKT + (nb0 + i16) * kTS + KtCol(nb0 + i16, 4 * g4));
-            v4f k4;
-            if constexpr (L::KCOPY) k4 = LdsF4(bf + L::oK + i16 * QS + nb0 + 4 * g4);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int kr = nb0 + 4 * g4 + ks;
-                qa[kb][ks] = q4[ks];                                       // q^[t = i16][key nb0 + 4 g4 + ks]
-                if constexpr (L::KCOPY) ka[kb][ks] = k4[ks];               // k^[s = i16][same key]
-                else ka[kb][ks] = bf[L::oKT + kr * kTS + KtCol(kr, i16)];
-                kt[kb][ks] = t4[ks];                                       // k^[s = 4 g4 + ks][key nb0 + i16]
-            }
+            for (int ks = 0; ks < 4; ++ks) kt[kb][ks] = t4[ks];   // k^[s = 4 g4 + ks][key nb0 + i16]
+        }
+        if (w >= 2) {
+#pragma unroll
+            for (int x = 0; x < GX; ++x) load_qk(bf, 16 * (KBW * (w - 2) + GK0 + x), qx[x], kx[x]);
         }
         const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4);
         const v4f w4 = LdsF4(bf + L::oW + 4 * g4);
@@ -478,9 +503,19 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 
         v4f gp = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kb = 0; kb < KBW; ++kb)
+        for (int kb = 0; kb < GK0; ++kb)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) gp = Mfma(ka[kb][ks], qa[kb][ks], gp);   // G^T[s][t]
+        if (w >= 2) {
+#pragma unroll
+            for (int kb = GK0; kb < KBW; ++kb)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) gp = Mfma(ka[kb][ks], qa[kb][ks], gp);
+#pragma unroll
+            for (int x = 0; x < GX; ++x)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) gp = Mfma(kx[x][ks], qx[x][ks], gp);
+        }
         v4f yp[2];
 #pragma unroll
         for (int pt = 0; pt < 2; ++pt) {
@@ -490,7 +525,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) yp[pt] = Mfma(qa[kb][ks], S[kb][pt][ks], yp[pt]);   // Y[t][row]
         }
-        StF4(pp + ((w * 3 + 0) * 64 + lane) * 4, gp);
+        if (GK0 > 0 || w >= 2) StF4(pp + ((w * 3 + 0) * 64 + lane) * 4, gp);
         StF4(pp + ((w * 3 + 1) * 64 + lane) * 4, yp[0]);
         StF4(pp + ((w * 3 + 2) * 64 + lane) * 4, yp[1]);
 
@@ -533,44 +568,38 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
             else zr[r] = BufF(rz, off(ooff[r], c0 * vs4));
         }
     };
-    // y of chunk c0 (tokens past the end and rows >= P are dropped), or with
-    // ok false nothing: every wave issues the same four stores in every
-    // iteration, so the wait counts do not fall to those of a path without
-    // them.  The values stay in their four registers until every store is
-    // issued: a store's data register rewritten behind it waits for the store
-    // to complete (stores count in vmcnt on gfx950).
-    auto store_y = [&](int c0, const float (&y)[4], bool ok) __attribute__((always_inline)) {
+    // y of chunk c0 (tokens past the end and rows >= P are dropped).  The
+    // values stay in their four registers until every store is issued: a
+    // store's data register rewritten behind it waits for the store to
+    // complete (stores count in vmcnt on gfx950).
+    auto store_y = [&](int c0, const float (&y)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            if constexpr (LONG) BufStF(ok ? chunk_rsrc(p.out + vbase, v_stride, c0) : rnone, ooff[r], y[r]);
-            else BufStF(ro, ok ? off(ooff[r], c0 * vs4) : kOutOfRange, y[r]);
+            if constexpr (LONG) BufStF(chunk_rsrc(p.out + vbase, v_stride, c0), ooff[r], y[r]);
+            else BufStF(ro, off(ooff[r], c0 * vs4), y[r]);
         }
         asm volatile("" ::"v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
     };
     auto finish = [&](const float *bf, const float *pp, const float (&zr)[4], float (&y)[4])
                       __attribute__((always_inline)) {
         const int pt = w;
-        v4f g = LdsF4(pp + lane * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
-        v4f qk4 = LdsF4(bf + L::oQK + 4 * g4);
+        constexpr int GW0 = GK0 > 0 ? 0 : 2;   // first wave with a G^T partial
+        v4f g = LdsF4(pp + ((GW0 * 3) * 64 + lane) * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
+        const v4f qk4 = LdsF4(bf + L::oQKT + 4 * g4);   // the preparation waves' q.k, summed
+        const v4f l4 = LdsF4(bf + L::oLm + lane * 4);
 #pragma unroll
-        for (int w2 = 1; w2 < NW; ++w2) {   // product waves' partials
-            g += LdsF4(pp + ((w2 * 3 + 0) * 64 + lane) * 4);
-            ys += LdsF4(pp + ((w2 * 3 + 1 + pt) * 64 + lane) * 4);
-        }
+        for (int w2 = GW0 + 1; w2 < NW; ++w2) g += LdsF4(pp + ((w2 * 3 + 0) * 64 + lane) * 4);   // product waves' partials
 #pragma unroll
-        for (int w2 = 1; w2 < NPW; ++w2) qk4 += LdsF4(bf + L::oQK + w2 * kC + 4 * g4);   // preparation waves' q.k
-        const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4);
+        for (int w2 = 1; w2 < NW; ++w2) ys += LdsF4(pp + ((w2 * 3 + 1 + pt) * 64 + lane) * 4);
         const v4f ecum4 = LdsF4(bf + L::oEcum + 4 * g4);
-        const v4f w4 = LdsF4(bf + L::oW + 4 * g4);
         const v4f gam4 = LdsF4(bf + L::oGam + 4 * g4);
-        const float cumt = bf[L::oCum + i16];
         const v4f vt = LdsF4(bf + L::oVT + (16 * pt + i16) * kTS + 4 * g4);
         // M[t = i16][s = 4 g4 + ks] = G[t][s] e^{cum_t - cum_s} w_s for s < t (A operand)
         float m[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int s = 4 * g4 + ks;
-            m[ks] = s < i16 ? g[ks] * (__expf(cumt - cum4[ks]) * w4[ks]) : 0.0f;
+            m[ks] = s < i16 ? g[ks] * l4[ks] : 0.0f;
         }
         // acc[r] (t = 4 g4 + r, this lane's row): e^{cum_t} Y + (D + qk_t gamma_t) v_t
         v4f acc;
@@ -585,15 +614,41 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         }
     };
 
+    // What both finishing waves of chunk bf would otherwise each form (the
+    // finishing waves' SIMDs carry the most issue): wave 2 sums the q.k
+    // partials (in preparation-wave order), wave 3 forms the decay mask, while
+    // the chunk's products run; the chunk is finished after the next barrier.
+    auto shared_finish = [&](float *bf) __attribute__((always_inline)) {
+        if (w == 2) {
+            if (lane < kC) {
+                float v = bf[L::oQK + lane];
+#pragma unroll
+                for (int w2 = 1; w2 < NPW; ++w2) v += bf[L::oQK + w2 * kC + lane];
+                bf[L::oQKT + lane] = v;
+            }
+        } else if (w == 3) {
+            const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4), w4 = LdsF4(bf + L::oW + 4 * g4);
+            const float cumt = bf[L::oCum + i16];
+            v4f l4;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) l4[ks] = __expf(cumt - cum4[ks]) * w4[ks];
+            StF4(bf + L::oLm + lane * 4, l4);
+        }
+    };
+
     const int nch = (T + kC - 1) / kC;
     auto buf = [&](int j) { return smem + (j % kBufs) * L::kBuf; };
     auto par = [&](int j) { return part + (j & 1) * L::kPart; };
     // Each role runs its own loop (the same barriers, in the same order), so
     // the registers one role carries across chunks (the state S; the
-    // prefetched inputs and angle carries) never have to coexist.
-    // Iteration j: products of chunk j and finishing of chunk j-1 | prefetch of
-    // chunk j+2, preparation of chunk j+1.  The last chunk is peeled.
-    if (nch > 0 && product_wave) {   // workgroup-uniform: an empty sequence passes its states through
+    // prefetched inputs and angle carries) never have to coexist, and no wave
+    // carries another role's predicated-off work (waves 2 and 3 issue no Z
+    // loads or output stores: 0.395 -> 0.387 ms at 4 x 4096 x 32 heads, 128
+    // keys).  Iteration j: products of chunk j, finishing of chunk j-1 (waves
+    // 0 and 1) or the shared finishing work of chunk j (waves 2 and 3) |
+    // prefetch of chunk j+2, preparation of chunk j+1.  Chunk 0's products and
+    // the last chunk's finishing are peeled.
+    if (nch > 0 && product_wave && w < 2) {   // workgroup-uniform: an empty sequence passes its states through
         __syncthreads();
         // Z of chunk j is loaded in iteration j (before its products) into
         // the register set of j's parity and gated in iteration j + 1, where
@@ -603,36 +658,37 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         // complete.  The sets are written only by the Z loads: a zeroing in
         // every iteration landed on registers the previous stores read.
         float za[4] = {0.0f, 0.0f, 0.0f, 0.0f}, zb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        // zl: the set for chunk j's Z; zu: chunk j - 1's, finished here
-        auto step = [&](int j, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
+        load_z(0, za);
+        products(buf(0), par(0));
+        __syncthreads();
+        // zl: the set for chunk j's Z; zu: chunk j - 1's, finished here.  The
+        // values stay in their four registers until every store is issued: a
+        // store's data register rewritten behind it waits for the store to
+        // complete (stores count in vmcnt on gfx950).
+        auto iter = [&](int j, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
             load_z(j * kC, zl);
             products(buf(j), par(j));
-            const bool fin = j > 0 && w < 2;
-            float y[4] = {zu[0], zu[1], zu[2], zu[3]};   // stored only where fin
-            if (fin) finish(buf(j - 1), par(j - 1), zu, y);
-            store_y((j - 1) * kC, y, fin);
-        };
-        auto iter = [&](int j, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
-            step(j, zl, zu);
+            float y[4];
+            finish(buf(j - 1), par(j - 1), zu, y);
+            store_y((j - 1) * kC, y);
             __syncthreads();
         };
-        for (int j = 0; j + 1 < nch; j += 2) {   // unrolled by two for the sets
-            iter(j, za, zb);
-            if (j + 2 >= nch) break;
-            iter(j + 1, zb, za);
+        for (int j = 1; j < nch; j += 2) {   // unrolled by two for the sets
+            iter(j, zb, za);
+            if (j + 1 >= nch) break;
+            iter(j + 1, za, zb);
         }
-        auto last = [&](float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
-            const int j = nch - 1;
-            step(j, zl, zu);
+        float y[4];
+        if ((nch - 1) & 1) finish(buf(nch - 1), par(nch - 1), zb, y);
+        else finish(buf(nch - 1), par(nch - 1), za, y);
+        store_y((nch - 1) * kC, y);
+    } else if (nch > 0 && product_wave) {   // waves 2 and 3: products and the shared finishing work
+        __syncthreads();
+        for (int j = 0; j < nch; ++j) {
+            products(buf(j), par(j));
+            shared_finish(buf(j));
             __syncthreads();
-            if (w < 2) {
-                float y[4];
-                finish(buf(j), par(j), zl, y);
-                store_y(j * kC, y, true);
-            }
-        };
-        if ((nch - 1) & 1) last(zb, za);
-        else last(za, zb);
+        }
     } else if (nch > 0) {
         load_prep(0, raw0);
         if constexpr (DB) load_prep(min(1, nch - 1) * kC, raw1);
