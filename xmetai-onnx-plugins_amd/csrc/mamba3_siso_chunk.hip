@@ -103,14 +103,16 @@ struct M3CLayout {
     static constexpr int oEcum = oCum + kC;           // e^{cum_t}
     static constexpr int oW = oEcum + kC;             // w_t = gamma_t + look_t
     static constexpr int oGam = oW + kC;              // gamma_t
-    static constexpr int oQK = oGam + kC;             // partial q.k per preparation wave [NPW][kC]
+    static constexpr int oCs = oGam + kC;             // e^{cum_15 - cum_t} w_t (the update's V' scale)
+    static constexpr int oQK = oCs + kC;              // partial q.k per preparation wave [NPW][kC]
     // formed once per chunk for both finishing waves, by product waves 2 and 3
     // while the chunk's products run: the decay mask L_ts = e^{cum_t - cum_s}
     // w_s in the finishing MFMA's A layout (lane t + 16 g, register k: s = 4 g
-    // + k; s >= t selected away at use) and the sum of the q.k partials
+    // + k; s >= t selected away at use) and D + qk_t gamma_t with qk_t the sum
+    // of the q.k partials
     static constexpr int oLm = oQK + NPW * kC;        // [64 lanes][4]
-    static constexpr int oQKT = oLm + 256;            // q.k [kC]
-    static constexpr int oK = oQKT + kC;              // k^   [kC][QS] (KCOPY)
+    static constexpr int oDg = oLm + 256;             // D + qk_t gamma_t [kC]
+    static constexpr int oK = oDg + kC;               // k^   [kC][QS] (KCOPY)
     // partial products per parity: [NW][3 tiles: G^T, Y rows 0-15, Y rows 16-31][64 lanes][4]
     static constexpr int kPart = NW * 3 * 64 * 4;
     // k^ also in [token][key] order where LDS holds it (up to 128 keys): the
@@ -427,11 +429,13 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
             const float gam = r.sdt * FastSigmoid(r.strap);
             const float look = r.sdt1 * (1.0f - FastSigmoid(r.strap1));   // zero DT past the end
             const float cum = RowInclusiveScan16(r.sadt);   // over the chunk's 16 tokens (lanes 0-15)
+            const float cum15 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cum), kC - 1));
             if (lane < kC) {
                 bf[L::oCum + lane] = cum;
                 bf[L::oEcum + lane] = __expf(cum);
                 bf[L::oW + lane] = gam + look;
                 bf[L::oGam + lane] = gam;
+                bf[L::oCs + lane] = __expf(cum15 - cum) * (gam + look);
             }
         }
     };
@@ -494,9 +498,8 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 #pragma unroll
             for (int x = 0; x < GX; ++x) load_qk(bf, 16 * (KBW * (w - 2) + GK0 + x), qx[x], kx[x]);
         }
-        const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4);
-        const v4f w4 = LdsF4(bf + L::oW + 4 * g4);
-        const float cum15 = bf[L::oCum + kC - 1], ecum15 = bf[L::oEcum + kC - 1];
+        const v4f cs = LdsF4(bf + L::oCs + 4 * g4);
+        const float ecum15 = bf[L::oEcum + kC - 1];
         v4f vt[2];
 #pragma unroll
         for (int pt = 0; pt < 2; ++pt) vt[pt] = LdsF4(bf + L::oVT + (16 * pt + i16) * kTS + 4 * g4);
@@ -530,9 +533,6 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         StF4(pp + ((w * 3 + 2) * 64 + lane) * 4, yp[1]);
 
         // S^T = e^{cum_15} S^T + K^T V',  V'[s][row] = e^{cum_15 - cum_s} w_s v_s[row]
-        float cs[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) cs[r] = __expf(cum15 - cum4[r]) * w4[r];
 #pragma unroll
         for (int pt = 0; pt < 2; ++pt) {
             float vs[4];
@@ -585,14 +585,13 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         const int pt = w;
         constexpr int GW0 = GK0 > 0 ? 0 : 2;   // first wave with a G^T partial
         v4f g = LdsF4(pp + ((GW0 * 3) * 64 + lane) * 4), ys = LdsF4(pp + ((1 + pt) * 64 + lane) * 4);
-        const v4f qk4 = LdsF4(bf + L::oQKT + 4 * g4);   // the preparation waves' q.k, summed
+        const v4f dg4 = LdsF4(bf + L::oDg + 4 * g4);   // D + qk_t gamma_t
         const v4f l4 = LdsF4(bf + L::oLm + lane * 4);
 #pragma unroll
         for (int w2 = GW0 + 1; w2 < NW; ++w2) g += LdsF4(pp + ((w2 * 3 + 0) * 64 + lane) * 4);   // product waves' partials
 #pragma unroll
         for (int w2 = 1; w2 < NW; ++w2) ys += LdsF4(pp + ((w2 * 3 + 1 + pt) * 64 + lane) * 4);
         const v4f ecum4 = LdsF4(bf + L::oEcum + 4 * g4);
-        const v4f gam4 = LdsF4(bf + L::oGam + 4 * g4);
         const v4f vt = LdsF4(bf + L::oVT + (16 * pt + i16) * kTS + 4 * g4);
         // M[t = i16][s = 4 g4 + ks] = G[t][s] e^{cum_t - cum_s} w_s for s < t (A operand)
         float m[4];
@@ -604,7 +603,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         // acc[r] (t = 4 g4 + r, this lane's row): e^{cum_t} Y + (D + qk_t gamma_t) v_t
         v4f acc;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(ecum4[r], ys[r], fmaf(qk4[r], gam4[r], dval) * vt[r]);
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(ecum4[r], ys[r], dg4[r] * vt[r]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) acc = Mfma(m[ks], vt[ks], acc);   // + sum_{s<t} M[t][s] v_s
 #pragma unroll
@@ -616,15 +615,16 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 
     // What both finishing waves of chunk bf would otherwise each form (the
     // finishing waves' SIMDs carry the most issue): wave 2 sums the q.k
-    // partials (in preparation-wave order), wave 3 forms the decay mask, while
-    // the chunk's products run; the chunk is finished after the next barrier.
+    // partials (in preparation-wave order) into D + qk_t gamma_t, wave 3 forms
+    // the decay mask, while the chunk's products run; the chunk is finished
+    // after the next barrier.
     auto shared_finish = [&](float *bf) __attribute__((always_inline)) {
         if (w == 2) {
             if (lane < kC) {
                 float v = bf[L::oQK + lane];
 #pragma unroll
                 for (int w2 = 1; w2 < NPW; ++w2) v += bf[L::oQK + w2 * kC + lane];
-                bf[L::oQKT + lane] = v;
+                bf[L::oDg + lane] = fmaf(v, bf[L::oGam + lane], dval);
             }
         } else if (w == 3) {
             const v4f cum4 = LdsF4(bf + L::oCum + 4 * g4), w4 = LdsF4(bf + L::oW + 4 * g4);
