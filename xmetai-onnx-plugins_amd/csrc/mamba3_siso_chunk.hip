@@ -282,13 +282,19 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         vtok[u] = 8 * (blk / 4) + (lane & 7);
         voff[u] = r0 + vrow[u] < P ? (vtok[u] * static_cast<int>(v_stride) + r0 + vrow[u]) * 4 : kOutOfRange;
     }
-    // One descriptor per tensor, fixed for the whole sequence: it ends at the
-    // sequence's last token, so a token past the end is out of range.  A
-    // chunk's token offset goes into the per-lane offset (the range check
-    // covers only that operand); kOutOfRange plus any in-range offset stays
-    // out of range (no wrap below 2^32).  Without LONG the host keeps
-    // T * stride * 4 < 2^31; with LONG (below) each chunk has its own
-    // descriptors, from its first token to its last valid one.
+    // Without LONG (the host keeps T * stride * 4 < 2^31): one descriptor per
+    // tensor for the whole sequence, ending at its last token; the range
+    // check covers the per-lane plus the scalar offset, so a token past the
+    // end (and kOutOfRange, which stays below 2^32 with any in-range addend)
+    // is out of range.  A lane's place within the chunk is the per-lane
+    // offset; the chunk's offset is added to it (off), or, for the
+    // preparation's loads at 128 and 256 keys (SOFF), passed as the scalar
+    // offset, which saves a vector add per load (4 x 4096 x 32 heads: 128 keys
+    // 0.388 -> 0.371 ms, 256 keys 0.772 -> 0.768; 192 keys 0.638 -> 0.648 and
+    // 64 keys 0.254 -> 0.255, where it stays off; the output stores and Z
+    // loads gain nothing measurable from it).  With LONG each chunk's
+    // descriptors start at its first token (the sequence's rows can pass
+    // 2 GiB).
     auto seq_bytes = [&](size_t stride) { return static_cast<int>(static_cast<size_t>(T) * stride * 4); };
     // (`rows` tokens from c0: DT and Trap reach one token into the next chunk,
     // the look-ahead of the chunk's last token)
@@ -305,6 +311,9 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     const int qs4 = static_cast<int>(q_stride) * 4, as4 = static_cast<int>(a_stride) * 4, vs4 = static_cast<int>(v_stride) * 4;
     // per-lane offset + chunk offset, added as unsigned (no signed overflow near 2^31)
     auto off = [](int a, int b) { return static_cast<int>(static_cast<unsigned>(a) + static_cast<unsigned>(b)); };
+    constexpr bool SOFF = KBW == 2 || KBW == 4;
+    auto ld = [&](Rsrc r, int v, int c) __attribute__((always_inline)) { return SOFF ? BufF(r, v, c) : BufF(r, off(v, c)); };
+    auto ld2 = [&](Rsrc r, int v, int c) __attribute__((always_inline)) { return SOFF ? BufF2(r, v, c) : BufF2(r, off(v, c)); };
 
     // Raw inputs of one chunk, prefetched two chunks ahead into one of two
     // register sets (chunk parity), or, where registers are short (more than
@@ -332,22 +341,22 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         const Rsrc v_ = LONG ? chunk_rsrc(p.V + vbase, v_stride, c0) : rv;
 #pragma unroll
         for (int s = 0; s < TPL; ++s) {
-            dts[s] = BufF(d_, off(cd, (TPL * tg + s) * 4));
+            dts[s] = ld(d_, (TPL * tg + s) * 4, cd);
 #pragma unroll
             for (int x = 0; x < PB; ++x) {
-                qv[x][s] = BufF2(q_, off(qoff[x][s], cq));
-                kv[x][s] = BufF2(k_, off(qoff[x][s], cq));
-                ang[x][s] = BufF(a_, off(aoff[x][s], ca));
+                qv[x][s] = ld2(q_, qoff[x][s], cq);
+                kv[x][s] = ld2(k_, qoff[x][s], cq);
+                ang[x][s] = ld(a_, aoff[x][s], ca);
             }
         }
 #pragma unroll
-        for (int u = 0; u < VPT; ++u) vreg[u] = BufF(v_, off(voff[u], cv));
+        for (int u = 0; u < VPT; ++u) vreg[u] = ld(v_, voff[u], cv);
         // every preparation wave loads them (same load count on every path); wave NPW-1 uses them
-        r.sdt = BufF(d_, off(cd, i16 * 4));
-        r.strap = BufF(t_, off(cd, i16 * 4));
-        r.sadt = BufF(ad_, off(cd, i16 * 4));
-        r.sdt1 = BufF(d_, off(cd, (i16 + 1) * 4));
-        r.strap1 = BufF(t_, off(cd, (i16 + 1) * 4));
+        r.sdt = ld(d_, i16 * 4, cd);
+        r.strap = ld(t_, i16 * 4, cd);
+        r.sadt = ld(ad_, i16 * 4, cd);
+        r.sdt1 = ld(d_, (i16 + 1) * 4, cd);
+        r.strap1 = ld(t_, (i16 + 1) * 4, cd);
     };
 
     // rotated q^ / k^ (and the unrotated q.k), V^T and the per-token scalars of

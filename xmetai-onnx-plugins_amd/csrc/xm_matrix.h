@@ -16,11 +16,12 @@ __device__ __forceinline__ v4f Mfma(float a, float b, v4f c) {
 __device__ __forceinline__ v4f LdsF4(const float *p) { return *reinterpret_cast<const v4f *>(p); }
 __device__ __forceinline__ void StF4(float *p, v4f v) { *reinterpret_cast<v4f *>(p) = v; }
 
-// Raw buffer access: a wave-uniform descriptor (base address, size in bytes)
-// and per-lane byte offsets.  Loads at offsets at or beyond the size return
-// zeros and stores there are dropped, which masks tokens past the sequence
-// end and columns past dv with no branch.  Offsets that must be checked go in
-// the per-lane operand; the scalar operand only ever carries in-range bases.
+// Raw buffer access: a wave-uniform descriptor (base address, size in bytes),
+// per-lane byte offsets and an optional wave-uniform byte offset.  Loads
+// whose per-lane plus scalar offset is at or beyond the size return zeros and
+// stores there are dropped (the range check covers the sum: measured on
+// gfx950, size 256 with scalar offset 128 drops per-lane offsets from 128 on),
+// which masks tokens past the sequence end and columns past dv with no branch.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 constexpr int kRawBufferWord3 = 0x00020000;                       // untyped 32-bit data format
 constexpr int kOutOfRange = static_cast<int>(0x80000000u);        // beyond any descriptor size used here
@@ -33,8 +34,8 @@ __device__ __forceinline__ v4f BufF4(Rsrc r, int voff, int soff) {
 __device__ __forceinline__ float BufF(Rsrc r, int voff, int soff = 0) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
-__device__ __forceinline__ void BufStF(Rsrc r, int voff, float x) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, voff, 0, 0);
+__device__ __forceinline__ void BufStF(Rsrc r, int voff, float x, int soff = 0) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, voff, soff, 0);
 }
 // Orders this wave's LDS accesses before and after (the LDS unit serves one
 // wave's operations in order; this stops the compiler from moving them), so
@@ -50,8 +51,8 @@ __device__ __forceinline__ size_t Uniform64(size_t x) {
     const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(x >> 32));
     return (static_cast<size_t>(hi) << 32) | lo;
 }
-__device__ __forceinline__ float2 BufF2(Rsrc r, int voff) {
-    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0));
+__device__ __forceinline__ float2 BufF2(Rsrc r, int voff, int soff = 0) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
 }  // namespace xm
