@@ -34,9 +34,10 @@
 // state never moves.
 //
 // Preparation of chunk j+1 (rotated q^ and k^, V, per-token scalars) runs
-// while chunk j's products are formed, into one of three LDS buffers (chunk j
-// is read by the products, chunk j-1 by the finishing waves); one barrier per
-// chunk.  Lane (pair lane pq, token group tg) of preparation wave w rotates the pairs
+// while chunk j's products are formed: the q^ / k^ tiles into one of two LDS
+// buffers (chunk parity; chunk j's are read by its products), V^T and the
+// per-token fields into one of three (chunk j-1's are read by the finishing
+// waves); one barrier per chunk.  Lane (pair lane pq, token group tg) of preparation wave w rotates the pairs
 // w PPW + PL x + pq for tokens TPL tg .. TPL tg + TPL - 1.  The angle of a
 // pair is a prefix sum over the chunk (fp64: the token groups' sums are
 // scanned across lanes) on top of the carried wrapped angle, wrapped once per token
@@ -52,6 +53,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "mamba3_math.h"
 #include "xm_hip.h"
@@ -95,10 +97,16 @@ struct M3CLayout {
     // writes, 15.8 against 7.9 LDS cycles per instruction, and the products'
     // 16-byte reads, 7.9 against 4.0).
     static constexpr int QS = NP + 8;
-    // one chunk buffer (floats)
+    // A chunk's tiles (floats), double-buffered by chunk parity: only the
+    // chunk's products and the next chunk's preparation touch them, and in
+    // loops unrolled by two the parity, so every tile address, is a
+    // compile-time offset from one per-lane base.
     static constexpr int oQ = 0;                      // q^   [kC][QS]
     static constexpr int oKT = oQ + kC * QS;          // k^T  [NP][kTS]
-    static constexpr int oVT = oKT + NP * kTS;        // V^T  [kRows][kTS]
+    static constexpr int oK = oKT + NP * kTS;         // k^   [kC][QS] (KCOPY)
+    // A chunk's V^T and per-token fields, in three buffers (the finishing
+    // waves read them one chunk later).
+    static constexpr int oVT = 0;                     // V^T  [kRows][kTS]
     static constexpr int oCum = oVT + kRows * kTS;    // cum_t
     static constexpr int oEcum = oCum + kC;           // e^{cum_t}
     static constexpr int oW = oEcum + kC;             // w_t = gamma_t + look_t
@@ -112,18 +120,18 @@ struct M3CLayout {
     // of the q.k partials
     static constexpr int oLm = oQK + NPW * kC;        // [64 lanes][4]
     static constexpr int oDg = oLm + 256;             // D + qk_t gamma_t [kC]
-    static constexpr int oK = oDg + kC;               // k^   [kC][QS] (KCOPY)
+    static constexpr int kSmall = oDg + kC;
     // partial products per parity: [NW][3 tiles: G^T, Y rows 0-15, Y rows 16-31][64 lanes][4]
     static constexpr int kPart = NW * 3 * 64 * 4;
-    // k^ also in [token][key] order where LDS holds it (up to 128 keys): the
+    // k^ also in [token][key] order where LDS holds it (up to 256 keys): the
     // G^T product's A operands then come as one 16-byte read per key block
     // (the q^ tile's conflict-free pattern) instead of four 4-byte reads of k^T
     // (2 conflict cycles each)
-    static constexpr bool KCOPY = sizeof(float) * (kBufs * (oK + kC * QS) + 2 * kPart) <= 160 * 1024;
-    static constexpr int kBuf = oK + (KCOPY ? kC * QS : 0);
-    static constexpr int oPart = kBufs * kBuf;
+    static constexpr bool KCOPY = sizeof(float) * (2 * (oK + kC * QS) + kBufs * kSmall + 2 * kPart) <= 160 * 1024;
+    static constexpr int kBig = oK + (KCOPY ? kC * QS : 0);
+    static constexpr int oBig = 0, oSmall = 2 * kBig, oPart = oSmall + kBufs * kSmall;
     static constexpr size_t kBytes = sizeof(float) * (oPart + 2 * kPart);
-    static_assert(kBuf % 4 == 0 && QS % 4 == 0 && kTS % 4 == 0, "16-byte aligned tiles");
+    static_assert(kBig % 4 == 0 && kSmall % 4 == 0 && QS % 4 == 0 && kTS % 4 == 0, "16-byte aligned tiles");
     static_assert(kBytes <= 160 * 1024, "LDS budget");
     static_assert(PPW % 8 == 0 && PB * PL == PPW && TPL * TG == kC && VPT * 64 * NPW == kRows * kC, "lane mapping");
     static_assert(VPT * NPW == 8 && kRows == 32 && kC == 16, "V^T: 4 row blocks x 2 token blocks of 8 x 8");
@@ -288,10 +296,10 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // end (and kOutOfRange, which stays below 2^32 with any in-range addend)
     // is out of range.  A lane's place within the chunk is the per-lane
     // offset; the chunk's offset is added to it (off), or, for the
-    // preparation's loads at 128 and 256 keys (SOFF), passed as the scalar
+    // preparation's loads (SOFF, all but 192 keys), passed as the scalar
     // offset, which saves a vector add per load (4 x 4096 x 32 heads: 128 keys
-    // 0.388 -> 0.371 ms, 256 keys 0.772 -> 0.768; 192 keys 0.638 -> 0.648 and
-    // 64 keys 0.254 -> 0.255, where it stays off; the output stores and Z
+    // 0.388 -> 0.371 ms, 64 keys 0.250 -> 0.243, 256 keys 0.772 -> 0.768;
+    // 192 keys 0.628 -> 0.639, where it stays off; the output stores and Z
     // loads gain nothing measurable from it).  With LONG each chunk's
     // descriptors start at its first token (the sequence's rows can pass
     // 2 GiB).
@@ -311,7 +319,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     const int qs4 = static_cast<int>(q_stride) * 4, as4 = static_cast<int>(a_stride) * 4, vs4 = static_cast<int>(v_stride) * 4;
     // per-lane offset + chunk offset, added as unsigned (no signed overflow near 2^31)
     auto off = [](int a, int b) { return static_cast<int>(static_cast<unsigned>(a) + static_cast<unsigned>(b)); };
-    constexpr bool SOFF = KBW == 2 || KBW == 4;
+    constexpr bool SOFF = KBW != 3;
     auto ld = [&](Rsrc r, int v, int c) __attribute__((always_inline)) { return SOFF ? BufF(r, v, c) : BufF(r, off(v, c)); };
     auto ld2 = [&](Rsrc r, int v, int c) __attribute__((always_inline)) { return SOFF ? BufF2(r, v, c) : BufF2(r, off(v, c)); };
 
@@ -359,9 +367,9 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         r.strap1 = ld(t_, (i16 + 1) * 4, cd);
     };
 
-    // rotated q^ / k^ (and the unrotated q.k), V^T and the per-token scalars of
-    // the chunk into buffer bf
-    auto prep = [&](float *bf, const Raw &r) __attribute__((always_inline)) {
+    // rotated q^ / k^ into the tiles bg, the unrotated q.k, V^T and the
+    // per-token scalars of the chunk into bf
+    auto prep = [&](float *bg, float *bf, const Raw &r) __attribute__((always_inline)) {
         const float2 (&qv)[PB][TPL] = r.qv;
         const float2 (&kv)[PB][TPL] = r.kv;
         const float (&ang)[PB][TPL] = r.ang;
@@ -395,20 +403,20 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
                 const float2 q = make_float2(qv[x][s].x + qbias[x].x, qv[x][s].y + qbias[x].y);
                 const float2 k = make_float2(kv[x][s].x + kbias[x].x, kv[x][s].y + kbias[x].y);
                 qk[s] = fmaf(q.x, k.x, fmaf(q.y, k.y, qk[s]));   // unrotated q.k (reference :89-106)
-                *reinterpret_cast<float2 *>(bf + L::oQ + (TPL * tg + s) * QS + 2 * pr[x]) =
+                *reinterpret_cast<float2 *>(bg + L::oQ + (TPL * tg + s) * QS + 2 * pr[x]) =
                     make_float2(q.x * c - q.y * sn, q.x * sn + q.y * c);
                 kc0[s] = k.x * c - k.y * sn;
                 kc1[s] = k.x * sn + k.y * c;
                 if constexpr (L::KCOPY)
-                    *reinterpret_cast<float2 *>(bf + L::oK + (TPL * tg + s) * QS + 2 * pr[x]) = make_float2(kc0[s], kc1[s]);
+                    *reinterpret_cast<float2 *>(bg + L::oK + (TPL * tg + s) * QS + 2 * pr[x]) = make_float2(kc0[s], kc1[s]);
             }
             const int r0k = 2 * pr[x], r1k = 2 * pr[x] + 1;   // this lane's tokens stay in one swizzled group
             if constexpr (TPL == 4) {
-                StF4(bf + L::oKT + r0k * kTS + KtCol(r0k, 4 * tg), v4f{kc0[0], kc0[1], kc0[2], kc0[3]});
-                StF4(bf + L::oKT + r1k * kTS + KtCol(r1k, 4 * tg), v4f{kc1[0], kc1[1], kc1[2], kc1[3]});
+                StF4(bg + L::oKT + r0k * kTS + KtCol(r0k, 4 * tg), v4f{kc0[0], kc0[1], kc0[2], kc0[3]});
+                StF4(bg + L::oKT + r1k * kTS + KtCol(r1k, 4 * tg), v4f{kc1[0], kc1[1], kc1[2], kc1[3]});
             } else {
-                *reinterpret_cast<float2 *>(bf + L::oKT + r0k * kTS + KtCol(r0k, TPL * tg)) = make_float2(kc0[0], kc0[1]);
-                *reinterpret_cast<float2 *>(bf + L::oKT + r1k * kTS + KtCol(r1k, TPL * tg)) = make_float2(kc1[0], kc1[1]);
+                *reinterpret_cast<float2 *>(bg + L::oKT + r0k * kTS + KtCol(r0k, TPL * tg)) = make_float2(kc0[0], kc0[1]);
+                *reinterpret_cast<float2 *>(bg + L::oKT + r1k * kTS + KtCol(r1k, TPL * tg)) = make_float2(kc1[0], kc1[1]);
             }
             // the chunk's last token
             if constexpr (PL == 16) {
@@ -476,36 +484,36 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // over the first GK0 of their key blocks only, waves 2 and 3 over theirs
     // and the remaining GX of wave w - 2's.  Measured (4 x 4096 x 32 heads,
     // 2 x at 192 and 256 keys): up to 128 keys nothing moves (one block
-    // moved: 0.398 -> 0.421 ms, both: 0.431); at 192 and 256 keys, where the
-    // k^ copy does not fit and the A operands come as 4-byte k^T reads, all
-    // of them move (0.711 -> 0.656, 0.822 -> 0.795 ms; one of three or two of
-    // four: 0.659, 0.806).
+    // moved: 0.398 -> 0.421 ms, both: 0.431); at 192 and 256 keys all of
+    // them move (0.684 -> 0.628, 0.809 -> 0.763 ms; with the A operands as
+    // 4-byte k^T reads, before the k^ copy fitted there: 0.711 -> 0.656,
+    // 0.822 -> 0.795, one of three or two of four 0.659, 0.806).
     constexpr int GK0 = KBW <= 2 ? KBW : 0, GX = KBW - GK0;
-    auto load_qk = [&](const float *bf, int nb0, float (&q)[4], float (&k)[4]) __attribute__((always_inline)) {
-        const v4f q4 = LdsF4(bf + L::oQ + i16 * QS + nb0 + 4 * g4);
+    auto load_qk = [&](const float *bg, int nb0, float (&q)[4], float (&k)[4]) __attribute__((always_inline)) {
+        const v4f q4 = LdsF4(bg + L::oQ + i16 * QS + nb0 + 4 * g4);
         v4f k4;
-        if constexpr (L::KCOPY) k4 = LdsF4(bf + L::oK + i16 * QS + nb0 + 4 * g4);
+        if constexpr (L::KCOPY) k4 = LdsF4(bg + L::oK + i16 * QS + nb0 + 4 * g4);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int kr = nb0 + 4 * g4 + ks;
             q[ks] = q4[ks];                                       // q^[t = i16][key nb0 + 4 g4 + ks]
             if constexpr (L::KCOPY) k[ks] = k4[ks];               // k^[s = i16][same key]
-            else k[ks] = bf[L::oKT + kr * kTS + KtCol(kr, i16)];
+            else k[ks] = bg[L::oKT + kr * kTS + KtCol(kr, i16)];
         }
     };
-    auto products = [&](const float *bf, float *pp) __attribute__((always_inline)) {
+    auto products = [&](const float *bg, const float *bf, float *pp) __attribute__((always_inline)) {
         float qa[KBW][4], ka[KBW][4], kt[KBW][4], qx[GX > 0 ? GX : 1][4], kx[GX > 0 ? GX : 1][4];
 #pragma unroll
         for (int kb = 0; kb < KBW; ++kb) {
             const int nb0 = 16 * (KBW * w + kb);
-            load_qk(bf, nb0, qa[kb], ka[kb]);
-            const v4f t4 = LdsF4(bf + L::oKT + (nb0 + i16) * kTS + KtCol(nb0 + i16, 4 * g4));
+            load_qk(bg, nb0, qa[kb], ka[kb]);
+            const v4f t4 = LdsF4(bg + L::oKT + (nb0 + i16) * kTS + KtCol(nb0 + i16, 4 * g4));
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) kt[kb][ks] = t4[ks];   // k^[s = 4 g4 + ks][key nb0 + i16]
         }
         if (w >= 2) {
 #pragma unroll
-            for (int x = 0; x < GX; ++x) load_qk(bf, 16 * (KBW * (w - 2) + GK0 + x), qx[x], kx[x]);
+            for (int x = 0; x < GX; ++x) load_qk(bg, 16 * (KBW * (w - 2) + GK0 + x), qx[x], kx[x]);
         }
         const v4f cs = LdsF4(bf + L::oCs + 4 * g4);
         const float ecum15 = bf[L::oEcum + kC - 1];
@@ -646,8 +654,11 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     };
 
     const int nch = (T + kC - 1) / kC;
-    auto buf = [&](int j) { return smem + (j % kBufs) * L::kBuf; };
-    auto par = [&](int j) { return part + (j & 1) * L::kPart; };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    auto big = [&](auto P) { return smem + L::oBig + decltype(P)::value * L::kBig; };      // chunk parity P
+    auto par = [&](auto P) { return part + decltype(P)::value * L::kPart; };
+    auto small = [&](int j) { return smem + L::oSmall + (j % kBufs) * L::kSmall; };
     // Each role runs its own loop (the same barriers, in the same order), so
     // the registers one role carries across chunks (the state S; the
     // prefetched inputs and angle carries) never have to coexist, and no wave
@@ -668,54 +679,61 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         // every iteration landed on registers the previous stores read.
         float za[4] = {0.0f, 0.0f, 0.0f, 0.0f}, zb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         load_z(0, za);
-        products(buf(0), par(0));
+        products(big(P0{}), small(0), par(P0{}));
         __syncthreads();
         // zl: the set for chunk j's Z; zu: chunk j - 1's, finished here.  The
         // values stay in their four registers until every store is issued: a
         // store's data register rewritten behind it waits for the store to
         // complete (stores count in vmcnt on gfx950).
-        auto iter = [&](int j, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
+        // P: chunk j's parity.
+        auto iter = [&](int j, auto P, float (&zl)[4], const float (&zu)[4]) __attribute__((always_inline)) {
+            using Q = std::integral_constant<int, 1 - decltype(P)::value>;
             load_z(j * kC, zl);
-            products(buf(j), par(j));
+            products(big(P), small(j), par(P));
             float y[4];
-            finish(buf(j - 1), par(j - 1), zu, y);
+            finish(small(j - 1), par(Q{}), zu, y);
             store_y((j - 1) * kC, y);
             __syncthreads();
         };
-        for (int j = 1; j < nch; j += 2) {   // unrolled by two for the sets
-            iter(j, zb, za);
+        for (int j = 1; j < nch; j += 2) {   // unrolled by two for the sets and the parity
+            iter(j, P1{}, zb, za);
             if (j + 1 >= nch) break;
-            iter(j + 1, za, zb);
+            iter(j + 1, P0{}, za, zb);
         }
         float y[4];
-        if ((nch - 1) & 1) finish(buf(nch - 1), par(nch - 1), zb, y);
-        else finish(buf(nch - 1), par(nch - 1), za, y);
+        if ((nch - 1) & 1) finish(small(nch - 1), par(P1{}), zb, y);
+        else finish(small(nch - 1), par(P0{}), za, y);
         store_y((nch - 1) * kC, y);
     } else if (nch > 0 && product_wave) {   // waves 2 and 3: products and the shared finishing work
         __syncthreads();
-        for (int j = 0; j < nch; ++j) {
-            products(buf(j), par(j));
-            shared_finish(buf(j));
+        auto step = [&](int j, auto P) __attribute__((always_inline)) {
+            products(big(P), small(j), par(P));
+            shared_finish(small(j));
             __syncthreads();
+        };
+        for (int j = 0; j < nch; j += 2) {   // unrolled by two for the parity
+            step(j, P0{});
+            if (j + 1 >= nch) break;
+            step(j + 1, P1{});
         }
     } else if (nch > 0) {
         load_prep(0, raw0);
         if constexpr (DB) load_prep(min(1, nch - 1) * kC, raw1);
-        prep(buf(0), raw0);
+        prep(big(P0{}), small(0), raw0);
         if constexpr (!DB) load_prep(min(1, nch - 1) * kC, raw0);
         __syncthreads();
-        // unrolled by two for the register sets (chunk parity)
-        auto iter = [&](int j, Raw &ld, const Raw &pr_) __attribute__((always_inline)) {
+        // unrolled by two for the register sets and the parity (P: chunk j + 1's)
+        auto iter = [&](int j, auto P, Raw &ld, const Raw &pr_) __attribute__((always_inline)) {
             if constexpr (DB) load_prep(min(j + 2, nch - 1) * kC, ld);
-            prep(buf(j + 1), pr_);
+            prep(big(P), small(j + 1), pr_);
             if constexpr (!DB) load_prep(min(j + 2, nch - 1) * kC, ld);
             __syncthreads();
         };
         if (nch > 1) {
             for (int j = 0;; j += 2) {
-                iter(j, raw0, DB ? raw1 : raw0);
+                iter(j, P1{}, raw0, DB ? raw1 : raw0);
                 if (j + 2 >= nch) break;
-                iter(j + 1, DB ? raw1 : raw0, raw0);
+                iter(j + 1, P0{}, DB ? raw1 : raw0, raw0);
                 if (j + 3 >= nch) break;
             }
         }
@@ -745,9 +763,9 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
                              : (p.in_v != nullptr ? p.in_v[o] : 0.0f);
         }
         if (rb == 0) {
-            // the last chunk's buffer is intact: its k^T column of the last token
+            // the last chunk's tiles are intact: its k^T column of the last token
             const int tl = T > 0 ? (T - 1) - (nch - 1) * kC : 0;
-            const float *kt = smem + ((nch > 0 ? nch - 1 : 0) % kBufs) * L::kBuf + L::oKT;
+            const float *kt = smem + L::oBig + ((nch > 0 ? nch - 1 : 0) & 1) * L::kBig + L::oKT;
             for (int i = tid; i < N; i += NT) {
                 const size_t o = static_cast<size_t>(bh) * N + i;
                 p.f_k[o] = T > 0 ? kt[i * kTS + KtCol(i, tl)] : (p.in_k != nullptr ? p.in_k[o] : 0.0f);
