@@ -12,6 +12,7 @@ constexpr float kPiF = 3.14159265358979323846f;                     // reference
 constexpr double kTwoPiF = 2.0 * static_cast<double>(kPiF);         // reference kTwoPi = 2 * kPi: the wrap period
 constexpr double kRevPerRad = 0.15915494309189533577;               // 1 / (2 pi): radians -> revolutions
 constexpr double kInvTwoPiF = 1.0 / kTwoPiF;
+constexpr double kRevPerTurn = kTwoPiF * kRevPerRad;                 // turns of the wrap period -> revolutions of 2 pi
 
 // 1 / (1 + e^-x) with the hardware exp and reciprocal (about 2 ulp).
 __device__ __forceinline__ float FastSigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }

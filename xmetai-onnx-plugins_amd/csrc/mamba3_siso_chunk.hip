@@ -40,9 +40,11 @@
 // waves); one barrier per chunk.  Lane (pair lane pq, token group tg) of preparation wave w rotates the pairs
 // w PPW + PL x + pq for tokens TPL tg .. TPL tg + TPL - 1.  The angle of a
 // pair is a prefix sum over the chunk (fp64: the token groups' sums are
-// scanned across lanes) on top of the carried wrapped angle, wrapped once per token
-// with the reference's period 2 (float)pi (equal to its wrap after every step
-// in exact arithmetic; mamba3_siso.hip does the same).  Tokens past the end
+// scanned across lanes) on top of the carried wrapped angle, wrapped once per
+// token with the reference's period 2 (float)pi (equal to its wrap after every
+// step in exact arithmetic; mamba3_siso.hip does the same).  It is kept in
+// turns of that period, where an increment tanh(a) dt (float)pi is the exact
+// double tanh(a) dt / 2 and the wrap is one fract.  Tokens past the end
 // of the sequence are identity tokens: zero q, k and v, zero ADT and w.
 //
 // States, packed sequences and the look-ahead hand-over are those of the
@@ -263,7 +265,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     const int pq = lane % PL, tg = lane / PL;
     int pr[PB], qoff[PB][TPL], aoff[PB][TPL];
     float2 qbias[PB], kbias[PB];
-    double carry[PB];   // wrapped angle after the last prepared token
+    double carry[PB];   // wrapped angle after the last prepared token, in turns of the wrap period
 #pragma unroll
     for (int x = 0; x < PB; ++x) {
         pr[x] = w * PPW + PL * x + pq;
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         const float2 kb = *reinterpret_cast<const float2 *>(p.K_bias + static_cast<size_t>(h) * N + 2 * pc);
         qbias[x] = real ? qb : make_float2(0.0f, 0.0f);
         kbias[x] = real ? kb : make_float2(0.0f, 0.0f);
-        carry[x] = (p.in_angle != nullptr && rot) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + pr[x]]) : 0.0;
+        carry[x] = (p.in_angle != nullptr && rot) ? static_cast<double>(p.in_angle[static_cast<size_t>(bh) * A + pr[x]]) * kInvTwoPiF : 0.0;
 #pragma unroll
         for (int s = 0; s < TPL; ++s) {
             qoff[x][s] = real ? ((TPL * tg + s) * static_cast<int>(q_stride) + 2 * pr[x]) * 4 : kOutOfRange;
@@ -381,9 +383,12 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 #pragma unroll
         for (int x = 0; x < PB; ++x) {
             double pre[TPL], acc = 0.0;
+            // The angle in turns of the wrap period 2 (float)pi (reference
+            // :26-28): the increment tanh(a) dt (float)pi is tanh(a) dt / 2
+            // turns, exact in double (a product of two floats).
 #pragma unroll
             for (int s = 0; s < TPL; ++s) {
-                acc += static_cast<double>(TanhF(ang[x][s])) * static_cast<double>(dts[s]) * static_cast<double>(kPiF);
+                acc += static_cast<double>(0.5f * TanhF(ang[x][s])) * static_cast<double>(dts[s]);
                 pre[s] = acc;
             }
             // exclusive prefix of the token groups' sums (lanes pq + PL tg)
@@ -396,9 +401,9 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 #pragma unroll
             for (int s = 0; s < TPL; ++s) {
                 th = base + pre[s];
-                th -= kTwoPiF * floor(th * kInvTwoPiF);   // wrap_two_pi (reference :26-28)
+                th = __builtin_amdgcn_fract(th);   // wrap_two_pi (reference :26-28), in turns: th - floor(th), kept below 1
                 // a pair without an angle keeps theta = 0: sin 0 = 0, cos 0 = 1
-                const float rev = static_cast<float>(th * kRevPerRad);
+                const float rev = static_cast<float>(th * kRevPerTurn);
                 const float sn = __builtin_amdgcn_sinf(rev), c = __builtin_amdgcn_cosf(rev);
                 const float2 q = make_float2(qv[x][s].x + qbias[x].x, qv[x][s].y + qbias[x].y);
                 const float2 k = make_float2(kv[x][s].x + kbias[x].x, kv[x][s].y + kbias[x].y);
@@ -755,7 +760,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 #pragma unroll
             for (int x = 0; x < PB; ++x)
                 if (tg == 0 && pr[x] < A)
-                    p.f_angle[static_cast<size_t>(bh) * A + pr[x]] = static_cast<float>(carry[x]);
+                    p.f_angle[static_cast<size_t>(bh) * A + pr[x]] = static_cast<float>(carry[x] * kTwoPiF);
         }
         if (tid < kRows && r0 + tid < P) {
             const size_t o = static_cast<size_t>(bh) * P + r0 + tid;
