@@ -329,10 +329,19 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     // register sets (chunk parity), or, where registers are short (more than
     // 128 keys), one chunk ahead into one set.
     constexpr bool DB = KBW <= 2;
+    // The preparation wave that also forms the per-token scalars (gamma, w,
+    // the decay scan and its exponentials).  With 8 preparation waves the one
+    // on SIMD 2 (waves w of a role sit on SIMD w % 4), the SIMD a per-wave
+    // barrier-arrival trace shows with spare issue (4 x 4096 x 32 heads, 128
+    // keys: 0.356 -> 0.354 ms against the last wave, on SIMD 3).  With 4 the
+    // last: on SIMD 0 instead, where the trace also showed spare issue, it
+    // measured slower (64 keys 0.241 -> 0.265 ms, 192 keys 0.623 -> 0.650,
+    // 256 keys 0.754 -> 0.764).
+    constexpr int kScalarWave = NPW == 8 ? 6 : NPW - 1;
     struct Raw {
         float2 qv[PB][TPL], kv[PB][TPL];
         float ang[PB][TPL], dts[TPL], vreg[VPT];
-        float sdt, strap, sadt, sdt1, strap1;   // preparation wave 3, lane t < kC
+        float sdt, strap, sadt, sdt1, strap1;   // preparation wave kScalarWave, lane t < kC
     };
     Raw raw0, raw1;
     auto load_prep = [&](int c0, Raw &r) __attribute__((always_inline)) {
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         }
 #pragma unroll
         for (int u = 0; u < VPT; ++u) vreg[u] = ld(v_, voff[u], cv);
-        // every preparation wave loads them (same load count on every path); wave NPW-1 uses them
+        // every preparation wave loads them (same load count on every path); wave kScalarWave uses them
         r.sdt = ld(d_, i16 * 4, cd);
         r.strap = ld(t_, i16 * 4, cd);
         r.sadt = ld(ad_, i16 * 4, cd);
@@ -447,7 +456,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
         }
 #pragma unroll
         for (int u = 0; u < VPT; ++u) bf[L::oVT + vrow[u] * kTS + vtok[u]] = vreg[u];
-        if (w == NPW - 1) {
+        if (w == kScalarWave) {
             const float gam = r.sdt * FastSigmoid(r.strap);
             const float look = r.sdt1 * (1.0f - FastSigmoid(r.strap1));   // zero DT past the end
             const float cum = RowInclusiveScan16(r.sadt);   // over the chunk's 16 tokens (lanes 0-15)
