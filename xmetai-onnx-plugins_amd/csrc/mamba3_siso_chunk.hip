@@ -203,7 +203,9 @@ __device__ __forceinline__ float RowInclusiveScan16(float x) {
 // LONG: some tensor's token rows of one sequence span 2 GiB or more, beyond a
 // buffer descriptor's 32-bit range; every chunk then reads and writes through
 // descriptors that start at its own first token.
-template <int KBW, int NW, int NPW, bool LONG>
+// HASZ: a Z input (the SiLU gate); without one the finishing waves issue no Z
+// loads and no gate.
+template <int KBW, int NW, int NPW, bool LONG, bool HASZ>
 __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoParams p) {
     using L = M3CLayout<KBW, NW, NPW>;
     static_assert(NW == 4, "product waves 0 and 1 finish, 2 and 3 take shared work off them");
@@ -589,10 +591,8 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     const Rsrc rz = MakeRsrc(p.Z != nullptr ? p.Z + vbase : p.out, p.Z != nullptr ? seq_bytes(v_stride) : 0);
     const Rsrc ro = MakeRsrc(p.out + vbase, seq_bytes(v_stride));
     const Rsrc rnone = MakeRsrc(p.out, 0);   // every access dropped
-    // Issued whether or not there is a Z (then every load reads zero): paths
-    // with and without the loads would leave the compiler's wait counts at
-    // the smaller one.
     auto load_z = [&](int c0, float (&zr)[4]) __attribute__((always_inline)) {
+        if constexpr (!HASZ) return;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (LONG) zr[r] = BufF(p.Z != nullptr ? chunk_rsrc(p.Z + vbase, v_stride, c0) : rnone, ooff[r]);
@@ -640,7 +640,7 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             y[r] = acc[r];
-            if (p.Z != nullptr) y[r] *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
+            if constexpr (HASZ) y[r] *= zr[r] * FastSigmoid(zr[r]);   // silu gate (reference :155-158)
         }
     };
 
@@ -788,15 +788,21 @@ __global__ __launch_bounds__(64 * (NW + NPW)) void Mamba3ChunkKernel(Mamba3SisoP
     }
 }
 
-template <int KBW, int NW, int NPW, bool LONG>
-void LaunchChunkL(const Mamba3SisoParams &p, hipStream_t stream) {
+template <int KBW, int NW, int NPW, bool LONG, bool HASZ>
+void LaunchChunkZ(const Mamba3SisoParams &p, hipStream_t stream) {
     using L = M3CLayout<KBW, NW, NPW>;
     const long long blocks = static_cast<long long>(p.batch) * p.nheads * ((p.p + kRows - 1) / kRows);
     if (blocks > 2147483647LL) throw Error(XM_ERR_INVALID_ARGUMENT, "Mamba3SisoFn launch exceeds the grid limit");
-    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW, LONG>), static_cast<int>(L::kBytes));
+    EnsureDynamicLds(reinterpret_cast<const void *>(&Mamba3ChunkKernel<KBW, NW, NPW, LONG, HASZ>), static_cast<int>(L::kBytes));
     XM_NOTE_LAUNCH("Mamba3ChunkKernel", {}, KBW, NW, NPW, LONG);
-    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NW, NPW, LONG>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT), L::kBytes,
-                       stream, p);
+    hipLaunchKernelGGL((Mamba3ChunkKernel<KBW, NW, NPW, LONG, HASZ>), dim3(static_cast<unsigned>(blocks)), dim3(L::NT),
+                       L::kBytes, stream, p);
+}
+
+template <int KBW, int NW, int NPW, bool LONG>
+void LaunchChunkL(const Mamba3SisoParams &p, hipStream_t stream) {
+    if (p.Z != nullptr) LaunchChunkZ<KBW, NW, NPW, LONG, true>(p, stream);
+    else LaunchChunkZ<KBW, NW, NPW, LONG, false>(p, stream);
 }
 
 template <int KBW, int NW, int NPW>
